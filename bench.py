@@ -1,0 +1,203 @@
+"""Benchmark of the DeepSeek-V4 attention pre-processing hot path on one MI355X.
+
+A "step" is one call of fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert over
+one batch of the headline workload c2 (T=8192 prefill tokens from 4 sequences,
+H=64, D=512, rope 64, 16384 x 64-slot FP8 cache), inputs already resident in
+HBM.  Prints ONE JSON line with tokens/s, the HBM roofline fraction of the
+kernel (algorithmic bytes / HIP-event kernel time / 8 TB/s) and the reference
+PyTorch path timed on this host's CPU cores on a bounded sample of the same
+workload.
+
+    python bench.py [--steps K] [--warmup W] [--config 0..4] [--op main|inv_rope]
+"""
+import argparse
+import json
+import os
+import re
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for p in (os.path.join(ROOT, "flaggems-vllm_amd"), ROOT):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+METRIC = "tokens/s and achieved HBM GB/s (% of roofline) at T=8192, H=64, D=512"
+HBM_PEAK_GBPS = 8000.0
+PROFILES = os.path.join(ROOT, "profiles")
+
+
+def parse_args():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", type=int, default=2, help="main-op workload c0..c4 (default c2)")
+    ap.add_argument("--op", choices=["main", "inv_rope"], default="main")
+    ap.add_argument("--tma", action="store_true", help="inv_rope: packed UE8M0 scales")
+    ap.add_argument("--cpu-sample-tokens", type=int, default=2048)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    return ap.parse_args()
+
+
+def measured_traffic(kernel: str, workload: str):
+    """HBM bytes per launch from the committed rocprofv3 PMC summary
+    profiles/<kernel>_<workload>_pmc.md (line 'traffic_bytes_per_launch: N'),
+    or None when no such summary exists."""
+    path = os.path.join(PROFILES, f"{kernel}_{workload}_pmc.md")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", f.read())
+    return float(m.group(1)) if m else None
+
+
+def time_gpu(fn, steps, warmup):
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(steps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return wall / steps, start.elapsed_time(end) / 1000.0 / steps
+
+
+def cpu_baseline_main(w, sample_tokens):
+    """The reference's PyTorch formulation (oracle.torch_ref) on the host CPU,
+    over the first `sample_tokens` tokens of the workload with all heads;
+    median of 3 runs, tokens/s."""
+    import torch
+
+    from oracle import torch_ref
+
+    n = min(sample_tokens, w.num_tokens)
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    times = []
+    for _ in range(3):
+        q = w.q[:n].clone()
+        cache = w.k_cache  # CPU copy; the GPU has its own
+        t0 = time.perf_counter()
+        torch_ref.qnorm_rope_kv_insert(q, w.kv[:n], cache, w.slot_mapping[:n], w.position_ids[:n],
+                                       w.cos_sin_cache, w.eps, w.block_size)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    return {"value": n / t, "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"first {n} of {w.num_tokens} tokens of {w.name}, all {w.num_heads} heads, "
+                      f"torch CPU restatement of the reference's torch oracle, median of 3 "
+                      f"({t:.2f} s per run)"}
+
+
+def cpu_baseline_inv(w, tma, sample_tokens):
+    import torch
+
+    from oracle import torch_ref
+
+    n = min(sample_tokens, w.o.shape[0])
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        torch_ref.inv_rope_fp8_quant(w.o[:n], w.positions[:n], w.cos_sin_cache, w.n_groups,
+                                     w.heads_per_group, tma_aligned_scales=tma)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    return {"value": n / t, "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"first {n} of {w.o.shape[0]} tokens, torch CPU restatement, median of 3 "
+                      f"({t:.2f} s per run)"}
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this op needs no exchange between GPUs "
+              "(tokens and heads shard independently), and this build runs on single-GPU "
+              "boxes. Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import flaggems_vllm
+    from flaggems_vllm import testing as W
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    if args.op == "main":
+        w_cpu = W.make_workload(args.config)
+        w = w_cpu.to(dev)
+        T, H, nv = w.num_tokens, w.num_heads, w.num_inserted
+        bytes_call = w.bytes_per_call()
+        a = w.args()
+
+        def step():
+            flaggems_vllm.fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert(*a)
+
+        kernel = "qnorm_rope_kv_insert_kernel"
+        workload = f"c{args.config}"
+        config = {"workload": f"c{args.config}: fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert, "
+                              f"T={T}, H={H}, D=512 (448 nope + 64 rope), kv rows inserted={nv}, "
+                              f"cache {w.k_cache.shape[0]} blocks x {w.block_size} slots x 584 B",
+                  "num_tokens": T, "num_heads": H, "head_dim": 512, "rope_dim": 64,
+                  "inserted_tokens": nv, "cache_block_size": w.block_size,
+                  "io": "bf16 q/kv in, bf16 q out, fp8-e4m3 + UE8M0 cache"}
+    else:
+        w_cpu = W.make_inv_rope_workload(8192, 64, 8, seed=0)
+        w = w_cpu.to(dev)
+        T, H = w.o.shape[0], w.o.shape[1]
+        bytes_call = W.inv_rope_bytes(T, H, args.tma)
+
+        def step():
+            flaggems_vllm.fused_inv_rope_fp8_quant(w.o, w.positions, w.cos_sin_cache, w.n_groups,
+                                                   w.heads_per_group, tma_aligned_scales=args.tma)
+
+        kernel = "inv_rope_fp8_quant_kernel"
+        workload = "T8192_H64_G8" + ("_ue8m0" if args.tma else "_f32")
+        config = {"workload": f"fused_inv_rope_fp8_quant T={T}, H={H}, G=8, "
+                              f"{'packed UE8M0' if args.tma else 'fp32'} scales",
+                  "num_tokens": T, "num_heads": H, "n_groups": 8}
+
+    ms_step, t_kernel = time_gpu(step, args.steps, args.warmup)
+    achieved = bytes_call / t_kernel / 1e9
+    traffic = measured_traffic(kernel, workload)
+    result = {
+        "metric": METRIC,
+        "value": T / ms_step,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_step * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: seeded N(0,1) bf16 q/kv, fp32 cos/sin (theta 1e4), vLLM-style paged slots",
+        "config": config,
+        "kernel_us": t_kernel * 1e6,
+        "gbps": achieved,
+        "bytes_per_call": bytes_call,
+        "bytes_per_token": bytes_call / T,
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic,
+                     "kernel": kernel},
+    }
+    if not args.no_cpu_baseline:
+        if args.op == "main":
+            result["cpu_baseline"] = cpu_baseline_main(w_cpu, args.cpu_sample_tokens)
+        else:
+            result["cpu_baseline"] = cpu_baseline_inv(w_cpu, args.tma, args.cpu_sample_tokens)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,235 @@
+// gfx950 kernel for the fused DeepSeek-V4 inverse RoPE + per-128 FP8 quant of
+// the attention output, ahead of the grouped FP8 output projection.
+//
+// Reference semantics: src/flaggems_vllm/ops/fused_inv_rope_fp8_quant.py:37-256
+// and its torch oracle tests/test_fused_inv_rope_fp8_quant.py:150-198.  The
+// rotated rope values are rounded to bf16 before the amax and the quant, as the
+// torch oracle does (the Triton kernel keeps them in fp32); this makes codes
+// and scales equal to the oracle's bit for bit.
+//
+// Workgroups of 256 threads own kRowsPerBlock (token, head) rows; each row is
+// one 16-lane DPP row holding four 128-element chunks, one per 16-byte piece k
+// (see fgv_device.h), so a chunk's amax is one 16-lane DPP max.  One extra
+// workgroup zeroes the scales of the padding tokens T..Tpad-1.
+#include "fgv_device.h"
+#include "fgv_host.h"
+
+namespace fgv {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kRowsPerPass = kThreads / 16;
+constexpr int kPasses = 2;
+constexpr int kRowsPerBlock = kRowsPerPass * kPasses;
+
+struct InvRopeArgs {
+    const uint16_t* o;
+    const int64_t* positions;
+    const float* cos_sin;
+    uint8_t* fp8;
+    void* scale;
+    int64_t o_st, o_sh;
+    int64_t cs_stride, max_pos;
+    int64_t fp8_sg, fp8_st;
+    int64_t sc_sg, sc_sk;
+    uint32_t num_rows;     // num_tokens * num_heads
+    uint32_t num_heads, heads_per_group;
+    uint32_t num_tokens, padded_tokens, n_groups;
+    uint32_t row_blocks;
+    float eps;
+    int tma;
+};
+
+__device__ __forceinline__ void unpack8(uint4 v, float (&x)[8]) {
+    x[0] = bf16_lo(v.x); x[1] = bf16_hi(v.x);
+    x[2] = bf16_lo(v.y); x[3] = bf16_hi(v.y);
+    x[4] = bf16_lo(v.z); x[5] = bf16_hi(v.z);
+    x[6] = bf16_lo(v.w); x[7] = bf16_hi(v.w);
+}
+
+// Inverse GPT-J rotation of four pairs, separately rounded binary32, result
+// rounded to bf16 and widened back (the values the quantiser sees).
+__device__ __forceinline__ void inv_rope_piece(float (&x)[8], float4 c, float4 s) {
+    const float cc[4] = {c.x, c.y, c.z, c.w};
+    const float ss[4] = {s.x, s.y, s.z, s.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float e = x[2 * i], o = x[2 * i + 1];
+        float ec = e * cc[i], os = o * ss[i];
+        float oc = o * cc[i], es = e * ss[i];
+        uint32_t w = pack_bf16x2(ec + os, oc - es);
+        x[2 * i] = bf16_lo(w);
+        x[2 * i + 1] = bf16_hi(w);
+    }
+}
+
+__device__ void row_block(const InvRopeArgs& a, uint32_t rb, int lane16, int row_in_pass) {
+    uint4 v[kPasses][4];
+    float4 cs_c[kPasses], cs_s[kPasses];
+    uint32_t tok[kPasses], head[kPasses];
+    bool valid[kPasses];
+    const bool rope_lane = lane16 >= 8;
+
+#pragma unroll
+    for (int p = 0; p < kPasses; ++p) {
+        uint32_t row = rb * kRowsPerBlock + p * kRowsPerPass + row_in_pass;
+        valid[p] = row < a.num_rows;
+        tok[p] = valid[p] ? row / a.num_heads : 0;
+        head[p] = valid[p] ? row - tok[p] * a.num_heads : 0;
+        if (valid[p]) {
+            const uint16_t* x = a.o + (int64_t)tok[p] * a.o_st + (int64_t)head[p] * a.o_sh;
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                v[p][k] = load16(x + (lane16 + 16 * k) * 8);
+            if (rope_lane) {
+                int64_t pos = clamp_position(a.positions[tok[p]], a.max_pos);
+                const float* cs = a.cos_sin + pos * a.cs_stride + (lane16 - 8) * 4;
+                cs_c[p] = *reinterpret_cast<const float4*>(cs);
+                cs_s[p] = *reinterpret_cast<const float4*>(cs + kHalfRope);
+            }
+        }
+    }
+
+    const float inv_max = (float)(1.0 / 448.0);
+    const uint32_t eps_bits = __float_as_uint(a.eps);
+#pragma unroll
+    for (int p = 0; p < kPasses; ++p) {
+        if (!valid[p])
+            continue;
+        const uint32_t t = tok[p];
+        const uint32_t g = head[p] / a.heads_per_group;
+        const uint32_t hig = head[p] - g * a.heads_per_group;
+        uint8_t* out = a.fp8 + (int64_t)g * a.fp8_sg + (int64_t)t * a.fp8_st + hig * kHeadDim;
+        uint32_t packed = 0;
+        float my_scale = 0.0f;  // lane k (k < 4) keeps chunk k's fp32 scale
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            float x[8];
+            unpack8(v[p][k], x);
+            if (k == 3 && rope_lane)
+                inv_rope_piece(x, cs_c[p], cs_s[p]);
+            uint32_t m = 0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                m = max(m, __float_as_uint(x[i]) & 0x7fffffffu);
+            m = row16_max(m);
+            m = m > eps_bits ? m : eps_bits;  // max(amax, eps), eps > 0
+            float sc = __uint_as_float(m) * inv_max;
+            uint32_t lo, hi;
+            if (a.tma) {
+                // 2^ceil(log2(max(sc, 1e-10))) from the binary32 fields.
+                uint32_t b = __float_as_uint(sc);
+                b = b > 0x2EDBE6FFu ? b : 0x2EDBE6FFu;  // 1e-10f
+                int e = (int)(b >> 23) - 127 + ((b & 0x7fffffu) ? 1 : 0);
+                packed |= (uint32_t)(e + 127) << (8 * k);
+                const float inv = exp2_neg_int(e);
+                lo = pack_fp8x4(clamp_fp8(x[0] * inv), clamp_fp8(x[1] * inv),
+                                clamp_fp8(x[2] * inv), clamp_fp8(x[3] * inv));
+                hi = pack_fp8x4(clamp_fp8(x[4] * inv), clamp_fp8(x[5] * inv),
+                                clamp_fp8(x[6] * inv), clamp_fp8(x[7] * inv));
+            } else {
+                if (lane16 == k)
+                    my_scale = sc;
+                lo = pack_fp8x4(clamp_fp8(x[0] / sc), clamp_fp8(x[1] / sc),
+                                clamp_fp8(x[2] / sc), clamp_fp8(x[3] / sc));
+                hi = pack_fp8x4(clamp_fp8(x[4] / sc), clamp_fp8(x[5] / sc),
+                                clamp_fp8(x[6] / sc), clamp_fp8(x[7] / sc));
+            }
+            store8(out + (lane16 + 16 * k) * 8, lo, hi);
+        }
+        if (a.tma) {
+            if (lane16 == 0)
+                static_cast<int32_t*>(a.scale)[(int64_t)g * a.sc_sg + (int64_t)hig * a.sc_sk + t] =
+                    (int32_t)packed;
+        } else if (lane16 < 4) {
+            static_cast<float*>(a.scale)[(int64_t)g * a.sc_sg +
+                                         (int64_t)(hig * 4 + lane16) * a.sc_sk + t] = my_scale;
+        }
+    }
+}
+
+// Zero the scales of padding tokens T..Tpad-1 (ops/fused_inv_rope_fp8_quant.py:69-88).
+__device__ void pad_block(const InvRopeArgs& a) {
+    const uint32_t per_group = a.tma ? a.heads_per_group : a.heads_per_group * 4;
+    const uint32_t npad = a.padded_tokens - a.num_tokens;
+    const uint32_t total = a.n_groups * per_group * npad;
+    for (uint32_t i = threadIdx.x; i < total; i += kThreads) {
+        uint32_t tp = i % npad, rest = i / npad;
+        uint32_t k = rest % per_group, g = rest / per_group;
+        int64_t off = (int64_t)g * a.sc_sg + (int64_t)k * a.sc_sk + a.num_tokens + tp;
+        static_cast<uint32_t*>(a.scale)[off] = 0u;  // 0.0f and int32 0 share bits
+    }
+}
+
+__global__ void __launch_bounds__(kThreads)
+inv_rope_fp8_quant_kernel(InvRopeArgs a) {
+    if (blockIdx.x < a.row_blocks)
+        row_block(a, blockIdx.x, threadIdx.x & 15, threadIdx.x >> 4);
+    else
+        pad_block(a);
+}
+
+}  // namespace
+}  // namespace fgv
+
+extern "C" int fgv_inv_rope_fp8_quant(
+    const void* o, int64_t o_stride_token, int64_t o_stride_head,
+    const int64_t* positions,
+    const float* cos_sin_cache, int64_t cos_sin_stride, int64_t max_pos,
+    int64_t num_tokens, int64_t n_groups, int64_t heads_per_group,
+    void* fp8_out, int64_t fp8_stride_group, int64_t fp8_stride_token,
+    void* scale_out, int64_t scale_stride_group, int64_t scale_stride_k,
+    int64_t padded_tokens, float eps, int tma_aligned_scales,
+    void* stream) {
+    using namespace fgv;
+    if (num_tokens < 0 || n_groups <= 0 || heads_per_group <= 0)
+        return fail(FGV_E_BAD_SHAPE, "bad num_tokens, n_groups or heads_per_group");
+    if (padded_tokens < num_tokens || padded_tokens > num_tokens + 3)
+        return fail(FGV_E_BAD_SHAPE, "padded_tokens must be num_tokens rounded up to 4");
+    const int64_t num_heads = n_groups * heads_per_group;
+    const int64_t rows = num_tokens * num_heads;
+    if (rows > 0x7fffffffLL || padded_tokens * num_heads * 4 > 0x7fffffffLL)
+        return fail(FGV_E_TOO_LARGE, "num_tokens * num_heads must be below 2^29");
+    if (padded_tokens == 0)
+        return FGV_OK;
+    if (!scale_out || (rows > 0 && (!o || !positions || !cos_sin_cache || !fp8_out)))
+        return fail(FGV_E_NULL_POINTER, "null pointer argument");
+    if (max_pos <= 0 && rows > 0)
+        return fail(FGV_E_BAD_SHAPE, "cos_sin_cache has no rows");
+    if (!(eps > 0.0f))
+        return fail(FGV_E_BAD_SHAPE, "eps must be positive");
+    if (!aligned(o, 16) || !aligned(cos_sin_cache, 16) || !aligned(fp8_out, 8) ||
+        !aligned(scale_out, 4))
+        return fail(FGV_E_MISALIGNED, "o and cos_sin_cache must be 16-byte aligned, fp8_out 8");
+    if (o_stride_token % 8 || o_stride_head % 8 || cos_sin_stride % 4 ||
+        fp8_stride_group % 8 || fp8_stride_token % 8)
+        return fail(FGV_E_BAD_STRIDE, "o/fp8 strides must be multiples of 8, cos_sin of 4");
+
+    InvRopeArgs a;
+    a.o = static_cast<const uint16_t*>(o);
+    a.positions = positions;
+    a.cos_sin = cos_sin_cache;
+    a.fp8 = static_cast<uint8_t*>(fp8_out);
+    a.scale = scale_out;
+    a.o_st = o_stride_token;
+    a.o_sh = o_stride_head;
+    a.cs_stride = cos_sin_stride;
+    a.max_pos = max_pos;
+    a.fp8_sg = fp8_stride_group;
+    a.fp8_st = fp8_stride_token;
+    a.sc_sg = scale_stride_group;
+    a.sc_sk = scale_stride_k;
+    a.num_rows = (uint32_t)rows;
+    a.num_heads = (uint32_t)num_heads;
+    a.heads_per_group = (uint32_t)heads_per_group;
+    a.num_tokens = (uint32_t)num_tokens;
+    a.padded_tokens = (uint32_t)padded_tokens;
+    a.n_groups = (uint32_t)n_groups;
+    a.row_blocks = (uint32_t)((rows + kRowsPerBlock - 1) / kRowsPerBlock);
+    a.eps = eps;
+    a.tma = tma_aligned_scales ? 1 : 0;
+    const uint32_t grid = a.row_blocks + (padded_tokens > num_tokens ? 1u : 0u);
+    hipLaunchKernelGGL(inv_rope_fp8_quant_kernel, dim3(grid), dim3(kThreads), 0,
+                       static_cast<hipStream_t>(stream), a);
+    return launch_status();
+}

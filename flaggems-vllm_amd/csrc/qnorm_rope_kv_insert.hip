@@ -1,0 +1,298 @@
+// gfx950 kernel for the fused DeepSeek-V4 q RMSNorm + RoPE and kv RoPE +
+// UE8M0 FP8 quant + paged-cache insert.
+//
+// Reference semantics: src/flaggems_vllm/ops/fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert.py
+//   q branch  :61-72, 79-97   kv branch :74-93, 98-286   wrapper :289-351
+//
+// One launch, two kinds of workgroup (256 threads = 4 waves = 16 DPP rows):
+//   blocks [0, kv_blocks)          : 16 tokens' kv rows each -> k_cache
+//   blocks [kv_blocks, grid)       : kQRowsPerBlock q rows each, in place
+// Each 1 KiB row is owned by one 16-lane DPP row (see fgv_device.h).  The op
+// is HBM bound (about 98.6% of its bytes are the in-place q read and write),
+// so the q blocks keep two passes of four 16-byte loads per lane in flight and
+// do the per-row math with DPP reductions only.
+#include "fgv_device.h"
+#include "fgv_host.h"
+
+namespace fgv {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kRowsPerPass = kThreads / 16;   // 16 rows per pass
+constexpr int kQPasses = 2;
+constexpr int kQRowsPerBlock = kRowsPerPass * kQPasses;
+constexpr int kKvTokensPerBlock = kRowsPerPass;
+
+struct QnormArgs {
+    uint16_t* q;
+    const uint16_t* kv;
+    uint8_t* k_cache;
+    const int64_t* slot_mapping;
+    const int64_t* positions;
+    const float* cos_sin;
+    int64_t q_st, q_sh, kv_st;
+    int64_t block_stride, num_blocks, block_size;
+    int64_t cs_stride, max_pos;
+    uint32_t num_q_rows;       // num_tokens * num_heads
+    uint32_t num_heads;
+    uint32_t num_tokens_insert;
+    uint32_t kv_blocks;
+    float eps;
+};
+
+// RMSNorm factor r = 1/sqrt(mean(x^2) + eps) of the row owned by this lane's
+// 16-lane group.  The sum of squares is accumulated in binary64 (squares of
+// bf16 values are exact there), so it does not depend on the reduction order;
+// mean and rsqrt are then correctly rounded to binary32.
+__device__ __forceinline__ float rms_factor(const uint4 (&v)[4], float eps) {
+    double s = 0.0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t w[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            double a = (double)bf16_lo(w[i]);
+            double b = (double)bf16_hi(w[i]);
+            s = __builtin_fma(a, a, s);
+            s = __builtin_fma(b, b, s);
+        }
+    }
+    s = row16_sum(s);
+    float var = (float)(s * (1.0 / kHeadDim));
+    var = var + eps;
+    return (float)(1.0 / __builtin_sqrt((double)var));
+}
+
+// GPT-J rotation of the four (even, odd) pairs in one 16-byte piece of bf16,
+// each product and sum rounded to binary32 separately (no FMA contraction;
+// the file is built with -ffp-contract=off), then packed to bf16 with RNE.
+__device__ __forceinline__ uint4 rope_piece(const float (&x)[8], float4 c, float4 s) {
+    const float cc[4] = {c.x, c.y, c.z, c.w};
+    const float ss[4] = {s.x, s.y, s.z, s.w};
+    uint32_t out[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float e = x[2 * i], o = x[2 * i + 1];
+        float ec = e * cc[i], os = o * ss[i];
+        float es = e * ss[i], oc = o * cc[i];
+        out[i] = pack_bf16x2(ec - os, es + oc);
+    }
+    return make_uint4(out[0], out[1], out[2], out[3]);
+}
+
+__device__ __forceinline__ void unpack8(uint4 v, float (&x)[8]) {
+    x[0] = bf16_lo(v.x); x[1] = bf16_hi(v.x);
+    x[2] = bf16_lo(v.y); x[3] = bf16_hi(v.y);
+    x[4] = bf16_lo(v.z); x[5] = bf16_hi(v.z);
+    x[6] = bf16_lo(v.w); x[7] = bf16_hi(v.w);
+}
+
+__device__ void q_block(const QnormArgs& a, uint32_t qb, int lane16, int row_in_pass) {
+    uint4 v[kQPasses][4];
+    float4 cs_c[kQPasses], cs_s[kQPasses];
+    uint16_t* rowp[kQPasses];
+    bool valid[kQPasses];
+    const bool rope_lane = lane16 >= 8;
+
+#pragma unroll
+    for (int p = 0; p < kQPasses; ++p) {
+        uint32_t row = qb * kQRowsPerBlock + p * kRowsPerPass + row_in_pass;
+        valid[p] = row < a.num_q_rows;
+        uint32_t t = valid[p] ? row / a.num_heads : 0;
+        uint32_t h = valid[p] ? row - t * a.num_heads : 0;
+        rowp[p] = a.q + (int64_t)t * a.q_st + (int64_t)h * a.q_sh;
+        if (valid[p]) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                v[p][k] = load16(rowp[p] + (lane16 + 16 * k) * 8);
+            if (rope_lane) {
+                int64_t pos = clamp_position(a.positions[t], a.max_pos);
+                const float* cs = a.cos_sin + pos * a.cs_stride + (lane16 - 8) * 4;
+                cs_c[p] = *reinterpret_cast<const float4*>(cs);
+                cs_s[p] = *reinterpret_cast<const float4*>(cs + kHalfRope);
+            }
+        }
+    }
+
+#pragma unroll
+    for (int p = 0; p < kQPasses; ++p) {
+        if (!valid[p])
+            continue;
+        const float r = rms_factor(v[p], a.eps);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            float x[8];
+            unpack8(v[p][k], x);
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                x[i] = x[i] * r;
+            uint4 out;
+            if (k == 3 && rope_lane) {
+                out = rope_piece(x, cs_c[p], cs_s[p]);
+            } else {
+                out = make_uint4(pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3]),
+                                 pack_bf16x2(x[4], x[5]), pack_bf16x2(x[6], x[7]));
+            }
+            store16(rowp[p] + (lane16 + 16 * k) * 8, out);
+        }
+    }
+}
+
+// UE8M0 exponent of a 64-element group: ceil(log2(max(amax, 1e-4) / 448)).
+// With a = m * 2^E (1 <= m < 2) and 448 = 1.75 * 2^8 this is
+// E - 8 + (m > 1.75), read straight from the binary32 fields of a.
+__device__ __forceinline__ int kv_group_exponent(uint32_t amax_bits) {
+    const uint32_t kFloor = 0x38D1B717u;  // 1e-4f
+    uint32_t a = amax_bits > kFloor ? amax_bits : kFloor;
+    int e = (int)(a >> 23) - 127;
+    return e - 8 + ((a & 0x7fffffu) > 0x600000u ? 1 : 0);
+}
+
+__device__ void kv_block(const QnormArgs& a, uint32_t kvb, int lane16, int row_in_pass) {
+    const uint32_t t = kvb * kKvTokensPerBlock + row_in_pass;
+    if (t >= a.num_tokens_insert)
+        return;
+    const int64_t slot = a.slot_mapping[t];
+    if (slot < 0)
+        return;
+    const int64_t blk = slot / a.block_size;
+    const int64_t pib = slot - blk * a.block_size;
+    if (blk >= a.num_blocks)
+        return;
+
+    const uint16_t* x = a.kv + (int64_t)t * a.kv_st;
+    uint4 v[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        v[k] = load16(x + (lane16 + 16 * k) * 8);
+    const bool rope_lane = lane16 >= 8;
+    float4 c = make_float4(0.f, 0.f, 0.f, 0.f), s = c;
+    if (rope_lane) {
+        int64_t pos = clamp_position(a.positions[t], a.max_pos);
+        const float* cs = a.cos_sin + pos * a.cs_stride + (lane16 - 8) * 4;
+        c = *reinterpret_cast<const float4*>(cs);
+        s = *reinterpret_cast<const float4*>(cs + kHalfRope);
+    }
+
+    uint8_t* base = a.k_cache + blk * a.block_stride;
+    uint8_t* tok = base + pib * kTokenDataBytes;
+    uint8_t* scl = base + a.block_size * kTokenDataBytes + pib * kScaleBytesPerToken;
+
+    uint32_t my_bytes = 0;  // byte k = scale byte of the group in piece k
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        float xf[8];
+        unpack8(v[k], xf);
+        uint32_t m = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            m = max(m, __float_as_uint(xf[i]) & 0x7fffffffu);
+        m = row8_max(m);  // lanes 0..7: group 2k, lanes 8..15: group 2k+1
+        const int e = kv_group_exponent(m);
+        const float inv = exp2_neg_int(e);  // exact, so x * 2^-e == x / 2^e
+        const int enc = e + 127;
+        my_bytes |= (uint32_t)(enc < 0 ? 0 : (enc > 255 ? 255 : enc)) << (8 * k);
+        if (k == 3 && rope_lane) {
+            uint4 r = rope_piece(xf, c, s);
+            uint8_t* dst = tok + kNopeDim + (lane16 - 8) * 16;
+            store8(dst, r.x, r.y);
+            store8(dst + 8, r.z, r.w);
+        } else {
+            uint32_t lo = pack_fp8x4(clamp_fp8(xf[0] * inv), clamp_fp8(xf[1] * inv),
+                                     clamp_fp8(xf[2] * inv), clamp_fp8(xf[3] * inv));
+            uint32_t hi = pack_fp8x4(clamp_fp8(xf[4] * inv), clamp_fp8(xf[5] * inv),
+                                     clamp_fp8(xf[6] * inv), clamp_fp8(xf[7] * inv));
+            store8(tok + (lane16 + 16 * k) * 8, lo, hi);
+        }
+    }
+    // Lane 0 holds groups 0,2,4,6 and lane 8 holds groups 1,3,5: gather the
+    // seven scale bytes plus the zero pad byte into one 8-byte store.
+    const uint32_t other = dpp_u32<kDppRowRor8>(my_bytes);
+    if (lane16 == 0) {
+        uint32_t lo = (my_bytes & 0xffu) | ((other & 0xffu) << 8) |
+                      ((my_bytes & 0xff00u) << 8) | ((other & 0xff00u) << 16);
+        uint32_t hi = ((my_bytes >> 16) & 0xffu) | (((other >> 16) & 0xffu) << 8) |
+                      (((my_bytes >> 24) & 0xffu) << 16);
+        store8(scl, lo, hi);
+    }
+}
+
+__global__ void __launch_bounds__(kThreads)
+qnorm_rope_kv_insert_kernel(QnormArgs a) {
+    const int lane16 = threadIdx.x & 15;
+    const int row_in_pass = threadIdx.x >> 4;
+    if (blockIdx.x < a.kv_blocks)
+        kv_block(a, blockIdx.x, lane16, row_in_pass);
+    else
+        q_block(a, blockIdx.x - a.kv_blocks, lane16, row_in_pass);
+}
+
+}  // namespace
+}  // namespace fgv
+
+extern "C" int fgv_qnorm_rope_kv_rope_quant_insert(
+    void* q, int64_t q_stride_token, int64_t q_stride_head,
+    const void* kv, int64_t kv_stride_token,
+    void* k_cache, int64_t cache_block_stride, int64_t num_blocks,
+    const int64_t* slot_mapping, int64_t num_tokens_insert,
+    const int64_t* position_ids,
+    const float* cos_sin_cache, int64_t cos_sin_stride, int64_t max_pos,
+    int64_t num_tokens, int64_t num_heads,
+    float eps, int64_t cache_block_size,
+    void* stream) {
+    using namespace fgv;
+    if (num_tokens < 0 || num_heads < 0 || num_tokens_insert < 0)
+        return fail(FGV_E_BAD_SHAPE, "negative size");
+    if (num_tokens_insert > num_tokens)
+        return fail(FGV_E_BAD_SHAPE, "slot_mapping is longer than the number of tokens");
+    const int64_t q_rows = num_tokens * num_heads;
+    if (q_rows == 0 && num_tokens_insert == 0)
+        return FGV_OK;
+    if (q_rows > 0x7fffffffLL || num_tokens > 0x7fffffffLL)
+        return fail(FGV_E_TOO_LARGE, "num_tokens * num_heads must be below 2^31");
+    if (!q || !kv || !position_ids || !cos_sin_cache)
+        return fail(FGV_E_NULL_POINTER, "null q, kv, position_ids or cos_sin_cache");
+    if (num_tokens_insert > 0 && (!k_cache || !slot_mapping))
+        return fail(FGV_E_NULL_POINTER, "null k_cache or slot_mapping");
+    if (max_pos <= 0)
+        return fail(FGV_E_BAD_SHAPE, "cos_sin_cache has no rows");
+    if (cache_block_size <= 0)
+        return fail(FGV_E_BAD_SHAPE, "cache_block_size must be positive");
+    if (!aligned(q, 16) || !aligned(kv, 16) || !aligned(cos_sin_cache, 16))
+        return fail(FGV_E_MISALIGNED, "q, kv and cos_sin_cache must be 16-byte aligned");
+    if (q_stride_token % 8 || q_stride_head % 8 || kv_stride_token % 8 || cos_sin_stride % 4)
+        return fail(FGV_E_BAD_STRIDE,
+                    "q/kv strides must be multiples of 8 elements, cos_sin stride of 4");
+    if (num_tokens_insert > 0) {
+        if (!aligned(k_cache, 8) || cache_block_stride % 8)
+            return fail(FGV_E_MISALIGNED, "k_cache and its block stride must be 8-byte aligned");
+        if (cache_block_stride < cache_block_size * (kTokenDataBytes + kScaleBytesPerToken))
+            return fail(FGV_E_BAD_STRIDE, "k_cache block stride is below cache_block_size * 584");
+    }
+
+    QnormArgs a;
+    a.q = static_cast<uint16_t*>(q);
+    a.kv = static_cast<const uint16_t*>(kv);
+    a.k_cache = static_cast<uint8_t*>(k_cache);
+    a.slot_mapping = slot_mapping;
+    a.positions = position_ids;
+    a.cos_sin = cos_sin_cache;
+    a.q_st = q_stride_token;
+    a.q_sh = q_stride_head;
+    a.kv_st = kv_stride_token;
+    a.block_stride = cache_block_stride;
+    a.num_blocks = num_blocks;
+    a.block_size = cache_block_size;
+    a.cs_stride = cos_sin_stride;
+    a.max_pos = max_pos;
+    a.num_q_rows = (uint32_t)q_rows;
+    a.num_heads = (uint32_t)(num_heads > 0 ? num_heads : 1);
+    a.num_tokens_insert = (uint32_t)num_tokens_insert;
+    a.kv_blocks = (uint32_t)((num_tokens_insert + kKvTokensPerBlock - 1) / kKvTokensPerBlock);
+    a.eps = eps;
+    const uint32_t q_blocks = (uint32_t)((q_rows + kQRowsPerBlock - 1) / kQRowsPerBlock);
+    const uint32_t grid = a.kv_blocks + q_blocks;
+    hipLaunchKernelGGL(qnorm_rope_kv_insert_kernel, dim3(grid), dim3(kThreads), 0,
+                       static_cast<hipStream_t>(stream), a);
+    return launch_status();
+}

@@ -1,0 +1,31 @@
+"""flaggems_vllm for MI355X (gfx950): the DeepSeek-V4 attention pre-processing path.
+
+Public names follow the reference package (src/flaggems_vllm/__init__.py:21-46):
+``fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert``, ``fused_inv_rope_fp8_quant``,
+their compatibility aliases ``ops_deepseek_v4_qnorm_rope_kv_rope_quant_insert`` and
+``ops_inv_rope_fp8_quant``, ``SUPPORTED_FP8_DTYPE``, ``device`` and ``vendor_name``.
+Both ops run hand-written HIP kernels through the C ABI declared in
+include/flaggems_vllm_amd.h; there is no Triton, no vendor dispatch and no
+CPU fallback.
+"""
+from . import ops  # noqa: F401
+from .ops import (  # noqa: F401
+    SUPPORTED_FP8_DTYPE,
+    fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert,
+    fused_inv_rope_fp8_quant,
+)
+
+device = "cuda"
+vendor_name = "amd"
+__version__ = "0.1.0"
+
+ops_deepseek_v4_qnorm_rope_kv_rope_quant_insert = fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert
+ops_inv_rope_fp8_quant = fused_inv_rope_fp8_quant
+
+__all__ = [
+    "fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert",
+    "fused_inv_rope_fp8_quant",
+    "ops_deepseek_v4_qnorm_rope_kv_rope_quant_insert",
+    "ops_inv_rope_fp8_quant",
+    "SUPPORTED_FP8_DTYPE",
+]

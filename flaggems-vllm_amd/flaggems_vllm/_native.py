@@ -1,0 +1,114 @@
+"""Build and load the gfx950 HIP library ``libflaggems_vllm_amd.so``.
+
+The library is built in-tree (next to this file) by ``build()`` and loaded
+with ctypes by ``lib()``.  There is no fallback: if the library is missing or
+cannot be loaded, every op raises.
+"""
+import ctypes
+import glob
+import os
+import subprocess
+
+_PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+_ROOT = os.path.dirname(_PKG_DIR)  # flaggems-vllm_amd/
+_CSRC = os.path.join(_ROOT, "csrc")
+_INCLUDE = os.path.join(os.path.dirname(_ROOT), "include")
+LIB_PATH = os.path.join(_PKG_DIR, "libflaggems_vllm_amd.so")
+
+ARCH = "gfx950"
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-shared",
+    # RoPE and FP8 parity rely on separately rounded products and sums.
+    "-ffp-contract=off",
+    # Packed FP32 (v_pk_*_f32) is kept out of the generated code.
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+]
+
+
+def sources():
+    return sorted(glob.glob(os.path.join(_CSRC, "*.hip")))
+
+
+def build(verbose=False):
+    """Compile every HIP source into LIB_PATH (always recompiles)."""
+    hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+    tmp = LIB_PATH + ".tmp"
+    cmd = [hipcc, *HIPCC_FLAGS, f"-I{_INCLUDE}", f"-I{_CSRC}", *sources(), "-o", tmp]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+_lib = None
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+
+
+def lib():
+    """The loaded library; raises RuntimeError if it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(
+            f"{LIB_PATH} is missing: build it with `python -c 'import __graft_entry__ as g; "
+            "g.build()'` (hipcc, gfx950). flaggems_vllm has no non-HIP fallback."
+        )
+    L = ctypes.CDLL(LIB_PATH)
+    L.fgv_version.restype = ctypes.c_int
+    L.fgv_version.argtypes = []
+    L.fgv_last_error.restype = ctypes.c_char_p
+    L.fgv_last_error.argtypes = []
+    L.fgv_qnorm_rope_kv_rope_quant_insert.restype = ctypes.c_int
+    L.fgv_qnorm_rope_kv_rope_quant_insert.argtypes = [
+        _P, _I64, _I64,  # q, q_stride_token, q_stride_head
+        _P, _I64,  # kv, kv_stride_token
+        _P, _I64, _I64,  # k_cache, cache_block_stride, num_blocks
+        _P, _I64,  # slot_mapping, num_tokens_insert
+        _P,  # position_ids
+        _P, _I64, _I64,  # cos_sin_cache, cos_sin_stride, max_pos
+        _I64, _I64,  # num_tokens, num_heads
+        ctypes.c_float, _I64,  # eps, cache_block_size
+        _P,  # stream
+    ]
+    L.fgv_inv_rope_fp8_quant.restype = ctypes.c_int
+    L.fgv_inv_rope_fp8_quant.argtypes = [
+        _P, _I64, _I64,  # o, o_stride_token, o_stride_head
+        _P,  # positions
+        _P, _I64, _I64,  # cos_sin_cache, cos_sin_stride, max_pos
+        _I64, _I64, _I64,  # num_tokens, n_groups, heads_per_group
+        _P, _I64, _I64,  # fp8_out, fp8_stride_group, fp8_stride_token
+        _P, _I64, _I64,  # scale_out, scale_stride_group, scale_stride_k
+        _I64, ctypes.c_float, ctypes.c_int,  # padded_tokens, eps, tma_aligned_scales
+        _P,  # stream
+    ]
+    _lib = L
+    return _lib
+
+
+def check(rc: int, what: str):
+    """Map a C-ABI status to a Python exception."""
+    if rc == 0:
+        return
+    if rc < 0:
+        msg = lib().fgv_last_error().decode(errors="replace")
+        raise ValueError(f"{what}: {msg} (code {rc})")
+    raise RuntimeError(f"{what}: HIP launch failed with hipError_t {rc}")
+
+
+# Exported symbols that include/flaggems_vllm_amd.h declares.
+EXPORTED_SYMBOLS = (
+    "fgv_version",
+    "fgv_last_error",
+    "fgv_qnorm_rope_kv_rope_quant_insert",
+    "fgv_inv_rope_fp8_quant",
+)

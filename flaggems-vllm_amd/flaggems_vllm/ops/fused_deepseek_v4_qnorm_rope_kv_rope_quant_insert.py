@@ -1,0 +1,93 @@
+"""Fused DeepSeek-V4 q RMSNorm + RoPE, kv RoPE + UE8M0 FP8 quant + paged insert.
+
+Drop-in for the reference op of the same name
+(src/flaggems_vllm/ops/fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert.py:289-351):
+same positional signature, same in-place contract (q and k_cache mutated, kv
+and the index tensors untouched), same AssertionError for the same bad inputs.
+The work is one launch of the gfx950 HIP kernel ``qnorm_rope_kv_insert_kernel``
+through the C ABI ``fgv_qnorm_rope_kv_rope_quant_insert``, on the current
+stream, with no host synchronisation and no allocation.
+
+Beyond the reference: q and kv may be strided views (unit last stride, row
+strides multiple of 8 elements), as when they are slices of one fused
+projection buffer; cos_sin_cache's row stride is honoured; slots whose block
+is past the end of k_cache are skipped and positions are clamped into the
+cache's rows instead of being read out of bounds.
+"""
+import torch
+
+from .. import _native
+from ._common import current_stream_ptr, on_device_of
+
+HEAD_DIM = 512
+ROPE_DIM = 64
+
+
+def fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert(
+    q: torch.Tensor,
+    kv: torch.Tensor,
+    k_cache: torch.Tensor,
+    slot_mapping: torch.Tensor,
+    position_ids: torch.Tensor,
+    cos_sin_cache: torch.Tensor,
+    eps: float,
+    cache_block_size: int,
+):
+    """Horizontally fused DeepSeek-V4 MLA pre-processing, in place.
+
+    Args:
+        q: [num_tokens, num_heads, 512] bf16, updated in place.
+        kv: [num_tokens, 512] bf16, read only.
+        k_cache: [num_blocks, block_bytes] uint8 paged cache.  Per block:
+            cache_block_size x 576 B token data (448 e4m3fn codes + 64 bf16
+            roped values), then cache_block_size x 8 B scales (7 UE8M0 bytes
+            + 1 zero byte).  Only stride(0) is used between blocks.
+        slot_mapping: [num_tokens_insert] int64, num_tokens_insert <= num_tokens;
+            -1 marks a token that is not inserted.
+        position_ids: [num_tokens] int64.
+        cos_sin_cache: [max_pos, 64] float32, cos | sin.
+        eps: RMSNorm epsilon.
+        cache_block_size: tokens per cache block.
+    """
+    assert q.dim() == 3 and kv.dim() == 2, "q must be 3-D and kv 2-D"
+    assert q.stride(-1) == 1 and kv.stride(-1) == 1, "q and kv need a unit last stride"
+    num_tokens, num_heads, head_dims = q.shape
+    assert head_dims == HEAD_DIM
+    assert kv.shape == (num_tokens, HEAD_DIM)
+    assert q.dtype == torch.bfloat16 and kv.dtype == torch.bfloat16
+    assert k_cache.dtype == torch.uint8
+    assert slot_mapping.dim() == 1
+    num_tokens_insert = slot_mapping.shape[0]
+    assert num_tokens_insert <= num_tokens
+    assert slot_mapping.dtype == torch.int64
+    assert position_ids.shape == (num_tokens,)
+    assert position_ids.dtype == torch.int64
+    assert cos_sin_cache.dim() == 2 and cos_sin_cache.shape[1] == ROPE_DIM
+    assert cos_sin_cache.dtype == torch.float32
+    assert cos_sin_cache.stride(1) == 1, "cos_sin_cache rows must be contiguous"
+    assert slot_mapping.stride(0) == 1 or num_tokens_insert <= 1
+    assert position_ids.stride(0) == 1 or num_tokens <= 1
+    assert k_cache.dim() >= 1 and (k_cache.dim() == 1 or k_cache[0].is_contiguous()), (
+        "each k_cache block must be contiguous bytes"
+    )
+    for t in (kv, k_cache, slot_mapping, position_ids, cos_sin_cache):
+        assert t.device == q.device, "all tensors must be on q's device"
+    assert q.device.type == "cuda", "flaggems_vllm runs on the GPU (HIP) only"
+
+    if num_tokens == 0:
+        return
+    num_blocks = k_cache.shape[0]
+    block_stride = k_cache.stride(0) if k_cache.dim() > 1 else k_cache.numel()
+    with on_device_of(q):
+        rc = _native.lib().fgv_qnorm_rope_kv_rope_quant_insert(
+            q.data_ptr(), q.stride(0), q.stride(1),
+            kv.data_ptr(), kv.stride(0),
+            k_cache.data_ptr(), block_stride, num_blocks,
+            slot_mapping.data_ptr(), num_tokens_insert,
+            position_ids.data_ptr(),
+            cos_sin_cache.data_ptr(), cos_sin_cache.stride(0), cos_sin_cache.shape[0],
+            num_tokens, num_heads,
+            float(eps), int(cache_block_size),
+            current_stream_ptr(q.device),
+        )
+    _native.check(rc, "fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert")

@@ -1,0 +1,109 @@
+/*
+ * flaggems_vllm_amd — C ABI of the MI355X (gfx950) DeepSeek-V4 attention
+ * pre-processing path.
+ *
+ * Plain pointers, element strides and sizes; no torch types.  Every launcher
+ * is asynchronous on the given HIP stream (NULL = the null stream), performs
+ * no host synchronisation, no device->host read and no allocation, so it can
+ * be recorded into a HIP graph.  Return value: 0 on success, a negative
+ * FGV_E_* code for an invalid argument (nothing is launched; fgv_last_error()
+ * describes it), or a positive hipError_t from the launch.
+ *
+ * Element strides are in elements of the tensor's own type (bf16 = 2 bytes,
+ * float = 4 bytes, int32 = 4 bytes); k_cache strides are in bytes.
+ */
+#ifndef FLAGGEMS_VLLM_AMD_H
+#define FLAGGEMS_VLLM_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FGV_OK 0
+#define FGV_E_NULL_POINTER (-1)
+#define FGV_E_BAD_SHAPE (-2)
+#define FGV_E_MISALIGNED (-3)
+#define FGV_E_BAD_STRIDE (-4)
+#define FGV_E_TOO_LARGE (-5)
+
+/* Library version as MAJOR*10000 + MINOR*100 + PATCH. */
+int fgv_version(void);
+
+/* Human-readable description of the last negative return on this thread. */
+const char* fgv_last_error(void);
+
+/*
+ * Fused DeepSeek-V4 q RMSNorm + RoPE, kv RoPE + UE8M0 FP8 quant + paged insert.
+ *
+ * Replaces flaggems_vllm.fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert
+ * (reference: src/flaggems_vllm/ops/fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert.py:289-351,
+ * kernel :20-286) and vLLM's torch.ops._C op of the same name.
+ *
+ *   q             bf16 [num_tokens, num_heads, 512], element (t,h,i) at
+ *                 q + t*q_stride_token + h*q_stride_head + i.  Updated in place:
+ *                 i < 448 -> bf16(x_i * r); i >= 448 -> GPT-J RoPE of x*r,
+ *                 r = 1/sqrt(mean(x^2) + eps) over all 512 dims.
+ *   kv            bf16 [num_tokens, 512] (row stride kv_stride_token); read only.
+ *   k_cache       uint8 paged cache, block b at k_cache + b*cache_block_stride
+ *                 bytes; per block: cache_block_size x 576 B token data
+ *                 (448 e4m3fn codes, 64 bf16 roped values), then
+ *                 cache_block_size x 8 B scales (7 UE8M0 bytes, 1 zero byte).
+ *   slot_mapping  int64 [num_tokens_insert]; token t < num_tokens_insert with
+ *                 slot s >= 0 is written to block s / cache_block_size, row
+ *                 s % cache_block_size.  Slots < 0 (padding) are skipped, as
+ *                 are slots whose block is >= num_blocks.
+ *   position_ids  int64 [num_tokens]; clamped into [0, max_pos).
+ *   cos_sin_cache float [max_pos, 64] (row stride cos_sin_stride): cos in
+ *                 columns 0..31, sin in 32..63.
+ *
+ * Alignment: q, kv 16-byte aligned with strides multiple of 8 elements;
+ * k_cache 8-byte aligned with cache_block_stride multiple of 8;
+ * cos_sin_cache 16-byte aligned with cos_sin_stride multiple of 4.
+ */
+int fgv_qnorm_rope_kv_rope_quant_insert(
+    void* q, int64_t q_stride_token, int64_t q_stride_head,
+    const void* kv, int64_t kv_stride_token,
+    void* k_cache, int64_t cache_block_stride, int64_t num_blocks,
+    const int64_t* slot_mapping, int64_t num_tokens_insert,
+    const int64_t* position_ids,
+    const float* cos_sin_cache, int64_t cos_sin_stride, int64_t max_pos,
+    int64_t num_tokens, int64_t num_heads,
+    float eps, int64_t cache_block_size,
+    void* stream);
+
+/*
+ * Fused DeepSeek-V4 inverse GPT-J RoPE + per-128 FP8 e4m3fn group quant.
+ *
+ * Replaces flaggems_vllm.fused_inv_rope_fp8_quant
+ * (reference: src/flaggems_vllm/ops/fused_inv_rope_fp8_quant.py:157-256,
+ * kernel :37-154) for nope_dim=448, rope_dim=64, quant_group_size=128.
+ *
+ *   o          bf16 [num_tokens, n_groups*heads_per_group, 512], element
+ *              (t,h,i) at o + t*o_stride_token + h*o_stride_head + i.
+ *   positions  int64 [num_tokens], clamped into [0, max_pos).
+ *   fp8_out    uint8 e4m3fn codes, element (g,t,i), i < heads_per_group*512,
+ *              at fp8_out + g*fp8_stride_group + t*fp8_stride_token + i.
+ *   scale_out  tma_aligned_scales == 0: float scale of chunk k
+ *              (k < 4*heads_per_group) at scale_out + g*scale_stride_group
+ *              + k*scale_stride_k + t;  != 0: int32 with the four UE8M0
+ *              bytes of head j at scale_out + g*scale_stride_group
+ *              + j*scale_stride_k + t.  Tokens num_tokens..padded_tokens-1
+ *              get zero scales.
+ */
+int fgv_inv_rope_fp8_quant(
+    const void* o, int64_t o_stride_token, int64_t o_stride_head,
+    const int64_t* positions,
+    const float* cos_sin_cache, int64_t cos_sin_stride, int64_t max_pos,
+    int64_t num_tokens, int64_t n_groups, int64_t heads_per_group,
+    void* fp8_out, int64_t fp8_stride_group, int64_t fp8_stride_token,
+    void* scale_out, int64_t scale_stride_group, int64_t scale_stride_k,
+    int64_t padded_tokens, float eps, int tma_aligned_scales,
+    void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLAGGEMS_VLLM_AMD_H */

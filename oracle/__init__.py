@@ -1,0 +1,173 @@
+"""CPU oracle for the DeepSeek-V4 attention pre-processing path.
+
+TEST INFRASTRUCTURE ONLY.  Only ``tests/``, ``__graft_entry__.smoke()`` and
+the ``cpu_baseline`` leg of ``bench.py`` import this package, and only as the
+checker.  The product (``flaggems_vllm`` and its HIP library) never imports it.
+
+Two restatements of the reference live here:
+
+* ``liboracle_dsv4.so`` (``dsv4_oracle.c``): scalar C, the bit-level checker.
+  Its RMSNorm factor is the correctly rounded one (see the C header), which the
+  HIP kernel shares, so q is compared bit for bit against it.
+* ``torch_ref``: the reference's own PyTorch formulation
+  (tests/test_fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert.py:68-333,
+  tests/test_fused_inv_rope_fp8_quant.py:132-198) restated on CPU tensors.  It
+  is what the north-star tolerance (q within 1 bf16 ulp) is measured against,
+  and it is the "reference PyTorch path" timed as the CPU baseline.
+
+The C library is pinned by tests/test_oracle_pins.py; the torch restatement is
+pinned against the C library and against closed forms there as well.
+"""
+import ctypes
+import os
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle_dsv4.so")
+_lib = None
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+
+
+def build():
+    """Compile the C oracle in place (gcc, via the Makefile next to it)."""
+    import subprocess
+
+    subprocess.run(["make", "-s", "-B", "-C", _HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            raise RuntimeError(
+                f"oracle library {_LIB_PATH} is not built; run `make -C oracle`"
+            )
+        L = ctypes.CDLL(_LIB_PATH)
+        L.oracle_e4m3fn.restype = ctypes.c_uint8
+        L.oracle_e4m3fn.argtypes = [ctypes.c_float]
+        L.oracle_f32_to_bf16.restype = ctypes.c_uint16
+        L.oracle_f32_to_bf16.argtypes = [ctypes.c_float]
+        L.oracle_kv_ue8m0_exponent.restype = ctypes.c_int
+        L.oracle_kv_ue8m0_exponent.argtypes = [ctypes.c_float]
+        L.oracle_rms_factor.restype = ctypes.c_float
+        L.oracle_rms_factor.argtypes = [_P, ctypes.c_float]
+        L.oracle_e4m3fn_array.restype = None
+        L.oracle_e4m3fn_array.argtypes = [_P, _P, _I64]
+        L.oracle_f32_to_bf16_array.restype = None
+        L.oracle_f32_to_bf16_array.argtypes = [_P, _P, _I64]
+        L.oracle_qnorm_rope_kv_insert.restype = None
+        L.oracle_qnorm_rope_kv_insert.argtypes = [
+            _P, _I64, _I64,  # q, q_st, q_sh
+            _P, _I64,  # kv, kv_st
+            _P, _I64, _I64,  # k_cache, block_stride, num_blocks
+            _P, _I64,  # slot_mapping, num_tokens_insert
+            _P,  # position_ids
+            _P, _I64, _I64,  # cos_sin, cs_stride, max_pos
+            _I64, _I64,  # num_tokens, num_heads
+            ctypes.c_float, _I64, ctypes.c_int,  # eps, block_size, nthreads
+        ]
+        L.oracle_inv_rope_fp8_quant.restype = None
+        L.oracle_inv_rope_fp8_quant.argtypes = [
+            _P, _I64, _I64,  # o, o_st, o_sh
+            _P, _P, _I64, _I64,  # positions, cos_sin, cs_stride, max_pos
+            _I64, _I64, _I64,  # num_tokens, n_groups, heads_per_group
+            _P, _I64, _I64,  # fp8, fp8_sg, fp8_st
+            _P, _I64, _I64, _I64,  # scale, sc_sg, sc_sk, tpad
+            ctypes.c_float, ctypes.c_int, ctypes.c_int,  # eps, tma, nthreads
+        ]
+        _lib = L
+    return _lib
+
+
+def _threads(nthreads):
+    if nthreads is None:
+        return len(os.sched_getaffinity(0))
+    return int(nthreads)
+
+
+def _cpu(t, dtype=None):
+    assert t.device.type == "cpu", "the oracle works on CPU tensors"
+    if dtype is not None:
+        assert t.dtype == dtype, f"expected {dtype}, got {t.dtype}"
+    return t
+
+
+def e4m3fn_codes(x: torch.Tensor) -> torch.Tensor:
+    """uint8 e4m3fn codes of a float32 CPU tensor (RNE, no saturation)."""
+    x = _cpu(x, torch.float32).contiguous()
+    out = torch.empty(x.shape, dtype=torch.uint8)
+    lib().oracle_e4m3fn_array(x.data_ptr(), out.data_ptr(), x.numel())
+    return out
+
+
+def bf16_bits(x: torch.Tensor) -> torch.Tensor:
+    """bf16 bit patterns (as int16) of a float32 CPU tensor, RNE."""
+    x = _cpu(x, torch.float32).contiguous()
+    out = torch.empty(x.shape, dtype=torch.int16)
+    lib().oracle_f32_to_bf16_array(x.data_ptr(), out.data_ptr(), x.numel())
+    return out
+
+
+def kv_ue8m0_exponent(amax: float) -> int:
+    return lib().oracle_kv_ue8m0_exponent(amax)
+
+
+def rms_factor(row: torch.Tensor, eps: float) -> float:
+    row = _cpu(row, torch.bfloat16).contiguous()
+    assert row.numel() == 512
+    return lib().oracle_rms_factor(row.data_ptr(), eps)
+
+
+def qnorm_rope_kv_insert(q, kv, k_cache, slot_mapping, position_ids, cos_sin_cache,
+                         eps, cache_block_size, nthreads=None):
+    """In-place CPU restatement of the main op on CPU tensors (same argument
+    meaning as flaggems_vllm.fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert).
+    q and kv may be strided views with a unit last stride."""
+    _cpu(q, torch.bfloat16), _cpu(kv, torch.bfloat16), _cpu(k_cache, torch.uint8)
+    _cpu(slot_mapping, torch.int64), _cpu(position_ids, torch.int64)
+    _cpu(cos_sin_cache, torch.float32)
+    T, H, D = q.shape
+    assert D == 512 and q.stride(2) == 1 and kv.stride(1) == 1
+    assert cos_sin_cache.stride(1) == 1 and cos_sin_cache.shape[1] == 64
+    slot_mapping = slot_mapping.contiguous()
+    position_ids = position_ids.contiguous()
+    lib().oracle_qnorm_rope_kv_insert(
+        q.data_ptr(), q.stride(0), q.stride(1),
+        kv.data_ptr(), kv.stride(0),
+        k_cache.data_ptr(), k_cache.stride(0), k_cache.shape[0],
+        slot_mapping.data_ptr(), slot_mapping.shape[0],
+        position_ids.data_ptr(),
+        cos_sin_cache.data_ptr(), cos_sin_cache.stride(0), cos_sin_cache.shape[0],
+        T, H, float(eps), int(cache_block_size), _threads(nthreads),
+    )
+
+
+def inv_rope_fp8_quant(o, positions, cos_sin_cache, n_groups, heads_per_group,
+                       eps=1e-10, tma_aligned_scales=False, nthreads=None):
+    """CPU restatement of the sibling op.  Returns (fp8 codes as uint8 [T, G, d]
+    with the reference's strides, scales [T, G, K] with the reference's
+    token-fastest padded storage: float32, or int32 when packed)."""
+    _cpu(o, torch.bfloat16), _cpu(positions, torch.int64), _cpu(cos_sin_cache, torch.float32)
+    T, H, D = o.shape
+    assert D == 512 and o.stride(2) == 1 and H == n_groups * heads_per_group
+    d = heads_per_group * 512
+    k_blocks = d // 128
+    tpad = (T + 3) // 4 * 4
+    inner = (k_blocks + 3) // 4 if tma_aligned_scales else k_blocks
+    fp8 = torch.empty((n_groups, T, d), dtype=torch.uint8)
+    sdt = torch.int32 if tma_aligned_scales else torch.float32
+    scale = torch.empty(n_groups * inner * tpad, dtype=sdt).as_strided(
+        (n_groups, T, inner), (inner * tpad, 1, tpad))
+    positions = positions.contiguous()
+    lib().oracle_inv_rope_fp8_quant(
+        o.data_ptr(), o.stride(0), o.stride(1),
+        positions.data_ptr(), cos_sin_cache.data_ptr(), cos_sin_cache.stride(0),
+        cos_sin_cache.shape[0], T, n_groups, heads_per_group,
+        fp8.data_ptr(), fp8.stride(0), fp8.stride(1),
+        scale.data_ptr(), scale.stride(0), scale.stride(2), tpad,
+        float(eps), int(bool(tma_aligned_scales)), _threads(nthreads),
+    )
+    return fp8.transpose(0, 1), scale.transpose(0, 1)

@@ -1,0 +1,306 @@
+/*
+ * CPU oracle for the DeepSeek-V4 attention pre-processing path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Nothing in the product (the HIP library or the
+ * flaggems_vllm Python package) links, loads or calls this file.  It is loaded
+ * by tests/, by __graft_entry__.smoke() and by the cpu_baseline leg of
+ * bench.py, always as the checker and never as the thing measured or shipped.
+ *
+ * It restates, in plain scalar C, what the reference computes:
+ *
+ *   oracle_qnorm_rope_kv_insert
+ *     reference op   src/flaggems_vllm/ops/fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert.py:20-351
+ *     reference test tests/test_fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert.py:93-243, 316-333
+ *   oracle_inv_rope_fp8_quant
+ *     reference op   src/flaggems_vllm/ops/fused_inv_rope_fp8_quant.py:37-256
+ *     reference test tests/test_fused_inv_rope_fp8_quant.py:150-198
+ *
+ * Numerics (compile with -ffp-contract=off and without -ffast-math):
+ *   - every product and sum is a separately rounded binary32 operation, as in
+ *     the torch oracle, so RoPE output and FP8 codes are fully determined;
+ *   - float -> bf16 is round-to-nearest-even;
+ *   - float -> e4m3fn is round-to-nearest-even with subnormals kept and no
+ *     saturation (values rounding past 448 become NaN 0x7f), which is what
+ *     torch's CPU cast does; the op clamps to +-448 first;
+ *   - the RMSNorm factor is evaluated as
+ *         w = (float)(sum_i (double)x_i^2 / 512) + eps      (binary32 add)
+ *         r = (float)(1 / sqrt((double)w))
+ *     i.e. the variance and the reciprocal square root are correctly rounded.
+ *     The reference's fp32 sum (tl.sum / torch mean) and rsqrt are within a
+ *     few fp32 ulps of this; the bar on q is 1 bf16 ulp.  The HIP kernel uses
+ *     the same formulation so that it can be compared bit for bit.
+ *
+ * Parity pins (tests/test_oracle_*.py): e4m3fn encoder against torch's cast
+ * exhaustively over every bf16 value times every reachable power-of-two scale;
+ * bf16 rounding against torch's cast; the UE8M0 exponent against log2/ceil and
+ * against exact rational arithmetic; RMS factor against exact rational
+ * arithmetic; RoPE against closed-form rotations (identity, quarter turn,
+ * forward-then-inverse); cache placement by brute force over small caches.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+
+#define HEAD_DIM 512
+#define NOPE_DIM 448
+#define ROPE_DIM 64
+#define HALF_ROPE 32
+#define KV_QUANT_BLOCK 64
+#define KV_NUM_QUANT_BLOCKS 7
+#define TOKEN_DATA_BYTES 576
+#define SCALE_BYTES_PER_TOKEN 8
+#define FP8_MAX 448.0f
+
+static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+float oracle_bf16_to_f32(uint16_t h) { return u2f((uint32_t)h << 16); }
+
+/* binary32 -> bfloat16, round to nearest, ties to even. NaN -> quiet NaN. */
+uint16_t oracle_f32_to_bf16(float f)
+{
+    uint32_t u = f2u(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u)
+        return (uint16_t)((u >> 16) | 0x0040u);
+    uint32_t keep_lsb = (u >> 16) & 1u;
+    return (uint16_t)((u + 0x7fffu + keep_lsb) >> 16);
+}
+
+/*
+ * binary32 -> OCP e4m3fn code, round to nearest even.
+ * Grid: subnormals m * 2^-9 (m = 0..7), normals (1 + m/8) * 2^e, e = -6..8,
+ * code 0x7e = 448 is the largest finite value, 0x7f / 0xff are NaN.
+ */
+uint8_t oracle_e4m3fn(float x)
+{
+    uint32_t u = f2u(x);
+    uint8_t sign = (uint8_t)((u >> 24) & 0x80u);
+    uint32_t a = u & 0x7fffffffu;
+    if (a > 0x7f800000u) /* NaN */
+        return (uint8_t)(sign | 0x7f);
+    uint32_t code;
+    if (a < 0x3c800000u) {
+        /* |x| < 2^-6: the grid is k * 2^-9 for k = 0..8 (k = 8 is the
+           smallest normal 2^-6, code 0x08).  |x| * 2^9 is exact. */
+        float scaled = u2f(a) * 512.0f;
+        code = (uint32_t)nearbyintf(scaled); /* default mode: ties to even */
+    } else {
+        int e = (int)(a >> 23) - 127; /* >= -6 */
+        if (e > 15)
+            return (uint8_t)(sign | 0x7f); /* far beyond 448, incl. inf */
+        uint32_t mant = a & 0x7fffffu;
+        code = ((uint32_t)(e + 7) << 3) | (mant >> 20);
+        uint32_t rest = mant & 0xfffffu;
+        if (rest > 0x80000u || (rest == 0x80000u && (code & 1u)))
+            code += 1; /* a carry moves into the exponent field, as it should */
+    }
+    if (code > 0x7eu)
+        code = 0x7fu; /* rounds past 448: NaN, there is no infinity */
+    return (uint8_t)(sign | code);
+}
+
+void oracle_e4m3fn_array(const float* x, uint8_t* out, int64_t n)
+{
+    for (int64_t i = 0; i < n; ++i)
+        out[i] = oracle_e4m3fn(x[i]);
+}
+
+void oracle_f32_to_bf16_array(const float* x, uint16_t* out, int64_t n)
+{
+    for (int64_t i = 0; i < n; ++i)
+        out[i] = oracle_f32_to_bf16(x[i]);
+}
+
+/* The KV UE8M0 exponent as the reference writes it:
+   k = ceil(log2(max(amax, 1e-4) / 448))   (ops/...insert.py:127-132). */
+int oracle_kv_ue8m0_exponent(float amax)
+{
+    float a = amax > 1e-4f ? amax : 1e-4f;
+    float raw = a / FP8_MAX;
+    return (int)ceilf(log2f(raw));
+}
+
+/* RMSNorm factor of one 512-element bf16 row (see the header comment). */
+float oracle_rms_factor(const uint16_t* row, float eps)
+{
+    double s = 0.0;
+    for (int i = 0; i < HEAD_DIM; ++i) {
+        double v = (double)oracle_bf16_to_f32(row[i]);
+        s += v * v;
+    }
+    float w = (float)(s / (double)HEAD_DIM);
+    w = w + eps;
+    return (float)(1.0 / sqrt((double)w));
+}
+
+/* GPT-J pair rotation, separately rounded binary32 (tests/...insert.py:134-135). */
+static inline void rope_pair(float e, float o, float c, float s, float* e_out, float* o_out)
+{
+    float ec = e * c, os = o * s, es = e * s, oc = o * c;
+    *e_out = ec - os;
+    *o_out = es + oc;
+}
+
+static inline int64_t clamp_pos(int64_t p, int64_t max_pos)
+{
+    if (p < 0) return 0;
+    if (p >= max_pos) return max_pos - 1;
+    return p;
+}
+
+/*
+ * Main op.  q[t, h, :] at q + t*q_st + h*q_sh (bf16 elements), updated in place.
+ * kv[t, :] at kv + t*kv_st, read only.  k_cache block b at k_cache + b*block_stride.
+ */
+void oracle_qnorm_rope_kv_insert(uint16_t* q, int64_t q_st, int64_t q_sh,
+                                 const uint16_t* kv, int64_t kv_st,
+                                 uint8_t* k_cache, int64_t block_stride, int64_t num_blocks,
+                                 const int64_t* slot_mapping, int64_t num_tokens_insert,
+                                 const int64_t* position_ids,
+                                 const float* cos_sin, int64_t cs_stride, int64_t max_pos,
+                                 int64_t num_tokens, int64_t num_heads,
+                                 float eps, int64_t block_size, int nthreads)
+{
+    (void)nthreads;
+    /* Q: RMSNorm over all 512 dims, store nope, rotate rope (ops/...insert.py:61-97). */
+#pragma omp parallel for schedule(static) num_threads(nthreads > 0 ? nthreads : 1)
+    for (int64_t row = 0; row < num_tokens * num_heads; ++row) {
+        int64_t t = row / num_heads, h = row % num_heads;
+        uint16_t* x = q + t * q_st + h * q_sh;
+        const float* cs = cos_sin + clamp_pos(position_ids[t], max_pos) * cs_stride;
+        float r = oracle_rms_factor(x, eps);
+        float y[ROPE_DIM];
+        for (int i = 0; i < ROPE_DIM; ++i)
+            y[i] = oracle_bf16_to_f32(x[NOPE_DIM + i]) * r;
+        for (int i = 0; i < NOPE_DIM; ++i)
+            x[i] = oracle_f32_to_bf16(oracle_bf16_to_f32(x[i]) * r);
+        for (int j = 0; j < HALF_ROPE; ++j) {
+            float e2, o2;
+            rope_pair(y[2 * j], y[2 * j + 1], cs[j], cs[HALF_ROPE + j], &e2, &o2);
+            x[NOPE_DIM + 2 * j] = oracle_f32_to_bf16(e2);
+            x[NOPE_DIM + 2 * j + 1] = oracle_f32_to_bf16(o2);
+        }
+    }
+
+    /* KV: rope slice to bf16, UE8M0 FP8 quant of the nope slice, paged insert
+       (ops/...insert.py:98-286; tests/...insert.py:178-243). */
+#pragma omp parallel for schedule(static) num_threads(nthreads > 0 ? nthreads : 1)
+    for (int64_t t = 0; t < num_tokens_insert; ++t) {
+        int64_t slot = slot_mapping[t];
+        if (slot < 0)
+            continue;
+        int64_t blk = slot / block_size, pos_in_block = slot % block_size;
+        if (blk >= num_blocks)
+            continue; /* the HIP kernel ignores out-of-range slots likewise */
+        uint8_t* base = k_cache + blk * block_stride;
+        uint8_t* tok = base + pos_in_block * TOKEN_DATA_BYTES;
+        uint8_t* scl = base + block_size * TOKEN_DATA_BYTES + pos_in_block * SCALE_BYTES_PER_TOKEN;
+        const uint16_t* x = kv + t * kv_st;
+        const float* cs = cos_sin + clamp_pos(position_ids[t], max_pos) * cs_stride;
+
+        for (int j = 0; j < HALF_ROPE; ++j) {
+            float e2, o2;
+            rope_pair(oracle_bf16_to_f32(x[NOPE_DIM + 2 * j]), oracle_bf16_to_f32(x[NOPE_DIM + 2 * j + 1]),
+                      cs[j], cs[HALF_ROPE + j], &e2, &o2);
+            uint16_t be = oracle_f32_to_bf16(e2), bo = oracle_f32_to_bf16(o2);
+            memcpy(tok + NOPE_DIM + 4 * j, &be, 2); /* little-endian bf16 */
+            memcpy(tok + NOPE_DIM + 4 * j + 2, &bo, 2);
+        }
+        for (int g = 0; g < KV_NUM_QUANT_BLOCKS; ++g) {
+            float v[KV_QUANT_BLOCK];
+            float amax = 0.0f;
+            for (int i = 0; i < KV_QUANT_BLOCK; ++i) {
+                v[i] = oracle_bf16_to_f32(x[g * KV_QUANT_BLOCK + i]);
+                float a = fabsf(v[i]);
+                amax = a > amax ? a : amax;
+            }
+            int k = oracle_kv_ue8m0_exponent(amax);
+            float scale = ldexpf(1.0f, k); /* exact power of two */
+            for (int i = 0; i < KV_QUANT_BLOCK; ++i) {
+                float s = v[i] / scale;
+                s = s < -FP8_MAX ? -FP8_MAX : (s > FP8_MAX ? FP8_MAX : s);
+                tok[g * KV_QUANT_BLOCK + i] = oracle_e4m3fn(s);
+            }
+            int enc = k + 127;
+            scl[g] = (uint8_t)(enc < 0 ? 0 : (enc > 255 ? 255 : enc));
+        }
+        scl[KV_NUM_QUANT_BLOCKS] = 0;
+    }
+}
+
+/*
+ * Sibling op.  Inverse GPT-J RoPE on dims 448..511 of each head, rope part
+ * rounded to bf16 (tests/test_fused_inv_rope_fp8_quant.py:163-170), then one
+ * scale per 128-element chunk and e4m3fn codes (:177-198).
+ *
+ * fp8 output element (g, t, i) at fp8 + g*fp8_sg + t*fp8_st + i.
+ * Scales: fp32 (tma == 0) at scale + g*sc_sg + k*sc_sk + t with k = hig*4 + c;
+ * packed int32 (tma != 0) at scale + g*sc_sg + hig*sc_sk + t.  Tokens
+ * T..Tpad-1 get zero scales (ops/fused_inv_rope_fp8_quant.py:69-88).
+ */
+void oracle_inv_rope_fp8_quant(const uint16_t* o, int64_t o_st, int64_t o_sh,
+                               const int64_t* positions, const float* cos_sin, int64_t cs_stride,
+                               int64_t max_pos, int64_t num_tokens, int64_t n_groups,
+                               int64_t heads_per_group, uint8_t* fp8, int64_t fp8_sg, int64_t fp8_st,
+                               void* scale, int64_t sc_sg, int64_t sc_sk, int64_t tpad,
+                               float eps, int tma, int nthreads)
+{
+    (void)nthreads;
+    const float inv_max = (float)(1.0 / 448.0);
+    int64_t num_heads = n_groups * heads_per_group;
+#pragma omp parallel for schedule(static) num_threads(nthreads > 0 ? nthreads : 1)
+    for (int64_t row = 0; row < num_tokens * num_heads; ++row) {
+        int64_t t = row / num_heads, h = row % num_heads;
+        int64_t g = h / heads_per_group, hig = h % heads_per_group;
+        const uint16_t* x = o + t * o_st + h * o_sh;
+        const float* cs = cos_sin + clamp_pos(positions[t], max_pos) * cs_stride;
+        float v[HEAD_DIM];
+        for (int i = 0; i < NOPE_DIM; ++i)
+            v[i] = oracle_bf16_to_f32(x[i]);
+        for (int j = 0; j < HALF_ROPE; ++j) {
+            float e = oracle_bf16_to_f32(x[NOPE_DIM + 2 * j]);
+            float od = oracle_bf16_to_f32(x[NOPE_DIM + 2 * j + 1]);
+            float c = cs[j], s = cs[HALF_ROPE + j];
+            float ec = e * c, os = od * s, oc = od * c, es = e * s;
+            float e2 = ec + os; /* inverse rotation */
+            float o2 = oc - es;
+            v[NOPE_DIM + 2 * j] = oracle_bf16_to_f32(oracle_f32_to_bf16(e2));
+            v[NOPE_DIM + 2 * j + 1] = oracle_bf16_to_f32(oracle_f32_to_bf16(o2));
+        }
+        uint8_t* out = fp8 + g * fp8_sg + t * fp8_st + hig * HEAD_DIM;
+        uint32_t packed = 0;
+        for (int c = 0; c < 4; ++c) {
+            float amax = 0.0f;
+            for (int i = 0; i < 128; ++i) {
+                float a = fabsf(v[c * 128 + i]);
+                amax = a > amax ? a : amax;
+            }
+            float absmax = amax > eps ? amax : eps;
+            float sc = absmax * inv_max;
+            if (tma) {
+                float cl = sc > 1e-10f ? sc : 1e-10f;
+                sc = ldexpf(1.0f, (int)ceilf(log2f(cl)));
+                packed |= ((f2u(sc) >> 23) & 0xffu) << (8 * c);
+            } else {
+                ((float*)scale)[g * sc_sg + (hig * 4 + c) * sc_sk + t] = sc;
+            }
+            for (int i = 0; i < 128; ++i) {
+                float qv = v[c * 128 + i] / sc;
+                qv = qv < -FP8_MAX ? -FP8_MAX : (qv > FP8_MAX ? FP8_MAX : qv);
+                out[c * 128 + i] = oracle_e4m3fn(qv);
+            }
+        }
+        if (tma)
+            ((int32_t*)scale)[g * sc_sg + hig * sc_sk + t] = (int32_t)packed;
+    }
+    for (int64_t t = num_tokens; t < tpad; ++t)
+        for (int64_t g = 0; g < n_groups; ++g) {
+            if (tma) {
+                for (int64_t hig = 0; hig < heads_per_group; ++hig)
+                    ((int32_t*)scale)[g * sc_sg + hig * sc_sk + t] = 0;
+            } else {
+                for (int64_t k = 0; k < heads_per_group * 4; ++k)
+                    ((float*)scale)[g * sc_sg + k * sc_sk + t] = 0.0f;
+            }
+        }
+}

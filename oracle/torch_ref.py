@@ -1,0 +1,112 @@
+"""The reference's PyTorch formulation of both ops, restated on CPU tensors.
+
+TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).  This follows the torch
+oracle that the reference's own tests compare its Triton kernels against:
+
+* main op: tests/test_fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert.py
+  ``rmsnorm_no_weight_f32`` :143-148, ``apply_rope_gptj_last_k`` :93-140,
+  ``_exact_pow2`` :154-163, ``torch_quantize_and_insert_k_cache`` :178-243,
+  ``ref_impl`` :316-333 (q processed 2**19 rows at a time);
+* sibling: tests/test_fused_inv_rope_fp8_quant.py
+  ``native_fused_inv_rope_fp8_quant`` :150-198, ``_pack_ue8m0_scales`` :82-90.
+
+Arithmetic is whatever torch's CPU kernels do in float32: the sum of squares
+and rsqrt are torch's, which is why q is compared against this restatement
+with a 1-bf16-ulp tolerance rather than bit for bit.  FP8 codes come from
+torch's own float8_e4m3fn cast.
+
+Unlike the reference oracle, ``kv`` is not modified (the op leaves it alone).
+"""
+import torch
+
+HEAD_DIM, NOPE_DIM, ROPE_DIM, HALF_ROPE = 512, 448, 64, 32
+KV_GROUP, KV_GROUPS = 64, 7
+TOKEN_DATA_BYTES, SCALE_BYTES = 576, 8
+FP8_MAX = 448.0
+ROWS_PER_CHUNK = 1 << 19
+
+
+def _pow2_exact(k: torch.Tensor) -> torch.Tensor:
+    """2**k as float32 for integer-valued k, built from the exponent field."""
+    field = (k.to(torch.int32) + 127).clamp(0, 255) << 23
+    return field.view(torch.float32)
+
+
+def _rotate_pairs(x_f32, cos, sin):
+    """GPT-J rotation of interleaved (even, odd) pairs, separately rounded."""
+    even, odd = x_f32[..., 0::2], x_f32[..., 1::2]
+    new_even = even * cos - odd * sin
+    new_odd = even * sin + odd * cos
+    return torch.stack((new_even, new_odd), dim=-1).flatten(-2)
+
+
+def qnorm_rope_kv_insert(q, kv, k_cache, slot_mapping, position_ids, cos_sin_cache,
+                         eps, cache_block_size):
+    """In place on q and k_cache (CPU tensors); kv is left untouched."""
+    T, H, _ = q.shape
+    tok_per_chunk = max(1, ROWS_PER_CHUNK // max(H, 1))
+    for s in range(0, T, tok_per_chunk):
+        qc = q[s:s + tok_per_chunk]
+        cs = cos_sin_cache[position_ids[s:s + tok_per_chunk]].float()
+        cos, sin = cs[:, None, :HALF_ROPE], cs[:, None, HALF_ROPE:]
+        xf = qc.float()
+        y = xf * torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + eps)
+        qc[..., NOPE_DIM:] = _rotate_pairs(y[..., NOPE_DIM:], cos, sin).to(q.dtype)
+        qc[..., :NOPE_DIM] = y[..., :NOPE_DIM].to(q.dtype)
+
+    n_ins = slot_mapping.shape[0]
+    tok = torch.arange(n_ins)
+    slots = slot_mapping[:n_ins]
+    keep = slots >= 0
+    tok, slots = tok[keep], slots[keep]
+    if tok.numel() == 0:
+        return
+    cs = cos_sin_cache[position_ids[tok]].float()
+    rope = _rotate_pairs(kv[tok, NOPE_DIM:].float(), cs[:, :HALF_ROPE], cs[:, HALF_ROPE:])
+    rope_bytes = rope.to(torch.bfloat16).contiguous().view(torch.uint8)  # [n, 128]
+
+    groups = kv[tok, :NOPE_DIM].float().reshape(-1, KV_GROUPS, KV_GROUP)
+    amax = groups.abs().amax(dim=-1).clamp(min=1e-4)
+    expo = torch.ceil(torch.log2(amax / FP8_MAX))
+    scaled = (groups / _pow2_exact(expo)[..., None]).clamp(-FP8_MAX, FP8_MAX)
+    codes = scaled.to(torch.float8_e4m3fn).view(torch.uint8).reshape(-1, NOPE_DIM)
+    scale_bytes = torch.zeros(tok.numel(), SCALE_BYTES, dtype=torch.uint8)
+    scale_bytes[:, :KV_GROUPS] = (expo + 127.0).clamp(0.0, 255.0).to(torch.uint8)
+
+    bs = cache_block_size
+    blk, pib = slots // bs, slots % bs
+    base = blk * k_cache.stride(0)
+    flat = k_cache.as_strided((k_cache.shape[0] * k_cache.stride(0),), (1,))
+    data_at = base + pib * TOKEN_DATA_BYTES
+    scale_at = base + bs * TOKEN_DATA_BYTES + pib * SCALE_BYTES
+    flat[data_at[:, None] + torch.arange(NOPE_DIM)] = codes
+    flat[data_at[:, None] + NOPE_DIM + torch.arange(2 * ROPE_DIM)] = rope_bytes
+    flat[scale_at[:, None] + torch.arange(SCALE_BYTES)] = scale_bytes
+
+
+def inv_rope_fp8_quant(o, positions, cos_sin_cache, n_groups, heads_per_group,
+                       eps=1e-10, tma_aligned_scales=False):
+    """Returns (fp8 codes as uint8 [T, G, d], scales [T, G, K] float32 or
+    packed int32 [T, G, hpg]) as plain contiguous tensors."""
+    T, H, D = o.shape
+    cs = cos_sin_cache[positions].float()
+    cos, sin = cs[:, None, :HALF_ROPE], cs[:, None, HALF_ROPE:]
+    rf = o[..., NOPE_DIM:].float()
+    even, odd = rf[..., 0::2], rf[..., 1::2]
+    inv = torch.stack((even * cos + odd * sin, odd * cos - even * sin), dim=-1).flatten(-2)
+    x = torch.cat((o[..., :NOPE_DIM], inv.to(o.dtype)), dim=-1).float()
+    d = heads_per_group * D
+    blocks = x.reshape(T, n_groups, d // 128, 128)
+    scales = blocks.abs().amax(dim=-1).clamp(min=eps) * (1.0 / FP8_MAX)
+    if tma_aligned_scales:
+        scales = _pow2_exact(torch.ceil(torch.log2(scales.clamp(min=1e-10))))
+    codes = (blocks / scales[..., None]).clamp(-FP8_MAX, FP8_MAX)
+    codes = codes.to(torch.float8_e4m3fn).view(torch.uint8).reshape(T, n_groups, d)
+    if not tma_aligned_scales:
+        return codes, scales
+    byte = (scales.view(torch.int32) >> 23) & 0xFF
+    byte = byte.reshape(T, n_groups, heads_per_group, 4)
+    packed = torch.zeros(T, n_groups, heads_per_group, dtype=torch.int32)
+    for c in range(4):
+        packed |= byte[..., c] << (8 * c)
+    return codes, packed

@@ -1,0 +1,183 @@
+"""GPU parity of the main op against the CPU oracle (bit for bit) and against
+the reference's torch formulation.
+
+Reference tests mirrored: tests/test_fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert.py
+  test_q_path_matches_reference :358-402, test_kv_path_matches_reference :419-462,
+  test_kv_path_with_dp_padding :468-515, test_combined_q_and_kv :521-573.
+"""
+import pytest
+import torch
+
+import flaggems_vllm
+import oracle
+from flaggems_vllm import testing as W
+from oracle import torch_ref
+
+from ._helpers import (bf16_ulp_distance, bf16_ulp_size, oracle_main, rope_cancellation_bound,
+                       slot_byte_index, sub_workload)
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+OP = flaggems_vllm.fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert
+
+
+def _say(msg):
+    print(f"\n[case] {msg}", flush=True)
+
+
+def run_gpu(w: W.Workload):
+    g = w.to(DEV)
+    OP(*g.args())
+    torch.cuda.synchronize()
+    return g
+
+
+def assert_q_exact(q_gpu_cpu, q_ref, what):
+    d = bf16_ulp_distance(q_gpu_cpu, q_ref)
+    n_bad = int((d > 0).sum())
+    assert n_bad == 0, f"{what}: {n_bad} q elements differ from the oracle (max {int(d.max())} ulp)"
+
+
+def assert_q_within_torch_ref(q_gpu_cpu, w_in: W.Workload, what):
+    """North-star bar against the reference's torch formulation: nope elements
+    within 1 bf16 ulp; rope elements within 1 ulp plus the cancellation term of
+    rope_cancellation_bound."""
+    r = w_in.clone()
+    torch_ref.qnorm_rope_kv_insert(*r.args())
+    d = bf16_ulp_distance(q_gpu_cpu, r.q)
+    assert int(d[..., :448].max()) <= 1, f"{what}: nope beyond 1 ulp"
+    rope_d = d[..., 448:]
+    if int(rope_d.max()) > 1:
+        xf = w_in.q.float()
+        y = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + w_in.eps)
+        cs = w_in.cos_sin_cache[w_in.position_ids][:, None, :]
+        bound = rope_cancellation_bound(y[..., 448:], cs) + bf16_ulp_size(r.q[..., 448:])
+        diff = (q_gpu_cpu[..., 448:].float() - r.q[..., 448:].float()).abs()
+        assert bool((diff <= bound).all()), f"{what}: rope beyond the cancellation bound"
+
+
+@pytest.mark.parametrize("config", [0, 1, 2])
+def test_benchmark_configs_full(config):
+    """c0-c2 at full size: q and the whole cache bit-exact vs the oracle."""
+    _say(f"main op c{config} full size")
+    w = W.make_workload(config)
+    g = run_gpu(w)
+    ref = oracle_main(w)
+    assert_q_exact(g.q.cpu(), ref.q, f"c{config}")
+    assert torch.equal(g.k_cache.cpu(), ref.k_cache), f"c{config}: k_cache differs"
+    assert torch.equal(g.kv.cpu(), w.kv), f"c{config}: kv modified"
+    if config < 2:
+        assert_q_within_torch_ref(g.q.cpu(), w, f"c{config}")
+
+
+@pytest.mark.parametrize("config", [3, 4])
+def test_benchmark_configs_sampled(config):
+    """c3 (T=32768, H=128, 2^31 q elements: int64 addressing) and c4 (ragged,
+    strided q/kv views of one buffer, 10% padding) at full size; 2048 sampled
+    tokens compared bit for bit with the oracle, and size-independent checks on
+    everything: cache bytes outside inserted slots untouched, every inserted
+    token's dequantised nope within e4m3 error of kv, kv unchanged."""
+    _say(f"main op c{config} full size, sampled oracle")
+    w = W.make_workload(config)
+    g = run_gpu(w)
+    gen = torch.Generator().manual_seed(100 + config)
+    toks = torch.randperm(w.num_tokens, generator=gen)[:2048].sort().values
+    sub = sub_workload(w, toks)
+    ref = oracle_main(sub)
+    assert_q_exact(g.q[toks.to(DEV)].cpu(), ref.q, f"c{config} sampled q")
+    keep = sub.slot_mapping >= 0
+    idx = slot_byte_index(sub.slot_mapping[keep], w.block_size, w.k_cache.stride(0))
+    flat_g = g.k_cache.view(-1)
+    assert torch.equal(flat_g[idx.to(DEV)].cpu(), ref.k_cache.view(-1)[idx]), f"c{config}: slots differ"
+
+    # every inserted slot, on the GPU: outside bytes zero, nope round trip
+    slots = g.slot_mapping[g.slot_mapping >= 0]
+    tok_ids = torch.nonzero(g.slot_mapping >= 0).flatten()
+    all_idx = slot_byte_index(slots, w.block_size, w.k_cache.stride(0))
+    bytes_ = flat_g[all_idx]
+    rest = g.k_cache.clone().view(-1)
+    rest[all_idx] = 0
+    assert int(torch.count_nonzero(rest)) == 0, f"c{config}: bytes outside slots written"
+    codes = bytes_[:, :448].contiguous().view(torch.float8_e4m3fn).float().view(-1, 7, 64)
+    expo = bytes_[:, 576:583].to(torch.float32) - 127.0
+    deq = codes * torch.exp2(expo)[..., None]
+    x = g.kv[tok_ids, :448].float().view(-1, 7, 64)
+    tol = torch.maximum(x.abs() * 2.0 ** -4, torch.exp2(expo - 10.0)[..., None])
+    assert bool(((deq - x).abs() <= tol).all()), f"c{config}: dequantised kv out of e4m3 error"
+    assert int(bytes_[:, 583].abs().sum()) == 0, "pad byte not zero"
+    assert torch.equal(g.kv.cpu(), w.kv), f"c{config}: kv modified"
+    # q rows are RMS-normalised: mean square within bf16 rounding of 1
+    ms = g.q.float().pow(2).mean(-1)
+    assert float((ms - 1).abs().max()) < 2e-2
+
+
+def _ref_style(T, H, bs, *, kv_random, q_random, slots, seed, pad=0):
+    """Inputs built like the reference tests (positions = arange, cos/sin
+    base chosen by max_pos as in tests/...insert.py:68-90)."""
+    g = torch.Generator().manual_seed(seed)
+    total = T + pad
+    max_pos = max(4096, total)
+    base = 10000.0 if max_pos <= 8192 else 20000.0 if max_pos <= 32768 else 40000.0 \
+        if max_pos <= 65536 else 60000.0 if max_pos <= 98304 else 100000.0
+    q = W.randn_bf16((total, H, 512), g) if q_random else torch.zeros(total, H, 512, dtype=torch.bfloat16)
+    kv = W.randn_bf16((total, 512), g) if kv_random else torch.zeros(total, 512, dtype=torch.bfloat16)
+    nblk = (T + bs - 1) // bs + 1
+    cache = torch.zeros(nblk, bs * W.HEAD_BYTES, dtype=torch.uint8)
+    return W.Workload(f"ref T{T} H{H} bs{bs}", q, kv, cache, slots,
+                      torch.arange(total, dtype=torch.int64), W.make_cos_sin_cache(max_pos, base=base),
+                      1e-6, bs)
+
+
+def _check_ref_case(w):
+    g = run_gpu(w)
+    ref = oracle_main(w)
+    assert_q_exact(g.q.cpu(), ref.q, w.name)
+    assert torch.equal(g.k_cache.cpu(), ref.k_cache), f"{w.name}: cache differs"
+    t = w.clone()
+    torch_ref.qnorm_rope_kv_insert(*t.args())
+    # the reference's own assertions: q at 1e-2, fp8 codes and scales exact,
+    # and under DP padding the whole cache exact
+    torch.testing.assert_close(g.q.cpu(), t.q, rtol=1e-2, atol=1e-2)
+    assert torch.equal(g.k_cache.cpu(), t.k_cache), f"{w.name}: cache differs from torch ref"
+    assert_q_within_torch_ref(g.q.cpu(), w, w.name)
+
+
+@pytest.mark.parametrize("T", [1, 4, 17, 64])
+@pytest.mark.parametrize("H", [8, 64])
+def test_q_path(T, H):
+    _say(f"q path T={T} H={H}")
+    _check_ref_case(_ref_style(T, H, 16, kv_random=False, q_random=True,
+                               slots=torch.full((T,), -1, dtype=torch.int64), seed=0))
+
+
+@pytest.mark.parametrize("T", [1, 4, 17, 64])
+@pytest.mark.parametrize("bs", [16, 64])
+def test_kv_path(T, bs):
+    _say(f"kv path T={T} bs={bs}")
+    _check_ref_case(_ref_style(T, 1, bs, kv_random=True, q_random=False,
+                               slots=torch.arange(T, dtype=torch.int64), seed=1))
+
+
+@pytest.mark.parametrize("T", [4, 17])
+@pytest.mark.parametrize("pad", [1, 5])
+@pytest.mark.parametrize("bs", [16, 64])
+def test_kv_path_dp_padding(T, pad, bs):
+    _say(f"dp padding T={T} pad={pad} bs={bs}")
+    _check_ref_case(_ref_style(T, 1, bs, kv_random=True, q_random=False,
+                               slots=torch.arange(T, dtype=torch.int64), seed=3, pad=pad))
+
+
+@pytest.mark.parametrize("T", [1, 4, 17, 64, 1000, 8192])
+@pytest.mark.parametrize("H", [64, 128])
+@pytest.mark.parametrize("bs", [16, 64])
+def test_combined(T, H, bs):
+    _say(f"combined T={T} H={H} bs={bs}")
+    w = _ref_style(T, H, bs, kv_random=True, q_random=True,
+                   slots=torch.arange(T, dtype=torch.int64), seed=2)
+    if T * H > (1 << 20):
+        g = run_gpu(w)
+        ref = oracle_main(w)
+        assert_q_exact(g.q.cpu(), ref.q, w.name)
+        assert torch.equal(g.k_cache.cpu(), ref.k_cache)
+    else:
+        _check_ref_case(w)
