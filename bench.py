@@ -34,7 +34,8 @@ def parse_args():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", type=int, default=2, help="main-op workload c0..c4 (default c2)")
-    ap.add_argument("--op", choices=["main", "inv_rope"], default="main")
+    ap.add_argument("--op", choices=["main", "inv_rope", "copy"], default="main",
+                    help="copy: torch device copy of 512 MiB, the HBM calibration kernel")
     ap.add_argument("--tma", action="store_true", help="inv_rope: packed UE8M0 scales")
     ap.add_argument("--cpu-sample-tokens", type=int, default=2048)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -150,6 +151,18 @@ def main():
                   "num_tokens": T, "num_heads": H, "head_dim": 512, "rope_dim": 64,
                   "inserted_tokens": nv, "cache_block_size": w.block_size,
                   "io": "bf16 q/kv in, bf16 q out, fp8-e4m3 + UE8M0 cache"}
+    elif args.op == "copy":
+        n = 512 << 20
+        src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        T, bytes_call = n, 2 * n
+
+        def step():
+            dst.copy_(src)
+
+        kernel, workload = "copy", "512MiB"
+        config = {"workload": "calibration: torch device copy, 512 MiB read + 512 MiB write"}
+        args.no_cpu_baseline = True
     else:
         w_cpu = W.make_inv_rope_workload(8192, 64, 8, seed=0)
         w = w_cpu.to(dev)

@@ -52,9 +52,19 @@ def slot_byte_index(slots: torch.Tensor, block_size: int, block_stride: int):
     """Flat byte offsets [n, 584] of each slot's token data and scale bytes."""
     blk, p = slots // block_size, slots % block_size
     base = blk * block_stride
-    data = base[:, None] + p[:, None] * 576 + torch.arange(576)
-    scale = base[:, None] + block_size * 576 + p[:, None] * 8 + torch.arange(8)
+    data = base[:, None] + p[:, None] * 576 + torch.arange(576, device=slots.device)
+    scale = base[:, None] + block_size * 576 + p[:, None] * 8 + torch.arange(8, device=slots.device)
     return torch.cat((data, scale), dim=1)
+
+
+def split_cache(cache: torch.Tensor, block_size: int):
+    """(token data [num_blocks * bs, 576], scale bytes [num_blocks * bs, 8]) of
+    a paged cache, indexed by slot."""
+    nblk = cache.shape[0]
+    rows = cache.view(nblk, -1)
+    data = rows[:, :block_size * 576].reshape(nblk * block_size, 576)
+    scales = rows[:, block_size * 576:block_size * 584].reshape(nblk * block_size, 8)
+    return data, scales
 
 
 def oracle_main(w: W.Workload) -> W.Workload:

@@ -1,0 +1,164 @@
+"""CPU tests of the drop-in boundary: the C-ABI library loads and exports what
+include/flaggems_vllm_amd.h declares, its argument checks return the
+documented codes without launching anything, and the Python wrappers keep the
+reference's signatures and AssertionErrors (reference wrappers:
+ops/fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert.py:320-333,
+ops/fused_inv_rope_fp8_quant.py:184-205)."""
+import ctypes
+import inspect
+import os
+import re
+
+import pytest
+import torch
+
+import flaggems_vllm
+from flaggems_vllm import _native
+from flaggems_vllm import testing as W
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_symbols():
+    syms = set()
+    for name in os.listdir(os.path.join(ROOT, "include")):
+        if name.endswith(".h"):
+            text = open(os.path.join(ROOT, "include", name)).read()
+            syms |= set(re.findall(r"^\s*(?:int|const char\s*\*)\s+(fgv_\w+)\s*\(", text, re.M))
+    return syms
+
+
+def test_library_exports_every_declared_symbol():
+    syms = declared_symbols()
+    assert syms == set(_native.EXPORTED_SYMBOLS)
+    L = ctypes.CDLL(_native.LIB_PATH)
+    for s in syms:
+        assert hasattr(L, s), s
+    assert _native.lib().fgv_version() == 100
+
+
+def _call_main(**kw):
+    args = dict(q=16, q_st=8 * 512, q_sh=512, kv=16, kv_st=512, cache=16, stride=64 * 584,
+                nblk=4, slots=16, n_ins=4, pos=16, cs=16, cs_st=64, max_pos=16, T=4, H=8,
+                eps=1e-6, bs=64)
+    args.update(kw)
+    a = args
+    return _native.lib().fgv_qnorm_rope_kv_rope_quant_insert(
+        a["q"], a["q_st"], a["q_sh"], a["kv"], a["kv_st"], a["cache"], a["stride"], a["nblk"],
+        a["slots"], a["n_ins"], a["pos"], a["cs"], a["cs_st"], a["max_pos"], a["T"], a["H"],
+        a["eps"], a["bs"], None)
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(n_ins=5), -2),                       # slot_mapping longer than q
+    (dict(T=-1), -2),
+    (dict(q=None), -1),
+    (dict(q=17), -3),                          # q not 16-byte aligned
+    (dict(q_st=8 * 512 + 4), -4),              # token stride not a multiple of 8
+    (dict(cs_st=66), -4),
+    (dict(stride=64 * 584 - 8), -4),           # block stride below bs * 584
+    (dict(cache=20), -3),                      # cache not 8-byte aligned
+    (dict(max_pos=0), -2),
+    (dict(bs=0), -2),
+    (dict(T=1 << 20, H=1 << 12, n_ins=0), -5),  # 2^32 q rows
+])
+def test_c_abi_rejects_bad_arguments(kw, code):
+    assert _call_main(**kw) == code
+    assert _native.lib().fgv_last_error()
+
+
+def test_c_abi_empty_call_is_a_no_op():
+    assert _call_main(T=0, n_ins=0, q=None, kv=None) == 0
+
+
+def test_inv_rope_c_abi_rejects_bad_arguments():
+    f = _native.lib().fgv_inv_rope_fp8_quant
+    ok = dict(o=16, ost=64 * 512, osh=512, pos=16, cs=16, css=64, mp=16, T=4, G=8, hpg=8,
+              f8=16, f8g=4 * 4096, f8t=4096, sc=16, scg=32 * 4, sck=4, tpad=4, eps=1e-10, tma=0)
+
+    def call(**kw):
+        a = dict(ok, **kw)
+        return f(a["o"], a["ost"], a["osh"], a["pos"], a["cs"], a["css"], a["mp"], a["T"], a["G"],
+                 a["hpg"], a["f8"], a["f8g"], a["f8t"], a["sc"], a["scg"], a["sck"], a["tpad"],
+                 a["eps"], a["tma"], None)
+
+    assert call(tpad=9) == -2
+    assert call(G=0) == -2
+    assert call(o=24) == -3
+    assert call(eps=0.0) == -2
+    assert call(T=0, tpad=0) == 0
+
+
+def test_signatures_match_reference():
+    p = inspect.signature(flaggems_vllm.fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert).parameters
+    assert list(p) == ["q", "kv", "k_cache", "slot_mapping", "position_ids", "cos_sin_cache",
+                       "eps", "cache_block_size"]
+    p = inspect.signature(flaggems_vllm.fused_inv_rope_fp8_quant).parameters
+    assert list(p) == ["o", "positions", "cos_sin_cache", "n_groups", "heads_per_group",
+                       "nope_dim", "rope_dim", "quant_group_size", "eps", "dtype",
+                       "tma_aligned_scales"]
+    assert [p[k].default for k in ("nope_dim", "rope_dim", "quant_group_size", "eps", "dtype",
+                                   "tma_aligned_scales")] == [448, 64, 128, 1e-10, None, False]
+    assert flaggems_vllm.ops_deepseek_v4_qnorm_rope_kv_rope_quant_insert is \
+        flaggems_vllm.fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert
+    assert flaggems_vllm.ops_inv_rope_fp8_quant is flaggems_vllm.fused_inv_rope_fp8_quant
+    assert flaggems_vllm.SUPPORTED_FP8_DTYPE == torch.float8_e4m3fn
+
+
+def _args(**over):
+    w = W.make_workload(0)
+    a = dict(q=w.q, kv=w.kv, k_cache=w.k_cache, slot_mapping=w.slot_mapping,
+             position_ids=w.position_ids, cos_sin_cache=w.cos_sin_cache, eps=1e-6,
+             cache_block_size=64)
+    a.update(over)
+    return a
+
+
+@pytest.mark.parametrize("bad", [
+    dict(q=torch.zeros(16, 8, 256, dtype=torch.bfloat16)),
+    dict(kv=torch.zeros(15, 512, dtype=torch.bfloat16)),
+    dict(q=torch.zeros(16, 8, 512, dtype=torch.float16)),
+    dict(k_cache=torch.zeros(4, 64 * 584, dtype=torch.int8)),
+    dict(slot_mapping=torch.zeros(17, dtype=torch.int64)),
+    dict(slot_mapping=torch.zeros(16, dtype=torch.int32)),
+    dict(position_ids=torch.zeros(16, dtype=torch.int32)),
+    dict(cos_sin_cache=torch.zeros(16, 32)),
+    dict(cos_sin_cache=torch.zeros(16, 64, dtype=torch.float64)),
+])
+def test_main_wrapper_asserts_like_reference(bad):
+    with pytest.raises(AssertionError):
+        flaggems_vllm.fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert(**_args(**bad))
+
+
+def test_main_wrapper_refuses_cpu_tensors():
+    """No CPU fallback: valid CPU inputs fail loudly instead of computing."""
+    with pytest.raises(AssertionError, match="GPU"):
+        flaggems_vllm.fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert(**_args())
+
+
+@pytest.mark.parametrize("bad,kw", [
+    ({}, dict(dtype=torch.float16)),
+    ({}, dict(n_groups=3)),
+    ({"o": torch.zeros(4, 64, 256, dtype=torch.bfloat16)}, {}),
+    ({"positions": torch.zeros(5, dtype=torch.int64)}, {}),
+    ({}, dict(nope_dim=192, rope_dim=64)),
+    ({"cos_sin_cache": torch.zeros(16, 64, dtype=torch.float64)}, {}),
+    ({}, {}),  # valid, but CPU tensors
+])
+def test_sibling_wrapper_asserts(bad, kw):
+    a = dict(o=torch.zeros(4, 64, 512, dtype=torch.bfloat16), positions=torch.zeros(4, dtype=torch.int64),
+             cos_sin_cache=torch.zeros(16, 64), n_groups=8, heads_per_group=8)
+    a.update(bad)
+    a.update(kw)
+    with pytest.raises(AssertionError):
+        flaggems_vllm.fused_inv_rope_fp8_quant(**a)
+
+
+def test_product_never_imports_the_oracle():
+    pkg = os.path.join(ROOT, "flaggems-vllm_amd")
+    for dirpath, _, files in os.walk(pkg):
+        for f in files:
+            if f.endswith((".py", ".hip", ".h", ".cpp")):
+                text = open(os.path.join(dirpath, f)).read()
+                assert "import oracle" not in text and "from oracle" not in text, f
+                assert "liboracle" not in text, f
