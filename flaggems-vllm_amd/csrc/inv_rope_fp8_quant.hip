@@ -19,7 +19,7 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kRowsPerPass = kThreads / 16;
-constexpr int kPasses = 2;
+constexpr int kPasses = 1;
 constexpr int kRowsPerBlock = kRowsPerPass * kPasses;
 
 struct InvRopeArgs {
@@ -61,6 +61,21 @@ __device__ __forceinline__ void inv_rope_piece(float (&x)[8], float4 c, float4 s
         x[2 * i] = bf16_lo(w);
         x[2 * i + 1] = bf16_hi(w);
     }
+}
+
+// Correctly rounded x / s (s > 0, normal) from y = RN(1/s), which is one IEEE
+// division per 128-element chunk instead of one per element.  q0 = RN(x*y) is
+// within one ulp of x/s, the remainder r = x - s*q0 is exact in one fma, and
+// RN(q0 + r*y) = RN(x/s) by Markstein's theorem (P. Markstein, IBM J. Res.
+// Dev. 34(1), 1990; J.-M. Muller et al., Handbook of Floating-Point
+// Arithmetic, 2nd ed., section 4.7).  The remainder stays exact for every
+// quotient large enough to reach a non-zero e4m3 code (|x/s| >= 2^-10 keeps
+// r far above the binary32 underflow threshold); below that only the sign
+// matters to the code, and copysign restores it for zero quotients.
+__device__ __forceinline__ float div_by_scale(float x, float s, float y) {
+    float q0 = x * y;
+    float r = __builtin_fmaf(-s, q0, x);
+    return __builtin_copysignf(__builtin_fmaf(r, y, q0), x);
 }
 
 __device__ void row_block(const InvRopeArgs& a, uint32_t rb, int lane16, int row_in_pass) {
@@ -130,10 +145,13 @@ __device__ void row_block(const InvRopeArgs& a, uint32_t rb, int lane16, int row
             } else {
                 if (lane16 == k)
                     my_scale = sc;
-                lo = pack_fp8x4(clamp_fp8(x[0] / sc), clamp_fp8(x[1] / sc),
-                                clamp_fp8(x[2] / sc), clamp_fp8(x[3] / sc));
-                hi = pack_fp8x4(clamp_fp8(x[4] / sc), clamp_fp8(x[5] / sc),
-                                clamp_fp8(x[6] / sc), clamp_fp8(x[7] / sc));
+                const float y = 1.0f / sc;
+                float qv[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+                    qv[i] = clamp_fp8(div_by_scale(x[i], sc, y));
+                lo = pack_fp8x4(qv[0], qv[1], qv[2], qv[3]);
+                hi = pack_fp8x4(qv[4], qv[5], qv[6], qv[7]);
             }
             store8(out + (lane16 + 16 * k) * 8, lo, hi);
         }

@@ -8,9 +8,10 @@
 //   blocks [0, kv_blocks)          : 16 tokens' kv rows each -> k_cache
 //   blocks [kv_blocks, grid)       : kQRowsPerBlock q rows each, in place
 // Each 1 KiB row is owned by one 16-lane DPP row (see fgv_device.h).  The op
-// is HBM bound (about 98.6% of its bytes are the in-place q read and write),
-// so the q blocks keep two passes of four 16-byte loads per lane in flight and
-// do the per-row math with DPP reductions only.
+// is HBM bound (about 98.6% of its bytes are the in-place q read and write):
+// every global access is a non-temporal 16-byte (8-byte for the cache) access,
+// the per-row math uses DPP reductions only, and q blocks hold one pass of 16
+// rows (16 KiB in, 16 KiB out) so that 8 waves per SIMD keep loads in flight.
 #include "fgv_device.h"
 #include "fgv_host.h"
 
@@ -19,7 +20,9 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kRowsPerPass = kThreads / 16;   // 16 rows per pass
-constexpr int kQPasses = 2;
+// One pass of four 16-byte loads per lane: 62 VGPRs, 8 waves per SIMD.  More
+// passes per block (more loads per wave, fewer waves) measured slower.
+constexpr int kQPasses = 1;
 constexpr int kQRowsPerBlock = kRowsPerPass * kQPasses;
 constexpr int kKvTokensPerBlock = kRowsPerPass;
 
