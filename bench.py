@@ -37,7 +37,9 @@ def parse_args():
     ap.add_argument("--op", choices=["main", "inv_rope", "copy"], default="main",
                     help="copy: torch device copy of 512 MiB, the HBM calibration kernel")
     ap.add_argument("--tma", action="store_true", help="inv_rope: packed UE8M0 scales")
-    ap.add_argument("--cpu-sample-tokens", type=int, default=2048)
+    ap.add_argument("--cpu-sample-tokens", type=int, default=8192)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="repeat the CPU sample until this much CPU time is spent (min 3 runs)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     return ap.parse_args()
 
@@ -71,10 +73,20 @@ def time_gpu(fn, steps, warmup):
     return wall / steps, start.elapsed_time(end) / 1000.0 / steps
 
 
-def cpu_baseline_main(w, sample_tokens):
+def _repeat(run, seconds):
+    """Median wall time of run(), repeated until `seconds` are spent (3..200 runs)."""
+    times = []
+    while len(times) < 3 or (sum(times) < seconds and len(times) < 200):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times)
+
+
+def cpu_baseline_main(w, sample_tokens, seconds):
     """The reference's PyTorch formulation (oracle.torch_ref) on the host CPU,
     over the first `sample_tokens` tokens of the workload with all heads;
-    median of 3 runs, tokens/s."""
+    median over repeated runs, tokens/s."""
     import torch
 
     from oracle import torch_ref
@@ -82,22 +94,20 @@ def cpu_baseline_main(w, sample_tokens):
     n = min(sample_tokens, w.num_tokens)
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    times = []
-    for _ in range(3):
-        q = w.q[:n].clone()
-        cache = w.k_cache  # CPU copy; the GPU has its own
-        t0 = time.perf_counter()
-        torch_ref.qnorm_rope_kv_insert(q, w.kv[:n], cache, w.slot_mapping[:n], w.position_ids[:n],
-                                       w.cos_sin_cache, w.eps, w.block_size)
-        times.append(time.perf_counter() - t0)
-    t = statistics.median(times)
+    q = w.q[:n].clone()
+
+    def run():
+        torch_ref.qnorm_rope_kv_insert(q, w.kv[:n], w.k_cache, w.slot_mapping[:n],
+                                       w.position_ids[:n], w.cos_sin_cache, w.eps, w.block_size)
+
+    t, reps = _repeat(run, seconds)
     return {"value": n / t, "unit": "tokens/s", "cores": cores, "kind": "port",
-            "sample": f"first {n} of {w.num_tokens} tokens of {w.name}, all {w.num_heads} heads, "
-                      f"torch CPU restatement of the reference's torch oracle, median of 3 "
-                      f"({t:.2f} s per run)"}
+            "sample": f"first {n} of {w.num_tokens} tokens of {w.name}, all {w.num_heads} heads: "
+                      f"torch CPU restatement of the reference's torch oracle (oracle/torch_ref.py), "
+                      f"median of {reps} runs, {t:.3f} s per run"}
 
 
-def cpu_baseline_inv(w, tma, sample_tokens):
+def cpu_baseline_inv(w, tma, sample_tokens, seconds):
     import torch
 
     from oracle import torch_ref
@@ -105,16 +115,15 @@ def cpu_baseline_inv(w, tma, sample_tokens):
     n = min(sample_tokens, w.o.shape[0])
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    times = []
-    for _ in range(3):
-        t0 = time.perf_counter()
+
+    def run():
         torch_ref.inv_rope_fp8_quant(w.o[:n], w.positions[:n], w.cos_sin_cache, w.n_groups,
                                      w.heads_per_group, tma_aligned_scales=tma)
-        times.append(time.perf_counter() - t0)
-    t = statistics.median(times)
+
+    t, reps = _repeat(run, seconds)
     return {"value": n / t, "unit": "tokens/s", "cores": cores, "kind": "port",
-            "sample": f"first {n} of {w.o.shape[0]} tokens, torch CPU restatement, median of 3 "
-                      f"({t:.2f} s per run)"}
+            "sample": f"first {n} of {w.o.shape[0]} tokens, torch CPU restatement "
+                      f"(oracle/torch_ref.py), median of {reps} runs, {t:.3f} s per run"}
 
 
 def main():
@@ -206,9 +215,11 @@ def main():
     }
     if not args.no_cpu_baseline:
         if args.op == "main":
-            result["cpu_baseline"] = cpu_baseline_main(w_cpu, args.cpu_sample_tokens)
+            result["cpu_baseline"] = cpu_baseline_main(w_cpu, args.cpu_sample_tokens,
+                                                       args.cpu_seconds)
         else:
-            result["cpu_baseline"] = cpu_baseline_inv(w_cpu, args.tma, args.cpu_sample_tokens)
+            result["cpu_baseline"] = cpu_baseline_inv(w_cpu, args.tma, args.cpu_sample_tokens,
+                                                      args.cpu_seconds)
     print(json.dumps(result), flush=True)
 
 
