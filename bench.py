@@ -34,7 +34,7 @@ def parse_args():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", type=int, default=2, help="main-op workload c0..c4 (default c2)")
-    ap.add_argument("--op", choices=["main", "inv_rope", "copy"], default="main",
+    ap.add_argument("--op", choices=["main", "inv_rope", "gather", "copy"], default="main",
                     help="copy: torch device copy of 512 MiB, the HBM calibration kernel")
     ap.add_argument("--tma", action="store_true", help="inv_rope: packed UE8M0 scales")
     ap.add_argument("--cpu-sample-tokens", type=int, default=8192)
@@ -160,6 +160,27 @@ def main():
                   "num_tokens": T, "num_heads": H, "head_dim": 512, "rope_dim": 64,
                   "inserted_tokens": nv, "cache_block_size": w.block_size,
                   "io": "bf16 q/kv in, bf16 q out, fp8-e4m3 + UE8M0 cache"}
+    elif args.op == "gather":
+        # c2's cache after the insert; gather every position of its 4 sequences
+        w_cpu = W.make_workload(args.config)
+        w = w_cpu.to(dev)
+        flaggems_vllm.fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert(*w.args())
+        m = w_cpu.meta
+        bt, seq_lens = m["block_table"].to(dev), m["seq_lens"].to(dev)
+        rows = int(m["seq_lens"].max())
+        out = torch.empty(bt.shape[0], rows, 512, dtype=torch.bfloat16, device=dev)
+        T = int(m["seq_lens"].sum())
+        bytes_call = W.gather_bytes(T)
+
+        def step():
+            flaggems_vllm.dequantize_and_gather_k_cache(out, w.k_cache, seq_lens, None, bt,
+                                                        w.block_size)
+
+        kernel, workload = "dequantize_gather_kernel", f"c{args.config}_whole_seqs"
+        config = {"workload": f"dequantize_and_gather_k_cache: all positions of c{args.config}'s "
+                              f"{bt.shape[0]} sequences ({T} rows) from its 584 B/token FP8 cache",
+                  "rows": T, "num_reqs": int(bt.shape[0])}
+        args.no_cpu_baseline = True
     elif args.op == "copy":
         n = 512 << 20
         src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)

@@ -11,6 +11,7 @@ CPU fallback.
 from . import ops  # noqa: F401
 from .ops import (  # noqa: F401
     SUPPORTED_FP8_DTYPE,
+    dequantize_and_gather_k_cache,
     fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert,
     fused_inv_rope_fp8_quant,
 )
@@ -23,6 +24,7 @@ ops_deepseek_v4_qnorm_rope_kv_rope_quant_insert = fused_deepseek_v4_qnorm_rope_k
 ops_inv_rope_fp8_quant = fused_inv_rope_fp8_quant
 
 __all__ = [
+    "dequantize_and_gather_k_cache",
     "fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert",
     "fused_inv_rope_fp8_quant",
     "ops_deepseek_v4_qnorm_rope_kv_rope_quant_insert",

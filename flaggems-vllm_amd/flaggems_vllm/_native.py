@@ -91,6 +91,16 @@ def lib():
         _I64, ctypes.c_float, ctypes.c_int,  # padded_tokens, eps, tma_aligned_scales
         _P,  # stream
     ]
+    L.fgv_dequantize_and_gather_k_cache.restype = ctypes.c_int
+    L.fgv_dequantize_and_gather_k_cache.argtypes = [
+        _P, _I64, _I64, _I64,  # out, out_stride_req, out_stride_row, out_rows
+        _P, _I64, _I64,  # k_cache, cache_block_stride, num_blocks
+        _P, _P,  # seq_lens, gather_lens
+        _P, _I64, _I64,  # block_table, block_table_stride, max_blocks_per_seq
+        _I64, _I64, _I64,  # num_reqs, block_size, offset
+        _I64, _I64, _I64,  # nope_dim, rope_dim, scale_slots
+        _P,  # stream
+    ]
     _lib = L
     return _lib
 
@@ -111,4 +121,5 @@ EXPORTED_SYMBOLS = (
     "fgv_last_error",
     "fgv_qnorm_rope_kv_rope_quant_insert",
     "fgv_inv_rope_fp8_quant",
+    "fgv_dequantize_and_gather_k_cache",
 )

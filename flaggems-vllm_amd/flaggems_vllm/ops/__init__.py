@@ -1,10 +1,12 @@
-"""The two DeepSeek-V4 attention pre-processing ops (reference: src/flaggems_vllm/ops/__init__.py:61-64)."""
+"""DeepSeek-V4 attention pre-processing ops (reference: src/flaggems_vllm/ops/__init__.py:34-38, 61-65)."""
+from .deepseek_v4_attention_dequantize_and_gather_k_cache import dequantize_and_gather_k_cache
 from .fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert import (
     fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert,
 )
 from .fused_inv_rope_fp8_quant import SUPPORTED_FP8_DTYPE, fused_inv_rope_fp8_quant
 
 __all__ = [
+    "dequantize_and_gather_k_cache",
     "fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert",
     "fused_inv_rope_fp8_quant",
     "SUPPORTED_FP8_DTYPE",

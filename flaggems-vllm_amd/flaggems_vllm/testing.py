@@ -79,6 +79,12 @@ def inv_rope_bytes(num_tokens: int, num_heads: int, tma_aligned_scales: bool) ->
     return num_tokens * num_heads * (1024 + 512 + scale_bytes) + (8 + 256) * num_tokens
 
 
+def gather_bytes(rows: int) -> int:
+    """Algorithmic HBM bytes of gathering `rows` cached tokens: 584 cache bytes
+    read, 1024 bf16 bytes written and a 4-byte block-table entry per row."""
+    return rows * (HEAD_BYTES + 2 * HEAD_DIM + 4)
+
+
 @dataclass
 class Workload:
     name: str
@@ -211,11 +217,13 @@ def make_workload(config: int, seed: Optional[int] = None, num_heads: Optional[i
         need = (65536 + per) // bs + 1
         tables = [(perm[s * need:(s + 1) * need], 0) for s in range(nseq)]
         slots = _paged_slots(positions, seq_ids, tables, bs)
+        seq_lens, new_lens = starts + per, torch.full((nseq,), per)
     elif config == 3:
         positions = torch.arange(T, dtype=torch.int64)
         perm = torch.randperm(nblk, generator=g)
-        slots = _paged_slots(positions, torch.zeros(T, dtype=torch.int64),
-                             [(perm[:(T + bs - 1) // bs], 0)], bs)
+        tables = [(perm[:(T + bs - 1) // bs], 0)]
+        slots = _paged_slots(positions, torch.zeros(T, dtype=torch.int64), tables, bs)
+        seq_lens, new_lens = torch.tensor([T]), torch.tensor([T])
     else:  # config 4
         starts = (torch.rand(64, generator=g, dtype=torch.float64) *
                   (max_pos - lens).to(torch.float64)).to(torch.int64)
@@ -231,11 +239,22 @@ def make_workload(config: int, seed: Optional[int] = None, num_heads: Optional[i
             at += c
         slots = _paged_slots(positions, seq_ids, tables, bs)
         slots = _pad_some(slots, round(0.10 * T), g)
+        seq_lens, new_lens = starts + lens, lens
 
+    meta = {"config": config, "max_pos": max_pos, "num_blocks": nblk}
+    if config >= 2:
+        # per-sequence block tables (int32, [num_seqs, max_blocks]; entries before a
+        # sequence's first touched block are 0 and never read), the sequence
+        # lengths after this chunk and the number of tokens it added
+        width = max(f + len(t) for t, f in tables)
+        bt = torch.zeros(len(tables), width, dtype=torch.int32)
+        for i, (t, f) in enumerate(tables):
+            bt[i, f:f + len(t)] = t.to(torch.int32)
+        meta.update(block_table=bt, seq_lens=seq_lens.to(torch.int32),
+                    new_lens=new_lens.to(torch.int32))
     cos_sin = make_cos_sin_cache(max_pos)
     return Workload(f"c{config}", q, kv, _cache(nblk, bs), slots.contiguous(),
-                    positions.contiguous(), cos_sin, EPS, bs, weight, buf,
-                    {"config": config, "max_pos": max_pos, "num_blocks": nblk})
+                    positions.contiguous(), cos_sin, EPS, bs, weight, buf, meta)
 
 
 @dataclass

@@ -102,6 +102,39 @@ int fgv_inv_rope_fp8_quant(
     int64_t padded_tokens, float eps, int tma_aligned_scales,
     void* stream);
 
+/*
+ * Dequantise and gather cached K rows into bf16.
+ *
+ * Replaces flaggems_vllm.dequantize_and_gather_k_cache
+ * (reference: src/flaggems_vllm/ops/deepseek_v4_attention_dequantize_and_gather_k_cache.py:123-172,
+ * kernel :38-120), the consumer of the cache that
+ * fgv_qnorm_rope_kv_rope_quant_insert writes.
+ *
+ *   out          bf16 [>= num_reqs, out_rows, >= nope_dim + rope_dim]; element
+ *                (r, j, c) at out + r*out_stride_req + j*out_stride_row + c.
+ *   k_cache      uint8 paged cache: block b at k_cache + b*cache_block_stride;
+ *                per block block_size x (nope_dim + 2*rope_dim) token bytes, then
+ *                block_size x scale_slots UE8M0 bytes.
+ *   seq_lens     int32 [num_reqs]; gather_lens int32 [num_reqs] or NULL (= seq_lens).
+ *   block_table  int32 [num_reqs, max_blocks_per_seq], row stride block_table_stride.
+ *
+ * For request r and i < gather_lens[r] (and offset + i < out_rows), position
+ * p = seq_lens[r] - gather_lens[r] + i is read from block
+ * block_table[r, p / block_size] and written to out row offset + i:
+ * columns < nope_dim get e4m3(code) * 2^(scale_byte - 127) of their 64-element
+ * group, the next rope_dim columns the cached bf16 values.  Rows whose block
+ * index or physical block is out of range are left untouched.
+ * nope_dim and rope_dim must be multiples of 8.
+ */
+int fgv_dequantize_and_gather_k_cache(
+    void* out, int64_t out_stride_req, int64_t out_stride_row, int64_t out_rows,
+    const void* k_cache, int64_t cache_block_stride, int64_t num_blocks,
+    const int32_t* seq_lens, const int32_t* gather_lens,
+    const int32_t* block_table, int64_t block_table_stride, int64_t max_blocks_per_seq,
+    int64_t num_reqs, int64_t block_size, int64_t offset,
+    int64_t nope_dim, int64_t rope_dim, int64_t scale_slots,
+    void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -78,6 +78,19 @@ def lib():
             _P, _I64, _I64, _I64,  # scale, sc_sg, sc_sk, tpad
             ctypes.c_float, ctypes.c_int, ctypes.c_int,  # eps, tma, nthreads
         ]
+        L.oracle_e4m3fn_to_f32.restype = ctypes.c_float
+        L.oracle_e4m3fn_to_f32.argtypes = [ctypes.c_uint8]
+        L.oracle_e4m3fn_decode_array.restype = None
+        L.oracle_e4m3fn_decode_array.argtypes = [_P, _P, _I64]
+        L.oracle_dequantize_and_gather_k_cache.restype = None
+        L.oracle_dequantize_and_gather_k_cache.argtypes = [
+            _P, _I64, _I64, _I64,  # out, out_s0, out_s1, out_rows
+            _P, _I64, _I64,  # cache, block_stride, num_blocks
+            _P, _P,  # seq_lens, gather_lens
+            _P, _I64, _I64,  # block_table, bt_stride, max_blocks
+            _I64, _I64, _I64,  # num_reqs, bs, offset
+            _I64, _I64, _I64,  # nope, rope, scale_slots
+        ]
         _lib = L
     return _lib
 
@@ -171,3 +184,35 @@ def inv_rope_fp8_quant(o, positions, cos_sin_cache, n_groups, heads_per_group,
         float(eps), int(bool(tma_aligned_scales)), _threads(nthreads),
     )
     return fp8.transpose(0, 1), scale.transpose(0, 1)
+
+
+def e4m3fn_decode(codes: torch.Tensor) -> torch.Tensor:
+    """float32 values of uint8 e4m3fn codes."""
+    codes = _cpu(codes, torch.uint8).contiguous()
+    out = torch.empty(codes.shape, dtype=torch.float32)
+    lib().oracle_e4m3fn_decode_array(codes.data_ptr(), out.data_ptr(), codes.numel())
+    return out
+
+
+def dequantize_and_gather_k_cache(out, k_cache, seq_lens, gather_lens, block_table, block_size,
+                                  offset=0, rope_dim=64, nope_dim=None, scale_slots=None):
+    """CPU restatement, in place on ``out`` (same arguments as
+    flaggems_vllm.dequantize_and_gather_k_cache; int32 index tensors)."""
+    _cpu(out, torch.bfloat16), _cpu(k_cache, torch.uint8)
+    if nope_dim is None:
+        nope_dim = out.shape[-1] - rope_dim
+    if scale_slots is None:
+        scale_slots = (nope_dim + 63) // 64 + (1 if nope_dim % 64 == 0 else 0)
+    seq_lens = _cpu(seq_lens, torch.int32).contiguous()
+    if gather_lens is not None:
+        gather_lens = _cpu(gather_lens, torch.int32).contiguous()
+    block_table = _cpu(block_table, torch.int32)
+    assert out.stride(-1) == 1 and block_table.stride(-1) == 1
+    lib().oracle_dequantize_and_gather_k_cache(
+        out.data_ptr(), out.stride(0), out.stride(1), out.shape[1],
+        k_cache.data_ptr(), k_cache.stride(0), k_cache.shape[0],
+        seq_lens.data_ptr(), gather_lens.data_ptr() if gather_lens is not None else None,
+        block_table.data_ptr(), block_table.stride(0), block_table.shape[1],
+        seq_lens.shape[0], int(block_size), int(offset), int(nope_dim), int(rope_dim),
+        int(scale_slots),
+    )

@@ -14,6 +14,9 @@
  *   oracle_inv_rope_fp8_quant
  *     reference op   src/flaggems_vllm/ops/fused_inv_rope_fp8_quant.py:37-256
  *     reference test tests/test_fused_inv_rope_fp8_quant.py:150-198
+ *   oracle_dequantize_and_gather_k_cache
+ *     reference op   src/flaggems_vllm/ops/deepseek_v4_attention_dequantize_and_gather_k_cache.py:38-172
+ *     reference test tests/test_deepseek_v4_attention_dequantize_and_gather_k_cache.py:42-119
  *
  * Numerics (compile with -ffp-contract=off and without -ffast-math):
  *   - every product and sum is a separately rounded binary32 operation, as in
@@ -97,6 +100,27 @@ uint8_t oracle_e4m3fn(float x)
     if (code > 0x7eu)
         code = 0x7fu; /* rounds past 448: NaN, there is no infinity */
     return (uint8_t)(sign | code);
+}
+
+/* OCP e4m3fn code -> binary32 (exact): 0x7f / 0xff are NaN, codes 1..7 are
+   the subnormals m * 2^-9, others (1 + m/8) * 2^(e-7). */
+float oracle_e4m3fn_to_f32(uint8_t code)
+{
+    int sign = code >> 7, e = (code >> 3) & 15, m = code & 7;
+    float v;
+    if (e == 15 && m == 7)
+        v = NAN;
+    else if (e == 0)
+        v = ldexpf((float)m, -9);
+    else
+        v = ldexpf(1.0f + (float)m / 8.0f, e - 7);
+    return sign ? -v : v;
+}
+
+void oracle_e4m3fn_decode_array(const uint8_t* codes, float* out, int64_t n)
+{
+    for (int64_t i = 0; i < n; ++i)
+        out[i] = oracle_e4m3fn_to_f32(codes[i]);
 }
 
 void oracle_e4m3fn_array(const float* x, uint8_t* out, int64_t n)
@@ -303,4 +327,45 @@ void oracle_inv_rope_fp8_quant(const uint16_t* o, int64_t o_st, int64_t o_sh,
                     ((float*)scale)[g * sc_sg + k * sc_sk + t] = 0.0f;
             }
         }
+}
+
+/*
+ * dequantize_and_gather_k_cache: out element (r, j, c) at out + r*out_s0 +
+ * j*out_s1 + c (bf16).  For request r and i < gather_len (and offset + i <
+ * out_rows): pos = seq_len - gather_len + i, block block_table[r*bt_stride +
+ * pos / bs]; nope column c -> bf16(e4m3(code_c) * 2^(scale[c/64] - 127)),
+ * rope columns copy the cached bf16 values (reference kernel :61-120).  Rows
+ * whose block index or block is out of range are skipped, as in the kernel.
+ */
+void oracle_dequantize_and_gather_k_cache(uint16_t* out, int64_t out_s0, int64_t out_s1, int64_t out_rows,
+                                          const uint8_t* cache, int64_t block_stride, int64_t num_blocks,
+                                          const int32_t* seq_lens, const int32_t* gather_lens,
+                                          const int32_t* block_table, int64_t bt_stride, int64_t max_blocks,
+                                          int64_t num_reqs, int64_t bs, int64_t offset,
+                                          int64_t nope, int64_t rope, int64_t scale_slots)
+{
+    int64_t token_bytes = nope + 2 * rope;
+    for (int64_t r = 0; r < num_reqs; ++r) {
+        int64_t seq_len = seq_lens[r];
+        int64_t gl = gather_lens ? gather_lens[r] : seq_len;
+        for (int64_t i = 0; i < gl && offset + i < out_rows; ++i) {
+            int64_t pos = seq_len - gl + i;
+            if (pos < 0 || pos / bs >= max_blocks)
+                continue;
+            int64_t blk = block_table[r * bt_stride + pos / bs];
+            if (blk < 0 || blk >= num_blocks)
+                continue;
+            int64_t pib = pos % bs;
+            const uint8_t* base = cache + blk * block_stride;
+            const uint8_t* tok = base + pib * token_bytes;
+            const uint8_t* scl = base + bs * token_bytes + pib * scale_slots;
+            uint16_t* row = out + r * out_s0 + (offset + i) * out_s1;
+            for (int64_t c = 0; c < nope; ++c) {
+                float scale = ldexpf(1.0f, (int)scl[c / 64] - 127);
+                row[c] = oracle_f32_to_bf16(oracle_e4m3fn_to_f32(tok[c]) * scale);
+            }
+            for (int64_t c = 0; c < rope; ++c)
+                memcpy(row + nope + c, tok + nope + 2 * c, 2);
+        }
+    }
 }

@@ -8,7 +8,10 @@ oracle that the reference's own tests compare its Triton kernels against:
   ``_exact_pow2`` :154-163, ``torch_quantize_and_insert_k_cache`` :178-243,
   ``ref_impl`` :316-333 (q processed 2**19 rows at a time);
 * sibling: tests/test_fused_inv_rope_fp8_quant.py
-  ``native_fused_inv_rope_fp8_quant`` :150-198, ``_pack_ue8m0_scales`` :82-90.
+  ``native_fused_inv_rope_fp8_quant`` :150-198, ``_pack_ue8m0_scales`` :82-90;
+* dequantize_and_gather_k_cache: the reference kernel's per-row semantics
+  (ops/deepseek_v4_attention_dequantize_and_gather_k_cache.py:61-120) in torch
+  index arithmetic, with torch's float8 -> float cast and exp2 scale.
 
 Arithmetic is whatever torch's CPU kernels do in float32: the sum of squares
 and rsqrt are torch's, which is why q is compared against this restatement
@@ -110,3 +113,34 @@ def inv_rope_fp8_quant(o, positions, cos_sin_cache, n_groups, heads_per_group,
     for c in range(4):
         packed |= byte[..., c] << (8 * c)
     return codes, packed
+
+
+def dequantize_and_gather_k_cache(out, k_cache, seq_lens, gather_lens, block_table, block_size,
+                                  offset=0, rope_dim=64, nope_dim=None, scale_slots=None):
+    """In place on ``out`` (CPU tensors)."""
+    if nope_dim is None:
+        nope_dim = out.shape[-1] - rope_dim
+    if scale_slots is None:
+        scale_slots = (nope_dim + 63) // 64 + (1 if nope_dim % 64 == 0 else 0)
+    tb = nope_dim + 2 * rope_dim
+    flat = k_cache.reshape(k_cache.shape[0], -1)
+    for r in range(seq_lens.shape[0]):
+        sl = int(seq_lens[r])
+        gl = int(gather_lens[r]) if gather_lens is not None else sl
+        n = max(0, min(gl, out.shape[1] - offset))
+        if n == 0:
+            continue
+        pos = sl - gl + torch.arange(n)
+        blk = block_table[r, pos // block_size].long()
+        pib = pos % block_size
+        rows = flat[blk]  # [n, block bytes]
+        data_at = (pib * tb)[:, None] + torch.arange(tb)
+        data = torch.gather(rows, 1, data_at)
+        sc_at = (block_size * tb + pib * scale_slots)[:, None] + torch.arange(scale_slots)
+        sbytes = torch.gather(rows, 1, sc_at)
+        codes = data[:, :nope_dim].contiguous().view(torch.float8_e4m3fn).float()
+        grp = torch.arange(nope_dim) // 64
+        scale = torch.exp2(sbytes[:, grp].float() - 127.0)
+        out[r, offset:offset + n, :nope_dim] = (codes * scale).to(torch.bfloat16)
+        out[r, offset:offset + n, nope_dim:nope_dim + rope_dim] = (
+            data[:, nope_dim:].contiguous().view(torch.bfloat16))
