@@ -89,24 +89,39 @@ dequantize_gather_kernel(GatherArgs a) {
     const uint8_t* scl = base + (int64_t)bs * token_bytes + (int64_t)pib * slots;
     uint16_t* out = a.out + (int64_t)r * a.out_s0 + (int64_t)(a.offset + i) * a.out_s1;
 
-    uint2 sbytes = make_uint2(0, 0);
-    if (kDsv4)
-        sbytes = load8(scl);  // the 7 group bytes + pad, one load
     const int chunks = (nope + rope) / 8;
     const int nope_chunks = nope / 8;
-#pragma unroll(kDsv4 ? 4 : 1)
+    if (kDsv4) {
+        // All loads of the row are issued before any store (byte pointers
+        // would otherwise pin each load behind the previous store), and piece
+        // 3 takes one load shape for both its halves so no lane diverges.
+        const uint2 sbytes = load8(scl);  // the 7 group bytes + pad
+        uint2 in[3];
+#pragma unroll
+        for (int k = 0; k < 3; ++k)
+            in[k] = load8(tok + (lane16 + 16 * k) * 8);
+        // Piece 3 without divergence: lanes 0..7 read codes 384..447 (8 bytes
+        // used of 16), lanes 8..15 read the 16 bytes of rope values 4*(l-8)..+3;
+        // both stay inside the 576 token bytes.
+        const uint8_t* p3 = lane16 < 8 ? tok + 384 + 8 * lane16 : tok + kNopeDim + 16 * (lane16 - 8);
+        const uint2 in3a = load8(p3), in3b = load8(p3 + 8);
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+            const int g = 2 * k + (lane16 >> 3);
+            const uint32_t b = ((g < 4 ? sbytes.x : sbytes.y) >> (8 * (g & 3))) & 0xffu;
+            store16(out + (lane16 + 16 * k) * 8, decode8(in[k].x, in[k].y, ue8m0_value(b)));
+        }
+        const uint4 dec6 = decode8(in3a.x, in3a.y, ue8m0_value((sbytes.y >> 16) & 0xffu));
+        const uint4 v3 = lane16 < 8 ? dec6 : make_uint4(in3a.x, in3a.y, in3b.x, in3b.y);
+        store16(out + (lane16 + 48) * 8, v3);
+        return;
+    }
     for (int c = lane16; c < chunks; c += 16) {
         const int e = c * 8;
         uint4 v;
         if (c < nope_chunks) {
             const uint2 codes = load8(tok + e);
-            const int g = e >> 6;
-            uint32_t b;
-            if (kDsv4)
-                b = ((g < 4 ? sbytes.x : sbytes.y) >> (8 * (g & 3))) & 0xffu;
-            else
-                b = scl[g];
-            v = decode8(codes.x, codes.y, ue8m0_value(b));
+            v = decode8(codes.x, codes.y, ue8m0_value(scl[e >> 6]));
         } else {
             const uint8_t* src = tok + nope + 2 * (e - nope);
             const uint2 lo = load8(src), hi = load8(src + 8);

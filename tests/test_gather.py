@@ -173,8 +173,9 @@ def test_gpu_whole_sequences_offset_and_bounds():
     seq_lens = torch.tensor([200, 256, 150], dtype=torch.int32)
     for gl, offset, rows in ((None, 0, 256), (torch.tensor([50, 256, 70], dtype=torch.int32), 3, 100)):
         ref = torch.full((3, rows, 520), 3.0, dtype=torch.bfloat16)
-        oracle.dequantize_and_gather_k_cache(ref, r.k_cache, seq_lens, gl, bt, 64, offset=offset)
+        oracle.dequantize_and_gather_k_cache(ref, r.k_cache, seq_lens, gl, bt, 64, offset=offset,
+                                             nope_dim=448)
         got = _gpu_gather(torch.full((3, rows, 520), 3.0, dtype=torch.bfloat16), r.k_cache, seq_lens,
-                          gl, bt, 64, offset=offset)
+                          gl, bt, 64, offset=offset, nope_dim=448)
         assert torch.equal(got, ref)
     assert nblk == 4
