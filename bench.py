@@ -34,7 +34,8 @@ def parse_args():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", type=int, default=2, help="main-op workload c0..c4 (default c2)")
-    ap.add_argument("--op", choices=["main", "inv_rope", "gather", "copy"], default="main",
+    ap.add_argument("--op", choices=["main", "inv_rope", "gather", "rmsnorm", "copy"],
+                    default="main",
                     help="copy: torch device copy of 512 MiB, the HBM calibration kernel")
     ap.add_argument("--tma", action="store_true", help="inv_rope: packed UE8M0 scales")
     ap.add_argument("--cpu-sample-tokens", type=int, default=8192)
@@ -180,6 +181,23 @@ def main():
         config = {"workload": f"dequantize_and_gather_k_cache: all positions of c{args.config}'s "
                               f"{bt.shape[0]} sequences ({T} rows) from its 584 B/token FP8 cache",
                   "rows": T, "num_reqs": int(bt.shape[0])}
+        args.no_cpu_baseline = True
+    elif args.op == "rmsnorm":
+        # DeepSeek-V4 q LoRA rank 1536 and kv latent 512 for c2's 8192 tokens
+        g = torch.Generator().manual_seed(0)
+        T = 8192
+        qr = W.randn_bf16((T, 1536), g).to(dev)
+        kvr = W.randn_bf16((T, 512), g).to(dev)
+        qw = W.randn_bf16((1536,), g).to(dev)
+        kw = W.randn_bf16((512,), g).to(dev)
+        bytes_call = W.rmsnorm_bytes(T, 1536, 512)
+
+        def step():
+            flaggems_vllm.fused_q_kv_rmsnorm(qr, kvr, qw, kw, 1e-6)
+
+        kernel, workload = "fused_q_kv_rmsnorm_kernel", "T8192_q1536_kv512"
+        config = {"workload": "fused_q_kv_rmsnorm T=8192, q 1536, kv 512, bf16 weights",
+                  "num_tokens": T}
         args.no_cpu_baseline = True
     elif args.op == "copy":
         n = 512 << 20

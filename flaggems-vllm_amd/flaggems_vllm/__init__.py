@@ -14,6 +14,7 @@ from .ops import (  # noqa: F401
     dequantize_and_gather_k_cache,
     fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert,
     fused_inv_rope_fp8_quant,
+    fused_q_kv_rmsnorm,
 )
 
 device = "cuda"
@@ -25,6 +26,7 @@ ops_inv_rope_fp8_quant = fused_inv_rope_fp8_quant
 
 __all__ = [
     "dequantize_and_gather_k_cache",
+    "fused_q_kv_rmsnorm",
     "fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert",
     "fused_inv_rope_fp8_quant",
     "ops_deepseek_v4_qnorm_rope_kv_rope_quant_insert",

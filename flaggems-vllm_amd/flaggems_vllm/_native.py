@@ -101,6 +101,13 @@ def lib():
         _I64, _I64, _I64,  # nope_dim, rope_dim, scale_slots
         _P,  # stream
     ]
+    L.fgv_fused_q_kv_rmsnorm.restype = ctypes.c_int
+    L.fgv_fused_q_kv_rmsnorm.argtypes = [
+        _P, _I64, _P, _I64, _P, _I64,  # qr, stride, qr_out, stride, q_weight, q_size
+        _P, _I64, _P, _I64, _P, _I64,  # kv, stride, kv_out, stride, kv_weight, kv_size
+        _I64, ctypes.c_float, ctypes.c_int,  # num_tokens, eps, weight_is_fp32
+        _P,  # stream
+    ]
     _lib = L
     return _lib
 
@@ -122,4 +129,5 @@ EXPORTED_SYMBOLS = (
     "fgv_qnorm_rope_kv_rope_quant_insert",
     "fgv_inv_rope_fp8_quant",
     "fgv_dequantize_and_gather_k_cache",
+    "fgv_fused_q_kv_rmsnorm",
 )

@@ -1,5 +1,6 @@
 """DeepSeek-V4 attention pre-processing ops (reference: src/flaggems_vllm/ops/__init__.py:34-38, 61-65)."""
 from .deepseek_v4_attention_dequantize_and_gather_k_cache import dequantize_and_gather_k_cache
+from .deepseek_v4_attention_fused_q_kv_rmsnorm import fused_q_kv_rmsnorm
 from .fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert import (
     fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert,
 )
@@ -7,6 +8,7 @@ from .fused_inv_rope_fp8_quant import SUPPORTED_FP8_DTYPE, fused_inv_rope_fp8_qu
 
 __all__ = [
     "dequantize_and_gather_k_cache",
+    "fused_q_kv_rmsnorm",
     "fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert",
     "fused_inv_rope_fp8_quant",
     "SUPPORTED_FP8_DTYPE",

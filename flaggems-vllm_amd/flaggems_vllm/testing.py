@@ -85,6 +85,12 @@ def gather_bytes(rows: int) -> int:
     return rows * (HEAD_BYTES + 2 * HEAD_DIM + 4)
 
 
+def rmsnorm_bytes(rows: int, q_size: int, kv_size: int) -> int:
+    """Algorithmic HBM bytes of fused_q_kv_rmsnorm: each bf16 row read and
+    written once, plus the two bf16 weight vectors."""
+    return 4 * rows * (q_size + kv_size) + 2 * (q_size + kv_size)
+
+
 @dataclass
 class Workload:
     name: str

@@ -135,6 +135,24 @@ int fgv_dequantize_and_gather_k_cache(
     int64_t nope_dim, int64_t rope_dim, int64_t scale_slots,
     void* stream);
 
+/*
+ * Fused weighted RMSNorm of DeepSeek-V4's q LoRA rows and kv latent rows.
+ *
+ * Replaces flaggems_vllm.fused_q_kv_rmsnorm
+ * (reference: src/flaggems_vllm/ops/deepseek_v4_attention_fused_q_kv_rmsnorm.py:65-103,
+ * kernel :24-62).  For every token t:
+ *   qr_out[t] = (qr[t] * rsqrt(mean(qr[t]^2) + eps)) * q_weight
+ *   kv_out[t] = (kv[t] * rsqrt(mean(kv[t]^2) + eps)) * kv_weight
+ * Rows are bf16 with row strides in elements; weights are bf16, or float when
+ * weight_is_fp32.  Sizes must be multiples of 8, at most 4096.
+ */
+int fgv_fused_q_kv_rmsnorm(
+    const void* qr, int64_t qr_stride, void* qr_out, int64_t qr_out_stride,
+    const void* q_weight, int64_t q_size,
+    const void* kv, int64_t kv_stride, void* kv_out, int64_t kv_out_stride,
+    const void* kv_weight, int64_t kv_size,
+    int64_t num_tokens, float eps, int weight_is_fp32, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

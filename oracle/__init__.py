@@ -91,6 +91,12 @@ def lib():
             _I64, _I64, _I64,  # num_reqs, bs, offset
             _I64, _I64, _I64,  # nope, rope, scale_slots
         ]
+        L.oracle_fused_q_kv_rmsnorm.restype = None
+        L.oracle_fused_q_kv_rmsnorm.argtypes = [
+            _P, _I64, _P, _I64, _P, _I64,
+            _P, _I64, _P, _I64, _P, _I64,
+            _I64, ctypes.c_float, ctypes.c_int, ctypes.c_int,
+        ]
         _lib = L
     return _lib
 
@@ -216,3 +222,18 @@ def dequantize_and_gather_k_cache(out, k_cache, seq_lens, gather_lens, block_tab
         seq_lens.shape[0], int(block_size), int(offset), int(nope_dim), int(rope_dim),
         int(scale_slots),
     )
+
+
+def fused_q_kv_rmsnorm(qr, kv, q_weight, kv_weight, eps, nthreads=None):
+    """CPU restatement: returns (qr_out, kv_out) as contiguous bf16 tensors."""
+    _cpu(qr, torch.bfloat16), _cpu(kv, torch.bfloat16)
+    assert q_weight.dtype == kv_weight.dtype and q_weight.dtype in (torch.bfloat16, torch.float32)
+    assert qr.stride(-1) == 1 and kv.stride(-1) == 1
+    q_weight, kv_weight = q_weight.contiguous(), kv_weight.contiguous()
+    qo = torch.empty(qr.shape, dtype=torch.bfloat16)
+    ko = torch.empty(kv.shape, dtype=torch.bfloat16)
+    lib().oracle_fused_q_kv_rmsnorm(
+        qr.data_ptr(), qr.stride(0), qo.data_ptr(), qo.stride(0), q_weight.data_ptr(), qr.shape[1],
+        kv.data_ptr(), kv.stride(0), ko.data_ptr(), ko.stride(0), kv_weight.data_ptr(), kv.shape[1],
+        qr.shape[0], float(eps), int(q_weight.dtype == torch.float32), _threads(nthreads))
+    return qo, ko

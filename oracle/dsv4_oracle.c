@@ -14,6 +14,9 @@
  *   oracle_inv_rope_fp8_quant
  *     reference op   src/flaggems_vllm/ops/fused_inv_rope_fp8_quant.py:37-256
  *     reference test tests/test_fused_inv_rope_fp8_quant.py:150-198
+ *   oracle_fused_q_kv_rmsnorm
+ *     reference op   src/flaggems_vllm/ops/deepseek_v4_attention_fused_q_kv_rmsnorm.py:24-103
+ *     reference test tests/test_deepseek_v4_attention_fused_q_kv_rmsnorm.py:40-76
  *   oracle_dequantize_and_gather_k_cache
  *     reference op   src/flaggems_vllm/ops/deepseek_v4_attention_dequantize_and_gather_k_cache.py:38-172
  *     reference test tests/test_deepseek_v4_attention_dequantize_and_gather_k_cache.py:42-119
@@ -367,5 +370,39 @@ void oracle_dequantize_and_gather_k_cache(uint16_t* out, int64_t out_s0, int64_t
             for (int64_t c = 0; c < rope; ++c)
                 memcpy(row + nope + c, tok + nope + 2 * c, 2);
         }
+    }
+}
+
+/* Weighted RMSNorm of one bf16 row: y = (x * r) * w with r as in
+   oracle_rms_factor but over `size` elements (reference kernel :55-62). */
+static void rmsnorm_row(const uint16_t* x, uint16_t* y, const void* w, int w_f32, int64_t size,
+                        float eps)
+{
+    double s = 0.0;
+    for (int64_t i = 0; i < size; ++i) {
+        double v = (double)oracle_bf16_to_f32(x[i]);
+        s += v * v;
+    }
+    float var = (float)(s / (double)size);
+    var = var + eps;
+    float r = (float)(1.0 / sqrt((double)var));
+    for (int64_t i = 0; i < size; ++i) {
+        float wi = w_f32 ? ((const float*)w)[i] : oracle_bf16_to_f32(((const uint16_t*)w)[i]);
+        float t = oracle_bf16_to_f32(x[i]) * r;
+        y[i] = oracle_f32_to_bf16(t * wi);
+    }
+}
+
+void oracle_fused_q_kv_rmsnorm(const uint16_t* qr, int64_t qr_st, uint16_t* qr_out, int64_t qo_st,
+                               const void* q_w, int64_t q_size,
+                               const uint16_t* kv, int64_t kv_st, uint16_t* kv_out, int64_t ko_st,
+                               const void* kv_w, int64_t kv_size,
+                               int64_t num_tokens, float eps, int w_f32, int nthreads)
+{
+    (void)nthreads;
+#pragma omp parallel for schedule(static) num_threads(nthreads > 0 ? nthreads : 1)
+    for (int64_t t = 0; t < num_tokens; ++t) {
+        rmsnorm_row(qr + t * qr_st, qr_out + t * qo_st, q_w, w_f32, q_size, eps);
+        rmsnorm_row(kv + t * kv_st, kv_out + t * ko_st, kv_w, w_f32, kv_size, eps);
     }
 }

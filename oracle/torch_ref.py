@@ -9,6 +9,8 @@ oracle that the reference's own tests compare its Triton kernels against:
   ``ref_impl`` :316-333 (q processed 2**19 rows at a time);
 * sibling: tests/test_fused_inv_rope_fp8_quant.py
   ``native_fused_inv_rope_fp8_quant`` :150-198, ``_pack_ue8m0_scales`` :82-90;
+* fused_q_kv_rmsnorm: tests/test_deepseek_v4_attention_fused_q_kv_rmsnorm.py
+  ``_rmsnorm_ref`` :40-44;
 * dequantize_and_gather_k_cache: the reference kernel's per-row semantics
   (ops/deepseek_v4_attention_dequantize_and_gather_k_cache.py:61-120) in torch
   index arithmetic, with torch's float8 -> float cast and exp2 scale.
@@ -144,3 +146,14 @@ def dequantize_and_gather_k_cache(out, k_cache, seq_lens, gather_lens, block_tab
         out[r, offset:offset + n, :nope_dim] = (codes * scale).to(torch.bfloat16)
         out[r, offset:offset + n, nope_dim:nope_dim + rope_dim] = (
             data[:, nope_dim:].contiguous().view(torch.bfloat16))
+
+
+def rmsnorm(x, weight, eps):
+    """Weighted RMSNorm in float32, result in x's dtype."""
+    xf = x.float()
+    y = xf * torch.rsqrt(torch.mean(xf * xf, dim=-1, keepdim=True) + eps)
+    return (y * weight.float()).to(x.dtype)
+
+
+def fused_q_kv_rmsnorm(qr, kv, q_weight, kv_weight, eps):
+    return rmsnorm(qr, q_weight, eps), rmsnorm(kv, kv_weight, eps)
