@@ -34,10 +34,11 @@ def parse_args():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", type=int, default=2, help="main-op workload c0..c4 (default c2)")
-    ap.add_argument("--op", choices=["main", "inv_rope", "gather", "rmsnorm", "copy"],
+    ap.add_argument("--op", choices=["main", "inv_rope", "gather", "rmsnorm", "indexer", "copy"],
                     default="main",
                     help="copy: torch device copy of 512 MiB, the HBM calibration kernel")
     ap.add_argument("--tma", action="store_true", help="inv_rope: packed UE8M0 scales")
+    ap.add_argument("--fp4", action="store_true", help="indexer: MXFP4 instead of FP8")
     ap.add_argument("--cpu-sample-tokens", type=int, default=8192)
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="repeat the CPU sample until this much CPU time is spent (min 3 runs)")
@@ -198,6 +199,25 @@ def main():
         kernel, workload = "fused_q_kv_rmsnorm_kernel", "T8192_q1536_kv512"
         config = {"workload": "fused_q_kv_rmsnorm T=8192, q 1536, kv 512, bf16 weights",
                   "num_tokens": T}
+        args.no_cpu_baseline = True
+    elif args.op == "indexer":
+        # DeepSeek-V4 sparse indexer: 64 index heads of 128 dims for c2's 8192 tokens
+        g = torch.Generator().manual_seed(0)
+        T, H = 8192, 64
+        iq = W.randn_bf16((T, H, 128), g).to(dev)
+        pos = torch.randint(0, 65536, (T,), generator=g).to(dev)
+        cs = W.make_cos_sin_cache(65536).to(dev)
+        iw = W.randn_bf16((T, H), g).to(dev)
+        bytes_call = W.indexer_bytes(T, H, 128, args.fp4)
+
+        def step():
+            flaggems_vllm.fused_indexer_q_rope_quant(pos, iq, cs, iw, 128 ** -0.5, H ** -0.5,
+                                                     use_fp4=args.fp4)
+
+        kernel = "indexer_q_rope_quant_kernel"
+        workload = "T8192_H64_D128" + ("_mxfp4" if args.fp4 else "_fp8")
+        config = {"workload": f"fused_indexer_q_rope_quant T=8192, H=64, D=128, "
+                              f"{'MXFP4' if args.fp4 else 'FP8'}", "num_tokens": T}
         args.no_cpu_baseline = True
     elif args.op == "copy":
         n = 512 << 20

@@ -1,0 +1,319 @@
+// gfx950 kernel for DeepSeek-V4's sparse-indexer q pre-processing: GPT-J RoPE
+// on the last 64 dims of each index head, then FP8 e4m3 quant with one UE8M0
+// scale per (token, head) folded into the head weights, or MXFP4 (E2M1 with
+// one UE8M0 scale per 32 elements).
+//
+// Reference semantics: src/flaggems_vllm/ops/fused_indexer_q_rope_quant.py
+//   FP8   kernel :64-167   MXFP4 kernel :170-282   wrapper :285-410
+// and its test tests/test_fused_indexer_q_rope_quant.py:51-110 (exact codes,
+// scales and weights).  The rotated values are rounded to bf16 before the
+// amax, as the reference does.
+//
+// Layout: one (token, head) row per 16-lane DPP row (fgv_device.h); lane l16
+// owns elements (l16 + 16*p)*8 .. +8 for p < kPieces (head_dim = 128*kPieces),
+// so the 64 rope elements are lanes 8..15 of the last piece, an FP8 row amax
+// is one 16-lane DPP max and an MXFP4 32-element block is one lane quad.
+#include "fgv_device.h"
+#include "fgv_host.h"
+
+namespace fgv {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kRowsPerBlock = kThreads / 16;
+
+struct IndexerArgs {
+    const int64_t* positions;
+    const uint16_t* q;
+    const void* cos_sin;
+    const void* weights;
+    float* weights_out;
+    uint8_t* q_out;
+    uint8_t* scale_out;
+    int64_t q_st, q_sh;
+    int64_t cs_stride, max_pos;
+    int64_t w_st, wo_st;
+    int64_t qo_st, qo_sh;
+    int64_t so_st, so_sh;
+    uint32_t num_rows, num_heads;
+    float softmax_scale, head_scale;
+    int w_f32, fp4;
+};
+
+__device__ __forceinline__ float4 load_cs4(const void* base, int64_t off, bool bf16) {
+    if (bf16) {
+        const uint2 v = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(base) + off);
+        return make_float4(bf16_lo(v.x), bf16_hi(v.x), bf16_lo(v.y), bf16_hi(v.y));
+    }
+    return *reinterpret_cast<const float4*>(static_cast<const float*>(base) + off);
+}
+
+// MXFP4 block exponent k = ceil(log2(max(amax, 6*2^-126) / 6)) from the
+// binary32 fields of a = m * 2^E: 6 = 1.5 * 2^2, so k = E - 2 + (m > 1.5).
+// Exact for every bf16 amax (amax/6 never rounds across a power of two).
+__device__ __forceinline__ int mxfp4_exponent(uint32_t amax_bits) {
+    const uint32_t kFloor = 0x01C00000u;  // 6 * 2^-126 = 1.5 * 2^-124
+    const uint32_t a = amax_bits > kFloor ? amax_bits : kFloor;
+    return (int)(a >> 23) - 127 - 2 + ((a & 0x7fffffu) > 0x400000u ? 1 : 0);
+}
+
+// FP8 row exponent k = ceil(log2(max(amax, 1e-4) / 448)) (see the main op).
+__device__ __forceinline__ int fp8_row_exponent(uint32_t amax_bits) {
+    const uint32_t kFloor = 0x38D1B717u;  // 1e-4f
+    const uint32_t a = amax_bits > kFloor ? amax_bits : kFloor;
+    return (int)(a >> 23) - 127 - 8 + ((a & 0x7fffffu) > 0x600000u ? 1 : 0);
+}
+
+// Eight values (already scaled into [-6, 6]) -> eight E2M1 nibbles, element i
+// in bits 4i..4i+3 (even element in the low nibble of each byte), RNE.
+__device__ __forceinline__ uint32_t pack_fp4x8(const float (&x)[8]) {
+    uint32_t w = 0;
+    w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, x[0], x[1], 1.0f, 0);
+    w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, x[2], x[3], 1.0f, 1);
+    w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, x[4], x[5], 1.0f, 2);
+    w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, x[6], x[7], 1.0f, 3);
+    return w;
+}
+
+// One (token, head) row: rotate, quantise, store codes, scales and weight.
+template <int kPieces>
+__device__ __forceinline__ void indexer_row(const IndexerArgs& a, uint32_t t, uint32_t h,
+                                            const uint4 (&v)[kPieces], float4 c, float4 s,
+                                            float w_in, int lane16) {
+    const bool rope_lane = lane16 >= 8;
+    float xf[kPieces][8];
+#pragma unroll
+    for (int p = 0; p < kPieces; ++p) {
+        const uint32_t w4[4] = {v[p].x, v[p].y, v[p].z, v[p].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            xf[p][2 * i] = bf16_lo(w4[i]);
+            xf[p][2 * i + 1] = bf16_hi(w4[i]);
+        }
+    }
+    if (rope_lane) {
+        // x_even*cos - x_odd*sin, x_odd*cos + x_even*sin, each rounded to
+        // binary32 and the result to bf16 (reference kernel :113-123).
+        float* r = xf[kPieces - 1];
+        const float cc[4] = {c.x, c.y, c.z, c.w}, ss[4] = {s.x, s.y, s.z, s.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float e = r[2 * i], o = r[2 * i + 1];
+            const float ec = e * cc[i], os = o * ss[i], oc = o * cc[i], es = e * ss[i];
+            const uint32_t w = pack_bf16x2(ec - os, oc + es);
+            r[2 * i] = bf16_lo(w);
+            r[2 * i + 1] = bf16_hi(w);
+        }
+    }
+
+    uint8_t* qo = a.q_out + (int64_t)t * a.qo_st + (int64_t)h * a.qo_sh;
+    if (!a.fp4) {
+        uint32_t m = 0;
+#pragma unroll
+        for (int p = 0; p < kPieces; ++p)
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                m = max(m, __float_as_uint(xf[p][i]) & 0x7fffffffu);
+        m = row16_max(m);
+        const int k = fp8_row_exponent(m);
+        const float inv = exp2_neg_int(k);
+#pragma unroll
+        for (int p = 0; p < kPieces; ++p) {
+            const float* y = xf[p];
+            const uint32_t lo = pack_fp8x4(clamp_fp8(y[0] * inv), clamp_fp8(y[1] * inv),
+                                           clamp_fp8(y[2] * inv), clamp_fp8(y[3] * inv));
+            const uint32_t hi = pack_fp8x4(clamp_fp8(y[4] * inv), clamp_fp8(y[5] * inv),
+                                           clamp_fp8(y[6] * inv), clamp_fp8(y[7] * inv));
+            store8(qo + (lane16 + 16 * p) * 8, lo, hi);
+        }
+        if (lane16 == 0) {
+            const float q_scale = __uint_as_float((uint32_t)(k + 127) << 23);
+            float w = w_in * q_scale;
+            w = w * a.softmax_scale;
+            w = w * a.head_scale;
+            a.weights_out[(int64_t)t * a.wo_st + h] = w;
+        }
+        return;
+    }
+
+    // MXFP4: 32-element blocks are lane quads (4 lanes x 8 elements).
+    uint8_t* so = a.scale_out + (int64_t)t * a.so_st + (int64_t)h * a.so_sh;
+#pragma unroll
+    for (int p = 0; p < kPieces; ++p) {
+        uint32_t m = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            m = max(m, __float_as_uint(xf[p][i]) & 0x7fffffffu);
+        m = max(m, dpp_u32<kDppQuadXor1>(m));
+        m = max(m, dpp_u32<kDppQuadXor2>(m));
+        const int k = mxfp4_exponent(m);
+        const float inv = exp2_neg_int(k);
+        float y[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            y[i] = xf[p][i] * inv;
+        const uint32_t nib = pack_fp4x8(y);
+        *reinterpret_cast<uint32_t*>(qo + (lane16 + 16 * p) * 4) = nib;
+        if ((lane16 & 3) == 0)
+            so[(lane16 + 16 * p) >> 2] = (uint8_t)(k + 127);
+    }
+    if (lane16 == 0) {
+        float w = w_in * a.softmax_scale;
+        w = w * a.head_scale;
+        a.weights_out[(int64_t)t * a.wo_st + h] = w;
+    }
+}
+
+// Each 16-lane group owns kRows rows, 16 rows apart inside the block, so a
+// wave's load instruction covers 4 consecutive rows and every lane keeps
+// kRows * kPieces = 4 sixteen-byte loads in flight.  Index loads (position,
+// weight) are issued before the q loads and the cos/sin loads after them, so
+// no load waits on a later one (vmcnt counts in issue order).  kOneToken: all
+// rows of the block share one token and its position is a scalar load.
+template <int kPieces, bool kCsBf16, bool kOneToken>
+__global__ void __launch_bounds__(kThreads)
+indexer_q_rope_quant_kernel(IndexerArgs a) {
+    constexpr int kRows = 4 / kPieces;
+    const int lane16 = threadIdx.x & 15;
+    const bool rope_lane = lane16 >= 8;
+    const uint32_t row0 = blockIdx.x * (kRowsPerBlock * kRows);
+    uint32_t tt[kRows], hh[kRows];
+    bool valid[kRows];
+    int64_t praw[kRows];
+    uint32_t w_bits[kRows];
+    int64_t pos_block = 0;
+    if (kOneToken)
+        pos_block = a.positions[row0 / a.num_heads];
+#pragma unroll
+    for (int rr = 0; rr < kRows; ++rr) {
+        const uint32_t row = row0 + rr * kRowsPerBlock + (threadIdx.x >> 4);
+        valid[rr] = row < a.num_rows;
+        tt[rr] = (valid[rr] ? row : row0) / a.num_heads;
+        hh[rr] = (valid[rr] ? row : row0) - tt[rr] * a.num_heads;
+        praw[rr] = kOneToken ? pos_block : a.positions[tt[rr]];
+        const int64_t wi = (int64_t)tt[rr] * a.w_st + hh[rr];
+        // raw bits only: converting here would wait on the load inside the branch
+        w_bits[rr] = a.w_f32 ? static_cast<const uint32_t*>(a.weights)[wi]
+                             : (uint32_t) static_cast<const uint16_t*>(a.weights)[wi];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    uint4 v[kRows][kPieces];
+#pragma unroll
+    for (int rr = 0; rr < kRows; ++rr) {
+        const uint16_t* x = a.q + (int64_t)tt[rr] * a.q_st + (int64_t)hh[rr] * a.q_sh;
+#pragma unroll
+        for (int p = 0; p < kPieces; ++p)
+            v[rr][p] = valid[rr] ? load16(x + (lane16 + 16 * p) * 8) : make_uint4(0, 0, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    float4 c[kRows], s[kRows];
+#pragma unroll
+    for (int rr = 0; rr < kRows; ++rr) {
+        c[rr] = s[rr] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (rope_lane) {
+            const int64_t pos = clamp_position(praw[rr], a.max_pos);
+            const int64_t off = pos * a.cs_stride + (lane16 - 8) * 4;
+            c[rr] = load_cs4(a.cos_sin, off, kCsBf16);
+            s[rr] = load_cs4(a.cos_sin, off + kHalfRope, kCsBf16);
+        }
+    }
+#pragma unroll
+    for (int rr = 0; rr < kRows; ++rr) {
+        const float w_in = __uint_as_float(a.w_f32 ? w_bits[rr] : w_bits[rr] << 16);
+        if (valid[rr])
+            indexer_row<kPieces>(a, tt[rr], hh[rr], v[rr], c[rr], s[rr], w_in, lane16);
+    }
+}
+
+template <int kPieces>
+void launch_indexer(const IndexerArgs& a, bool cs_bf16, bool one_token, dim3 grid, hipStream_t s) {
+    if (cs_bf16) {
+        if (one_token)
+            hipLaunchKernelGGL((indexer_q_rope_quant_kernel<kPieces, true, true>), grid, dim3(kThreads), 0, s, a);
+        else
+            hipLaunchKernelGGL((indexer_q_rope_quant_kernel<kPieces, true, false>), grid, dim3(kThreads), 0, s, a);
+    } else {
+        if (one_token)
+            hipLaunchKernelGGL((indexer_q_rope_quant_kernel<kPieces, false, true>), grid, dim3(kThreads), 0, s, a);
+        else
+            hipLaunchKernelGGL((indexer_q_rope_quant_kernel<kPieces, false, false>), grid, dim3(kThreads), 0, s, a);
+    }
+}
+
+}  // namespace
+}  // namespace fgv
+
+extern "C" int fgv_fused_indexer_q_rope_quant(
+    const int64_t* positions, int64_t num_tokens,
+    const void* index_q, int64_t q_stride_token, int64_t q_stride_head,
+    int64_t num_heads, int64_t head_dim,
+    const void* cos_sin_cache, int64_t cos_sin_stride, int64_t max_pos, int cos_sin_is_bf16,
+    const void* weights, int64_t weights_stride, int weights_is_fp32,
+    float softmax_scale, float head_scale,
+    float* weights_out, int64_t weights_out_stride,
+    int use_fp4,
+    void* q_out, int64_t q_out_stride_token, int64_t q_out_stride_head,
+    void* scale_out, int64_t scale_out_stride_token, int64_t scale_out_stride_head,
+    void* stream) {
+    using namespace fgv;
+    if (num_tokens < 0 || num_heads < 0)
+        return fail(FGV_E_BAD_SHAPE, "negative size");
+    const int64_t rows = num_tokens * num_heads;
+    if (rows == 0)
+        return FGV_OK;
+    if (rows > 0x7fffffffLL)
+        return fail(FGV_E_TOO_LARGE, "num_tokens * num_heads must be below 2^31");
+    if (head_dim != 128 && head_dim != 256 && head_dim != 512)
+        return fail(FGV_E_BAD_SHAPE, "head_dim must be 128, 256 or 512 (rope 64)");
+    if (!positions || !index_q || !cos_sin_cache || !weights || !weights_out || !q_out ||
+        (use_fp4 && !scale_out))
+        return fail(FGV_E_NULL_POINTER, "null pointer argument");
+    if (max_pos <= 0)
+        return fail(FGV_E_BAD_SHAPE, "cos_sin_cache has no rows");
+    if (!aligned(index_q, 16) || q_stride_token % 8 || q_stride_head % 8)
+        return fail(FGV_E_MISALIGNED, "index_q must be 16-byte aligned, strides multiple of 8");
+    if (!aligned(cos_sin_cache, cos_sin_is_bf16 ? 8 : 16) || cos_sin_stride % 4)
+        return fail(FGV_E_MISALIGNED, "cos_sin_cache misaligned or row stride not a multiple of 4");
+    if (use_fp4) {
+        if (!aligned(q_out, 4) || q_out_stride_token % 4 || q_out_stride_head % 4)
+            return fail(FGV_E_MISALIGNED, "packed MXFP4 output must be 4-byte aligned");
+    } else if (!aligned(q_out, 8) || q_out_stride_token % 8 || q_out_stride_head % 8) {
+        return fail(FGV_E_MISALIGNED, "FP8 output must be 8-byte aligned, strides multiple of 8");
+    }
+
+    IndexerArgs a;
+    a.positions = positions;
+    a.q = static_cast<const uint16_t*>(index_q);
+    a.cos_sin = cos_sin_cache;
+    a.weights = weights;
+    a.weights_out = weights_out;
+    a.q_out = static_cast<uint8_t*>(q_out);
+    a.scale_out = static_cast<uint8_t*>(scale_out);
+    a.q_st = q_stride_token;
+    a.q_sh = q_stride_head;
+    a.cs_stride = cos_sin_stride;
+    a.max_pos = max_pos;
+    a.w_st = weights_stride;
+    a.wo_st = weights_out_stride;
+    a.qo_st = q_out_stride_token;
+    a.qo_sh = q_out_stride_head;
+    a.so_st = scale_out_stride_token;
+    a.so_sh = scale_out_stride_head;
+    a.num_rows = (uint32_t)rows;
+    a.num_heads = (uint32_t)num_heads;
+    a.softmax_scale = softmax_scale;
+    a.head_scale = head_scale;
+    a.w_f32 = weights_is_fp32 ? 1 : 0;
+    a.fp4 = use_fp4 ? 1 : 0;
+    const int rows_per_block = kRowsPerBlock * (head_dim == 128 ? 4 : head_dim == 256 ? 2 : 1);
+    const dim3 grid((unsigned)((rows + rows_per_block - 1) / rows_per_block));
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const bool one_token = num_heads % rows_per_block == 0;
+    if (head_dim == 128)
+        launch_indexer<1>(a, cos_sin_is_bf16, one_token, grid, s);
+    else if (head_dim == 256)
+        launch_indexer<2>(a, cos_sin_is_bf16, one_token, grid, s);
+    else
+        launch_indexer<4>(a, cos_sin_is_bf16, one_token, grid, s);
+    return launch_status();
+}

@@ -78,30 +78,45 @@ __device__ __forceinline__ float div_by_scale(float x, float s, float y) {
     return __builtin_copysignf(__builtin_fmaf(r, y, q0), x);
 }
 
+// Position first (the cos/sin loads depend on it; vmcnt counts in issue
+// order), then the row, then cos/sin.  kOneToken (num_heads a multiple of 16):
+// the block's rows share one token and the position is a scalar load.
+template <bool kOneToken>
 __device__ void row_block(const InvRopeArgs& a, uint32_t rb, int lane16, int row_in_pass) {
     uint4 v[kPasses][4];
     float4 cs_c[kPasses], cs_s[kPasses];
     uint32_t tok[kPasses], head[kPasses];
     bool valid[kPasses];
+    int64_t praw[kPasses];
     const bool rope_lane = lane16 >= 8;
+    const uint32_t row0 = rb * kRowsPerBlock;
+    const int64_t pos_block = kOneToken ? a.positions[row0 / a.num_heads] : 0;
 
 #pragma unroll
     for (int p = 0; p < kPasses; ++p) {
-        uint32_t row = rb * kRowsPerBlock + p * kRowsPerPass + row_in_pass;
+        const uint32_t row = row0 + p * kRowsPerPass + row_in_pass;
         valid[p] = row < a.num_rows;
-        tok[p] = valid[p] ? row / a.num_heads : 0;
-        head[p] = valid[p] ? row - tok[p] * a.num_heads : 0;
-        if (valid[p]) {
-            const uint16_t* x = a.o + (int64_t)tok[p] * a.o_st + (int64_t)head[p] * a.o_sh;
+        tok[p] = (valid[p] ? row : row0) / a.num_heads;
+        head[p] = (valid[p] ? row : row0) - tok[p] * a.num_heads;
+        praw[p] = kOneToken ? pos_block : a.positions[tok[p]];
+    }
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int k = 0; k < 4; ++k)
-                v[p][k] = load16(x + (lane16 + 16 * k) * 8);
-            if (rope_lane) {
-                int64_t pos = clamp_position(a.positions[tok[p]], a.max_pos);
-                const float* cs = a.cos_sin + pos * a.cs_stride + (lane16 - 8) * 4;
-                cs_c[p] = *reinterpret_cast<const float4*>(cs);
-                cs_s[p] = *reinterpret_cast<const float4*>(cs + kHalfRope);
-            }
+    for (int p = 0; p < kPasses; ++p) {
+        const uint16_t* x = a.o + (int64_t)tok[p] * a.o_st + (int64_t)head[p] * a.o_sh;
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            v[p][k] = valid[p] ? load16(x + (lane16 + 16 * k) * 8) : make_uint4(0, 0, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int p = 0; p < kPasses; ++p) {
+        cs_c[p] = cs_s[p] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (rope_lane) {
+            const int64_t pos = clamp_position(praw[p], a.max_pos);
+            const float* cs = a.cos_sin + pos * a.cs_stride + (lane16 - 8) * 4;
+            cs_c[p] = *reinterpret_cast<const float4*>(cs);
+            cs_s[p] = *reinterpret_cast<const float4*>(cs + kHalfRope);
         }
     }
 
@@ -179,10 +194,11 @@ __device__ void pad_block(const InvRopeArgs& a) {
     }
 }
 
+template <bool kOneToken>
 __global__ void __launch_bounds__(kThreads)
 inv_rope_fp8_quant_kernel(InvRopeArgs a) {
     if (blockIdx.x < a.row_blocks)
-        row_block(a, blockIdx.x, threadIdx.x & 15, threadIdx.x >> 4);
+        row_block<kOneToken>(a, blockIdx.x, threadIdx.x & 15, threadIdx.x >> 4);
     else
         pad_block(a);
 }
@@ -247,7 +263,11 @@ extern "C" int fgv_inv_rope_fp8_quant(
     a.eps = eps;
     a.tma = tma_aligned_scales ? 1 : 0;
     const uint32_t grid = a.row_blocks + (padded_tokens > num_tokens ? 1u : 0u);
-    hipLaunchKernelGGL(inv_rope_fp8_quant_kernel, dim3(grid), dim3(kThreads), 0,
-                       static_cast<hipStream_t>(stream), a);
+    if (num_heads % kRowsPerBlock == 0)
+        hipLaunchKernelGGL(inv_rope_fp8_quant_kernel<true>, dim3(grid), dim3(kThreads), 0,
+                           static_cast<hipStream_t>(stream), a);
+    else
+        hipLaunchKernelGGL(inv_rope_fp8_quant_kernel<false>, dim3(grid), dim3(kThreads), 0,
+                           static_cast<hipStream_t>(stream), a);
     return launch_status();
 }

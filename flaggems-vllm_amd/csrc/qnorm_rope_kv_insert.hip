@@ -20,10 +20,9 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kRowsPerPass = kThreads / 16;   // 16 rows per pass
-// One pass of four 16-byte loads per lane: 62 VGPRs, 8 waves per SIMD.  More
-// passes per block (more loads per wave, fewer waves) measured slower.
-constexpr int kQPasses = 1;
-constexpr int kQRowsPerBlock = kRowsPerPass * kQPasses;
+// One pass of four 16-byte loads per lane (8 waves per SIMD); more rows per
+// block (more loads per wave, fewer waves) measured slower.
+constexpr int kQRowsPerBlock = kRowsPerPass;
 constexpr int kKvTokensPerBlock = kRowsPerPass;
 
 struct QnormArgs {
@@ -90,54 +89,58 @@ __device__ __forceinline__ void unpack8(uint4 v, float (&x)[8]) {
     x[6] = bf16_lo(v.w); x[7] = bf16_hi(v.w);
 }
 
+// Loads are issued position first: the cos/sin row depends on it, and the
+// in-order vmcnt counter would otherwise make that dependent load wait for
+// the q loads issued before it.  kOneToken (num_heads a multiple of 16): all
+// rows of the block share one token, whose position is a scalar load.
+template <bool kOneToken>
 __device__ void q_block(const QnormArgs& a, uint32_t qb, int lane16, int row_in_pass) {
-    uint4 v[kQPasses][4];
-    float4 cs_c[kQPasses], cs_s[kQPasses];
-    uint16_t* rowp[kQPasses];
-    bool valid[kQPasses];
+    const uint32_t row0 = qb * kQRowsPerBlock;
+    const uint32_t row = row0 + row_in_pass;
+    const bool valid = row < a.num_q_rows;
     const bool rope_lane = lane16 >= 8;
-
+    uint32_t t;
+    int64_t pos_raw;
+    if (kOneToken) {
+        t = row0 / a.num_heads;  // uniform across the block
+        pos_raw = a.positions[t];
+    } else {
+        t = (valid ? row : row0) / a.num_heads;
+        pos_raw = a.positions[t];  // every lane loads: no branch before the q loads
+        __builtin_amdgcn_sched_barrier(0);  // keep it ahead of the q loads
+    }
+    const uint32_t h = row - t * a.num_heads;
+    uint16_t* rowp = a.q + (int64_t)t * a.q_st + (int64_t)h * a.q_sh;
+    if (!valid)
+        return;
+    uint4 v[4];
 #pragma unroll
-    for (int p = 0; p < kQPasses; ++p) {
-        uint32_t row = qb * kQRowsPerBlock + p * kRowsPerPass + row_in_pass;
-        valid[p] = row < a.num_q_rows;
-        uint32_t t = valid[p] ? row / a.num_heads : 0;
-        uint32_t h = valid[p] ? row - t * a.num_heads : 0;
-        rowp[p] = a.q + (int64_t)t * a.q_st + (int64_t)h * a.q_sh;
-        if (valid[p]) {
-#pragma unroll
-            for (int k = 0; k < 4; ++k)
-                v[p][k] = load16(rowp[p] + (lane16 + 16 * k) * 8);
-            if (rope_lane) {
-                int64_t pos = clamp_position(a.positions[t], a.max_pos);
-                const float* cs = a.cos_sin + pos * a.cs_stride + (lane16 - 8) * 4;
-                cs_c[p] = *reinterpret_cast<const float4*>(cs);
-                cs_s[p] = *reinterpret_cast<const float4*>(cs + kHalfRope);
-            }
-        }
+    for (int k = 0; k < 4; ++k)
+        v[k] = load16(rowp + (lane16 + 16 * k) * 8);
+    const int64_t pos = clamp_position(pos_raw, a.max_pos);
+    float4 cs_c = make_float4(0.f, 0.f, 0.f, 0.f), cs_s = cs_c;
+    if (rope_lane) {
+        const float* cs = a.cos_sin + pos * a.cs_stride + (lane16 - 8) * 4;
+        cs_c = *reinterpret_cast<const float4*>(cs);
+        cs_s = *reinterpret_cast<const float4*>(cs + kHalfRope);
     }
 
+    const float r = rms_factor(v, a.eps);
 #pragma unroll
-    for (int p = 0; p < kQPasses; ++p) {
-        if (!valid[p])
-            continue;
-        const float r = rms_factor(v[p], a.eps);
+    for (int k = 0; k < 4; ++k) {
+        float x[8];
+        unpack8(v[k], x);
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            float x[8];
-            unpack8(v[p][k], x);
-#pragma unroll
-            for (int i = 0; i < 8; ++i)
-                x[i] = x[i] * r;
-            uint4 out;
-            if (k == 3 && rope_lane) {
-                out = rope_piece(x, cs_c[p], cs_s[p]);
-            } else {
-                out = make_uint4(pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3]),
-                                 pack_bf16x2(x[4], x[5]), pack_bf16x2(x[6], x[7]));
-            }
-            store16(rowp[p] + (lane16 + 16 * k) * 8, out);
+        for (int i = 0; i < 8; ++i)
+            x[i] = x[i] * r;
+        uint4 out;
+        if (k == 3 && rope_lane) {
+            out = rope_piece(x, cs_c, cs_s);
+        } else {
+            out = make_uint4(pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3]),
+                             pack_bf16x2(x[4], x[5]), pack_bf16x2(x[6], x[7]));
         }
+        store16(rowp + (lane16 + 16 * k) * 8, out);
     }
 }
 
@@ -155,23 +158,26 @@ __device__ void kv_block(const QnormArgs& a, uint32_t kvb, int lane16, int row_i
     const uint32_t t = kvb * kKvTokensPerBlock + row_in_pass;
     if (t >= a.num_tokens_insert)
         return;
+    // slot and position first (see q_block), then the kv row, then cos/sin
     const int64_t slot = a.slot_mapping[t];
+    const int64_t pos_raw = a.positions[t];
+    __builtin_amdgcn_sched_barrier(0);  // both ahead of the kv loads
+    const uint16_t* x = a.kv + (int64_t)t * a.kv_st;
+    uint4 v[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        v[k] = load16(x + (lane16 + 16 * k) * 8);
+    __builtin_amdgcn_sched_barrier(0);
+    const int64_t pos = clamp_position(pos_raw, a.max_pos);
     if (slot < 0)
         return;
     const int64_t blk = slot / a.block_size;
     const int64_t pib = slot - blk * a.block_size;
     if (blk >= a.num_blocks)
         return;
-
-    const uint16_t* x = a.kv + (int64_t)t * a.kv_st;
-    uint4 v[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-        v[k] = load16(x + (lane16 + 16 * k) * 8);
     const bool rope_lane = lane16 >= 8;
     float4 c = make_float4(0.f, 0.f, 0.f, 0.f), s = c;
     if (rope_lane) {
-        int64_t pos = clamp_position(a.positions[t], a.max_pos);
         const float* cs = a.cos_sin + pos * a.cs_stride + (lane16 - 8) * 4;
         c = *reinterpret_cast<const float4*>(cs);
         s = *reinterpret_cast<const float4*>(cs + kHalfRope);
@@ -220,6 +226,7 @@ __device__ void kv_block(const QnormArgs& a, uint32_t kvb, int lane16, int row_i
     }
 }
 
+template <bool kOneToken>
 __global__ void __launch_bounds__(kThreads)
 qnorm_rope_kv_insert_kernel(QnormArgs a) {
     const int lane16 = threadIdx.x & 15;
@@ -227,7 +234,7 @@ qnorm_rope_kv_insert_kernel(QnormArgs a) {
     if (blockIdx.x < a.kv_blocks)
         kv_block(a, blockIdx.x, lane16, row_in_pass);
     else
-        q_block(a, blockIdx.x - a.kv_blocks, lane16, row_in_pass);
+        q_block<kOneToken>(a, blockIdx.x - a.kv_blocks, lane16, row_in_pass);
 }
 
 }  // namespace
@@ -295,7 +302,11 @@ extern "C" int fgv_qnorm_rope_kv_rope_quant_insert(
     a.eps = eps;
     const uint32_t q_blocks = (uint32_t)((q_rows + kQRowsPerBlock - 1) / kQRowsPerBlock);
     const uint32_t grid = a.kv_blocks + q_blocks;
-    hipLaunchKernelGGL(qnorm_rope_kv_insert_kernel, dim3(grid), dim3(kThreads), 0,
-                       static_cast<hipStream_t>(stream), a);
+    if (num_heads > 0 && num_heads % kQRowsPerBlock == 0)
+        hipLaunchKernelGGL(qnorm_rope_kv_insert_kernel<true>, dim3(grid), dim3(kThreads), 0,
+                           static_cast<hipStream_t>(stream), a);
+    else
+        hipLaunchKernelGGL(qnorm_rope_kv_insert_kernel<false>, dim3(grid), dim3(kThreads), 0,
+                           static_cast<hipStream_t>(stream), a);
     return launch_status();
 }

@@ -13,6 +13,7 @@ from .ops import (  # noqa: F401
     SUPPORTED_FP8_DTYPE,
     dequantize_and_gather_k_cache,
     fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert,
+    fused_indexer_q_rope_quant,
     fused_inv_rope_fp8_quant,
     fused_q_kv_rmsnorm,
 )
@@ -28,6 +29,7 @@ __all__ = [
     "dequantize_and_gather_k_cache",
     "fused_q_kv_rmsnorm",
     "fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert",
+    "fused_indexer_q_rope_quant",
     "fused_inv_rope_fp8_quant",
     "ops_deepseek_v4_qnorm_rope_kv_rope_quant_insert",
     "ops_inv_rope_fp8_quant",

@@ -108,6 +108,19 @@ def lib():
         _I64, ctypes.c_float, ctypes.c_int,  # num_tokens, eps, weight_is_fp32
         _P,  # stream
     ]
+    L.fgv_fused_indexer_q_rope_quant.restype = ctypes.c_int
+    L.fgv_fused_indexer_q_rope_quant.argtypes = [
+        _P, _I64,  # positions, num_tokens
+        _P, _I64, _I64, _I64, _I64,  # index_q, strides, num_heads, head_dim
+        _P, _I64, _I64, ctypes.c_int,  # cos_sin, stride, max_pos, is_bf16
+        _P, _I64, ctypes.c_int,  # weights, stride, is_fp32
+        ctypes.c_float, ctypes.c_float,  # softmax_scale, head_scale
+        _P, _I64,  # weights_out, stride
+        ctypes.c_int,  # use_fp4
+        _P, _I64, _I64,  # q_out, strides
+        _P, _I64, _I64,  # scale_out, strides
+        _P,  # stream
+    ]
     _lib = L
     return _lib
 
@@ -130,4 +143,5 @@ EXPORTED_SYMBOLS = (
     "fgv_inv_rope_fp8_quant",
     "fgv_dequantize_and_gather_k_cache",
     "fgv_fused_q_kv_rmsnorm",
+    "fgv_fused_indexer_q_rope_quant",
 )

@@ -4,12 +4,14 @@ from .deepseek_v4_attention_fused_q_kv_rmsnorm import fused_q_kv_rmsnorm
 from .fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert import (
     fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert,
 )
+from .fused_indexer_q_rope_quant import fused_indexer_q_rope_quant
 from .fused_inv_rope_fp8_quant import SUPPORTED_FP8_DTYPE, fused_inv_rope_fp8_quant
 
 __all__ = [
     "dequantize_and_gather_k_cache",
     "fused_q_kv_rmsnorm",
     "fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert",
+    "fused_indexer_q_rope_quant",
     "fused_inv_rope_fp8_quant",
     "SUPPORTED_FP8_DTYPE",
 ]

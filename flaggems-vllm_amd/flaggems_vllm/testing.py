@@ -91,6 +91,14 @@ def rmsnorm_bytes(rows: int, q_size: int, kv_size: int) -> int:
     return 4 * rows * (q_size + kv_size) + 2 * (q_size + kv_size)
 
 
+def indexer_bytes(rows: int, heads: int, head_dim: int, fp4: bool) -> int:
+    """Algorithmic HBM bytes of fused_indexer_q_rope_quant: bf16 q read, FP8
+    codes (or E2M1 nibbles + one scale byte per 32) written, bf16 weight read
+    and float32 weight written, position and cos/sin row per token."""
+    per_head = 2 * head_dim + (head_dim // 2 + head_dim // 32 if fp4 else head_dim) + 2 + 4
+    return rows * heads * per_head + rows * (8 + 256)
+
+
 @dataclass
 class Workload:
     name: str

@@ -153,6 +153,38 @@ int fgv_fused_q_kv_rmsnorm(
     const void* kv_weight, int64_t kv_size,
     int64_t num_tokens, float eps, int weight_is_fp32, void* stream);
 
+/*
+ * Fused sparse-indexer q RoPE + quant with head-weight folding.
+ *
+ * Replaces flaggems_vllm.fused_indexer_q_rope_quant
+ * (reference: src/flaggems_vllm/ops/fused_indexer_q_rope_quant.py:285-410,
+ * kernels :64-167 (FP8) and :170-282 (MXFP4)).
+ *
+ *   index_q      bf16 [num_tokens, num_heads, head_dim], head_dim 128/256/512;
+ *                GPT-J RoPE on the last 64 dims, result rounded to bf16.
+ *   cos_sin      [max_pos, 64] float (or bf16 if cos_sin_is_bf16), cos | sin.
+ *   weights      [num_tokens, num_heads] bf16 (or float), row stride given.
+ *   use_fp4 == 0: q_out = e4m3fn codes of x * 2^-k per (t, h), with
+ *                k = ceil(log2(max(amax, 1e-4) / 448));
+ *                weights_out = ((w * 2^k) * softmax_scale) * head_scale.
+ *   use_fp4 != 0: q_out = packed E2M1 nibbles [.., head_dim/2] (even element
+ *                in the low nibble), scale_out = UE8M0 byte per 32 elements,
+ *                k = ceil(log2(max(amax, 6*2^-126) / 6));
+ *                weights_out = (w * softmax_scale) * head_scale.
+ */
+int fgv_fused_indexer_q_rope_quant(
+    const int64_t* positions, int64_t num_tokens,
+    const void* index_q, int64_t q_stride_token, int64_t q_stride_head,
+    int64_t num_heads, int64_t head_dim,
+    const void* cos_sin_cache, int64_t cos_sin_stride, int64_t max_pos, int cos_sin_is_bf16,
+    const void* weights, int64_t weights_stride, int weights_is_fp32,
+    float softmax_scale, float head_scale,
+    float* weights_out, int64_t weights_out_stride,
+    int use_fp4,
+    void* q_out, int64_t q_out_stride_token, int64_t q_out_stride_head,
+    void* scale_out, int64_t scale_out_stride_token, int64_t scale_out_stride_head,
+    void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -97,6 +97,17 @@ def lib():
             _P, _I64, _P, _I64, _P, _I64,
             _I64, ctypes.c_float, ctypes.c_int, ctypes.c_int,
         ]
+        L.oracle_e2m1.restype = ctypes.c_uint8
+        L.oracle_e2m1.argtypes = [ctypes.c_float]
+        L.oracle_e2m1_array.restype = None
+        L.oracle_e2m1_array.argtypes = [_P, _P, _I64]
+        L.oracle_fused_indexer_q_rope_quant.restype = None
+        L.oracle_fused_indexer_q_rope_quant.argtypes = [
+            _P, _I64, _P, _I64, _I64, _I64, _I64,
+            _P, _I64, _I64, ctypes.c_int, _P, _I64, ctypes.c_int,
+            ctypes.c_float, ctypes.c_float, _P, _I64, ctypes.c_int,
+            _P, _I64, _I64, _P, _I64, _I64,
+        ]
         _lib = L
     return _lib
 
@@ -237,3 +248,38 @@ def fused_q_kv_rmsnorm(qr, kv, q_weight, kv_weight, eps, nthreads=None):
         kv.data_ptr(), kv.stride(0), ko.data_ptr(), ko.stride(0), kv_weight.data_ptr(), kv.shape[1],
         qr.shape[0], float(eps), int(q_weight.dtype == torch.float32), _threads(nthreads))
     return qo, ko
+
+
+def e2m1_codes(x: torch.Tensor) -> torch.Tensor:
+    """uint8 E2M1 nibbles (sign in bit 3) of a float32 CPU tensor."""
+    x = _cpu(x, torch.float32).contiguous()
+    out = torch.empty(x.shape, dtype=torch.uint8)
+    lib().oracle_e2m1_array(x.data_ptr(), out.data_ptr(), x.numel())
+    return out
+
+
+def fused_indexer_q_rope_quant(positions, index_q, cos_sin, weights, softmax_scale, head_scale,
+                               use_fp4=False):
+    """CPU restatement.  Returns (q_fp8 codes uint8 [T, H, D], weights_out) or
+    ((packed uint8 [T, H, D/2], scale bytes uint8 [T, H, D/32]), weights_out)."""
+    _cpu(index_q, torch.bfloat16)
+    T = positions.shape[0]
+    _, H, D = index_q.shape
+    positions = positions.to(torch.int64).contiguous()
+    weights_out = torch.empty(weights.shape, dtype=torch.float32)
+    if use_fp4:
+        qo = torch.empty(T, H, D // 2, dtype=torch.uint8)
+        so = torch.empty(T, H, D // 32, dtype=torch.uint8)
+    else:
+        qo = torch.empty(T, H, D, dtype=torch.uint8)
+        so = torch.empty(1, 1, 1, dtype=torch.uint8)
+    lib().oracle_fused_indexer_q_rope_quant(
+        positions.data_ptr(), T, index_q.data_ptr(), index_q.stride(0), index_q.stride(1), H, D,
+        cos_sin.data_ptr(), cos_sin.stride(0), cos_sin.shape[0], int(cos_sin.dtype == torch.bfloat16),
+        weights.data_ptr(), weights.stride(0), int(weights.dtype == torch.float32),
+        float(softmax_scale), float(head_scale), weights_out.data_ptr(), weights_out.stride(0),
+        int(bool(use_fp4)), qo.data_ptr(), qo.stride(0), qo.stride(1),
+        so.data_ptr(), so.stride(0), so.stride(1))
+    if use_fp4:
+        return (qo, so), weights_out
+    return qo, weights_out

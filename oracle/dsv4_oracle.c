@@ -17,6 +17,9 @@
  *   oracle_fused_q_kv_rmsnorm
  *     reference op   src/flaggems_vllm/ops/deepseek_v4_attention_fused_q_kv_rmsnorm.py:24-103
  *     reference test tests/test_deepseek_v4_attention_fused_q_kv_rmsnorm.py:40-76
+ *   oracle_fused_indexer_q_rope_quant
+ *     reference op   src/flaggems_vllm/ops/fused_indexer_q_rope_quant.py:64-410
+ *     reference test tests/test_fused_indexer_q_rope_quant.py:51-110
  *   oracle_dequantize_and_gather_k_cache
  *     reference op   src/flaggems_vllm/ops/deepseek_v4_attention_dequantize_and_gather_k_cache.py:38-172
  *     reference test tests/test_deepseek_v4_attention_dequantize_and_gather_k_cache.py:42-119
@@ -404,5 +407,111 @@ void oracle_fused_q_kv_rmsnorm(const uint16_t* qr, int64_t qr_st, uint16_t* qr_o
     for (int64_t t = 0; t < num_tokens; ++t) {
         rmsnorm_row(qr + t * qr_st, qr_out + t * qo_st, q_w, w_f32, q_size, eps);
         rmsnorm_row(kv + t * kv_st, kv_out + t * ko_st, kv_w, w_f32, kv_size, eps);
+    }
+}
+
+/*
+ * binary32 -> E2M1 nibble (FP4: values 0, 0.5, 1, 1.5, 2, 3, 4, 6), round to
+ * nearest with ties to the even code, saturating at 6; bit 3 is the sign of x
+ * (so -0 and negative values that round to 0 keep it).  On [0, 2) the grid
+ * step is 0.5, on [2, 4) 1 and on [4, 6] 2, so the code is the step index
+ * rounded to nearest even, offset by the first code of the interval.
+ */
+uint8_t oracle_e2m1(float x)
+{
+    uint8_t sign = (uint8_t)((f2u(x) >> 31) << 3);
+    float a = fabsf(x);
+    if (a > 6.0f)
+        a = 6.0f;
+    uint32_t code;
+    if (a < 2.0f)
+        code = (uint32_t)nearbyintf(a * 2.0f);
+    else if (a < 4.0f)
+        code = 4u + (uint32_t)nearbyintf(a - 2.0f);
+    else
+        code = 6u + (uint32_t)nearbyintf((a - 4.0f) * 0.5f);
+    return (uint8_t)(sign | code);
+}
+
+void oracle_e2m1_array(const float* x, uint8_t* out, int64_t n)
+{
+    for (int64_t i = 0; i < n; ++i)
+        out[i] = oracle_e2m1(x[i]);
+}
+
+/*
+ * fused_indexer_q_rope_quant.  q[t, h, i] at q + t*q_st + h*q_sh (bf16);
+ * GPT-J RoPE on the last 64 dims rounded to bf16 (reference kernel :113-123),
+ * then FP8 (one 2^k per row, folded into the weights, :125-167) or MXFP4
+ * (one 2^k per 32 elements, :39-58, :211-282).
+ */
+void oracle_fused_indexer_q_rope_quant(const int64_t* positions, int64_t T,
+                                       const uint16_t* q, int64_t q_st, int64_t q_sh, int64_t H, int64_t D,
+                                       const void* cs, int64_t cs_st, int64_t max_pos, int cs_bf16,
+                                       const void* w, int64_t w_st, int w_f32,
+                                       float softmax_scale, float head_scale,
+                                       float* wo, int64_t wo_st, int fp4,
+                                       uint8_t* qo, int64_t qo_st, int64_t qo_sh,
+                                       uint8_t* so, int64_t so_st, int64_t so_sh)
+{
+    int64_t nope = D - ROPE_DIM;
+    float x[4096];
+    for (int64_t t = 0; t < T; ++t) {
+        int64_t pos = clamp_pos(positions[t], max_pos);
+        for (int64_t h = 0; h < H; ++h) {
+            const uint16_t* row = q + t * q_st + h * q_sh;
+            for (int64_t i = 0; i < D; ++i)
+                x[i] = oracle_bf16_to_f32(row[i]);
+            for (int j = 0; j < HALF_ROPE; ++j) {
+                float c, s;
+                if (cs_bf16) {
+                    c = oracle_bf16_to_f32(((const uint16_t*)cs)[pos * cs_st + j]);
+                    s = oracle_bf16_to_f32(((const uint16_t*)cs)[pos * cs_st + HALF_ROPE + j]);
+                } else {
+                    c = ((const float*)cs)[pos * cs_st + j];
+                    s = ((const float*)cs)[pos * cs_st + HALF_ROPE + j];
+                }
+                float e = x[nope + 2 * j], o = x[nope + 2 * j + 1];
+                float ec = e * c, os = o * s, oc = o * c, es = e * s;
+                float re = ec - os, ro = oc + es;
+                x[nope + 2 * j] = oracle_bf16_to_f32(oracle_f32_to_bf16(re));
+                x[nope + 2 * j + 1] = oracle_bf16_to_f32(oracle_f32_to_bf16(ro));
+            }
+            float wv = w_f32 ? ((const float*)w)[t * w_st + h]
+                             : oracle_bf16_to_f32(((const uint16_t*)w)[t * w_st + h]);
+            uint8_t* out = qo + t * qo_st + h * qo_sh;
+            if (!fp4) {
+                float amax = 0.0f;
+                for (int64_t i = 0; i < D; ++i)
+                    amax = fabsf(x[i]) > amax ? fabsf(x[i]) : amax;
+                float a = amax > 1e-4f ? amax : 1e-4f;
+                float scale = ldexpf(1.0f, (int)ceilf(log2f(a / FP8_MAX)));
+                for (int64_t i = 0; i < D; ++i)
+                    out[i] = oracle_e4m3fn(x[i] / scale);
+                float r = wv * scale;
+                r = r * softmax_scale;
+                wo[t * wo_st + h] = r * head_scale;
+            } else {
+                uint8_t* sc = so + t * so_st + h * so_sh;
+                for (int64_t b = 0; b < D / 32; ++b) {
+                    float amax = 0.0f;
+                    for (int i = 0; i < 32; ++i)
+                        amax = fabsf(x[b * 32 + i]) > amax ? fabsf(x[b * 32 + i]) : amax;
+                    const float floor6 = 6.0f * 0x1p-126f;
+                    float a = amax > floor6 ? amax : floor6;
+                    float k = ceilf(log2f(a * (1.0f / 6.0f)));
+                    k = k < -127.0f ? -127.0f : (k > 127.0f ? 127.0f : k);
+                    float scale = ldexpf(1.0f, (int)k);
+                    sc[b] = (uint8_t)(k + 127.0f);
+                    for (int i = 0; i < 32; i += 2) {
+                        uint8_t lo = oracle_e2m1(x[b * 32 + i] / scale);
+                        uint8_t hi = oracle_e2m1(x[b * 32 + i + 1] / scale);
+                        out[(b * 32 + i) / 2] = (uint8_t)(lo | (hi << 4));
+                    }
+                }
+                float r = wv * softmax_scale;
+                wo[t * wo_st + h] = r * head_scale;
+            }
+        }
     }
 }

@@ -11,6 +11,9 @@ oracle that the reference's own tests compare its Triton kernels against:
   ``native_fused_inv_rope_fp8_quant`` :150-198, ``_pack_ue8m0_scales`` :82-90;
 * fused_q_kv_rmsnorm: tests/test_deepseek_v4_attention_fused_q_kv_rmsnorm.py
   ``_rmsnorm_ref`` :40-44;
+* fused_indexer_q_rope_quant: tests/test_fused_indexer_q_rope_quant.py
+  ``_rotate_tail_gptj`` :51-66, ``_reference_fp8`` :69-74, the E2M1 threshold
+  table of ``_quantize_to_mxfp4`` :77-104;
 * dequantize_and_gather_k_cache: the reference kernel's per-row semantics
   (ops/deepseek_v4_attention_dequantize_and_gather_k_cache.py:61-120) in torch
   index arithmetic, with torch's float8 -> float cast and exp2 scale.
@@ -157,3 +160,45 @@ def rmsnorm(x, weight, eps):
 
 def fused_q_kv_rmsnorm(qr, kv, q_weight, kv_weight, eps):
     return rmsnorm(qr, q_weight, eps), rmsnorm(kv, kv_weight, eps)
+
+
+def indexer_rotate(q, positions, cos_sin):
+    """float32 copy of q with GPT-J RoPE on the last 64 dims, rounded to bf16."""
+    nope = q.shape[-1] - ROPE_DIM
+    cs = cos_sin[positions].float()
+    cos, sin = cs[:, None, :HALF_ROPE], cs[:, None, HALF_ROPE:]
+    x = q.float()
+    even, odd = x[..., nope::2].clone(), x[..., nope + 1::2].clone()
+    x[..., nope::2] = (even * cos - odd * sin).to(torch.bfloat16).float()
+    x[..., nope + 1::2] = (odd * cos + even * sin).to(torch.bfloat16).float()
+    return x
+
+
+def e2m1_threshold_codes(xs):
+    """E2M1 nibbles by the reference test's threshold table (ties to even)."""
+    a = xs.abs()
+    code = torch.zeros_like(a, dtype=torch.int32)
+    for thr, c, inclusive in ((0.25, 1, False), (0.75, 2, True), (1.25, 3, False),
+                              (1.75, 4, True), (2.5, 5, False), (3.5, 6, True), (5.0, 7, False)):
+        code = torch.where(a >= thr if inclusive else a > thr, c, code)
+    sign = ((xs.contiguous().view(torch.int32) >> 31) & 1).to(torch.uint8)
+    return code.to(torch.uint8) | (sign << 3)
+
+
+def fused_indexer_q_rope_quant(positions, index_q, cos_sin, weights, softmax_scale, head_scale,
+                               use_fp4=False):
+    x = indexer_rotate(index_q[:positions.shape[0]], positions, cos_sin)
+    T, H, D = x.shape
+    if not use_fp4:
+        amax = x.abs().amax(dim=-1)
+        q_scale = torch.exp2(torch.ceil(torch.log2(amax.clamp(min=1e-4) / FP8_MAX)))
+        codes = (x / q_scale[..., None]).to(torch.float8_e4m3fn).view(torch.uint8)
+        return codes, weights.float() * q_scale * softmax_scale * head_scale
+    blocks = x.reshape(T, H, D // 32, 32)
+    amax = blocks.abs().amax(dim=-1, keepdim=True).clamp(min=6 * (2 ** -126))
+    k = (amax / 6.0).log2().ceil().clamp(-127.0, 127.0)
+    xs = (blocks / k.exp2()).clamp(-6.0, 6.0)
+    nib = e2m1_threshold_codes(xs).reshape(T, H, D)
+    packed = (nib[..., 0::2] | (nib[..., 1::2] << 4)).contiguous()
+    scales = (k + 127.0).to(torch.uint8).reshape(T, H, D // 32)
+    return (packed, scales), weights.float() * softmax_scale * head_scale
