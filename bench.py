@@ -34,7 +34,8 @@ def parse_args():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", type=int, default=2, help="main-op workload c0..c4 (default c2)")
-    ap.add_argument("--op", choices=["main", "inv_rope", "gather", "rmsnorm", "indexer", "copy"],
+    ap.add_argument("--op", choices=["main", "inv_rope", "gather", "rmsnorm", "indexer",
+                                     "slot_mapping", "copy"],
                     default="main",
                     help="copy: torch device copy of 512 MiB, the HBM calibration kernel")
     ap.add_argument("--tma", action="store_true", help="inv_rope: packed UE8M0 scales")
@@ -218,6 +219,26 @@ def main():
         workload = "T8192_H64_D128" + ("_mxfp4" if args.fp4 else "_fp8")
         config = {"workload": f"fused_indexer_q_rope_quant T=8192, H=64, D=128, "
                               f"{'MXFP4' if args.fp4 else 'FP8'}", "num_tokens": T}
+        args.no_cpu_baseline = True
+    elif args.op == "slot_mapping":
+        # slots of c4's ragged batch (64 requests) from its block tables
+        w_cpu = W.make_workload(4 if args.config == 2 else args.config)
+        m = w_cpu.meta
+        qsl = torch.zeros(m["new_lens"].numel() + 1, dtype=torch.int32)
+        qsl[1:] = torch.cumsum(m["new_lens"], 0)
+        T = w_cpu.num_tokens
+        qsl_d, pos_d = qsl.to(dev), w_cpu.position_ids.to(dev)
+        bt_d = m["block_table"].to(dev)
+        out = torch.empty(T, dtype=torch.int64, device=dev)
+        bytes_call = T * (8 + 4 + 8) + 4 * qsl.numel()
+
+        def step():
+            flaggems_vllm.compute_slot_mapping_parallel(T, T, qsl_d, qsl.numel() - 1, pos_d, bt_d,
+                                                        out, 64)
+
+        kernel, workload = "slot_mapping_kernel", f"{w_cpu.name}"
+        config = {"workload": f"compute_slot_mapping_parallel over {w_cpu.name}: {T} tokens, "
+                              f"{qsl.numel() - 1} requests", "num_tokens": T}
         args.no_cpu_baseline = True
     elif args.op == "copy":
         n = 512 << 20

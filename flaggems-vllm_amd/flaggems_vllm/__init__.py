@@ -11,6 +11,7 @@ CPU fallback.
 from . import ops  # noqa: F401
 from .ops import (  # noqa: F401
     SUPPORTED_FP8_DTYPE,
+    compute_slot_mapping_parallel,
     dequantize_and_gather_k_cache,
     fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert,
     fused_indexer_q_rope_quant,
@@ -26,6 +27,7 @@ ops_deepseek_v4_qnorm_rope_kv_rope_quant_insert = fused_deepseek_v4_qnorm_rope_k
 ops_inv_rope_fp8_quant = fused_inv_rope_fp8_quant
 
 __all__ = [
+    "compute_slot_mapping_parallel",
     "dequantize_and_gather_k_cache",
     "fused_q_kv_rmsnorm",
     "fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert",

@@ -121,6 +121,15 @@ def lib():
         _P, _I64, _I64,  # scale_out, strides
         _P,  # stream
     ]
+    L.fgv_compute_slot_mapping.restype = ctypes.c_int
+    L.fgv_compute_slot_mapping.argtypes = [
+        _I64, _I64, _P, _I64,  # num_tokens, max_num_tokens, query_start_loc, num_reqs
+        _P, ctypes.c_int,  # positions, positions_are_int64
+        _P, _I64, _I64,  # block_table, stride, max_blocks_per_req
+        _P, _I64,  # slot_mapping, block_size
+        _I64, _I64, _I64, _I64,  # cp_world_size, cp_rank, interleave, pad_id
+        _P,  # stream
+    ]
     _lib = L
     return _lib
 
@@ -144,4 +153,5 @@ EXPORTED_SYMBOLS = (
     "fgv_dequantize_and_gather_k_cache",
     "fgv_fused_q_kv_rmsnorm",
     "fgv_fused_indexer_q_rope_quant",
+    "fgv_compute_slot_mapping",
 )

@@ -6,8 +6,10 @@ from .fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert import (
 )
 from .fused_indexer_q_rope_quant import fused_indexer_q_rope_quant
 from .fused_inv_rope_fp8_quant import SUPPORTED_FP8_DTYPE, fused_inv_rope_fp8_quant
+from .slot_mapping import compute_slot_mapping_parallel
 
 __all__ = [
+    "compute_slot_mapping_parallel",
     "dequantize_and_gather_k_cache",
     "fused_q_kv_rmsnorm",
     "fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert",

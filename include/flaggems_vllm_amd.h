@@ -185,6 +185,30 @@ int fgv_fused_indexer_q_rope_quant(
     void* scale_out, int64_t scale_out_stride_token, int64_t scale_out_stride_head,
     void* stream);
 
+/*
+ * Paged-KV slot mapping, parallel over tokens.
+ *
+ * Replaces flaggems_vllm.compute_slot_mapping_parallel
+ * (reference: src/flaggems_vllm/runtime/backend/_ascend/ops/slot_mapping.py:109-144,
+ * kernel :42-106).  For token t of request r (query_start_loc[r] <= t <
+ * query_start_loc[r + 1], t < num_tokens):
+ *   pos = positions[t] (int32, or int64 if positions_are_int64)
+ *   v = block_size * cp_world_size; blk = block_table[r, pos / v]; o = pos % v
+ *   slot_mapping[t] = blk * block_size + (o / (cp_world_size * il)) * il + o % il
+ *     if (o / il) % cp_world_size == cp_rank, else pad_id   (il = interleave size)
+ * and slot_mapping[t] = pad_id for num_tokens <= t < max_num_tokens.  Tokens
+ * outside every request are not written; positions outside the block table
+ * give pad_id.
+ */
+int fgv_compute_slot_mapping(
+    int64_t num_tokens, int64_t max_num_tokens,
+    const int32_t* query_start_loc, int64_t num_reqs,
+    const void* positions, int positions_are_int64,
+    const int32_t* block_table, int64_t block_table_stride, int64_t max_blocks_per_req,
+    int64_t* slot_mapping, int64_t block_size,
+    int64_t cp_world_size, int64_t cp_rank, int64_t cp_kv_cache_interleave_size,
+    int64_t pad_id, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

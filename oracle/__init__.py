@@ -108,6 +108,11 @@ def lib():
             ctypes.c_float, ctypes.c_float, _P, _I64, ctypes.c_int,
             _P, _I64, _I64, _P, _I64, _I64,
         ]
+        L.oracle_compute_slot_mapping.restype = None
+        L.oracle_compute_slot_mapping.argtypes = [
+            _I64, _I64, _P, _I64, _P, ctypes.c_int, _P, _I64, _I64, _P, _I64,
+            _I64, _I64, _I64, _I64,
+        ]
         _lib = L
     return _lib
 
@@ -283,3 +288,18 @@ def fused_indexer_q_rope_quant(positions, index_q, cos_sin, weights, softmax_sca
     if use_fp4:
         return (qo, so), weights_out
     return qo, weights_out
+
+
+def compute_slot_mapping(num_tokens, max_num_tokens, query_start_loc, num_reqs, positions,
+                         block_table, slot_mapping, block_size, cp_world_size=1, cp_rank=0,
+                         cp_kv_cache_interleave_size=1, pad_id=-1):
+    """CPU restatement, in place on ``slot_mapping`` (int64 CPU tensor)."""
+    qsl = _cpu(query_start_loc, torch.int32).contiguous()
+    positions = _cpu(positions).contiguous()
+    bt = _cpu(block_table, torch.int32)
+    _cpu(slot_mapping, torch.int64)
+    lib().oracle_compute_slot_mapping(
+        int(num_tokens), int(max_num_tokens), qsl.data_ptr(), int(num_reqs), positions.data_ptr(),
+        int(positions.dtype == torch.int64), bt.data_ptr(), bt.stride(0), bt.shape[1],
+        slot_mapping.data_ptr(), int(block_size), int(cp_world_size), int(cp_rank),
+        int(cp_kv_cache_interleave_size), int(pad_id))

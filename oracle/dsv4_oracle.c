@@ -20,6 +20,9 @@
  *   oracle_fused_indexer_q_rope_quant
  *     reference op   src/flaggems_vllm/ops/fused_indexer_q_rope_quant.py:64-410
  *     reference test tests/test_fused_indexer_q_rope_quant.py:51-110
+ *   oracle_compute_slot_mapping
+ *     reference op   src/flaggems_vllm/runtime/backend/_ascend/ops/slot_mapping.py:42-144
+ *     reference test tests/test_slot_mapping.py:53-66
  *   oracle_dequantize_and_gather_k_cache
  *     reference op   src/flaggems_vllm/ops/deepseek_v4_attention_dequantize_and_gather_k_cache.py:38-172
  *     reference test tests/test_deepseek_v4_attention_dequantize_and_gather_k_cache.py:42-119
@@ -512,6 +515,34 @@ void oracle_fused_indexer_q_rope_quant(const int64_t* positions, int64_t T,
                 float r = wv * softmax_scale;
                 wo[t * wo_st + h] = r * head_scale;
             }
+        }
+    }
+}
+
+/* Slot mapping, request by request as the stock per-request kernel walks it
+   (reference test :53-66 for cp_world = 1, CP arithmetic from the op :88-105). */
+void oracle_compute_slot_mapping(int64_t num_tokens, int64_t max_num_tokens, const int32_t* qsl,
+                                 int64_t num_reqs, const void* positions, int pos64,
+                                 const int32_t* block_table, int64_t bt_stride, int64_t max_blocks,
+                                 int64_t* out, int64_t bs, int64_t cpw, int64_t cp_rank, int64_t il,
+                                 int64_t pad_id)
+{
+    for (int64_t t = num_tokens; t < max_num_tokens; ++t)
+        out[t] = pad_id;
+    for (int64_t r = 0; r < num_reqs; ++r) {
+        for (int64_t t = qsl[r]; t < qsl[r + 1] && t < num_tokens && t < max_num_tokens; ++t) {
+            int64_t pos = pos64 ? (int32_t)((const int64_t*)positions)[t] : ((const int32_t*)positions)[t];
+            int64_t vbs = bs * cpw;
+            int64_t bi = pos / vbs;
+            if (pos < 0 || bi >= max_blocks) {
+                out[t] = pad_id;
+                continue;
+            }
+            int64_t blk = block_table[r * bt_stride + bi];
+            int64_t voff = pos - bi * vbs;
+            int local = (voff / il) % cpw == cp_rank;
+            int64_t loff = voff / (cpw * il) * il + voff % il;
+            out[t] = local ? blk * bs + loff : pad_id;
         }
     }
 }

@@ -14,6 +14,9 @@ oracle that the reference's own tests compare its Triton kernels against:
 * fused_indexer_q_rope_quant: tests/test_fused_indexer_q_rope_quant.py
   ``_rotate_tail_gptj`` :51-66, ``_reference_fp8`` :69-74, the E2M1 threshold
   table of ``_quantize_to_mxfp4`` :77-104;
+* compute_slot_mapping_parallel: tests/test_slot_mapping.py ``_ref_slot_mapping``
+  :53-66 (per-request loop), with the op's context-parallel arithmetic
+  (runtime/backend/_ascend/ops/slot_mapping.py:88-105);
 * dequantize_and_gather_k_cache: the reference kernel's per-row semantics
   (ops/deepseek_v4_attention_dequantize_and_gather_k_cache.py:61-120) in torch
   index arithmetic, with torch's float8 -> float cast and exp2 scale.
@@ -202,3 +205,20 @@ def fused_indexer_q_rope_quant(positions, index_q, cos_sin, weights, softmax_sca
     packed = (nib[..., 0::2] | (nib[..., 1::2] << 4)).contiguous()
     scales = (k + 127.0).to(torch.uint8).reshape(T, H, D // 32)
     return (packed, scales), weights.float() * softmax_scale * head_scale
+
+
+def slot_mapping(num_tokens, qsl, positions, block_table, block_size, max_num_tokens=None,
+                 cp_world_size=1, cp_rank=0, interleave=1, pad_id=-1):
+    """int64 slot of every token, pad_id past num_tokens (Python loop)."""
+    n = max_num_tokens if max_num_tokens is not None else len(positions)
+    out = torch.full((n,), pad_id, dtype=torch.int64)
+    vbs = block_size * cp_world_size
+    for r in range(len(qsl) - 1):
+        for t in range(int(qsl[r]), min(int(qsl[r + 1]), num_tokens, n)):
+            pos = int(positions[t])
+            voff = pos % vbs
+            if (voff // interleave) % cp_world_size != cp_rank:
+                continue
+            blk = int(block_table[r][pos // vbs])
+            out[t] = blk * block_size + voff // (cp_world_size * interleave) * interleave + voff % interleave
+    return out
