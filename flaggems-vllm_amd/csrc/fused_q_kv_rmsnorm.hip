@@ -4,11 +4,12 @@
 // Reference semantics: src/flaggems_vllm/ops/deepseek_v4_attention_fused_q_kv_rmsnorm.py:24-103
 //   y = (x * rsqrt(mean(x^2) + eps)) * w, stored in x's dtype (bf16).
 //
-// Layout: one row per 16-lane DPP row (fgv_device.h); lane l16 owns the
-// 16-byte pieces c = l16 + 16*j, j < kMaxPieces, of its row, so a 1536-wide
-// q row is 12 pieces per lane and a 512-wide kv row 4.  Workgroups
-// [0, q_blocks) take 16 q rows, the rest 16 kv rows.  As in the main op the
-// sum of squares is exact in binary64 and mean and rsqrt are correctly
+// Layout: a row of up to 512 elements is one 16-lane DPP row (fgv_device.h),
+// a longer one a whole wave; lane l owns the 16-byte pieces l + L*j of its
+// row, so DeepSeek-V4's 1536-wide q row is 3 pieces on each of 64 lanes and
+// its 512-wide kv row 4 pieces on each of 16 lanes, keeping 8 waves per SIMD.
+// Workgroups [0, q_blocks) take q rows, the rest kv rows.  As in the main op
+// the sum of squares is exact in binary64 and mean and rsqrt are correctly
 // rounded, so results do not depend on the reduction order.
 #include "fgv_device.h"
 #include "fgv_host.h"
@@ -17,7 +18,6 @@ namespace fgv {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kRowsPerBlock = kThreads / 16;
 
 struct RmsArgs {
     const uint16_t* x[2];
@@ -46,13 +46,19 @@ __device__ __forceinline__ void weights8(const void* w, int e, bool f32, float (
     }
 }
 
-template <int kMaxPieces>
-__global__ void __launch_bounds__(kThreads)
-fused_q_kv_rmsnorm_kernel(RmsArgs a) {
-    const int lane16 = threadIdx.x & 15;
-    const bool is_kv = blockIdx.x >= a.q_blocks;
-    const int which = is_kv ? 1 : 0;
-    const uint32_t row = (blockIdx.x - (is_kv ? a.q_blocks : 0)) * kRowsPerBlock + (threadIdx.x >> 4);
+// Sum over the 64 lanes of the wave: DPP inside each 16-lane row, then the
+// four row totals combined with two cross-row lane shuffles (ds_bpermute).
+__device__ __forceinline__ double wave_sum(double v) {
+    v = row16_sum(v);
+    v += __shfl_xor(v, 16);
+    v += __shfl_xor(v, 32);
+    return v;
+}
+
+// One row of kPieces * 16-byte pieces per lane over kLanes lanes (16: a DPP
+// row, 64: the whole wave).
+template <int kPieces, int kLanes>
+__device__ __forceinline__ void rms_row(const RmsArgs& a, int which, uint32_t row, int lane) {
     if (row >= a.num_rows)
         return;
     const int size = a.size[which];
@@ -60,15 +66,15 @@ fused_q_kv_rmsnorm_kernel(RmsArgs a) {
     const uint16_t* x = a.x[which] + (int64_t)row * a.x_stride[which];
     uint16_t* y = a.y[which] + (int64_t)row * a.y_stride[which];
 
-    uint4 v[kMaxPieces];
+    uint4 v[kPieces];
 #pragma unroll
-    for (int j = 0; j < kMaxPieces; ++j) {
-        const int c = lane16 + 16 * j;
+    for (int j = 0; j < kPieces; ++j) {
+        const int c = lane + kLanes * j;
         v[j] = c < pieces ? load16(x + c * 8) : make_uint4(0, 0, 0, 0);
     }
     double s = 0.0;
 #pragma unroll
-    for (int j = 0; j < kMaxPieces; ++j) {
+    for (int j = 0; j < kPieces; ++j) {
         const uint32_t w4[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -77,14 +83,14 @@ fused_q_kv_rmsnorm_kernel(RmsArgs a) {
             s = __builtin_fma(hi, hi, s);
         }
     }
-    s = row16_sum(s);
+    s = kLanes == 64 ? wave_sum(s) : row16_sum(s);
     float var = (float)(s / (double)size);
     var = var + a.eps;
     const float r = (float)(1.0 / __builtin_sqrt((double)var));
 
 #pragma unroll
-    for (int j = 0; j < kMaxPieces; ++j) {
-        const int c = lane16 + 16 * j;
+    for (int j = 0; j < kPieces; ++j) {
+        const int c = lane + kLanes * j;
         if (c < pieces) {
             float wv[8];
             weights8(a.w[which], c * 8, a.weight_f32, wv);
@@ -99,6 +105,35 @@ fused_q_kv_rmsnorm_kernel(RmsArgs a) {
             store16(y + c * 8, make_uint4(o[0], o[1], o[2], o[3]));
         }
     }
+}
+
+// Workgroups [0, q_blocks) normalise q rows, the rest kv rows; each row kind
+// has its own (pieces per lane, lanes per row) shape.
+template <int kQP, int kQL, int kKP, int kKL>
+__global__ void __launch_bounds__(kThreads)
+fused_q_kv_rmsnorm_kernel(RmsArgs a) {
+    if (blockIdx.x < a.q_blocks) {
+        const uint32_t row = blockIdx.x * (kThreads / kQL) + threadIdx.x / kQL;
+        rms_row<kQP, kQL>(a, 0, row, threadIdx.x % kQL);
+    } else {
+        const uint32_t row = (blockIdx.x - a.q_blocks) * (kThreads / kKL) + threadIdx.x / kKL;
+        rms_row<kKP, kKL>(a, 1, row, threadIdx.x % kKL);
+    }
+}
+
+// Row shapes: up to 512 elements -> 16 lanes x 4 pieces; up to 2048 -> 64
+// lanes x 4 pieces; up to 4096 -> 64 lanes x 8 pieces.
+inline int shape_of(int64_t size) { return size <= 512 ? 0 : size <= 2048 ? 1 : 2; }
+inline int lanes_of(int shape) { return shape == 0 ? 16 : 64; }
+
+template <int kQP, int kQL>
+void launch_kv_shape(const RmsArgs& a, int kv_shape, dim3 grid, hipStream_t st) {
+    if (kv_shape == 0)
+        hipLaunchKernelGGL((fused_q_kv_rmsnorm_kernel<kQP, kQL, 4, 16>), grid, dim3(kThreads), 0, st, a);
+    else if (kv_shape == 1)
+        hipLaunchKernelGGL((fused_q_kv_rmsnorm_kernel<kQP, kQL, 4, 64>), grid, dim3(kThreads), 0, st, a);
+    else
+        hipLaunchKernelGGL((fused_q_kv_rmsnorm_kernel<kQP, kQL, 8, 64>), grid, dim3(kThreads), 0, st, a);
 }
 
 }  // namespace
@@ -143,17 +178,19 @@ extern "C" int fgv_fused_q_kv_rmsnorm(
     a.size[0] = (int32_t)q_size;
     a.size[1] = (int32_t)kv_size;
     a.num_rows = (uint32_t)num_tokens;
-    a.q_blocks = (uint32_t)((num_tokens + kRowsPerBlock - 1) / kRowsPerBlock);
     a.eps = eps;
     a.weight_f32 = weight_is_fp32 ? 1 : 0;
-    const dim3 grid(2 * a.q_blocks);
-    const int64_t most = q_size > kv_size ? q_size : kv_size;
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    if (most <= 512)
-        hipLaunchKernelGGL(fused_q_kv_rmsnorm_kernel<4>, grid, dim3(kThreads), 0, s, a);
-    else if (most <= 1536)
-        hipLaunchKernelGGL(fused_q_kv_rmsnorm_kernel<12>, grid, dim3(kThreads), 0, s, a);
+    const int qs = shape_of(q_size), ks = shape_of(kv_size);
+    const int64_t q_rows_per_block = kThreads / lanes_of(qs);
+    const int64_t kv_rows_per_block = kThreads / lanes_of(ks);
+    a.q_blocks = (uint32_t)((num_tokens + q_rows_per_block - 1) / q_rows_per_block);
+    const dim3 grid(a.q_blocks + (uint32_t)((num_tokens + kv_rows_per_block - 1) / kv_rows_per_block));
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (qs == 0)
+        launch_kv_shape<4, 16>(a, ks, grid, st);
+    else if (qs == 1)
+        launch_kv_shape<4, 64>(a, ks, grid, st);
     else
-        hipLaunchKernelGGL(fused_q_kv_rmsnorm_kernel<32>, grid, dim3(kThreads), 0, s, a);
+        launch_kv_shape<8, 64>(a, ks, grid, st);
     return launch_status();
 }

@@ -65,17 +65,18 @@ __device__ __forceinline__ void inv_rope_piece(float (&x)[8], float4 c, float4 s
 
 // Correctly rounded x / s (s > 0, normal) from y = RN(1/s), which is one IEEE
 // division per 128-element chunk instead of one per element.  q0 = RN(x*y) is
-// within one ulp of x/s, the remainder r = x - s*q0 is exact in one fma, and
-// RN(q0 + r*y) = RN(x/s) by Markstein's theorem (P. Markstein, IBM J. Res.
-// Dev. 34(1), 1990; J.-M. Muller et al., Handbook of Floating-Point
+// within one ulp of x/s, the negated remainder rn = s*q0 - x is exact in one
+// fma, and RN(q0 - rn*y) = RN(x/s) by Markstein's theorem (P. Markstein, IBM
+// J. Res. Dev. 34(1), 1990; J.-M. Muller et al., Handbook of Floating-Point
 // Arithmetic, 2nd ed., section 4.7).  The remainder stays exact for every
 // quotient large enough to reach a non-zero e4m3 code (|x/s| >= 2^-10 keeps
-// r far above the binary32 underflow threshold); below that only the sign
-// matters to the code, and copysign restores it for zero quotients.
+// it far above the binary32 underflow threshold).  For x = +-0 the two fmas
+// add zeros of opposite / equal sign so the quotient keeps x's sign, which
+// decides between codes 0x00 and 0x80.
 __device__ __forceinline__ float div_by_scale(float x, float s, float y) {
-    float q0 = x * y;
-    float r = __builtin_fmaf(-s, q0, x);
-    return __builtin_copysignf(__builtin_fmaf(r, y, q0), x);
+    const float q0 = x * y;
+    const float rn = __builtin_fmaf(s, q0, -x);
+    return __builtin_fmaf(-rn, y, q0);
 }
 
 // Position first (the cos/sin loads depend on it; vmcnt counts in issue

@@ -4,9 +4,9 @@
  * positive finite bf16 amax, s = RN(amax * RN(1/448)) as the kernel forms it,
  * and numerators x = every bf16 value of magnitude <= amax drawn on a stride
  * (plus +-amax, +-0 and the smallest magnitudes), the Markstein quotient
- *     y = RN(1/s); q0 = RN(x*y); r = fma(-s, q0, x); q = copysign(fma(r, y, q0), x)
- * must equal IEEE x / s bit for bit whenever |x/s| >= 2^-12 (below that every
- * e4m3 code is +-0 and only the sign is compared).
+ *     y = RN(1/s); q0 = RN(x*y); rn = fma(s, q0, -x); q = fma(-rn, y, q0)
+ * must equal IEEE x / s bit for bit whenever |x/s| >= 2^-12, and have its sign
+ * below that (every e4m3 code there is +-0), including for x = +-0.
  * Prints the number of mismatches and exits non-zero if there is any.
  * Build: gcc -O2 -ffp-contract=off -mfma scale_division_check.c -lm
  */
@@ -22,8 +22,10 @@ static uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
 static float div_by_scale(float x, float s, float y)
 {
     float q0 = x * y;
-    float r = fmaf(-s, q0, x);
-    return copysignf(fmaf(r, y, q0), x);
+    /* volatile: gcc -O2 -mfma would otherwise fold the negation of rn into the
+       first fma, which is not exact for signed zeros */
+    volatile float rn = fmaf(s, q0, -x);
+    return fmaf(-rn, y, q0);
 }
 
 int main(int argc, char** argv)
