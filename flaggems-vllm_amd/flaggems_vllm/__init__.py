@@ -11,12 +11,15 @@ CPU fallback.
 from . import ops  # noqa: F401
 from .ops import (  # noqa: F401
     SUPPORTED_FP8_DTYPE,
+    FlashMLASchedMeta,
     compute_slot_mapping_parallel,
     dequantize_and_gather_k_cache,
+    flash_mla_with_kvcache,
     fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert,
     fused_indexer_q_rope_quant,
     fused_inv_rope_fp8_quant,
     fused_q_kv_rmsnorm,
+    get_mla_metadata,
 )
 
 device = "cuda"
@@ -27,7 +30,10 @@ ops_deepseek_v4_qnorm_rope_kv_rope_quant_insert = fused_deepseek_v4_qnorm_rope_k
 ops_inv_rope_fp8_quant = fused_inv_rope_fp8_quant
 
 __all__ = [
+    "FlashMLASchedMeta",
     "compute_slot_mapping_parallel",
+    "flash_mla_with_kvcache",
+    "get_mla_metadata",
     "dequantize_and_gather_k_cache",
     "fused_q_kv_rmsnorm",
     "fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert",

@@ -130,6 +130,19 @@ def lib():
         _I64, _I64, _I64, _I64,  # cp_world_size, cp_rank, interleave, pad_id
         _P,  # stream
     ]
+    L.fgv_sparse_mla_decode_model1.restype = ctypes.c_int
+    L.fgv_sparse_mla_decode_model1.argtypes = [
+        _P, _I64, _I64, _I64,  # q, strides (batch, seq_q, head)
+        _P, _I64, _I64, _I64,  # k_cache, block stride, num_blocks, page_size
+        _P, _I64, _I64, _I64, _P,  # indices, strides, topk, topk_length
+        _P, _I64, _I64, _I64,  # extra_k_cache, block stride, num_blocks, page_size
+        _P, _I64, _I64, _I64, _P,  # extra indices, strides, extra topk, extra lengths
+        _P, ctypes.c_float,  # attn_sink, softmax_scale
+        _P, _I64, _I64, _I64,  # out, strides
+        _P, _I64, _I64,  # lse, strides (batch, head)
+        _I64, _I64, _I64,  # batch, seq_q, num_heads
+        _P,  # stream
+    ]
     _lib = L
     return _lib
 
@@ -154,4 +167,5 @@ EXPORTED_SYMBOLS = (
     "fgv_fused_q_kv_rmsnorm",
     "fgv_fused_indexer_q_rope_quant",
     "fgv_compute_slot_mapping",
+    "fgv_sparse_mla_decode_model1",
 )

@@ -1,6 +1,7 @@
-"""DeepSeek-V4 attention pre-processing ops (reference: src/flaggems_vllm/ops/__init__.py:34-38, 61-65)."""
+"""DeepSeek-V4 attention pre-processing ops (reference: src/flaggems_vllm/ops/__init__.py:34-38, 55, 61-65)."""
 from .deepseek_v4_attention_dequantize_and_gather_k_cache import dequantize_and_gather_k_cache
 from .deepseek_v4_attention_fused_q_kv_rmsnorm import fused_q_kv_rmsnorm
+from .flash_mla_with_kvcache import FlashMLASchedMeta, flash_mla_with_kvcache, get_mla_metadata
 from .fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert import (
     fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert,
 )
@@ -9,7 +10,10 @@ from .fused_inv_rope_fp8_quant import SUPPORTED_FP8_DTYPE, fused_inv_rope_fp8_qu
 from .slot_mapping import compute_slot_mapping_parallel
 
 __all__ = [
+    "FlashMLASchedMeta",
     "compute_slot_mapping_parallel",
+    "flash_mla_with_kvcache",
+    "get_mla_metadata",
     "dequantize_and_gather_k_cache",
     "fused_q_kv_rmsnorm",
     "fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert",

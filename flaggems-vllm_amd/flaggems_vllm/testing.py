@@ -294,3 +294,139 @@ def make_inv_rope_workload(num_tokens: int = 8192, num_heads: int = 64, n_groups
     positions = torch.randint(0, max_pos, (num_tokens,), generator=g, dtype=torch.int64)
     return InvRopeWorkload(o, positions, make_cos_sin_cache(max_pos), n_groups,
                            num_heads // n_groups)
+
+
+# ------------------------------------------------------------ sparse MLA ----
+
+def make_model1_cache(num_pages: int, page: int, gen: torch.Generator, std: float = 0.1) -> torch.Tensor:
+    """A [num_pages, page, 1, 584] uint8 MODEL1 cache filled like the
+    reference's test generator (tests/test_flash_mla_with_kvcache.py:94-140):
+    NoPE = std * randn quantised per 64-group with a power-of-two scale
+    2^ceil(log2(max(amax, 1e-4) / 448)) (E8M0 byte = exponent + 127), RoPE =
+    std * randn in bf16; token data first in each page, then 8 scale bytes per
+    token (the 8th zero)."""
+    n = num_pages * page
+    nope = (torch.randn(n, NOPE_DIM, generator=gen) * std).to(torch.bfloat16).float()
+    groups = nope.view(n, 7, 64)
+    amax = groups.abs().amax(dim=-1).clamp_min(1e-4)
+    expo = torch.ceil(torch.log2(amax / 448.0))
+    codes = (groups / torch.exp2(expo)[:, :, None]).clamp(-448.0, 448.0).reshape(n, NOPE_DIM)
+    codes = codes.to(torch.float8_e4m3fn).view(torch.uint8)
+    rope = (torch.randn(n, ROPE_DIM, generator=gen) * std).to(torch.bfloat16)
+    data = torch.cat([codes, rope.view(torch.uint8).view(n, 2 * ROPE_DIM)], dim=1)
+    scales = torch.zeros(n, SCALE_BYTES_PER_TOKEN, dtype=torch.uint8)
+    scales[:, :7] = (expo + 127).clamp(0, 255).to(torch.uint8)
+    cache = torch.empty(num_pages, page * HEAD_BYTES, dtype=torch.uint8)
+    cache[:, :page * TOKEN_DATA_BYTES] = data.view(num_pages, page * TOKEN_DATA_BYTES)
+    cache[:, page * TOKEN_DATA_BYTES:] = scales.view(num_pages, page * SCALE_BYTES_PER_TOKEN)
+    return cache.view(num_pages, page, 1, HEAD_BYTES)
+
+
+@dataclass
+class MlaWorkload:
+    """Inputs of one flash_mla_with_kvcache sparse MODEL1 call (CPU tensors
+    until ``to``)."""
+    name: str
+    q: torch.Tensor
+    k_cache: torch.Tensor
+    indices: torch.Tensor
+    topk_length: Optional[torch.Tensor] = None
+    attn_sink: Optional[torch.Tensor] = None
+    extra_k_cache: Optional[torch.Tensor] = None
+    extra_indices: Optional[torch.Tensor] = None
+    extra_topk_length: Optional[torch.Tensor] = None
+
+    def kwargs(self):
+        return dict(topk_length=self.topk_length, attn_sink=self.attn_sink,
+                    extra_k_cache=self.extra_k_cache,
+                    extra_indices_in_kvcache=self.extra_indices,
+                    extra_topk_length=self.extra_topk_length)
+
+    def oracle_kwargs(self):
+        return dict(topk_length=self.topk_length, attn_sink=self.attn_sink,
+                    extra_k_cache=self.extra_k_cache, extra_indices=self.extra_indices,
+                    extra_topk_length=self.extra_topk_length)
+
+    def to(self, device):
+        mv = lambda t: None if t is None else t.to(device)
+        return MlaWorkload(self.name, mv(self.q), mv(self.k_cache), mv(self.indices),
+                           mv(self.topk_length), mv(self.attn_sink), mv(self.extra_k_cache),
+                           mv(self.extra_indices), mv(self.extra_topk_length))
+
+    def used_tokens(self) -> int:
+        """Selected entries the kernel attends (within the top-k lengths and
+        pointing inside their cache), summed over batch rows and query
+        positions."""
+        total = 0
+        for cache, idx, length in ((self.k_cache, self.indices, self.topk_length),
+                                   (self.extra_k_cache, self.extra_indices, self.extra_topk_length)):
+            if cache is None:
+                continue
+            limit = cache.shape[0] * cache.shape[1]
+            topk = idx.shape[-1]
+            n = torch.full((idx.shape[0],), topk) if length is None else length.cpu().long().clamp(0, topk)
+            pos = torch.arange(topk)
+            inside = (pos[None, None, :] < n[:, None, None]) & (idx.cpu() >= 0) & (idx.cpu() < limit)
+            total += int(inside.sum())
+        return total
+
+
+# The reference benchmark's MODEL1 cases (benchmark/test_flash_mla_with_kvcache.py:230-270):
+# batch 512, seq_q 1, 64 heads, top-k 128 over 512 pages of 64, attention sink, top-k lengths;
+# plus an extra cache of top-k 512 (64-token pages) or 8192 (2-token pages).
+MLA_CASES = {
+    "decode": dict(batch=512, topk=128, num_pages=512),
+    "extra512": dict(batch=512, topk=128, num_pages=512, extra_topk=512, extra_page=64,
+                     extra_pages=512),
+    "extra8192": dict(batch=512, topk=128, num_pages=512, extra_topk=8192, extra_page=2,
+                      extra_pages=512),
+}
+
+
+def make_mla_workload(batch: int = 8, topk: int = 128, num_pages: int = 16, page: int = 64,
+                      heads: int = 64, seq_q: int = 1, extra_topk: int = 0, extra_page: int = 64,
+                      extra_pages: int = 0, topk_length: bool = True, sink: bool = True,
+                      seed: int = 43, name: str = "mla", q_scale: float = 1.0) -> MlaWorkload:
+    """Seeded inputs shaped like the reference's MODEL1 tests and benchmark:
+    q ~ randn (times q_scale), indices uniform over the cache, top-k lengths
+    uniform in [1, topk], sink ~ randn."""
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(batch, seq_q, heads, HEAD_DIM, generator=g)
+    q = (q * q_scale).to(torch.bfloat16)
+    cache = make_model1_cache(num_pages, page, g)
+    idx = torch.randint(0, num_pages * page, (batch, seq_q, topk), generator=g, dtype=torch.int32)
+    lens = torch.randint(1, topk + 1, (batch,), generator=g, dtype=torch.int32) if topk_length else None
+    sink_t = torch.randn(heads, generator=g) if sink else None
+    w = MlaWorkload(name, q, cache, idx, lens, sink_t)
+    if extra_topk:
+        pages = extra_pages or (extra_topk + extra_page - 1) // extra_page + 4
+        w.extra_k_cache = make_model1_cache(pages, extra_page, g)
+        w.extra_indices = torch.randint(0, pages * extra_page, (batch, seq_q, extra_topk),
+                                        generator=g, dtype=torch.int32)
+        if topk_length:
+            w.extra_topk_length = torch.randint(1, extra_topk + 1, (batch,), generator=g,
+                                                dtype=torch.int32)
+    return w
+
+
+def make_mla_case(case: str, seed: int = 0) -> MlaWorkload:
+    """One of the MLA_CASES (bench workloads), q scaled by 1/10 as the
+    reference benchmark draws it."""
+    return make_mla_workload(seed=seed, name=case, q_scale=0.1, **MLA_CASES[case])
+
+
+def mla_bytes(w: MlaWorkload) -> int:
+    """Algorithmic bytes of one sparse MODEL1 decode call: q read and output
+    written (bf16, 512 per head), the LSE, and per attended cache entry its
+    4-byte index and 584 cache bytes, once per 64-head block."""
+    B, SQ, HQ, D = w.q.shape
+    head_blocks = HQ // 64
+    return (4 * B * SQ * HQ * D + 4 * B * HQ * SQ
+            + head_blocks * w.used_tokens() * (4 + HEAD_BYTES))
+
+
+def mla_flops(w: MlaWorkload) -> int:
+    """MFMA work of one call: QK^T and PV, 2 * 512 multiply-adds each per
+    (head, attended entry)."""
+    HQ = w.q.shape[2]
+    return 4 * HEAD_DIM * HQ * w.used_tokens()

@@ -209,6 +209,48 @@ int fgv_compute_slot_mapping(
     int64_t cp_world_size, int64_t cp_rank, int64_t cp_kv_cache_interleave_size,
     int64_t pad_id, void* stream);
 
+/*
+ * Sparse MLA decode over the 584-byte MODEL1 cache.
+ *
+ * Replaces the sparse MODEL1 branch of flaggems_vllm.flash_mla_with_kvcache
+ * (reference: src/flaggems_vllm/ops/flash_mla_with_kvcache.py:852-1073 wrapper,
+ * :1096-1171 dispatch, kernel :489-688; sm90 kernel
+ * src/flaggems_vllm/ops/flash_mla_with_kvcache_model1.py:1464-1695).
+ *
+ *   q    bf16 [batch, seq_q, num_heads, 512] (strides in elements, last dim contiguous)
+ *   k_cache / extra_k_cache  uint8 [num_blocks, page_size, 1, 584]: per page,
+ *        page_size x 576 token bytes (448 e4m3 + 64 bf16) then page_size x 8
+ *        E8M0 scale bytes; block strides in bytes
+ *   indices / extra_indices  int32 [batch, seq_q, topk] (last dim contiguous)
+ *   topk_length / extra_topk_length  int32 [batch] or NULL (then topk); clamped
+ *        to [0, topk]
+ *   attn_sink  float [num_heads] or NULL
+ *   out  bf16 [batch, seq_q, num_heads, 512];  lse  float [batch, num_heads, seq_q]
+ *        (stride over seq_q is 1)
+ *
+ * Entry t of a list is attended when t < its length, id >= 0 and
+ * id / page_size < num_blocks.  K = V = bf16(e4m3 * 2^(scale_byte - 127)) for
+ * dims 0..447 (one scale per 64) and the cached bf16 RoPE for 448..511.  Per
+ * head: s = softmax_scale * q.K, lse = m + log(sum exp(s - m)) (+inf if nothing
+ * is attended), out = sum exp(s - m) V / (sum exp(s - m) + exp(sink - m)) (no
+ * sink term without attn_sink; 0 if nothing is attended).  num_heads must be a
+ * multiple of 64.
+ */
+int fgv_sparse_mla_decode_model1(
+    const void* q, int64_t q_stride_b, int64_t q_stride_s, int64_t q_stride_h,
+    const void* k_cache, int64_t cache_block_stride, int64_t num_blocks, int64_t page_size,
+    const int32_t* indices, int64_t idx_stride_b, int64_t idx_stride_s, int64_t topk,
+    const int32_t* topk_length,
+    const void* extra_k_cache, int64_t extra_block_stride, int64_t extra_num_blocks,
+    int64_t extra_page_size,
+    const int32_t* extra_indices, int64_t extra_idx_stride_b, int64_t extra_idx_stride_s,
+    int64_t extra_topk,
+    const int32_t* extra_topk_length,
+    const float* attn_sink, float softmax_scale,
+    void* out, int64_t out_stride_b, int64_t out_stride_s, int64_t out_stride_h,
+    float* lse, int64_t lse_stride_b, int64_t lse_stride_h,
+    int64_t batch, int64_t seq_q, int64_t num_heads, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -113,6 +113,13 @@ def lib():
             _I64, _I64, _P, _I64, _P, ctypes.c_int, _P, _I64, _I64, _P, _I64,
             _I64, _I64, _I64, _I64,
         ]
+        L.oracle_model1_token_row.restype = None
+        L.oracle_model1_token_row.argtypes = [_P, _I64, _I64, _I64, _P]
+        L.oracle_sparse_mla_decode_model1.restype = None
+        L.oracle_sparse_mla_decode_model1.argtypes = [
+            _P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _I64, _P,
+            _P, _I64, _I64, _I64, _P, _I64, _P, _P, ctypes.c_double, _P, _P,
+        ]
         _lib = L
     return _lib
 
@@ -303,3 +310,55 @@ def compute_slot_mapping(num_tokens, max_num_tokens, query_start_loc, num_reqs, 
         int(positions.dtype == torch.int64), bt.data_ptr(), bt.stride(0), bt.shape[1],
         slot_mapping.data_ptr(), int(block_size), int(cp_world_size), int(cp_rank),
         int(cp_kv_cache_interleave_size), int(pad_id))
+
+
+def model1_token_row(k_cache, token_id):
+    """The dequantised 512-wide bf16 row of cache entry ``token_id`` of a
+    [num_blocks, page, 1, 584] uint8 MODEL1 cache."""
+    _cpu(k_cache, torch.uint8)
+    row = torch.empty(512, dtype=torch.bfloat16)
+    lib().oracle_model1_token_row(k_cache.data_ptr(), k_cache.stride(0), k_cache.shape[1],
+                                  int(token_id), row.data_ptr())
+    return row
+
+
+def sparse_mla_decode_model1(q, k_cache, indices, topk_length=None, attn_sink=None,
+                             extra_k_cache=None, extra_indices=None, extra_topk_length=None,
+                             softmax_scale=None):
+    """Exact (binary64) sparse MLA decode over MODEL1 caches.
+
+    Returns ``(out, lse)`` as float64 tensors shaped [B, SQ, HQ, 512] and
+    [B, HQ, SQ]; arguments as in flaggems_vllm.flash_mla_with_kvcache."""
+    q = _cpu(q, torch.bfloat16).contiguous()
+    B, SQ, HQ, D = q.shape
+    assert D == 512
+    if softmax_scale is None:
+        softmax_scale = D ** -0.5
+
+    def cache_args(cache, idx, length):
+        if cache is None:
+            return [None, 0, 1, 0, None, 0, None], []
+        _cpu(cache, torch.uint8)
+        idx = _cpu(idx, torch.int32).contiguous()
+        keep = [idx]
+        lp = None
+        if length is not None:
+            length = _cpu(length, torch.int32).contiguous()
+            keep.append(length)
+            lp = length.data_ptr()
+        return [cache.data_ptr(), cache.shape[0], cache.shape[1], cache.stride(0), idx.data_ptr(),
+                idx.shape[-1], lp], keep
+
+    main, keep0 = cache_args(k_cache, indices, topk_length)
+    extra, keep1 = cache_args(extra_k_cache, extra_indices, extra_topk_length)
+    sink = None
+    if attn_sink is not None:
+        sink = _cpu(attn_sink, torch.float32).contiguous()
+    out = torch.empty(B, SQ, HQ, D, dtype=torch.float64)
+    lse = torch.empty(B, HQ, SQ, dtype=torch.float64)
+    lib().oracle_sparse_mla_decode_model1(
+        q.data_ptr(), B, SQ, HQ, *main, *extra,
+        sink.data_ptr() if sink is not None else None, float(softmax_scale),
+        out.data_ptr(), lse.data_ptr())
+    del keep0, keep1
+    return out, lse

@@ -26,6 +26,10 @@
  *   oracle_dequantize_and_gather_k_cache
  *     reference op   src/flaggems_vllm/ops/deepseek_v4_attention_dequantize_and_gather_k_cache.py:38-172
  *     reference test tests/test_deepseek_v4_attention_dequantize_and_gather_k_cache.py:42-119
+ *   oracle_sparse_mla_decode_model1 (binary64 attention, see its comment)
+ *     reference op   src/flaggems_vllm/ops/flash_mla_with_kvcache.py:489-688, 852-1073
+ *                    src/flaggems_vllm/ops/flash_mla_with_kvcache_model1.py:389-470, 699-720
+ *     reference test tests/test_flash_mla_with_kvcache.py:94-140, 236-360
  *
  * Numerics (compile with -ffp-contract=off and without -ffast-math):
  *   - every product and sum is a separately rounded binary32 operation, as in
@@ -51,6 +55,7 @@
  */
 #include <math.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 
 #define HEAD_DIM 512
@@ -543,6 +548,144 @@ void oracle_compute_slot_mapping(int64_t num_tokens, int64_t max_num_tokens, con
             int local = (voff / il) % cpw == cp_rank;
             int64_t loff = voff / (cpw * il) * il + voff % il;
             out[t] = local ? blk * bs + loff : pad_id;
+        }
+    }
+}
+
+/*
+ * Sparse MLA decode over the 584-byte MODEL1 cache
+ * (reference portable kernel ops/flash_mla_with_kvcache.py:489-688 and the
+ * sm90 kernel ops/flash_mla_with_kvcache_model1.py:389-470, 699-720):
+ *
+ *   K = V = the dequantised 512-wide latent of each selected token:
+ *     dims [0,448):   bf16(e4m3(code) * 2^(scale_byte[d/64] - 127))  (f32 product, RNE)
+ *     dims [448,512): the cached bf16 RoPE values
+ *   A selected entry t of a list is used when t < len, id >= 0 and
+ *   id / page < num_blocks (len = topk, or topk_length[b] clamped to
+ *   [0, topk]).  The extra list is attended together with the main one.
+ *   For each head: s_t = sm_scale * q . K_t, m = max s_t,
+ *   l = sum exp(s_t - m), lse = m + log(l)   (+inf when nothing is used),
+ *   out = sum_t exp(s_t - m) V_t / (l + exp(sink - m))   (sink term only with
+ *   attn_sink; out = 0 when nothing is used).
+ *
+ * Everything after the dequantisation is evaluated in binary64, so this is
+ * the exact attention the reference's fp32/bf16 kernels approximate.
+ * q, out: [B][SQ][HQ][512] contiguous; lse: [B][HQ][SQ].
+ */
+void oracle_model1_token_row(const uint8_t* cache, int64_t block_stride, int64_t page, int64_t id,
+                             uint16_t* row)
+{
+    int64_t blk = id / page, rel = id % page;
+    const uint8_t* tok = cache + blk * block_stride + rel * TOKEN_DATA_BYTES;
+    const uint8_t* scl = cache + blk * block_stride + page * TOKEN_DATA_BYTES + rel * SCALE_BYTES_PER_TOKEN;
+    for (int c = 0; c < NOPE_DIM; ++c) {
+        float scale = u2f((uint32_t)scl[c / KV_QUANT_BLOCK] << 23);
+        row[c] = oracle_f32_to_bf16(oracle_e4m3fn_to_f32(tok[c]) * scale);
+    }
+    memcpy(row + NOPE_DIM, tok + NOPE_DIM, 2 * ROPE_DIM);
+}
+
+struct mla_list {
+    const uint8_t* cache;
+    int64_t num_blocks, page, block_stride;
+    const int32_t* idx;
+    int64_t topk;
+    const int32_t* len;
+};
+
+static int64_t mla_collect(const struct mla_list* L, int64_t b, int64_t sq, int64_t SQ, int64_t* ids)
+{
+    if (!L->cache)
+        return 0;
+    int64_t len = L->topk;
+    if (L->len) {
+        len = L->len[b];
+        len = len < 0 ? 0 : len > L->topk ? L->topk : len;
+    }
+    const int32_t* row = L->idx + (b * SQ + sq) * L->topk;
+    int64_t n = 0;
+    for (int64_t t = 0; t < len; ++t) {
+        int64_t id = row[t];
+        if (id >= 0 && id / L->page < L->num_blocks)
+            ids[n++] = id;
+    }
+    return n;
+}
+
+void oracle_sparse_mla_decode_model1(const uint16_t* q, int64_t B, int64_t SQ, int64_t HQ,
+                                     const uint8_t* cache, int64_t num_blocks, int64_t page,
+                                     int64_t block_stride, const int32_t* idx, int64_t topk,
+                                     const int32_t* topk_len,
+                                     const uint8_t* ecache, int64_t enum_blocks, int64_t epage,
+                                     int64_t eblock_stride, const int32_t* eidx, int64_t etopk,
+                                     const int32_t* etopk_len,
+                                     const float* sink, double sm_scale, double* out, double* lse)
+{
+    struct mla_list lists[2] = {
+        {cache, num_blocks, page, block_stride, idx, topk, topk_len},
+        {ecache, enum_blocks, epage, eblock_stride, eidx, etopk, etopk_len},
+    };
+    for (int64_t b = 0; b < B; ++b) {
+        for (int64_t sq = 0; sq < SQ; ++sq) {
+            int64_t cap = topk + (ecache ? etopk : 0);
+            int64_t* ids = (int64_t*)malloc(sizeof(int64_t) * (cap ? cap : 1));
+            int* which = (int*)malloc(sizeof(int) * (cap ? cap : 1));
+            int64_t n = 0;
+            for (int li = 0; li < 2; ++li) {
+                int64_t k = mla_collect(&lists[li], b, sq, SQ, ids + n);
+                for (int64_t i = 0; i < k; ++i)
+                    which[n + i] = li;
+                n += k;
+            }
+            double* kv = (double*)malloc(sizeof(double) * HEAD_DIM * (n ? n : 1));
+            uint16_t row[HEAD_DIM];
+            for (int64_t t = 0; t < n; ++t) {
+                const struct mla_list* L = &lists[which[t]];
+                oracle_model1_token_row(L->cache, L->block_stride, L->page, ids[t], row);
+                for (int d = 0; d < HEAD_DIM; ++d)
+                    kv[t * HEAD_DIM + d] = oracle_bf16_to_f32(row[d]);
+            }
+            #pragma omp parallel for schedule(static)
+            for (int64_t h = 0; h < HQ; ++h) {
+                const uint16_t* qh = q + ((b * SQ + sq) * HQ + h) * HEAD_DIM;
+                double* oh = out + ((b * SQ + sq) * HQ + h) * HEAD_DIM;
+                double* lh = lse + (b * HQ + h) * SQ + sq;
+                double qd[HEAD_DIM];
+                for (int d = 0; d < HEAD_DIM; ++d)
+                    qd[d] = oracle_bf16_to_f32(qh[d]);
+                for (int d = 0; d < HEAD_DIM; ++d)
+                    oh[d] = 0.0;
+                if (n == 0) {
+                    *lh = INFINITY;
+                    continue;
+                }
+                double* s = (double*)malloc(sizeof(double) * n);
+                double m = -INFINITY;
+                for (int64_t t = 0; t < n; ++t) {
+                    double acc = 0.0;
+                    for (int d = 0; d < HEAD_DIM; ++d)
+                        acc += qd[d] * kv[t * HEAD_DIM + d];
+                    s[t] = acc * sm_scale;
+                    if (s[t] > m)
+                        m = s[t];
+                }
+                double l = 0.0;
+                for (int64_t t = 0; t < n; ++t) {
+                    s[t] = exp(s[t] - m);
+                    l += s[t];
+                }
+                *lh = m + log(l);
+                double denom = l + (sink ? exp((double)sink[h] - m) : 0.0);
+                for (int64_t t = 0; t < n; ++t) {
+                    double w = s[t] / denom;
+                    for (int d = 0; d < HEAD_DIM; ++d)
+                        oh[d] += w * kv[t * HEAD_DIM + d];
+                }
+                free(s);
+            }
+            free(kv);
+            free(which);
+            free(ids);
         }
     }
 }

@@ -19,7 +19,9 @@ oracle that the reference's own tests compare its Triton kernels against:
   (runtime/backend/_ascend/ops/slot_mapping.py:88-105);
 * dequantize_and_gather_k_cache: the reference kernel's per-row semantics
   (ops/deepseek_v4_attention_dequantize_and_gather_k_cache.py:61-120) in torch
-  index arithmetic, with torch's float8 -> float cast and exp2 scale.
+  index arithmetic, with torch's float8 -> float cast and exp2 scale;
+* sparse MLA decode over the MODEL1 cache: the portable kernel's chunked
+  online softmax (ops/flash_mla_with_kvcache.py:489-688).
 
 Arithmetic is whatever torch's CPU kernels do in float32: the sum of squares
 and rsqrt are torch's, which is why q is compared against this restatement
@@ -222,3 +224,70 @@ def slot_mapping(num_tokens, qsl, positions, block_table, block_size, max_num_to
             blk = int(block_table[r][pos // vbs])
             out[t] = blk * block_size + voff // (cp_world_size * interleave) * interleave + voff % interleave
     return out
+
+
+def model1_rows(k_cache):
+    """Dequantise a whole [num_blocks, page, 1, 584] MODEL1 cache into
+    [num_blocks * page, 512] bf16 rows (reference kernel
+    ops/flash_mla_with_kvcache.py:508-559: f32 e4m3 value times the E8M0 scale
+    bitcast from ``byte << 23``, rounded to bf16; RoPE copied)."""
+    nb, page = k_cache.shape[0], k_cache.shape[1]
+    flat = k_cache.reshape(nb, -1)
+    data = flat[:, :page * 576].reshape(nb * page, 576)
+    scl = flat[:, page * 576:page * 584].reshape(nb * page, 8)
+    scale = (scl[:, :7].to(torch.int32) << 23).view(torch.float32)
+    nope = data[:, :448].contiguous().view(torch.float8_e4m3fn).to(torch.float32)
+    nope = (nope.view(-1, 7, 64) * scale[:, :, None]).reshape(-1, 448).to(torch.bfloat16)
+    rope = data[:, 448:].contiguous().view(torch.bfloat16)
+    return torch.cat([nope, rope], dim=1)
+
+
+def sparse_mla_decode_model1(q, k_cache, indices, topk_length=None, attn_sink=None,
+                             extra_k_cache=None, extra_indices=None, extra_topk_length=None,
+                             softmax_scale=None, chunk=32):
+    """The reference portable MODEL1 kernel's algorithm on CPU tensors
+    (ops/flash_mla_with_kvcache.py:489-688): 32-token chunks, fp32 scores,
+    online softmax with natural exp, probabilities rounded to bf16 before the
+    PV product, fp32 accumulation, bf16 output.  A chunk whose tokens are all
+    invalid before any valid one contributes nothing (the running max starts
+    at -inf and is treated as 0 for the exponent, as the sm90 kernel's -1e30
+    start does).  Returns (out bf16 [B,SQ,HQ,512], lse f32 [B,HQ,SQ])."""
+    B, SQ, HQ, D = q.shape
+    scale = D ** -0.5 if softmax_scale is None else softmax_scale
+    lists = [(model1_rows(k_cache), k_cache.shape[0], k_cache.shape[1], indices, topk_length)]
+    if extra_k_cache is not None:
+        lists.append((model1_rows(extra_k_cache), extra_k_cache.shape[0], extra_k_cache.shape[1],
+                      extra_indices, extra_topk_length))
+    out = torch.zeros(B, SQ, HQ, D, dtype=torch.bfloat16)
+    lse = torch.empty(B, HQ, SQ, dtype=torch.float32)
+    for b in range(B):
+        for s in range(SQ):
+            qf = q[b, s].float()
+            m = torch.full((HQ,), float("-inf"))
+            lsum = torch.zeros(HQ)
+            acc = torch.zeros(HQ, D)
+            for rows, nb, page, idx, length in lists:
+                topk = idx.shape[-1]
+                n = topk if length is None else max(0, min(int(length[b]), topk))
+                for c0 in range(0, n, chunk):
+                    ids = idx[b, s, c0:min(c0 + chunk, n)].long()
+                    valid = (ids >= 0) & (ids // page < nb)
+                    kv = rows[torch.where(valid, ids, 0)].float() * valid[:, None]
+                    qk = (qf @ kv.T) * scale
+                    qk = torch.where(valid[None, :], qk, float("-inf"))
+                    m_new = torch.maximum(m, qk.max(dim=1).values)
+                    m_use = torch.where(torch.isinf(m_new) & (m_new < 0), 0.0, m_new)
+                    p = torch.exp(qk - m_use[:, None])
+                    alpha = torch.exp(m - m_use)
+                    lsum = lsum * alpha + p.sum(dim=1)
+                    acc = acc * alpha[:, None] + p.to(torch.bfloat16).float() @ kv
+                    m = m_new
+            empty = torch.isinf(m) & (m < 0)
+            lse[b, :, s] = torch.where(empty, float("inf"), m + torch.log(lsum))
+            if attn_sink is not None:
+                denom = lsum + torch.exp(attn_sink.float() - m)
+            else:
+                denom = lsum
+            o = acc / torch.where(empty, 1.0, denom)[:, None]
+            out[b, s] = torch.where(empty[:, None], 0.0, o).to(torch.bfloat16)
+    return out, lse

@@ -1,0 +1,465 @@
+"""Sparse MLA decode over the 584-byte MODEL1 cache: oracle pins (CPU),
+wrapper checks (CPU) and GPU parity.
+
+Reference: src/flaggems_vllm/ops/flash_mla_with_kvcache.py:489-688 (portable
+MODEL1 kernel), :852-1073 (wrapper and its assertions);
+tests/test_flash_mla_with_kvcache.py:94-140 (cache generator), :236-360
+(MODEL1 cases: batch 8 / 64 heads / top-k 128 / 16 pages, seed 43, and the
+extra-cache cases (64, 512, 12), (2, 512, 260)), :420-486 (error cases).
+The reference checks its kernel against vLLM's CUDA FlashMLA with cosine
+similarity above 0.98; vLLM is not available here, so the bar is the binary64
+oracle with the rounding bound derived below, plus the reference's own
+algorithm restated in torch (oracle.torch_ref).
+
+Tolerance (stated per element): the kernel rounds each probability to bf16
+before the PV product (relative error <= 2^-9, as the reference does) and
+rounds the output to bf16 (<= 2^-9 relative); fp32 accumulation and exp2 add
+~1e-6 relative.  Hence
+    |out - out64| <= 2^-9 |out64| + 2^-9 * max_t |V[t, d]| + tiny
+and the test allows 2^-8 (|out64| + max_t |V[t, d]|), the maximum taken over
+the entries the row attends.  A dropped, duplicated or mis-scaled entry moves
+the output by about |V| / topk, far outside this for the shapes tested.
+"""
+import math
+
+import pytest
+import torch
+
+import oracle
+from flaggems_vllm import testing as W
+from oracle import torch_ref
+
+DEV = torch.device("cuda:0")
+
+
+# ------------------------------------------------------------ helpers ----
+
+def _attended(w):
+    """For each (b, sq): list of (rows tensor, ids) attended, main then extra."""
+    lists = [(torch_ref.model1_rows(w.k_cache.cpu()), w.k_cache.shape[0] * w.k_cache.shape[1],
+              w.indices.cpu(), w.topk_length)]
+    if w.extra_k_cache is not None:
+        lists.append((torch_ref.model1_rows(w.extra_k_cache.cpu()),
+                      w.extra_k_cache.shape[0] * w.extra_k_cache.shape[1],
+                      w.extra_indices.cpu(), w.extra_topk_length))
+    B, SQ = w.q.shape[:2]
+    out = {}
+    for b in range(B):
+        for s in range(SQ):
+            got = []
+            for rows, limit, idx, length in lists:
+                topk = idx.shape[-1]
+                n = topk if length is None else max(0, min(int(length[b]), topk))
+                ids = idx[b, s, :n].long()
+                ids = ids[(ids >= 0) & (ids < limit)]
+                got.append(rows[ids].float())
+            out[(b, s)] = torch.cat(got, 0)
+    return out
+
+
+def _vmax(w):
+    """[B, SQ, 1, 512]: max over attended entries of |V[t, d]| (0 if none)."""
+    B, SQ = w.q.shape[:2]
+    vm = torch.zeros(B, SQ, 1, 512, dtype=torch.float64)
+    for (b, s), rows in _attended(w).items():
+        if rows.shape[0]:
+            vm[b, s, 0] = rows.abs().amax(0).double()
+    return vm
+
+
+def _oracle(w):
+    return oracle.sparse_mla_decode_model1(w.q.cpu(), w.k_cache.cpu(), w.indices.cpu(),
+                                           **_cpu_kwargs(w))
+
+
+def _cpu_kwargs(w):
+    kw = w.oracle_kwargs()
+    return {k: (v.cpu() if isinstance(v, torch.Tensor) else v) for k, v in kw.items()}
+
+
+def _assert_within_bound(out, o64, vm, what=""):
+    out = out.cpu().double()
+    err = (out - o64).abs()
+    tol = 2.0 ** -8 * (o64.abs() + vm)
+    bad = err > tol
+    assert not bool(bad.any()), (
+        f"{what}: {int(bad.sum())} elements outside 2^-8 (|ref| + max|V|); "
+        f"worst excess {float((err - tol).max()):.3e}")
+
+
+def _combined_cache(w):
+    """A single cache holding the main cache's pages then the extra cache's
+    (same page size), and the index rows that address it."""
+    assert w.k_cache.shape[1] == w.extra_k_cache.shape[1]
+    cache = torch.cat([w.k_cache, w.extra_k_cache], 0)
+    offset = w.k_cache.shape[0] * w.k_cache.shape[1]
+    B, SQ = w.q.shape[:2]
+    rows = []
+    for b in range(B):
+        n0 = w.indices.shape[-1] if w.topk_length is None else int(w.topk_length[b])
+        n1 = w.extra_indices.shape[-1] if w.extra_topk_length is None else int(w.extra_topk_length[b])
+        r = torch.cat([w.indices[b, :, :n0], w.extra_indices[b, :, :n1] + offset], -1)
+        rows.append(r)
+    width = max(r.shape[-1] for r in rows)
+    width = (width + 63) // 64 * 64
+    idx = torch.full((B, SQ, width), -1, dtype=torch.int32)
+    lens = torch.zeros(B, dtype=torch.int32)
+    for b, r in enumerate(rows):
+        idx[b, :, :r.shape[-1]] = r
+        lens[b] = r.shape[-1]
+    return cache, idx, lens
+
+
+# ------------------------------------------------------- oracle pins ----
+
+def test_oracle_rows_match_the_gather_oracle():
+    """The decode oracle's dequantised rows are the rows the (separately
+    pinned) dequantize_and_gather oracle produces from the same pages."""
+    g = torch.Generator().manual_seed(1)
+    cache = W.make_model1_cache(6, 64, g)
+    out = torch.zeros(1, 6 * 64, 512, dtype=torch.bfloat16)
+    oracle.dequantize_and_gather_k_cache(out, cache.view(6, -1), torch.tensor([6 * 64], dtype=torch.int32),
+                                         None, torch.arange(6, dtype=torch.int32)[None], 64)
+    for tid in range(0, 6 * 64, 11):
+        assert torch.equal(oracle.model1_token_row(cache, tid), out[0, tid])
+    assert torch.equal(torch_ref.model1_rows(cache), out[0])
+
+
+def test_oracle_single_entry_is_that_entry():
+    """One attended entry: softmax weight 1, so out = its V row exactly and
+    lse = its score; n copies of it: same out, lse + ln(n)."""
+    w = W.make_mla_workload(batch=2, topk=64, num_pages=4, sink=False, topk_length=False, seed=3)
+    w.indices[:, :, :] = -1
+    w.indices[0, 0, 0] = 77
+    w.indices[1, 0, :8] = 130
+    o64, l64 = _oracle(w)
+    r77 = oracle.model1_token_row(w.k_cache, 77).double()
+    r130 = oracle.model1_token_row(w.k_cache, 130).double()
+    assert torch.equal(o64[0, 0], r77.expand(64, 512))
+    assert torch.allclose(o64[1, 0], r130.expand(64, 512), rtol=1e-14, atol=1e-15)
+    w.indices[1, 0, 1:8] = -1
+    _, l1 = _oracle(w)
+    assert torch.allclose(l64[1] - l1[1], torch.full_like(l1[1], math.log(8)), rtol=0, atol=1e-12)
+    w.indices[:, :, :] = -1
+    o0, l0 = _oracle(w)
+    assert bool((o0 == 0).all()) and bool(torch.isinf(l0).all()) and bool((l0 > 0).all())
+
+
+def test_oracle_sink_limits_and_half_weight():
+    """sink = -inf is no sink; sink = +inf zeroes the output; sink = lse gives
+    the sink the same weight as all entries together, halving the output."""
+    w = W.make_mla_workload(batch=3, topk=128, num_pages=8, seed=5)
+    o_none, l_none = _oracle(W.MlaWorkload(**{**w.__dict__, "attn_sink": None}))
+    w.attn_sink = torch.full((64,), -math.inf)
+    o_minus, l_minus = _oracle(w)
+    assert torch.equal(o_minus, o_none) and torch.equal(l_minus, l_none)
+    w.attn_sink = torch.full((64,), math.inf)
+    o_plus, l_plus = _oracle(w)
+    assert bool((o_plus == 0).all()) and torch.equal(l_plus, l_none)
+    w.attn_sink = l_none[0, :, 0].float()  # batch row 0's lse per head
+    o_half, _ = _oracle(w)
+    assert torch.allclose(o_half[0], o_none[0] / 2, rtol=1e-6, atol=1e-12)
+
+
+def test_oracle_extra_cache_is_a_second_list():
+    """Attending a main and an extra list equals attending their union from
+    one cache that holds both (invariance of the split), and permuting a
+    row's entries changes nothing."""
+    w = W.make_mla_workload(batch=4, topk=128, num_pages=6, extra_topk=192, extra_page=64,
+                            extra_pages=5, seed=7)
+    o_split, l_split = _oracle(w)
+    cache, idx, lens = _combined_cache(w)
+    o_one, l_one = oracle.sparse_mla_decode_model1(w.q, cache, idx, topk_length=lens,
+                                                   attn_sink=w.attn_sink)
+    assert torch.allclose(o_split, o_one, rtol=1e-12, atol=1e-14)
+    assert torch.allclose(l_split, l_one, rtol=1e-13, atol=0)
+    perm = torch.randperm(idx.shape[-1], generator=torch.Generator().manual_seed(0))
+    full = W.MlaWorkload("p", w.q, cache, idx[:, :, perm], None, w.attn_sink)
+    # without lengths, the -1 padding is what drops entries
+    o_perm, _ = _oracle(full)
+    assert torch.allclose(o_perm, o_one, rtol=1e-12, atol=1e-14)
+
+
+def test_oracle_ignores_invalid_entries():
+    """Entries past the top-k length, negative ids and ids past the cache are
+    not attended: the result equals that of the row with them removed."""
+    w = W.make_mla_workload(batch=2, topk=64, num_pages=4, topk_length=False, seed=9)
+    o_ref, l_ref = _oracle(w)
+    noisy = W.MlaWorkload("n", w.q, w.k_cache, torch.full((2, 1, 192), -1, dtype=torch.int32),
+                          torch.tensor([150, 192], dtype=torch.int32), w.attn_sink)
+    noisy.indices[:, :, 0:128:2] = w.indices            # valid entries at even slots
+    noisy.indices[:, :, 1:128:2] = 4 * 64 + 5            # one past the cache
+    noisy.indices[0, 0, 150:] = 3                        # past row 0's length
+    o_n, l_n = _oracle(noisy)
+    assert torch.allclose(o_n, o_ref, rtol=1e-12, atol=1e-14)
+    assert torch.allclose(l_n, l_ref, rtol=1e-13, atol=0)
+
+
+def test_oracle_against_direct_softmax():
+    """Brute force on a tiny case: softmax over the attended rows with
+    torch's float64 softmax and logsumexp (rows dequantised by torch's own
+    float8 cast)."""
+    w = W.make_mla_workload(batch=3, topk=64, num_pages=2, page=64, heads=64, seed=11)
+    o64, l64 = _oracle(w)
+    rows = _attended(w)
+    scale = 512 ** -0.5
+    for b in range(3):
+        kv = rows[(b, 0)].double()
+        s = (w.q[b, 0].double() @ kv.T) * scale
+        lse = torch.logsumexp(s, -1)
+        wts = torch.exp(s - lse[:, None])
+        denom = 1 + torch.exp(w.attn_sink.double() - lse)
+        assert torch.allclose(l64[b, :, 0], lse, rtol=1e-13, atol=0)
+        assert torch.allclose(o64[b, 0], (wts @ kv) / denom[:, None], rtol=1e-10, atol=1e-14)
+
+
+@pytest.mark.parametrize("case", ["ref_sink", "extra64", "extra2"])
+def test_reference_algorithm_within_bound(case):
+    """The reference's chunked bf16-P algorithm (torch restatement) stays
+    inside the stated bound of the exact result: the bound is the one the
+    reference's own arithmetic needs, not a loosening for the kernel."""
+    w = _case(case)
+    o64, l64 = _oracle(w)
+    out, lse = torch_ref.sparse_mla_decode_model1(w.q, w.k_cache, w.indices, **_cpu_kwargs(w))
+    _assert_within_bound(out, o64, _vmax(w), case)
+    fin = torch.isfinite(l64)
+    assert torch.allclose(lse.double()[fin], l64[fin], rtol=1e-5, atol=1e-5)
+
+
+def _case(name):
+    if name == "ref_sink":   # reference test :236-285
+        return W.make_mla_workload(batch=8, topk=128, num_pages=16, seed=43)
+    if name == "extra64":    # reference test :287-360, (64, 512, 12)
+        return W.make_mla_workload(batch=4, topk=128, num_pages=16, extra_topk=512, extra_page=64,
+                                   extra_pages=12, seed=43)
+    if name == "extra2":     # (2, 512, 260)
+        return W.make_mla_workload(batch=4, topk=128, num_pages=16, extra_topk=512, extra_page=2,
+                                   extra_pages=260, seed=43)
+    if name == "h128_sq2":
+        return W.make_mla_workload(batch=5, topk=192, num_pages=8, heads=128, seq_q=2,
+                                   topk_length=False, sink=False, seed=21)
+    raise KeyError(name)
+
+
+# ---------------------------------------------------- wrapper (CPU) ----
+
+def _meta():
+    from flaggems_vllm.ops.flash_mla_with_kvcache import get_mla_metadata
+
+    return get_mla_metadata()[0]
+
+
+def test_error_model1_extra_cache_requires_extra_indices():
+    """Reference test :420-438."""
+    import flaggems_vllm
+
+    g = torch.Generator().manual_seed(0)
+    q = torch.randn(1, 1, 64, 512).to(torch.bfloat16)
+    kv = W.make_model1_cache(4, 64, g)
+    extra = W.make_model1_cache(4, 64, g)
+    idx = torch.randint(0, 256, (1, 1, 64), dtype=torch.int32)
+    with pytest.raises(AssertionError, match="extra_indices_in_kvcache"):
+        flaggems_vllm.flash_mla_with_kvcache(q, kv, None, None, 512, _meta(), is_fp8_kvcache=True,
+                                             indices=idx, extra_k_cache=extra)
+
+
+def test_error_dense_rejects_sparse_only_args():
+    """Reference test :441-458."""
+    import flaggems_vllm
+
+    q = torch.randn(1, 1, 64, 576).to(torch.bfloat16)
+    kv = torch.randn(4, 64, 1, 576).to(torch.bfloat16)
+    bt = torch.arange(4, dtype=torch.int32).view(1, 4)
+    seqlens = torch.full((1,), 64, dtype=torch.int32)
+    with pytest.raises(AssertionError, match="must be None when dense"):
+        flaggems_vllm.flash_mla_with_kvcache(q, kv, bt, seqlens, 512, _meta(),
+                                             attn_sink=torch.randn(64))
+
+
+def test_error_sched_meta_reuse_mismatch():
+    """Reference test :461-484."""
+    import flaggems_vllm
+    from flaggems_vllm.ops.flash_mla_with_kvcache import FlashMLASchedMeta
+
+    q = torch.empty(1, 1, 64, 512, dtype=torch.bfloat16)
+    kv = torch.empty(4, 64, 1, 584, dtype=torch.uint8)
+    meta = FlashMLASchedMeta(have_initialized=True, config=FlashMLASchedMeta.Config(
+        b=2, s_q=1, h_q=64, page_block_size=64, h_k=1, causal=False, is_fp8_kvcache=True,
+        topk=64, extra_page_block_size=None, extra_topk=None))
+    with pytest.raises(AssertionError, match="sched_meta.config.b"):
+        flaggems_vllm.flash_mla_with_kvcache(q, kv, None, None, 512, meta)
+
+
+@pytest.mark.parametrize("bad,match", [
+    (dict(topk=96), "divisible by 64"),
+    (dict(heads=32), "h_q == 64 or 128"),
+    (dict(v32_topk_length=True), "dynamic topk length"),
+    (dict(cpu=True), "GPU"),
+])
+def test_wrapper_asserts(bad, match):
+    import flaggems_vllm
+
+    heads = bad.get("heads", 64)
+    topk = bad.get("topk", 64)
+    q = torch.zeros(1, 1, heads, 512, dtype=torch.bfloat16)
+    kv = torch.zeros(2, 64, 1, 584, dtype=torch.uint8)
+    idx = torch.zeros(1, 1, topk, dtype=torch.int32)
+    kw = {}
+    if bad.get("v32_topk_length"):
+        q = torch.zeros(1, 1, 64, 576, dtype=torch.bfloat16)
+        kv = torch.zeros(2, 64, 1, 656, dtype=torch.uint8)
+        kw["topk_length"] = torch.ones(1, dtype=torch.int32)
+    with pytest.raises(AssertionError, match=match):
+        flaggems_vllm.flash_mla_with_kvcache(q, kv, None, None, 512, _meta(), is_fp8_kvcache=True,
+                                             indices=idx, **kw)
+
+
+def test_c_abi_rejects_bad_arguments():
+    from flaggems_vllm import _native
+
+    f = _native.lib().fgv_sparse_mla_decode_model1
+
+    def call(**kw):
+        a = dict(q=16, qs=(512 * 64, 512 * 64, 512), cache=16, bst=64 * 584, nb=4, page=64,
+                 idx=16, topk=64, out=16, lse=16, B=1, SQ=1, H=64, ecache=None, eidx=None, elen=None)
+        a.update(kw)
+        return f(a["q"], *a["qs"],
+                 a["cache"], a["bst"], a["nb"], a["page"],
+                 a["idx"], a["topk"], a["topk"], a["topk"], None,
+                 a["ecache"], 64 * 584, 4, 64,
+                 a["eidx"], a["topk"], a["topk"], a["topk"], a["elen"],
+                 None, 0.05,
+                 a["out"], 512 * 64, 512 * 64, 512,
+                 a["lse"], 64, 1,
+                 a["B"], a["SQ"], a["H"], None)
+
+    assert call(H=96) == -2
+    assert call(B=-1) == -2
+    assert call(q=None) == -1
+    assert call(q=8) == -3
+    assert call(cache=8) == -3
+    assert call(bst=64 * 584 - 16) == -4
+    assert call(page=0) == -2
+    assert call(eidx=16) == -2      # extra indices without an extra cache
+    assert call(B=0) == 0           # nothing to do, nothing launched
+
+
+# --------------------------------------------------------------- GPU ----
+
+def _gpu(w, out=None, q=None):
+    import flaggems_vllm
+
+    d = w.to(DEV)
+    res = flaggems_vllm.flash_mla_with_kvcache(
+        d.q if q is None else q, d.k_cache, None, None, 512, _meta(), is_fp8_kvcache=True,
+        indices=d.indices, out=out, **d.kwargs())
+    torch.cuda.synchronize()
+    return res
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", ["ref_sink", "extra64", "extra2", "h128_sq2"])
+def test_gpu_reference_cases(case):
+    print(f"\n[case] sparse MLA {case}", flush=True)
+    w = _case(case)
+    out, lse = _gpu(w)
+    o64, l64 = _oracle(w)
+    _assert_within_bound(out, o64, _vmax(w), case)
+    fin = torch.isfinite(l64)
+    assert torch.equal(torch.isfinite(lse.cpu()), fin)
+    assert torch.allclose(lse.cpu().double()[fin], l64[fin], rtol=1e-5, atol=1e-5)
+    # the reference's own acceptance check (cosine similarity > 0.98)
+    cos = torch.nn.functional.cosine_similarity(out.cpu().double().flatten(), o64.flatten(), dim=0)
+    assert float(cos) > 0.999
+    # and against the reference's algorithm restated in torch
+    emu, _ = torch_ref.sparse_mla_decode_model1(w.q, w.k_cache, w.indices, **_cpu_kwargs(w))
+    diff = (out.cpu().double() - emu.double()).abs()
+    tol = 2.0 ** -8 * emu.double().abs() + 2.0 ** -10 * _vmax(w)
+    assert bool((diff <= tol).all()), float((diff - tol).max())
+
+
+@pytest.mark.gpu
+def test_gpu_single_and_repeated_entry_bit_exact():
+    """One attended entry, or 64 copies of one (weights 1 and 1/64, exact in
+    binary floating point), give that entry's bf16 V row bit for bit, with no
+    sink; the LSE is its score (plus ln 64)."""
+    print("\n[case] sparse MLA single/repeated entry", flush=True)
+    w = W.make_mla_workload(batch=4, topk=128, num_pages=8, sink=False, seed=13)
+    w.topk_length = torch.tensor([1, 64, 128, 0], dtype=torch.int32)
+    w.indices[1, 0, :64] = 300
+    w.indices[2, 0, :] = -1
+    w.indices[2, 0, 100] = 511
+    out, lse = _gpu(w)
+    out = out.cpu()
+    assert torch.equal(out[0, 0], oracle.model1_token_row(w.k_cache, int(w.indices[0, 0, 0])).expand(64, 512))
+    assert torch.equal(out[1, 0], oracle.model1_token_row(w.k_cache, 300).expand(64, 512))
+    assert torch.equal(out[2, 0], oracle.model1_token_row(w.k_cache, 511).expand(64, 512))
+    assert bool((out[3] == 0).all())
+    lse = lse.cpu()
+    assert bool(torch.isinf(lse[3]).all()) and bool((lse[3] > 0).all())
+    _, l64 = _oracle(w)
+    assert torch.allclose(lse[:3].double(), l64[:3], rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.gpu
+def test_gpu_invalid_entries_and_strided_views():
+    """Negative ids, ids past the cache, lengths past top-k, a row with only
+    invalid entries before its valid ones, and strided q / out views."""
+    print("\n[case] sparse MLA invalid entries + strided", flush=True)
+    w = W.make_mla_workload(batch=6, topk=256, num_pages=8, seed=17)
+    w.indices[0, 0, ::3] = -1
+    w.indices[1, 0, 1::2] = 8 * 64 + 3      # past the cache
+    w.indices[2, 0, :64] = -5               # the first two chunks attend nothing
+    w.topk_length[3] = 1000                 # clamped to top-k
+    w.topk_length[4] = -3                   # nothing attended
+    qbig = torch.zeros(6, 1, 64, 1024, dtype=torch.bfloat16)
+    qbig[..., 256:768] = w.q
+    qv = qbig.to(DEV)[..., 256:768]
+    obuf = torch.full((6, 1, 64, 640), 7.0, dtype=torch.bfloat16, device=DEV)
+    out, lse = _gpu(w, out=obuf[..., 64:576], q=qv)
+    o64, l64 = _oracle(w)
+    _assert_within_bound(out, o64, _vmax(w), "invalid/strided")
+    assert bool((obuf[..., :64] == 7).all()) and bool((obuf[..., 576:] == 7).all())
+    assert bool((out[4].cpu() == 0).all()) and bool(torch.isinf(lse[4]).all())
+
+
+@pytest.mark.gpu
+def test_gpu_extreme_scales():
+    """Scale bytes across the representable range (tiny and large powers of
+    two, and byte 0 = scale 0): the dequantised rows stay exact, so the
+    single-entry output is still the bf16 row."""
+    print("\n[case] sparse MLA extreme scales", flush=True)
+    w = W.make_mla_workload(batch=7, topk=64, num_pages=2, sink=False, seed=19)
+    page_bytes = w.k_cache.view(2, -1)
+    scl = page_bytes[:, 64 * 576:].view(2, 64, 8)
+    choices = torch.tensor([0, 1, 20, 100, 127, 150, 140], dtype=torch.uint8)
+    for i in range(7):
+        scl[0, i, :7] = choices[i]
+    w.topk_length = torch.ones(7, dtype=torch.int32)
+    w.indices[:, 0, 0] = torch.arange(7, dtype=torch.int32)
+    out, _ = _gpu(w)
+    out = out.cpu()
+    for i in range(7):
+        row = oracle.model1_token_row(w.k_cache, i)
+        assert torch.equal(out[i, 0], row.expand(64, 512)), int(choices[i])
+
+
+@pytest.mark.gpu
+def test_gpu_bench_case_against_oracle():
+    """The benchmark's decode case at full size (batch 512, top-k 128 over 512
+    pages, sink, top-k lengths)."""
+    print("\n[case] sparse MLA bench decode case", flush=True)
+    w = W.make_mla_case("decode")
+    out, lse = _gpu(w)
+    o64, l64 = _oracle(w)
+    _assert_within_bound(out, o64, _vmax(w), "decode")
+    assert torch.allclose(lse.cpu().double(), l64, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.gpu
+def test_gpu_deterministic():
+    print("\n[case] sparse MLA determinism", flush=True)
+    w = _case("extra64")
+    a, la = _gpu(w)
+    b, lb = _gpu(w)
+    assert torch.equal(a, b) and torch.equal(la, lb)
