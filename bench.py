@@ -35,11 +35,13 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", type=int, default=2, help="main-op workload c0..c4 (default c2)")
     ap.add_argument("--op", choices=["main", "inv_rope", "gather", "rmsnorm", "indexer",
-                                     "slot_mapping", "copy"],
+                                     "slot_mapping", "mla", "copy"],
                     default="main",
                     help="copy: torch device copy of 512 MiB, the HBM calibration kernel")
     ap.add_argument("--tma", action="store_true", help="inv_rope: packed UE8M0 scales")
     ap.add_argument("--fp4", action="store_true", help="indexer: MXFP4 instead of FP8")
+    ap.add_argument("--mla-case", choices=["decode", "extra512", "extra8192"], default="decode",
+                    help="mla: the reference benchmark's MODEL1 sparse-decode case")
     ap.add_argument("--cpu-sample-tokens", type=int, default=8192)
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="repeat the CPU sample until this much CPU time is spent (min 3 runs)")
@@ -127,6 +129,33 @@ def cpu_baseline_inv(w, tma, sample_tokens, seconds):
     return {"value": n / t, "unit": "tokens/s", "cores": cores, "kind": "port",
             "sample": f"first {n} of {w.o.shape[0]} tokens, torch CPU restatement "
                       f"(oracle/torch_ref.py), median of {reps} runs, {t:.3f} s per run"}
+
+
+def cpu_baseline_mla(w, sample_rows, seconds):
+    """The reference's portable MODEL1 algorithm restated in torch
+    (oracle.torch_ref) on the host CPU, over the first `sample_rows` batch
+    rows; decode rows (batch x seq_q) per second."""
+    import torch
+
+    from oracle import torch_ref
+
+    n = min(sample_rows, w.q.shape[0])
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    sub = lambda t: None if t is None else t[:n]
+    kw = dict(topk_length=sub(w.topk_length), attn_sink=w.attn_sink,
+              extra_k_cache=w.extra_k_cache, extra_indices=sub(w.extra_indices),
+              extra_topk_length=sub(w.extra_topk_length))
+
+    def run():
+        torch_ref.sparse_mla_decode_model1(w.q[:n], w.k_cache, w.indices[:n], **kw)
+
+    t, reps = _repeat(run, seconds)
+    rows = n * w.q.shape[1]
+    return {"value": rows / t, "unit": "decode rows/s", "cores": cores, "kind": "port",
+            "sample": f"first {n} of {w.q.shape[0]} batch rows of {w.name}, all heads: torch CPU "
+                      f"restatement of the reference's portable MODEL1 kernel (oracle/torch_ref.py), "
+                      f"median of {reps} runs, {t:.3f} s per run"}
 
 
 def main():
@@ -240,6 +269,32 @@ def main():
         config = {"workload": f"compute_slot_mapping_parallel over {w_cpu.name}: {T} tokens, "
                               f"{qsl.numel() - 1} requests", "num_tokens": T}
         args.no_cpu_baseline = True
+    elif args.op == "mla":
+        # the reference benchmark's MODEL1 sparse decode (batch 512, 64 heads, top-k 128)
+        w_cpu = W.make_mla_case(args.mla_case)
+        w = w_cpu.to(dev)
+        B, SQ, HQ = w.q.shape[:3]
+        T = B * SQ
+        bytes_call = W.mla_bytes(w_cpu)
+        flops_call = W.mla_flops(w_cpu)
+        meta, _ = flaggems_vllm.get_mla_metadata()
+        out = torch.empty(B, SQ, HQ, 512, dtype=torch.bfloat16, device=dev)
+        kw = w.kwargs()
+
+        def step():
+            flaggems_vllm.flash_mla_with_kvcache(w.q, w.k_cache, None, None, 512, meta,
+                                                 is_fp8_kvcache=True, indices=w.indices, out=out,
+                                                 **kw)
+
+        kernel, workload = "sparse_mla_decode_kernel", f"mla_{args.mla_case}"
+        case = W.MLA_CASES[args.mla_case]
+        config = {"workload": f"flash_mla_with_kvcache sparse MODEL1 decode '{args.mla_case}': "
+                              f"batch {B}, seq_q {SQ}, {HQ} heads, top-k {case['topk']} over "
+                              f"{case['num_pages']} pages of 64 x 584 B, top-k lengths, attention sink"
+                              + (f", extra top-k {case['extra_topk']} over {case['extra_pages']} pages "
+                                 f"of {case['extra_page']}" if "extra_topk" in case else ""),
+                  "batch": B, "seq_q": SQ, "num_heads": HQ, "attended_entries": w_cpu.used_tokens(),
+                  "flops_per_call": flops_call}
     elif args.op == "copy":
         n = 512 << 20
         src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
@@ -270,6 +325,9 @@ def main():
 
     ms_step, t_kernel = time_gpu(step, args.steps, args.warmup)
     achieved = bytes_call / t_kernel / 1e9
+    if args.op == "mla":
+        config["mfma_tflops"] = flops_call / t_kernel / 1e12
+        config["mfma_frac_of_bf16_dense_peak"] = flops_call / t_kernel / 2.5e15
     traffic = measured_traffic(kernel, workload)
     result = {
         "metric": METRIC,
@@ -282,8 +340,11 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
-        "data": "synthetic: seeded N(0,1) bf16 q/kv, fp32 cos/sin (theta 1e4), vLLM-style paged slots",
+        "dtype": "bf16" if args.op == "mla" else "f32",
+        "data": ("synthetic: seeded q ~ N(0,1)/10 bf16, cache NoPE ~ N(0,0.1) quantised to e4m3 + "
+                 "E8M0 per 64, RoPE ~ N(0,0.1) bf16, uniform indices and top-k lengths, sink ~ N(0,1)"
+                 if args.op == "mla" else
+                 "synthetic: seeded N(0,1) bf16 q/kv, fp32 cos/sin (theta 1e4), vLLM-style paged slots"),
         "config": config,
         "kernel_us": t_kernel * 1e6,
         "gbps": achieved,
@@ -297,6 +358,8 @@ def main():
         if args.op == "main":
             result["cpu_baseline"] = cpu_baseline_main(w_cpu, args.cpu_sample_tokens,
                                                        args.cpu_seconds)
+        elif args.op == "mla":
+            result["cpu_baseline"] = cpu_baseline_mla(w_cpu, 64, args.cpu_seconds)
         else:
             result["cpu_baseline"] = cpu_baseline_inv(w_cpu, args.tma, args.cpu_sample_tokens,
                                                       args.cpu_seconds)

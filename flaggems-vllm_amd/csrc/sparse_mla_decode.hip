@@ -8,22 +8,32 @@
 // 699-720 (sm90 kernel: mask, epilogue, attention sink).
 //
 // One workgroup of 4 waves per (batch row, query position, 64-head block);
-// wave w owns heads 16w..16w+15.  The selected entries stream through in
-// chunks of 32:
-//   1. every thread gathers 4 entries x 8 dims (coalesced 576-byte rows),
-//      dequantises them to bf16 (exact: e4m3 value times a power of two) and
-//      writes them to LDS twice: row-major K[entry][dim] and dim-major
-//      V^T[dim][entry];
-//   2. S^T = K q^T on v_mfma_f32_16x16x32_bf16 (A = K from LDS, B = q held in
-//      registers for the whole kernel), so each lane ends up with one head
-//      and 8 entries of the chunk;
-//   3. online softmax in base 2 per head (two cross-lane shuffles), the
-//      probabilities rounded to bf16 become the B operand of
-//   4. O^T += V^T P^T (A = V^T from LDS), accumulated in fp32 registers.
-// The chunk's 32 entries are placed in V^T columns in the order the S^T
-// accumulator hands them to each lane, so P needs no data movement between
-// the two products.  Both products reduce over the same k permutation in A
-// and B, so the MFMA's internal k order does not matter.
+// wave w owns heads 16w..16w+15 and keeps their q (B operand) and fp32 O^T
+// accumulators in registers.  The selected entries of the main list, then of
+// the extra list, stream through in chunks of 32 with a three-stage pipeline:
+//   - indices of chunk c+2 are loaded into registers,
+//   - the raw 576 token bytes and 8 scale bytes of each entry of chunk c+1 are
+//     gathered straight into LDS (global_load_lds_dwordx4: no registers, no
+//     wait), into the other half of a double buffer; 8 lanes move one entry,
+//     so each lane resolves one index per chunk,
+//   - chunk c, gathered one iteration earlier, is dequantised from LDS into a
+//     bf16 K tile [32 entries][512] (v_cvt_scalef32_pk_bf16_fp8: e4m3 times a
+//     power of two, exact) and attended:
+//       S^T = K q^T on v_mfma_f32_16x16x32_bf16 (A = K rows, B = q), giving
+//         each lane one head and 8 entries of the chunk;
+//       online softmax in base 2 per head (two cross-lane shuffles) against
+//         a reference maximum that is only raised, and O rescaled, when a
+//         score exceeds it by more than 2^8 (so probabilities stay below
+//         256); the probabilities, rounded to bf16, are the B operand of
+//       O^T += V^T P^T, whose A operand (V^T = K^T) is read from the same K
+//         tile with ds_read_b64_tr_b16 transposing loads.
+// The K tile is XOR-swizzled in 16-byte blocks (block b of row r stored at
+// b ^ f(r), f a permutation of 0..15) so that the row reads of QK, the
+// transposing reads of PV and the dequantising writes are all free of LDS
+// bank conflicts (256 bytes per LDS cycle).  Entries that are
+// not attended (past the top-k length, negative, or past the cache) are
+// gathered from a harmless address and zeroed, and their scores masked to
+// -inf.
 #include <math.h>
 
 #include "fgv_device.h"
@@ -34,13 +44,26 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kBlockHeads = 64;
-constexpr int kChunk = 32;    // entries per chunk
-constexpr int kKRow = 520;    // K row stride in bf16 (1040 B: 8 lanes of a b128 read hit distinct banks)
-constexpr int kVRow = 40;     // V^T row stride in bf16 (80 B, same reason)
+constexpr int kChunk = 32;                                    // entries per chunk
+constexpr int kPieces = kTokenDataBytes / 16;                 // 36 16-byte pieces per entry
+constexpr int kGathers = (kPieces + 7) / 8;                   // 5 wave-wide gathers per wave and chunk
+// Raw chunk layout in LDS: gather n of wave w lands at n * kRegion + 1024 w,
+// i.e. piece k of entry e at (k / 8) * kRegion + 128 e + 16 (k % 8); the
+// region stride is 4096 + 128 so that the 16 lanes of a dequantising read
+// that cross into the next region use the other half of the banks.  The
+// 8 scale bytes of entry e follow at kRawScaleOff + 32 e.
+constexpr int kRegion = kChunk * 128 + 128;
+constexpr int kRawScaleOff = kGathers * kRegion;
+constexpr int kRawBytes = kRawScaleOff + kChunk * 32;
 constexpr float kLn2 = 0.693147180559945309f;
+constexpr float kRescaleSlack = 8.0f;                         // log2 of the largest probability
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef short short4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) short4_t lds_short4_t;
+typedef __attribute__((address_space(3))) uint32_t lds_u32_t;
+typedef const __attribute__((address_space(1))) uint32_t global_u32_t;
 
 struct CacheList {
     const uint8_t* cache;
@@ -48,6 +71,7 @@ struct CacheList {
     const int32_t* lengths;  // [batch] or null
     int64_t block_stride;    // bytes
     int64_t idx_stride_b, idx_stride_s;
+    double inv_page;         // 1 / page_size
     int32_t num_blocks, page_size, topk, pad;
 };
 
@@ -65,43 +89,202 @@ struct MlaArgs {
     float scale_log2;  // softmax scale * log2(e)
 };
 
-// V^T column of the first of the 4 entries 4*quad..4*quad+3: lane group g of
-// the S^T accumulator holds entries 4g..4g+3 (first 16-entry tile) and
-// 16+4g..16+4g+3 (second tile), which become k = 8g..8g+7 of the PV product.
-__device__ __forceinline__ int vt_column(int quad) {
-    return quad < 4 ? 8 * quad : 8 * (quad - 4) + 4;
+// Swizzle of the K tile: 16-byte block b of row r lives at block b ^ f(r).
+// f maps rows 0..15 to distinct values (a 16-lane row read of QK touches 16
+// distinct 16-byte bank groups) and rows 0..7 and 8..15 each to distinct
+// pairs {2k, 2k+1} (a 32-lane transposing read of PV covers 8 rows x 32
+// bytes in 16 distinct groups).
+__device__ __forceinline__ int swz(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
+
+__device__ __forceinline__ int kbuf_byte(int row, int block) {
+    return row * (kHeadDim * 2) + ((block ^ swz(row)) << 4);
 }
 
+// 8 e4m3 codes times 2^(byte - 127) -> 8 bf16, as the reference computes
+// it: bf16(f32(code) * f32 bits (byte << 23)).  v_cvt_scalef32_pk_bf16_fp8
+// gives exactly that for bytes 1..254; it reads byte 0 as 2^-127 and 255 as
+// NaN where the bit cast gives 0 and infinity, so those take the f32 route.
 template <bool kHigh>
-__device__ __forceinline__ uint32_t dequant2(uint32_t word, float scale) {
+__device__ __forceinline__ uint32_t dequant2_f32(uint32_t word, float scale) {
     typedef float f32x2 __attribute__((ext_vector_type(2)));
     const f32x2 f = __builtin_amdgcn_cvt_pk_f32_fp8((int)word, kHigh);
     return pack_bf16x2(f.x * scale, f.y * scale);
 }
 
-// 8 e4m3 codes (two words) times a power-of-two scale -> 8 bf16.
-__device__ __forceinline__ uint4 dequant8(uint32_t lo, uint32_t hi, float scale) {
-    return make_uint4(dequant2<false>(lo, scale), dequant2<true>(lo, scale),
-                      dequant2<false>(hi, scale), dequant2<true>(hi, scale));
+__device__ __forceinline__ uint4 dequant8(uint2 codes, uint32_t byte) {
+    const float scale = __uint_as_float(byte << 23);
+    if (__builtin_expect(byte - 1u >= 254u, 0)) {
+        return make_uint4(dequant2_f32<false>(codes.x, scale), dequant2_f32<true>(codes.x, scale),
+                          dequant2_f32<false>(codes.y, scale), dequant2_f32<true>(codes.y, scale));
+    }
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    return make_uint4(
+        __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)codes.x, scale, false)),
+        __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)codes.x, scale, true)),
+        __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)codes.y, scale, false)),
+        __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)codes.y, scale, true)));
 }
 
-__device__ __forceinline__ uint32_t word_of(const uint4& v, int i) {
-    return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+// One list (main or extra) as one (batch row, query position) sees it.
+struct ListView {
+    const uint8_t* cache;
+    const int32_t* row;     // this query's index row
+    int64_t block_stride;
+    double inv_page;
+    int page_size, num_blocks, len;
+};
+
+__device__ __forceinline__ ListView make_view(const CacheList& L, bool present, int b, int sq) {
+    ListView v;
+    v.cache = L.cache;
+    v.row = L.indices + b * L.idx_stride_b + sq * L.idx_stride_s;
+    v.block_stride = L.block_stride;
+    v.inv_page = L.inv_page;
+    v.page_size = L.page_size;
+    v.num_blocks = L.num_blocks;
+    int len = 0;
+    if (present) {
+        len = L.topk;
+        if (L.lengths) {
+            const int n = L.lengths[b];
+            len = n < 0 ? 0 : (n > L.topk ? L.topk : n);
+        }
+    }
+    v.len = len;
+    return v;
+}
+
+// Chunk c of the concatenated (main, extra) sequence: its list and first entry.
+__device__ __forceinline__ ListView select(const ListView& v0, const ListView& v1, bool second) {
+    ListView v;
+    v.cache = second ? v1.cache : v0.cache;
+    v.row = second ? v1.row : v0.row;
+    v.block_stride = second ? v1.block_stride : v0.block_stride;
+    v.inv_page = second ? v1.inv_page : v0.inv_page;
+    v.page_size = second ? v1.page_size : v0.page_size;
+    v.num_blocks = second ? v1.num_blocks : v0.num_blocks;
+    v.len = second ? v1.len : v0.len;
+    return v;
+}
+
+// The chunk's 32 indices are themselves gathered into LDS (lanes 0..31 of
+// wave 0; entries past the list's length read the row's first index and are
+// masked where they are used).
+__device__ __forceinline__ void issue_ids(const ListView& v, int t0, int lane, int32_t* ids_lds) {
+    const int32_t* src = (lane < kChunk && t0 + lane < v.len) ? v.row + t0 + lane : v.row;
+    __builtin_amdgcn_global_load_lds((global_u32_t*)src, (lds_u32_t*)ids_lds, 4, 0, 0);
+}
+
+// Byte offset of entry `id` inside the cache (page * block stride + `unit` *
+// position in page), or -1 if the entry is not attended.
+__device__ __forceinline__ int64_t entry_offset(const ListView& v, int id, int64_t unit) {
+    if (id < 0)
+        return -1;
+    int page = (int)((double)id * v.inv_page);
+    int rel = id - page * v.page_size;
+    if (rel < 0) {
+        --page;
+        rel += v.page_size;
+    } else if (rel >= v.page_size) {
+        ++page;
+        rel -= v.page_size;
+    }
+    if (page >= v.num_blocks)
+        return -1;
+    return (int64_t)page * v.block_stride + unit * rel;
+}
+
+// Raw bytes of the chunk's 32 entries -> LDS.  Lane `lane` of wave `wave`
+// moves pieces sub, sub+8, ..., sub+32 (sub = lane % 8, pieces past 35 repeat
+// piece 35 into padding) of entry 8 * wave + lane / 8, then a 4-byte scale
+// word (word lane % 2 of that entry's 8 scale bytes), and lanes with sub 0
+// write the entry's score mask (0 or -inf).  The mask lives in its own LDS
+// array: LDS written by these gathers is only read after the wait at the top
+// of the next chunk.
+__device__ __forceinline__ void issue_gather(const ListView& v, int t0, const uint8_t* dummy, int wave, int lane,
+                                             const int32_t* ids_lds, uint8_t* raw, float* mask) {
+    __attribute__((address_space(3))) uint8_t* dst = (__attribute__((address_space(3))) uint8_t*)raw;
+    const int e = 8 * wave + (lane >> 3), sub = lane & 7;
+    const int id = t0 + e < v.len ? ids_lds[e] : -1;
+    const int64_t off = entry_offset(v, id, kTokenDataBytes);
+    const uint8_t* tok = off >= 0 ? v.cache + off : dummy;
+#pragma unroll
+    for (int n = 0; n < kGathers; ++n) {
+        const int k = sub + 8 * n < kPieces ? sub + 8 * n : kPieces - 1;
+        __builtin_amdgcn_global_load_lds((global_u32_t*)(tok + 16 * k),
+                                         (lds_u32_t*)(dst + n * kRegion + 1024 * wave), 16, 0, 0);
+    }
+    const int64_t soff = entry_offset(v, id, kScaleBytesPerToken);
+    const uint8_t* scl = (soff >= 0 ? v.cache + (int64_t)v.page_size * kTokenDataBytes + soff : dummy) +
+                         4 * (lane & 1);
+    __builtin_amdgcn_global_load_lds((global_u32_t*)scl, (lds_u32_t*)(dst + kRawScaleOff + 256 * wave), 4, 0, 0);
+    if (sub == 0)
+        mask[e] = off >= 0 ? 0.f : -INFINITY;
+}
+
+// Chunk in `raw` -> bf16 K tile: wave w converts entries w, w+4, ..., lane l
+// the 8 dims of block l (blocks 0..55 NoPE: piece l/2, half l%2; 56..63
+// RoPE: piece l-28).  An entry's validity is uniform across the wave.
+__device__ __forceinline__ void dequantize(const uint8_t* raw, const float* mask, uint8_t* kbuf, int wave,
+                                           int lane) {
+#pragma unroll
+    for (int j = 0; j < kChunk / 4; ++j) {
+        const int e = 4 * j + wave;
+        uint4 v = make_uint4(0, 0, 0, 0);
+        if (mask[e] == 0.f) {
+            if (lane < kNopeDim / 8) {
+                const int k = lane >> 1;
+                const uint2 codes = *reinterpret_cast<const uint2*>(raw + (k >> 3) * kRegion + 128 * e +
+                                                                    16 * (k & 7) + 8 * (lane & 1));
+                v = dequant8(codes, raw[kRawScaleOff + 32 * e + (lane >> 3)]);
+            } else {
+                const int k = lane - (kNopeDim / 8 - kNopeDim / 16);
+                v = *reinterpret_cast<const uint4*>(raw + (k >> 3) * kRegion + 128 * e + 16 * (k & 7));
+            }
+        }
+        *reinterpret_cast<uint4*>(kbuf + kbuf_byte(e, lane)) = v;
+    }
+}
+
+__device__ __forceinline__ uint2 read_tr(const uint8_t* kbuf, int byte) {
+    const short4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_short4_t*)((__attribute__((address_space(3))) uint8_t*)kbuf + byte));
+    return __builtin_bit_cast(uint2, v);
 }
 
 __global__ void __launch_bounds__(kThreads, 2)
 sparse_mla_decode_kernel(MlaArgs a) {
-    __shared__ __align__(16) uint16_t k_lds[kChunk * kKRow];
-    __shared__ __align__(16) uint16_t vt_lds[kHeadDim * kVRow];
-    __shared__ float mask_lds[kChunk];
+    __shared__ __align__(16) uint8_t raw[2][kRawBytes];
+    __shared__ __align__(16) uint8_t kbuf[kChunk * kHeadDim * 2];
+    __shared__ __align__(16) int32_t ids_lds[2][64];
+    __shared__ float mask_lds[2][kChunk];
 
     const int tid = threadIdx.x;
-    const int wave = tid >> 6, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int m16 = lane & 15, g = lane >> 4;
     const int hb = blockIdx.x % a.head_blocks;
     const int bs = blockIdx.x / a.head_blocks;
     const int sq = bs % a.seq_q, b = bs / a.seq_q;
     const int head = hb * kBlockHeads + wave * 16 + m16;
+
+    const ListView v0 = make_view(a.list[0], true, b, sq);
+    const ListView v1 = make_view(a.list[1], a.num_lists > 1, b, sq);
+    const int n0 = (v0.len + kChunk - 1) / kChunk;
+    const int nchunks = n0 + (v1.len + kChunk - 1) / kChunk;
+    const uint8_t* dummy = reinterpret_cast<const uint8_t*>(a.q);
+
+    // indices of chunks 0 and 1, then chunk 0's bytes, in flight before q
+    auto first_of = [&](int c) { return (c >= n0 ? c - n0 : c) * kChunk; };
+    if (wave == 0) {
+        if (nchunks > 0)
+            issue_ids(select(v0, v1, 0 >= n0), first_of(0), lane, ids_lds[0]);
+        if (nchunks > 1)
+            issue_ids(select(v0, v1, 1 >= n0), first_of(1), lane, ids_lds[1]);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (nchunks > 0)
+        issue_gather(select(v0, v1, 0 >= n0), first_of(0), dummy, wave, lane, ids_lds[0], raw[0], mask_lds[0]);
 
     // q as the B operand of S^T = K q^T: step s covers dims 32s..32s+31, lane
     // group g dims 32s+8g..32s+8g+7 of head m16.
@@ -117,138 +300,105 @@ sparse_mla_decode_kernel(MlaArgs a) {
         acc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     float m_run = -INFINITY, l_run = 0.f;
 
-    // Gather geometry: entries 4*quad..4*quad+3 of the chunk, dims 8*d8..8*d8+7
-    // for d8 = d8a (NoPE) and d8b = d8a + 32 (NoPE below 56, RoPE from 56 on:
-    // exactly wave 3).
-    const int quad = tid & 7;
-    const int d8a = tid >> 3, d8b = d8a + 32;
-    const bool rope_unit = d8b >= kNopeDim / 8;
-    const int col0 = vt_column(quad);
+    // LDS byte offsets of this lane's K-tile reads.  QK: block 4s+g of row
+    // m16.  PV: lane j of group g points at row 4g + j/4, dims 16dt + 4(j%4)
+    // (block 2dt + (j%4)/2, byte 8(j%2)).  The swizzle only touches the low 4
+    // block bits, so 4 bases (s & 3) and 8 bases (dt & 7) plus constant
+    // offsets cover all reads.
+    int qk_base[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        qk_base[k] = kbuf_byte(m16, 4 * k + g);
+    const int tr_row = 4 * g + (m16 >> 2);
+    int tr_base[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+        tr_base[k] = kbuf_byte(tr_row, 2 * k + ((m16 & 3) >> 1)) + 8 * (m16 & 1);
 
-    for (int li = 0; li < a.num_lists; ++li) {
-        const CacheList& L = a.list[li];
-        int len = L.topk;
-        if (L.lengths) {
-            const int n = L.lengths[b];
-            len = n < 0 ? 0 : (n > L.topk ? L.topk : n);
+    for (int c = 0; c < nchunks; ++c) {
+        uint8_t* cur = raw[c & 1];
+        // The gather and dequantisation addresses derive from the lane id; an
+        // opaque copy per chunk keeps them from being held (and spilled)
+        // across the MFMA loops, which need every register.
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's gathers of chunk c (and chunk c+1's indices)
+        __syncthreads();                // everyone's gathers landed; K tile no longer read
+        dequantize(cur, mask_lds[c & 1], kbuf, wave, ln);
+        __syncthreads();
+        if (c + 1 < nchunks)
+            issue_gather(select(v0, v1, c + 1 >= n0), first_of(c + 1), dummy, wave, ln, ids_lds[(c + 1) & 1],
+                         raw[(c + 1) & 1], mask_lds[(c + 1) & 1]);
+        if (wave == 0 && c + 2 < nchunks)
+            issue_ids(select(v0, v1, c + 2 >= n0), first_of(c + 2), ln, ids_lds[c & 1]);
+
+        // ---- S^T = K q^T for the chunk's two 16-entry tiles
+        f32x4_t s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 16; ++s) {
+            const int off = qk_base[s & 3] + 256 * (s >> 2);
+            const bf16x8_t a0 = *reinterpret_cast<const bf16x8_t*>(kbuf + off);
+            const bf16x8_t a1 = *reinterpret_cast<const bf16x8_t*>(kbuf + off + 16 * kHeadDim * 2);
+            s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, qf[s], s0, 0, 0, 0);
+            s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, qf[s], s1, 0, 0, 0);
         }
-        const int32_t* idx = L.indices + b * L.idx_stride_b + sq * L.idx_stride_s;
-        const int64_t scale_off = (int64_t)L.page_size * kTokenDataBytes;
 
-        for (int t0 = 0; t0 < len; t0 += kChunk) {
-            // ---- gather + dequantise 4 entries x 2 pieces of 8 dims
-            uint4 ka[4], kb[4];
-            bool valid[4];
+        // ---- online softmax (base 2) for head m16 over entries 4g+r, 16+4g+r
+        const float* mask = mask_lds[c & 1];
+        float sv[8];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int t = t0 + 4 * quad + r;
-                const int id = t < len ? idx[t] : -1;
-                const int page = id >= 0 ? id / L.page_size : 0;
-                valid[r] = id >= 0 && page < L.num_blocks;
-                ka[r] = make_uint4(0, 0, 0, 0);
-                kb[r] = make_uint4(0, 0, 0, 0);
-                if (valid[r]) {
-                    const int rel = id - page * L.page_size;
-                    const uint8_t* blk = L.cache + (int64_t)page * L.block_stride;
-                    const uint8_t* tok = blk + (int64_t)rel * kTokenDataBytes;
-                    const uint64_t scales =
-                        *reinterpret_cast<const uint64_t*>(blk + scale_off + (int64_t)rel * kScaleBytesPerToken);
-                    const uint2 na = *reinterpret_cast<const uint2*>(tok + 8 * d8a);
-                    const float sa = __uint_as_float((uint32_t)((scales >> (8 * (d8a >> 3))) & 0xff) << 23);
-                    ka[r] = dequant8(na.x, na.y, sa);
-                    if (rope_unit) {
-                        kb[r] = *reinterpret_cast<const uint4*>(tok + kNopeDim + 16 * (d8b - kNopeDim / 8));
-                    } else {
-                        const uint2 nb = *reinterpret_cast<const uint2*>(tok + 8 * d8b);
-                        const float sb = __uint_as_float((uint32_t)((scales >> (8 * (d8b >> 3))) & 0xff) << 23);
-                        kb[r] = dequant8(nb.x, nb.y, sb);
-                    }
-                }
-            }
-
-            __syncthreads();  // the previous chunk's LDS reads are done
+        for (int r = 0; r < 4; ++r) {
+            sv[r] = s0[r] * a.scale_log2 + mask[4 * g + r];
+            sv[4 + r] = s1[r] * a.scale_log2 + mask[16 + 4 * g + r];
+        }
+        float cmax = sv[0];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                *reinterpret_cast<uint4*>(&k_lds[(4 * quad + r) * kKRow + 8 * d8a]) = ka[r];
-                *reinterpret_cast<uint4*>(&k_lds[(4 * quad + r) * kKRow + 8 * d8b]) = kb[r];
-            }
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int w = j >> 1;
-                uint32_t x0, x1, y0, y1;
-                if (j & 1) {
-                    x0 = (word_of(ka[0], w) >> 16) | (word_of(ka[1], w) & 0xffff0000u);
-                    x1 = (word_of(ka[2], w) >> 16) | (word_of(ka[3], w) & 0xffff0000u);
-                    y0 = (word_of(kb[0], w) >> 16) | (word_of(kb[1], w) & 0xffff0000u);
-                    y1 = (word_of(kb[2], w) >> 16) | (word_of(kb[3], w) & 0xffff0000u);
-                } else {
-                    x0 = (word_of(ka[0], w) & 0xffffu) | (word_of(ka[1], w) << 16);
-                    x1 = (word_of(ka[2], w) & 0xffffu) | (word_of(ka[3], w) << 16);
-                    y0 = (word_of(kb[0], w) & 0xffffu) | (word_of(kb[1], w) << 16);
-                    y1 = (word_of(kb[2], w) & 0xffffu) | (word_of(kb[3], w) << 16);
-                }
-                *reinterpret_cast<uint2*>(&vt_lds[(8 * d8a + j) * kVRow + col0]) = make_uint2(x0, x1);
-                *reinterpret_cast<uint2*>(&vt_lds[(8 * d8b + j) * kVRow + col0]) = make_uint2(y0, y1);
-            }
-            if (tid < 8) {
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    mask_lds[4 * quad + r] = valid[r] ? 0.f : -INFINITY;
-            }
-            __syncthreads();
-
-            // ---- S^T = K q^T for the chunk's two 16-entry tiles
-            f32x4_t s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int s = 0; s < 16; ++s) {
-                const bf16x8_t a0 = *reinterpret_cast<const bf16x8_t*>(&k_lds[m16 * kKRow + 32 * s + 8 * g]);
-                const bf16x8_t a1 =
-                    *reinterpret_cast<const bf16x8_t*>(&k_lds[(16 + m16) * kKRow + 32 * s + 8 * g]);
-                s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, qf[s], s0, 0, 0, 0);
-                s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, qf[s], s1, 0, 0, 0);
-            }
-
-            // ---- online softmax (base 2) for head m16 over entries 4g+r, 16+4g+r
-            float sv[8];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                sv[r] = s0[r] * a.scale_log2 + mask_lds[4 * g + r];
-                sv[4 + r] = s1[r] * a.scale_log2 + mask_lds[16 + 4 * g + r];
-            }
-            float cmax = sv[0];
-#pragma unroll
-            for (int i = 1; i < 8; ++i)
-                cmax = fmaxf(cmax, sv[i]);
-            cmax = fmaxf(cmax, __shfl_xor(cmax, 16));
-            cmax = fmaxf(cmax, __shfl_xor(cmax, 32));
+        for (int i = 1; i < 8; ++i)
+            cmax = fmaxf(cmax, sv[i]);
+        cmax = fmaxf(cmax, __shfl_xor(cmax, 16));
+        cmax = fmaxf(cmax, __shfl_xor(cmax, 32));
+        // Raise the reference maximum (and rescale O and the sum) only when a
+        // score of this wave's heads exceeds it by more than kRescaleSlack.
+        if (__any(cmax > m_run + kRescaleSlack)) {
             const float m_new = fmaxf(m_run, cmax);
-            const float m_use = m_new == -INFINITY ? 0.f : m_new;
-            const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-            float p[8], psum = 0.f;
+            const float alpha = __builtin_amdgcn_exp2f(m_run - (m_new == -INFINITY ? 0.f : m_new));
+            l_run *= alpha;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                p[i] = __builtin_amdgcn_exp2f(sv[i] - m_use);
-                psum += p[i];
-            }
-            psum += __shfl_xor(psum, 16);
-            psum += __shfl_xor(psum, 32);
-            l_run = l_run * alpha + psum;
+            for (int dt = 0; dt < 32; ++dt)
+                acc[dt] *= alpha;
             m_run = m_new;
-            const uint4 pw = make_uint4(pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]),
-                                        pack_bf16x2(p[4], p[5]), pack_bf16x2(p[6], p[7]));
-            const bf16x8_t pb = __builtin_bit_cast(bf16x8_t, pw);
-
-            // ---- O^T = alpha * O^T + V^T P^T over the 32 16-dim tiles
+        }
+        const float m_use = m_run == -INFINITY ? 0.f : m_run;
+        float p[8], psum = 0.f;
 #pragma unroll
-            for (int dt = 0; dt < 32; ++dt) {
-                const bf16x8_t av = *reinterpret_cast<const bf16x8_t*>(&vt_lds[(16 * dt + m16) * kVRow + 8 * g]);
-                acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pb, acc[dt] * alpha, 0, 0, 0);
-            }
+        for (int i = 0; i < 8; ++i) {
+            p[i] = __builtin_amdgcn_exp2f(sv[i] - m_use);
+            psum += p[i];
+        }
+        psum += __shfl_xor(psum, 16);
+        psum += __shfl_xor(psum, 32);
+        l_run += psum;
+        // k = 8g+i of the PV product is entry 4g+i (i < 4) or 16+4g+i-4
+        const uint4 pw = make_uint4(pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]),
+                                    pack_bf16x2(p[4], p[5]), pack_bf16x2(p[6], p[7]));
+        const bf16x8_t pb = __builtin_bit_cast(bf16x8_t, pw);
+
+        // ---- O^T = alpha * O^T + V^T P^T over the 32 16-dim tiles: the
+        // transposing read hands lane j of group g dim 16dt+j of rows
+        // 4g..4g+3 (then 16+4g..16+4g+3), the A operand of k = 8g..8g+7.
+#pragma unroll
+        for (int dt = 0; dt < 32; ++dt) {
+            const int off = tr_base[dt & 7] + 256 * (dt >> 3);
+            const uint2 lo = read_tr(kbuf, off);
+            const uint2 hi = read_tr(kbuf, off + 16 * kHeadDim * 2);
+            const bf16x8_t av = __builtin_bit_cast(bf16x8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
+            acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pb, acc[dt], 0, 0, 0);
         }
     }
 
-    // ---- epilogue: lse excludes the sink; the sink only rescales O
-    const bool any = m_run != -INFINITY;
+    // ---- epilogue: lse excludes the sink; the sink only rescales O.  m_run
+    // is the reference maximum (base 2): l_run = sum 2^(s - m_run).
+    const bool any = l_run > 0.f;
     float factor = 0.f;
     if (any)
         factor = a.sink ? 1.f / (l_run + expf(a.sink[head] - m_run * kLn2)) : 1.f / l_run;
@@ -263,7 +413,7 @@ sparse_mla_decode_kernel(MlaArgs a) {
         a.lse[b * a.l_sb + head * a.l_sh + sq] = any ? m_run * kLn2 + logf(l_run) : INFINITY;
 }
 
-bool fill_list(CacheList& L, const void* cache, int64_t block_stride, int64_t num_blocks, int64_t page_size,
+void fill_list(CacheList& L, const void* cache, int64_t block_stride, int64_t num_blocks, int64_t page_size,
                const int32_t* indices, int64_t idx_sb, int64_t idx_ss, int64_t topk, const int32_t* lengths) {
     L.cache = static_cast<const uint8_t*>(cache);
     L.indices = indices;
@@ -271,16 +421,15 @@ bool fill_list(CacheList& L, const void* cache, int64_t block_stride, int64_t nu
     L.block_stride = block_stride;
     L.idx_stride_b = idx_sb;
     L.idx_stride_s = idx_ss;
+    L.inv_page = 1.0 / (double)page_size;
     L.num_blocks = (int32_t)num_blocks;
     L.page_size = (int32_t)page_size;
     L.topk = (int32_t)topk;
     L.pad = 0;
-    return true;
 }
 
-int check_list(const char* which, const void* cache, int64_t block_stride, int64_t num_blocks,
-               int64_t page_size, const int32_t* indices, int64_t topk) {
-    (void)which;
+int check_list(const void* cache, int64_t block_stride, int64_t num_blocks, int64_t page_size,
+               const int32_t* indices, int64_t topk) {
     if (!cache || !indices)
         return fail(FGV_E_NULL_POINTER, "null cache or indices");
     if (page_size <= 0 || num_blocks < 0 || topk < 0)
@@ -328,7 +477,7 @@ extern "C" int fgv_sparse_mla_decode_model1(
         return fail(FGV_E_MISALIGNED, "out must be 8-byte aligned with strides a multiple of 4 elements");
     if (!aligned(lse, 4))
         return fail(FGV_E_MISALIGNED, "lse must be 4-byte aligned");
-    int rc = check_list("main", k_cache, cache_block_stride, num_blocks, page_size, indices, topk);
+    int rc = check_list(k_cache, cache_block_stride, num_blocks, page_size, indices, topk);
     if (rc)
         return rc;
     MlaArgs a;
@@ -336,8 +485,8 @@ extern "C" int fgv_sparse_mla_decode_model1(
     fill_list(a.list[0], k_cache, cache_block_stride, num_blocks, page_size, indices, idx_stride_b,
               idx_stride_s, topk, topk_length);
     if (extra_k_cache) {
-        rc = check_list("extra", extra_k_cache, extra_block_stride, extra_num_blocks, extra_page_size,
-                        extra_indices, extra_topk);
+        rc = check_list(extra_k_cache, extra_block_stride, extra_num_blocks, extra_page_size, extra_indices,
+                        extra_topk);
         if (rc)
             return rc;
         fill_list(a.list[1], extra_k_cache, extra_block_stride, extra_num_blocks, extra_page_size,
