@@ -27,10 +27,11 @@
 //         256); the probabilities, rounded to bf16, are the B operand of
 //       O^T += V^T P^T, whose A operand (V^T = K^T) is read from the same K
 //         tile with ds_read_b64_tr_b16 transposing loads.
-// The K tile is XOR-swizzled in 16-byte blocks (block b of row r stored at
-// b ^ f(r), f a permutation of 0..15) so that the row reads of QK, the
-// transposing reads of PV and the dequantising writes are all free of LDS
-// bank conflicts (256 bytes per LDS cycle).  Entries that are
+// K tile rows are 1056 bytes apart (1024 + 32) and bit 0 of the 16-byte block
+// index is flipped in rows 8..15 of every 16, so that the 16-lane row reads
+// of QK, the 32-lane transposing reads of PV and the dequantising writes are
+// all free of LDS bank conflicts (256 bytes per LDS cycle), while each
+// lane's QK and PV addresses stay one base plus constant offsets.  Entries that are
 // not attended (past the top-k length, negative, or past the cache) are
 // gathered from a harmless address and zeroed, and their scores masked to
 // -inf.
@@ -89,15 +90,18 @@ struct MlaArgs {
     float scale_log2;  // softmax scale * log2(e)
 };
 
-// Swizzle of the K tile: 16-byte block b of row r lives at block b ^ f(r).
-// f maps rows 0..15 to distinct values (a 16-lane row read of QK touches 16
-// distinct 16-byte bank groups) and rows 0..7 and 8..15 each to distinct
-// pairs {2k, 2k+1} (a 32-lane transposing read of PV covers 8 rows x 32
-// bytes in 16 distinct groups).
-__device__ __forceinline__ int swz(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
+// K tile addressing: 16-byte block b of row r at r * kKRowBytes + 16 (b ^ x(r)),
+// x(r) = bit 3 of r.  In 16-byte bank groups (mod 16) row r starts at 2r, so
+//   - QK, 16 lanes reading block c of rows 0..15: groups 2r + (c ^ x(r)) are
+//     16 distinct values (rows r and r+8 differ in x, hence in parity);
+//   - PV, 32 lanes reading blocks {2d, 2d+1} of rows 0..7 (or 8..15): the
+//     pairs {2r + 2d, 2r + 2d + 1} are 8 disjoint pairs;
+//   - dequantisation, 16 lanes writing 16 consecutive blocks of one row:
+//     distinct.
+constexpr int kKRowBytes = kHeadDim * 2 + 32;
 
 __device__ __forceinline__ int kbuf_byte(int row, int block) {
-    return row * (kHeadDim * 2) + ((block ^ swz(row)) << 4);
+    return row * kKRowBytes + ((block ^ ((row >> 3) & 1)) << 4);
 }
 
 // 8 e4m3 codes times 2^(byte - 127) -> 8 bf16, as the reference computes
@@ -255,7 +259,7 @@ __device__ __forceinline__ uint2 read_tr(const uint8_t* kbuf, int byte) {
 __global__ void __launch_bounds__(kThreads, 2)
 sparse_mla_decode_kernel(MlaArgs a) {
     __shared__ __align__(16) uint8_t raw[2][kRawBytes];
-    __shared__ __align__(16) uint8_t kbuf[kChunk * kHeadDim * 2];
+    __shared__ __align__(16) uint8_t kbuf[kChunk * kKRowBytes];
     __shared__ __align__(16) int32_t ids_lds[2][64];
     __shared__ float mask_lds[2][kChunk];
 
@@ -301,19 +305,13 @@ sparse_mla_decode_kernel(MlaArgs a) {
     float m_run = -INFINITY, l_run = 0.f;
 
     // LDS byte offsets of this lane's K-tile reads.  QK: block 4s+g of row
-    // m16.  PV: lane j of group g points at row 4g + j/4, dims 16dt + 4(j%4)
-    // (block 2dt + (j%4)/2, byte 8(j%2)).  The swizzle only touches the low 4
-    // block bits, so 4 bases (s & 3) and 8 bases (dt & 7) plus constant
-    // offsets cover all reads.
-    int qk_base[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-        qk_base[k] = kbuf_byte(m16, 4 * k + g);
+    // m16 (then row 16+m16).  PV: lane j of group g points at row 4g + j/4,
+    // dims 16dt + 4(j%4), i.e. block 2dt + (j%4)/2, byte 8(j%2) (then row
+    // 16 + 4g + j/4).  The flip touches only block bit 0, so s and dt enter as
+    // constant offsets 64 s and 32 dt.
+    const int qk_base = kbuf_byte(m16, g);
     const int tr_row = 4 * g + (m16 >> 2);
-    int tr_base[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k)
-        tr_base[k] = kbuf_byte(tr_row, 2 * k + ((m16 & 3) >> 1)) + 8 * (m16 & 1);
+    const int tr_base = kbuf_byte(tr_row, (m16 & 3) >> 1) + 8 * (m16 & 1);
 
     for (int c = 0; c < nchunks; ++c) {
         uint8_t* cur = raw[c & 1];
@@ -333,14 +331,22 @@ sparse_mla_decode_kernel(MlaArgs a) {
             issue_ids(select(v0, v1, c + 2 >= n0), first_of(c + 2), ln, ids_lds[c & 1]);
 
         // ---- S^T = K q^T for the chunk's two 16-entry tiles
+        // K operands read two steps ahead of the MFMAs that consume them
         f32x4_t s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+        bf16x8_t ka[3], kb[3];
+        auto read_k = [&](int s, bf16x8_t& x, bf16x8_t& y) {
+            x = *reinterpret_cast<const bf16x8_t*>(kbuf + qk_base + 64 * s);
+            y = *reinterpret_cast<const bf16x8_t*>(kbuf + qk_base + 64 * s + 16 * kKRowBytes);
+        };
+        read_k(0, ka[0], kb[0]);
+        read_k(1, ka[1], kb[1]);
 #pragma unroll
         for (int s = 0; s < 16; ++s) {
-            const int off = qk_base[s & 3] + 256 * (s >> 2);
-            const bf16x8_t a0 = *reinterpret_cast<const bf16x8_t*>(kbuf + off);
-            const bf16x8_t a1 = *reinterpret_cast<const bf16x8_t*>(kbuf + off + 16 * kHeadDim * 2);
-            s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, qf[s], s0, 0, 0, 0);
-            s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, qf[s], s1, 0, 0, 0);
+            if (s + 2 < 16)
+                read_k(s + 2, ka[(s + 2) % 3], kb[(s + 2) % 3]);
+            s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[s % 3], qf[s], s0, 0, 0, 0);
+            s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb[s % 3], qf[s], s1, 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);  // keep the reads two steps ahead
         }
 
         // ---- online softmax (base 2) for head m16 over entries 4g+r, 16+4g+r
@@ -386,13 +392,21 @@ sparse_mla_decode_kernel(MlaArgs a) {
         // ---- O^T = alpha * O^T + V^T P^T over the 32 16-dim tiles: the
         // transposing read hands lane j of group g dim 16dt+j of rows
         // 4g..4g+3 (then 16+4g..16+4g+3), the A operand of k = 8g..8g+7.
+        uint2 vlo[3], vhi[3];
+        auto read_v = [&](int dt, uint2& x, uint2& y) {
+            x = read_tr(kbuf, tr_base + 32 * dt);
+            y = read_tr(kbuf, tr_base + 32 * dt + 16 * kKRowBytes);
+        };
+        read_v(0, vlo[0], vhi[0]);
+        read_v(1, vlo[1], vhi[1]);
 #pragma unroll
         for (int dt = 0; dt < 32; ++dt) {
-            const int off = tr_base[dt & 7] + 256 * (dt >> 3);
-            const uint2 lo = read_tr(kbuf, off);
-            const uint2 hi = read_tr(kbuf, off + 16 * kHeadDim * 2);
+            if (dt + 2 < 32)
+                read_v(dt + 2, vlo[(dt + 2) % 3], vhi[(dt + 2) % 3]);
+            const uint2 lo = vlo[dt % 3], hi = vhi[dt % 3];
             const bf16x8_t av = __builtin_bit_cast(bf16x8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
             acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pb, acc[dt], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
 
