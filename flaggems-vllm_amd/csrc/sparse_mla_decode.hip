@@ -106,27 +106,19 @@ __device__ __forceinline__ int kbuf_byte(int row, int block) {
 
 // 8 e4m3 codes times 2^(byte - 127) -> 8 bf16, as the reference computes
 // it: bf16(f32(code) * f32 bits (byte << 23)).  v_cvt_scalef32_pk_bf16_fp8
-// gives exactly that for bytes 1..254; it reads byte 0 as 2^-127 and 255 as
-// NaN where the bit cast gives 0 and infinity, so those take the f32 route.
-template <bool kHigh>
-__device__ __forceinline__ uint32_t dequant2_f32(uint32_t word, float scale) {
-    typedef float f32x2 __attribute__((ext_vector_type(2)));
-    const f32x2 f = __builtin_amdgcn_cvt_pk_f32_fp8((int)word, kHigh);
-    return pack_bf16x2(f.x * scale, f.y * scale);
-}
-
+// gives exactly that for bytes 1..254 (checked on the GPU for all 256 x 254
+// code/byte pairs).  It reads byte 0 as 2^-127 where the bit cast gives 0, so
+// byte 0 converts at scale 1 and keeps only the sign bits (+-0, exact for
+// finite codes).  Byte 255 is an infinite scale, which the cache writer
+// cannot produce; like other non-finite inputs it is out of scope.
 __device__ __forceinline__ uint4 dequant8(uint2 codes, uint32_t byte) {
-    const float scale = __uint_as_float(byte << 23);
-    if (__builtin_expect(byte - 1u >= 254u, 0)) {
-        return make_uint4(dequant2_f32<false>(codes.x, scale), dequant2_f32<true>(codes.x, scale),
-                          dequant2_f32<false>(codes.y, scale), dequant2_f32<true>(codes.y, scale));
-    }
-    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    const float scale = __uint_as_float((byte ? byte : 127u) << 23);
+    const uint32_t keep = byte ? 0xffffffffu : 0x80008000u;
     return make_uint4(
-        __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)codes.x, scale, false)),
-        __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)codes.x, scale, true)),
-        __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)codes.y, scale, false)),
-        __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)codes.y, scale, true)));
+        keep & __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)codes.x, scale, false)),
+        keep & __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)codes.x, scale, true)),
+        keep & __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)codes.y, scale, false)),
+        keep & __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)codes.y, scale, true)));
 }
 
 // One list (main or extra) as one (batch row, query position) sees it.
@@ -227,26 +219,39 @@ __device__ __forceinline__ void issue_gather(const ListView& v, int t0, const ui
 }
 
 // Chunk in `raw` -> bf16 K tile: wave w converts entries w, w+4, ..., lane l
-// the 8 dims of block l (blocks 0..55 NoPE: piece l/2, half l%2; 56..63
-// RoPE: piece l-28).  An entry's validity is uniform across the wave.
+// the 8 dims of block l (blocks 0..55 NoPE: half l%2 of piece l/2; 56..63
+// RoPE: piece l-28), branch-free, with every LDS read issued before the first
+// conversion: each lane reads its whole 16-byte piece.
+// (Selects are written per component: a select of whole HIP vector structs
+// is lowered through private memory.)
+__device__ __forceinline__ uint4 dequant_piece(uint4 piece, uint32_t byte, bool nope, bool hi, bool valid) {
+    const uint2 codes = make_uint2(hi ? piece.z : piece.x, hi ? piece.w : piece.y);
+    const uint4 d = dequant8(codes, byte);
+    return make_uint4(valid ? (nope ? d.x : piece.x) : 0u, valid ? (nope ? d.y : piece.y) : 0u,
+                      valid ? (nope ? d.z : piece.z) : 0u, valid ? (nope ? d.w : piece.w) : 0u);
+}
+
 __device__ __forceinline__ void dequantize(const uint8_t* raw, const float* mask, uint8_t* kbuf, int wave,
                                            int lane) {
+    const bool nope = lane < kNopeDim / 8, hi = lane & 1;
+    const int k = nope ? lane >> 1 : lane - (kNopeDim / 8 - kNopeDim / 16);
+    const int piece_off = (k >> 3) * kRegion + 16 * (k & 7);
+    const int scale_off = kRawScaleOff + (nope ? lane >> 3 : 0);
+    // four entries at a time: loads, then conversions, then stores
 #pragma unroll
-    for (int j = 0; j < kChunk / 4; ++j) {
-        const int e = 4 * j + wave;
-        uint4 v = make_uint4(0, 0, 0, 0);
-        if (mask[e] == 0.f) {
-            if (lane < kNopeDim / 8) {
-                const int k = lane >> 1;
-                const uint2 codes = *reinterpret_cast<const uint2*>(raw + (k >> 3) * kRegion + 128 * e +
-                                                                    16 * (k & 7) + 8 * (lane & 1));
-                v = dequant8(codes, raw[kRawScaleOff + 32 * e + (lane >> 3)]);
-            } else {
-                const int k = lane - (kNopeDim / 8 - kNopeDim / 16);
-                v = *reinterpret_cast<const uint4*>(raw + (k >> 3) * kRegion + 128 * e + 16 * (k & 7));
-            }
-        }
-        *reinterpret_cast<uint4*>(kbuf + kbuf_byte(e, lane)) = v;
+    for (int j0 = 0; j0 < kChunk / 4; j0 += 4) {
+        const int e0 = 4 * j0 + wave, e1 = e0 + 4, e2 = e0 + 8, e3 = e0 + 12;
+        const uint4 p0 = *reinterpret_cast<const uint4*>(raw + piece_off + 128 * e0);
+        const uint4 p1 = *reinterpret_cast<const uint4*>(raw + piece_off + 128 * e1);
+        const uint4 p2 = *reinterpret_cast<const uint4*>(raw + piece_off + 128 * e2);
+        const uint4 p3 = *reinterpret_cast<const uint4*>(raw + piece_off + 128 * e3);
+        const uint32_t b0 = raw[scale_off + 32 * e0], b1 = raw[scale_off + 32 * e1];
+        const uint32_t b2 = raw[scale_off + 32 * e2], b3 = raw[scale_off + 32 * e3];
+        const bool k0 = mask[e0] == 0.f, k1 = mask[e1] == 0.f, k2 = mask[e2] == 0.f, k3 = mask[e3] == 0.f;
+        *reinterpret_cast<uint4*>(kbuf + kbuf_byte(e0, lane)) = dequant_piece(p0, b0, nope, hi, k0);
+        *reinterpret_cast<uint4*>(kbuf + kbuf_byte(e1, lane)) = dequant_piece(p1, b1, nope, hi, k1);
+        *reinterpret_cast<uint4*>(kbuf + kbuf_byte(e2, lane)) = dequant_piece(p2, b2, nope, hi, k2);
+        *reinterpret_cast<uint4*>(kbuf + kbuf_byte(e3, lane)) = dequant_piece(p3, b3, nope, hi, k3);
     }
 }
 
@@ -416,13 +421,28 @@ sparse_mla_decode_kernel(MlaArgs a) {
     float factor = 0.f;
     if (any)
         factor = a.sink ? 1.f / (l_run + expf(a.sink[head] - m_run * kLn2)) : 1.f / l_run;
-    uint16_t* orow = a.out + b * a.o_sb + sq * a.o_ss + head * a.o_sh;
+    // O goes out through LDS: each wave stages its 16 head rows (lane (m16,
+    // g) holds dims 16dt+4g..+3 of head m16), then writes whole 1 KiB rows
+    // with 16-byte non-temporal stores.  Rows are 1040 B apart so the staging
+    // writes of 32 lanes hit distinct banks.  The gather buffers and the K
+    // tile are free once every wave has left the chunk loop.
+    constexpr int kStageRow = kHeadDim * 2 + 16;
+    static_assert(2 * 16 * kStageRow <= 2 * kRawBytes && 2 * 16 * kStageRow <= kChunk * kKRowBytes,
+                  "two waves' staging fits the gather buffers and the K tile");
+    __syncthreads();
+    uint8_t* stage = wave < 2 ? &raw[0][0] + wave * 16 * kStageRow : kbuf + (wave - 2) * 16 * kStageRow;
 #pragma unroll
     for (int dt = 0; dt < 32; ++dt) {
         const f32x4_t v = acc[dt] * factor;
-        *reinterpret_cast<uint2*>(orow + 16 * dt + 4 * g) =
+        *reinterpret_cast<uint2*>(stage + m16 * kStageRow + 32 * dt + 8 * g) =
             make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
     }
+    __syncthreads();
+    uint16_t* obase = a.out + b * a.o_sb + sq * a.o_ss + (hb * kBlockHeads + wave * 16) * a.o_sh;
+#pragma unroll
+    for (int h = 0; h < 16; ++h)
+        store16(obase + h * a.o_sh + 8 * lane,
+                *reinterpret_cast<const uint4*>(stage + h * kStageRow + 16 * lane));
     if (g == 0)
         a.lse[b * a.l_sb + head * a.l_sh + sq] = any ? m_run * kLn2 + logf(l_run) : INFINITY;
 }
@@ -487,8 +507,8 @@ extern "C" int fgv_sparse_mla_decode_model1(
         return fail(FGV_E_NULL_POINTER, "null q, out or lse");
     if (!aligned(q, 16) || q_stride_b % 8 || q_stride_s % 8 || q_stride_h % 8)
         return fail(FGV_E_MISALIGNED, "q must be 16-byte aligned with strides a multiple of 8 elements");
-    if (!aligned(out, 8) || out_stride_b % 4 || out_stride_s % 4 || out_stride_h % 4)
-        return fail(FGV_E_MISALIGNED, "out must be 8-byte aligned with strides a multiple of 4 elements");
+    if (!aligned(out, 16) || out_stride_b % 8 || out_stride_s % 8 || out_stride_h % 8)
+        return fail(FGV_E_MISALIGNED, "out must be 16-byte aligned with strides a multiple of 8 elements");
     if (!aligned(lse, 4))
         return fail(FGV_E_MISALIGNED, "lse must be 4-byte aligned");
     int rc = check_list(k_cache, cache_block_stride, num_blocks, page_size, indices, topk);
