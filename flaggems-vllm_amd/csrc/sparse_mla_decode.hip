@@ -57,6 +57,11 @@ constexpr int kRegion = kChunk * 128 + 128;
 constexpr int kRawScaleOff = kGathers * kRegion;
 constexpr int kRawBytes = kRawScaleOff + kChunk * 32;
 constexpr float kLn2 = 0.693147180559945309f;
+// Split mode: a partial slot holds O [64 heads][512] fp32, then 64 maxima and
+// 64 sums; the per-row prefix sums live in the K tile while the schedule is
+// computed, which bounds the batch.
+constexpr int kSlotFloats = 64 * 512 + 128;
+constexpr int kMaxSplitRows = 8000;
 constexpr float kRescaleSlack = 8.0f;                         // log2 of the largest probability
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -86,8 +91,12 @@ struct MlaArgs {
     const float* sink;
     CacheList list[2];
     int32_t num_lists;
-    int32_t seq_q, head_blocks;
+    int32_t batch, seq_q, head_blocks;
     float scale_log2;  // softmax scale * log2(e)
+    // split mode
+    float* partials;       // 2 slots per workgroup of kSlotFloats
+    int32_t* row_prefix;   // batch + 1 prefix sums of per-item chunk counts
+    int32_t split_grid;
 };
 
 // K tile addressing: 16-byte block b of row r at r * kKRowBytes + 16 (b ^ x(r)),
@@ -255,45 +264,52 @@ __device__ __forceinline__ void dequantize(const uint8_t* raw, const float* mask
     }
 }
 
+// The workgroup's LDS: the double-buffered raw gather, the bf16 K tile, the
+// gathered indices and the score masks.  They are separate __shared__ arrays
+// (declared in each kernel, passed down by reference) so that the compiler
+// can tell the LDS-DMA targets from the tile the MFMAs read; as members of
+// one object they would make every tile read wait for the gathers.
+#define FGV_MLA_LDS                                              \
+    __shared__ __align__(16) uint8_t lds_raw[2][kRawBytes];      \
+    __shared__ __align__(16) uint8_t lds_kbuf[kChunk * kKRowBytes]; \
+    __shared__ __align__(16) int32_t lds_ids[2][64];             \
+    __shared__ float lds_mask[2][kChunk]
+
 __device__ __forceinline__ uint2 read_tr(const uint8_t* kbuf, int byte) {
     const short4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
         (lds_short4_t*)((__attribute__((address_space(3))) uint8_t*)kbuf + byte));
     return __builtin_bit_cast(uint2, v);
 }
 
-__global__ void __launch_bounds__(kThreads, 2)
-sparse_mla_decode_kernel(MlaArgs a) {
-    __shared__ __align__(16) uint8_t raw[2][kRawBytes];
-    __shared__ __align__(16) uint8_t kbuf[kChunk * kKRowBytes];
-    __shared__ __align__(16) int32_t ids_lds[2][64];
-    __shared__ float mask_lds[2][kChunk];
-
-    const int tid = threadIdx.x;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+// Attends chunks [c_lo, c_hi) of the (b, sq, hb) item's concatenated (main,
+// extra) chunk sequence.  With slot < 0 the item is complete and out/lse are
+// written; otherwise the unnormalised O, the reference maximum and the sum go
+// to partial slot `slot` of the workspace for the combine kernel.
+__device__ __forceinline__ void run_segment(const MlaArgs& a, uint8_t (&raw)[2][kRawBytes], uint8_t* kbuf,
+                                            int32_t (&ids_lds)[2][64], float (&mask_lds)[2][kChunk], int b,
+                                            int sq, int hb, int c_lo, int c_hi, int slot, int wave, int lane) {
     const int m16 = lane & 15, g = lane >> 4;
-    const int hb = blockIdx.x % a.head_blocks;
-    const int bs = blockIdx.x / a.head_blocks;
-    const int sq = bs % a.seq_q, b = bs / a.seq_q;
     const int head = hb * kBlockHeads + wave * 16 + m16;
 
     const ListView v0 = make_view(a.list[0], true, b, sq);
     const ListView v1 = make_view(a.list[1], a.num_lists > 1, b, sq);
     const int n0 = (v0.len + kChunk - 1) / kChunk;
-    const int nchunks = n0 + (v1.len + kChunk - 1) / kChunk;
     const uint8_t* dummy = reinterpret_cast<const uint8_t*>(a.q);
 
-    // indices of chunks 0 and 1, then chunk 0's bytes, in flight before q
+    // indices of the first two chunks, then the first chunk's bytes, in
+    // flight before q
     auto first_of = [&](int c) { return (c >= n0 ? c - n0 : c) * kChunk; };
     if (wave == 0) {
-        if (nchunks > 0)
-            issue_ids(select(v0, v1, 0 >= n0), first_of(0), lane, ids_lds[0]);
-        if (nchunks > 1)
-            issue_ids(select(v0, v1, 1 >= n0), first_of(1), lane, ids_lds[1]);
+        if (c_lo < c_hi)
+            issue_ids(select(v0, v1, c_lo >= n0), first_of(c_lo), lane, ids_lds[c_lo & 1]);
+        if (c_lo + 1 < c_hi)
+            issue_ids(select(v0, v1, c_lo + 1 >= n0), first_of(c_lo + 1), lane, ids_lds[(c_lo + 1) & 1]);
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (nchunks > 0)
-        issue_gather(select(v0, v1, 0 >= n0), first_of(0), dummy, wave, lane, ids_lds[0], raw[0], mask_lds[0]);
+    if (c_lo < c_hi)
+        issue_gather(select(v0, v1, c_lo >= n0), first_of(c_lo), dummy, wave, lane, ids_lds[c_lo & 1],
+                     raw[c_lo & 1], mask_lds[c_lo & 1]);
 
     // q as the B operand of S^T = K q^T: step s covers dims 32s..32s+31, lane
     // group g dims 32s+8g..32s+8g+7 of head m16.
@@ -318,7 +334,7 @@ sparse_mla_decode_kernel(MlaArgs a) {
     const int tr_row = 4 * g + (m16 >> 2);
     const int tr_base = kbuf_byte(tr_row, (m16 & 3) >> 1) + 8 * (m16 & 1);
 
-    for (int c = 0; c < nchunks; ++c) {
+    for (int c = c_lo; c < c_hi; ++c) {
         uint8_t* cur = raw[c & 1];
         // The gather and dequantisation addresses derive from the lane id; an
         // opaque copy per chunk keeps them from being held (and spilled)
@@ -329,10 +345,10 @@ sparse_mla_decode_kernel(MlaArgs a) {
         __syncthreads();                // everyone's gathers landed; K tile no longer read
         dequantize(cur, mask_lds[c & 1], kbuf, wave, ln);
         __syncthreads();
-        if (c + 1 < nchunks)
+        if (c + 1 < c_hi)
             issue_gather(select(v0, v1, c + 1 >= n0), first_of(c + 1), dummy, wave, ln, ids_lds[(c + 1) & 1],
                          raw[(c + 1) & 1], mask_lds[(c + 1) & 1]);
-        if (wave == 0 && c + 2 < nchunks)
+        if (wave == 0 && c + 2 < c_hi)
             issue_ids(select(v0, v1, c + 2 >= n0), first_of(c + 2), ln, ids_lds[c & 1]);
 
         // ---- S^T = K q^T for the chunk's two 16-entry tiles
@@ -415,6 +431,21 @@ sparse_mla_decode_kernel(MlaArgs a) {
         }
     }
 
+    if (slot >= 0) {
+        // partial: O as [head][dim] fp32, then the reference maxima and sums
+        float* ws = a.partials + (int64_t)slot * kSlotFloats;
+        float* orow = ws + (wave * 16 + m16) * kHeadDim;
+#pragma unroll
+        for (int dt = 0; dt < 32; ++dt)
+            *reinterpret_cast<f32x4_t*>(orow + 16 * dt + 4 * g) = acc[dt];
+        if (g == 0) {
+            ws[kBlockHeads * kHeadDim + wave * 16 + m16] = m_run;
+            ws[kBlockHeads * kHeadDim + kBlockHeads + wave * 16 + m16] = l_run;
+        }
+        __syncthreads();  // the next segment reuses the LDS buffers
+        return;
+    }
+
     // ---- epilogue: lse excludes the sink; the sink only rescales O.  m_run
     // is the reference maximum (base 2): l_run = sum 2^(s - m_run).
     const bool any = l_run > 0.f;
@@ -445,6 +476,191 @@ sparse_mla_decode_kernel(MlaArgs a) {
                 *reinterpret_cast<const uint4*>(stage + h * kStageRow + 16 * lane));
     if (g == 0)
         a.lse[b * a.l_sb + head * a.l_sh + sq] = any ? m_run * kLn2 + logf(l_run) : INFINITY;
+    __syncthreads();  // the next segment reuses the staging buffers
+}
+
+
+// One workgroup per (batch row, query position, 64-head block).
+__global__ void __launch_bounds__(kThreads, 2)
+sparse_mla_decode_kernel(MlaArgs a) {
+    FGV_MLA_LDS;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int hb = blockIdx.x % a.head_blocks;
+    const int bs = blockIdx.x / a.head_blocks;
+    const int sq = bs % a.seq_q, b = bs / a.seq_q;
+    const ListView v0 = make_view(a.list[0], true, b, sq);
+    const ListView v1 = make_view(a.list[1], a.num_lists > 1, b, sq);
+    const int nchunks = (v0.len + kChunk - 1) / kChunk + (v1.len + kChunk - 1) / kChunk;
+    run_segment(a, lds_raw, lds_kbuf, lds_ids, lds_mask, b, sq, hb, 0, nchunks, -1, wave, lane);
+}
+
+// Chunks a batch row's items have (the same for every query position and
+// head block of the row).
+__device__ __forceinline__ int row_chunks(const MlaArgs& a, int b) {
+    const ListView v0 = make_view(a.list[0], true, b, 0);
+    const ListView v1 = make_view(a.list[1], a.num_lists > 1, b, 0);
+    return (v0.len + kChunk - 1) / kChunk + (v1.len + kChunk - 1) / kChunk;
+}
+
+// Split mode: the W chunks of all items, in item order (b, sq, hb), are cut
+// into gridDim.x equal ranges, one per workgroup (two per CU), so long and
+// short lists share the machine evenly.  A workgroup walks its range item by
+// item; an item wholly inside one range is finished there, the pieces of an
+// item that crosses range boundaries go to partial slots 2k+1 (the range
+// where it starts) and 2k (every later range), which the combine kernel
+// merges.  The per-row prefix sums Q are computed by every workgroup in LDS
+// (workgroup 0 also leaves them in the workspace for the combine kernel).
+__global__ void __launch_bounds__(kThreads, 2)
+sparse_mla_decode_split_kernel(MlaArgs a) {
+    FGV_MLA_LDS;
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int B = a.batch, R = a.seq_q * a.head_blocks, G = gridDim.x;
+    int32_t* Q = reinterpret_cast<int32_t*>(lds_kbuf);  // B + 1 prefix sums
+    int32_t* part = Q + kMaxSplitRows + 1;              // per-thread slice sums
+
+    // ---- Q[b] = chunks of rows 0..b-1 (per item)
+    const int per = (B + kThreads - 1) / kThreads;
+    const int lo = min(B, tid * per), hi = min(B, lo + per);
+    int sum = 0;
+    for (int r = lo; r < hi; ++r)
+        sum += row_chunks(a, r);
+    part[tid] = sum;
+    __syncthreads();
+    if (tid == 0) {
+        int run = 0;
+        for (int t = 0; t < kThreads; ++t) {
+            const int v = part[t];
+            part[t] = run;
+            run += v;
+        }
+        Q[B] = run;
+    }
+    __syncthreads();
+    {
+        int run = part[tid];
+        for (int r = lo; r < hi; ++r) {
+            Q[r] = run;
+            run += row_chunks(a, r);
+        }
+    }
+    __syncthreads();
+    const int64_t W = (int64_t)Q[B] * R;
+    if (blockIdx.x == 0) {
+        for (int r = tid; r <= B; r += kThreads)
+            a.row_prefix[r] = Q[r];
+    }
+    const int64_t start = (int64_t)blockIdx.x * W / G, end = ((int64_t)blockIdx.x + 1) * W / G;
+    // first row whose items reach past `start`
+    int rlo = 0, rhi = B - 1;
+    while (rlo < rhi) {
+        const int mid = (rlo + rhi + 1) >> 1;
+        if ((int64_t)Q[mid] * R <= start)
+            rlo = mid;
+        else
+            rhi = mid - 1;
+    }
+    int b = rlo;
+    int n = Q[b + 1] - Q[b];   // > 0: the largest row starting at or before `start`
+    const int64_t off = start - (int64_t)Q[b] * R;   // chunk offset inside row b's items
+    __syncthreads();  // Q lives in the K tile, which the segments overwrite
+    if (start >= end)
+        return;
+    int j = (int)(off / n), c = (int)(off - (int64_t)j * n);
+    int64_t pos = start;
+    while (pos < end) {
+        const int c_hi = (int)min((int64_t)n, c + (end - pos));
+        const bool whole = c == 0 && c_hi == n;
+        const int slot = whole ? -1 : 2 * (int)blockIdx.x + (c > 0 ? 0 : 1);
+        // an opaque lane id per segment keeps the lane-derived gather
+        // addresses from being held (and spilled) across the segment loop
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        run_segment(a, lds_raw, lds_kbuf, lds_ids, lds_mask, b, j / a.head_blocks, j % a.head_blocks, c, c_hi,
+                    slot, wave, ln);
+        pos += c_hi - c;
+        c = 0;
+        if (++j == R) {
+            j = 0;
+            do {
+                ++b;
+                n = b < B ? row_chunks(a, b) : 1;
+            } while (b < B && n == 0);
+        }
+    }
+}
+
+// Merges the partial slots of every item that crosses a split range
+// boundary, and writes the items that attend nothing.  One workgroup per
+// item; thread t handles head t/4, dims 128 (t%4) .. +127.
+__global__ void __launch_bounds__(kThreads)
+sparse_mla_combine_kernel(MlaArgs a) {
+    const int item = blockIdx.x;
+    const int R = a.seq_q * a.head_blocks, G = a.split_grid;
+    const int b = item / R, jr = item % R;
+    const int sq = jr / a.head_blocks, hb = jr % a.head_blocks;
+    const int64_t W = (int64_t)a.row_prefix[a.batch] * R;
+    const int n = a.row_prefix[b + 1] - a.row_prefix[b];
+    const int64_t p0 = (int64_t)a.row_prefix[b] * R + (int64_t)jr * n, p1 = p0 + n;
+    auto range_of = [&](int64_t p) { return (int)min((int64_t)G - 1, ((p + 1) * G - 1) / W); };
+    auto start_of = [&](int k) { return (int64_t)k * W / G; };
+    int k_lo = 0, k_hi = -1;
+    if (n > 0) {
+        k_lo = range_of(p0);
+        k_hi = range_of(p1 - 1);
+        if (k_lo == k_hi)
+            return;  // finished by its workgroup
+    }
+    const int tid = threadIdx.x, h = tid >> 2, q4 = tid & 3;
+    const float* mbase = nullptr;
+    float M = -INFINITY;
+    for (int k = k_lo; k <= k_hi; ++k) {
+        if (start_of(k) == start_of(k + 1))
+            continue;  // empty range
+        const float* ws = a.partials + (int64_t)(k == k_lo ? 2 * k + 1 : 2 * k) * kSlotFloats;
+        M = fmaxf(M, ws[kBlockHeads * kHeadDim + h]);
+        mbase = ws;
+    }
+    (void)mbase;
+    const float M_use = M == -INFINITY ? 0.f : M;
+    float o[128];
+#pragma unroll
+    for (int i = 0; i < 128; ++i)
+        o[i] = 0.f;
+    float L = 0.f;
+    for (int k = k_lo; k <= k_hi; ++k) {
+        if (start_of(k) == start_of(k + 1))
+            continue;
+        const float* ws = a.partials + (int64_t)(k == k_lo ? 2 * k + 1 : 2 * k) * kSlotFloats;
+        const float l = ws[kBlockHeads * kHeadDim + kBlockHeads + h];
+        if (!(l > 0.f))
+            continue;
+        const float w = __builtin_amdgcn_exp2f(ws[kBlockHeads * kHeadDim + h] - M_use);
+        L += l * w;
+        const float* row = ws + h * kHeadDim + 128 * q4;
+#pragma unroll
+        for (int i = 0; i < 128; i += 4) {
+            const f32x4_t v = *reinterpret_cast<const f32x4_t*>(row + i);
+            o[i] += v[0] * w;
+            o[i + 1] += v[1] * w;
+            o[i + 2] += v[2] * w;
+            o[i + 3] += v[3] * w;
+        }
+    }
+    const int head = hb * kBlockHeads + h;
+    const bool any = L > 0.f;
+    float factor = 0.f;
+    if (any)
+        factor = a.sink ? 1.f / (L + expf(a.sink[head] - M_use * kLn2)) : 1.f / L;
+    uint16_t* orow = a.out + b * a.o_sb + sq * a.o_ss + head * a.o_sh + 128 * q4;
+#pragma unroll
+    for (int i = 0; i < 128; i += 8)
+        store16(orow + i, make_uint4(pack_bf16x2(o[i] * factor, o[i + 1] * factor),
+                                     pack_bf16x2(o[i + 2] * factor, o[i + 3] * factor),
+                                     pack_bf16x2(o[i + 4] * factor, o[i + 5] * factor),
+                                     pack_bf16x2(o[i + 6] * factor, o[i + 7] * factor)));
+    if (q4 == 0)
+        a.lse[b * a.l_sb + head * a.l_sh + sq] = any ? M_use * kLn2 + logf(L) : INFINITY;
 }
 
 void fill_list(CacheList& L, const void* cache, int64_t block_stride, int64_t num_blocks, int64_t page_size,
@@ -479,8 +695,40 @@ int check_list(const void* cache, int64_t block_stride, int64_t num_blocks, int6
     return FGV_OK;
 }
 
+// Lists this long (in 32-entry chunks, main + extra) make the one-item-per-
+// workgroup grid wait on its longest rows; from here on the split grid's
+// balance outweighs the partials it writes.
+constexpr int64_t kSplitMinChunks = 64;
+
+int64_t chunks_of(int64_t topk) { return (topk + kChunk - 1) / kChunk; }
+
+// Workgroups of the split grid: two per CU of the current device.
+int split_grid() {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        cus = 256;
+    return 2 * cus;
+}
+
+int64_t split_bytes(int64_t batch, int64_t topk, int64_t extra_topk) {
+    if (chunks_of(topk) + chunks_of(extra_topk) < kSplitMinChunks || batch > kMaxSplitRows)
+        return 0;
+    const int64_t slots = 2 * (int64_t)split_grid() * kSlotFloats * 4;
+    return slots + ((batch + 1) * 4 + 255) / 256 * 256;
+}
+
 }  // namespace
 }  // namespace fgv
+
+extern "C" int64_t fgv_sparse_mla_decode_workspace_bytes(int64_t batch, int64_t seq_q, int64_t num_heads,
+                                                         int64_t topk, int64_t extra_topk) {
+    (void)seq_q;
+    (void)num_heads;
+    if (batch <= 0 || topk < 0 || extra_topk < 0)
+        return 0;
+    return fgv::split_bytes(batch, topk, extra_topk);
+}
 
 extern "C" int fgv_sparse_mla_decode_model1(
     const void* q, int64_t q_stride_b, int64_t q_stride_s, int64_t q_stride_h,
@@ -493,7 +741,8 @@ extern "C" int fgv_sparse_mla_decode_model1(
     const float* attn_sink, float softmax_scale,
     void* out, int64_t out_stride_b, int64_t out_stride_s, int64_t out_stride_h,
     float* lse, int64_t lse_stride_b, int64_t lse_stride_h,
-    int64_t batch, int64_t seq_q, int64_t num_heads, void* stream) {
+    int64_t batch, int64_t seq_q, int64_t num_heads,
+    void* workspace, int64_t workspace_bytes, void* stream) {
     using namespace fgv;
     if (batch < 0 || seq_q < 0 || num_heads < 0)
         return fail(FGV_E_BAD_SHAPE, "negative size");
@@ -543,10 +792,30 @@ extern "C" int fgv_sparse_mla_decode_model1(
     a.l_sb = lse_stride_b;
     a.l_sh = lse_stride_h;
     a.sink = attn_sink;
+    a.batch = (int32_t)batch;
     a.seq_q = (int32_t)seq_q;
     a.head_blocks = (int32_t)(num_heads / kBlockHeads);
     a.scale_log2 = (float)((double)softmax_scale * 1.4426950408889634);
-    const dim3 grid((unsigned)(batch * seq_q * a.head_blocks));
-    hipLaunchKernelGGL(sparse_mla_decode_kernel, grid, dim3(kThreads), 0, static_cast<hipStream_t>(stream), a);
+    a.partials = nullptr;
+    a.row_prefix = nullptr;
+    a.split_grid = 0;
+    const int64_t items = batch * seq_q * a.head_blocks;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int64_t need = split_bytes(batch, topk, extra_k_cache ? extra_topk : 0);
+    if (need > 0 && workspace && workspace_bytes >= need) {
+        if (!aligned(workspace, 256))
+            return fail(FGV_E_MISALIGNED, "workspace must be 256-byte aligned");
+        a.split_grid = split_grid();
+        a.partials = static_cast<float*>(workspace);
+        a.row_prefix = reinterpret_cast<int32_t*>(static_cast<uint8_t*>(workspace) +
+                                                  2 * (int64_t)a.split_grid * kSlotFloats * 4);
+        hipLaunchKernelGGL(sparse_mla_decode_split_kernel, dim3((unsigned)a.split_grid), dim3(kThreads), 0, st, a);
+        rc = launch_status();
+        if (rc)
+            return rc;
+        hipLaunchKernelGGL(sparse_mla_combine_kernel, dim3((unsigned)items), dim3(kThreads), 0, st, a);
+        return launch_status();
+    }
+    hipLaunchKernelGGL(sparse_mla_decode_kernel, dim3((unsigned)items), dim3(kThreads), 0, st, a);
     return launch_status();
 }

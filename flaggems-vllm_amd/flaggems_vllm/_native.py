@@ -141,8 +141,11 @@ def lib():
         _P, _I64, _I64, _I64,  # out, strides
         _P, _I64, _I64,  # lse, strides (batch, head)
         _I64, _I64, _I64,  # batch, seq_q, num_heads
+        _P, _I64,  # workspace, workspace_bytes
         _P,  # stream
     ]
+    L.fgv_sparse_mla_decode_workspace_bytes.restype = ctypes.c_int64
+    L.fgv_sparse_mla_decode_workspace_bytes.argtypes = [_I64, _I64, _I64, _I64, _I64]
     _lib = L
     return _lib
 
@@ -168,4 +171,5 @@ EXPORTED_SYMBOLS = (
     "fgv_fused_indexer_q_rope_quant",
     "fgv_compute_slot_mapping",
     "fgv_sparse_mla_decode_model1",
+    "fgv_sparse_mla_decode_workspace_bytes",
 )

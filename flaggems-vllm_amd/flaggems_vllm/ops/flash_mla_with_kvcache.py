@@ -213,6 +213,11 @@ def flash_mla_with_kvcache(
     ei = extra_indices_in_kvcache
     ptr = lambda t: t.data_ptr() if t is not None else None
     with on_device_of(q):
+        # long lists: a workspace for the balanced split schedule (cf. the
+        # reference's lse_part / o_part, flash_mla_with_kvcache_model1.py:1588-1595)
+        ws_bytes = _native.lib().fgv_sparse_mla_decode_workspace_bytes(
+            batch, seq_q, num_heads_q, topk, extra_topk or 0)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes > 0 else None
         rc = _native.lib().fgv_sparse_mla_decode_model1(
             q.data_ptr(), q.stride(0), q.stride(1), q.stride(2),
             kc.data_ptr(), kc.stride(0), kc.shape[0], kc.shape[1],
@@ -224,7 +229,7 @@ def flash_mla_with_kvcache(
             ptr(attn_sink), float(softmax_scale),
             out.data_ptr(), out.stride(0), out.stride(1), out.stride(2),
             lse.data_ptr(), lse.stride(0), lse.stride(1),
-            batch, seq_q, num_heads_q, current_stream_ptr(q.device),
+            batch, seq_q, num_heads_q, ptr(ws), ws_bytes, current_stream_ptr(q.device),
         )
     _native.check(rc, "flash_mla_with_kvcache")
     return out, lse

@@ -249,7 +249,23 @@ int fgv_sparse_mla_decode_model1(
     const float* attn_sink, float softmax_scale,
     void* out, int64_t out_stride_b, int64_t out_stride_s, int64_t out_stride_h,
     float* lse, int64_t lse_stride_b, int64_t lse_stride_h,
-    int64_t batch, int64_t seq_q, int64_t num_heads, void* stream);
+    int64_t batch, int64_t seq_q, int64_t num_heads,
+    void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Bytes of device workspace (256-byte aligned) with which
+ * fgv_sparse_mla_decode_model1 balances long lists across the GPU: a grid of
+ * two workgroups per CU splits all (row, head block) items' chunks evenly,
+ * and a combine kernel merges the items that cross a split (the reference's
+ * split-KV schedule and combine, ops/flash_mla_with_kvcache_model1.py:1212-1395).
+ * 0 when the lists are short enough (topk + extra_topk below 2048 entries) or
+ * the batch too large (above 8000 rows) for the split schedule: then the
+ * workspace argument is ignored.  Passing no workspace (NULL or too small)
+ * always works, with one workgroup per item.  The value depends on the
+ * current device's CU count.
+ */
+int64_t fgv_sparse_mla_decode_workspace_bytes(int64_t batch, int64_t seq_q, int64_t num_heads,
+                                              int64_t topk, int64_t extra_topk);
 
 #ifdef __cplusplus
 }

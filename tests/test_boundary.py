@@ -24,7 +24,7 @@ def declared_symbols():
     for name in os.listdir(os.path.join(ROOT, "include")):
         if name.endswith(".h"):
             text = open(os.path.join(ROOT, "include", name)).read()
-            syms |= set(re.findall(r"^\s*(?:int|const char\s*\*)\s+(fgv_\w+)\s*\(", text, re.M))
+            syms |= set(re.findall(r"^\s*(?:int|int64_t|const char\s*\*)\s+(fgv_\w+)\s*\(", text, re.M))
     return syms
 
 

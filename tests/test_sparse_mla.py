@@ -321,7 +321,8 @@ def test_c_abi_rejects_bad_arguments():
 
     def call(**kw):
         a = dict(q=16, qs=(512 * 64, 512 * 64, 512), cache=16, bst=64 * 584, nb=4, page=64,
-                 idx=16, topk=64, out=16, lse=16, B=1, SQ=1, H=64, ecache=None, eidx=None, elen=None)
+                 idx=16, topk=64, out=16, lse=16, B=1, SQ=1, H=64, ecache=None, eidx=None, elen=None,
+                 ws=None, ws_bytes=0)
         a.update(kw)
         return f(a["q"], *a["qs"],
                  a["cache"], a["bst"], a["nb"], a["page"],
@@ -331,7 +332,7 @@ def test_c_abi_rejects_bad_arguments():
                  None, 0.05,
                  a["out"], 512 * 64, 512 * 64, 512,
                  a["lse"], 64, 1,
-                 a["B"], a["SQ"], a["H"], None)
+                 a["B"], a["SQ"], a["H"], a["ws"], a["ws_bytes"], None)
 
     assert call(H=96) == -2
     assert call(B=-1) == -2
@@ -341,7 +342,24 @@ def test_c_abi_rejects_bad_arguments():
     assert call(bst=64 * 584 - 16) == -4
     assert call(page=0) == -2
     assert call(eidx=16) == -2      # extra indices without an extra cache
+    assert call(out=8) == -3        # output rows are written with 16-byte stores
     assert call(B=0) == 0           # nothing to do, nothing launched
+
+
+def test_workspace_query():
+    """The balanced split schedule is used for long lists only, and then needs
+    two partial slots per workgroup of the grid plus the row prefix sums."""
+    from flaggems_vllm import _native
+
+    f = _native.lib().fgv_sparse_mla_decode_workspace_bytes
+    assert f(512, 1, 64, 128, 0) == 0            # decode: one workgroup per item
+    assert f(512, 1, 64, 128, 512) == 0          # 20 chunks: still unsplit
+    big = f(512, 1, 64, 128, 8192)
+    slot = (64 * 512 + 128) * 4
+    prefix = (513 * 4 + 255) // 256 * 256
+    assert big > 0 and (big - prefix) % (2 * slot) == 0 and big % 256 == 0
+    assert f(9000, 1, 64, 128, 8192) == 0        # prefix sums must fit in LDS
+    assert f(0, 1, 64, 128, 8192) == 0
 
 
 # --------------------------------------------------------------- GPU ----
@@ -463,3 +481,69 @@ def test_gpu_deterministic():
     a, la = _gpu(w)
     b, lb = _gpu(w)
     assert torch.equal(a, b) and torch.equal(la, lb)
+
+
+# ------------------------------------------------------- GPU: split grid ----
+
+def _gpu_raw(w, workspace):
+    """Calls the C ABI directly, with or without a workspace."""
+    from flaggems_vllm import _native
+
+    d = w.to(DEV)
+    B, SQ, HQ, _ = d.q.shape
+    out = torch.empty(B, SQ, HQ, 512, dtype=torch.bfloat16, device=DEV)
+    lse = torch.empty(B, HQ, SQ, dtype=torch.float32, device=DEV)
+    L = _native.lib()
+    etopk = d.extra_indices.shape[-1] if d.extra_indices is not None else 0
+    nbytes = L.fgv_sparse_mla_decode_workspace_bytes(B, SQ, HQ, d.indices.shape[-1], etopk)
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=DEV) if workspace else None
+    ptr = lambda t: t.data_ptr() if t is not None else None
+    ek, ei = d.extra_k_cache, d.extra_indices
+    rc = L.fgv_sparse_mla_decode_model1(
+        d.q.data_ptr(), d.q.stride(0), d.q.stride(1), d.q.stride(2),
+        d.k_cache.data_ptr(), d.k_cache.stride(0), d.k_cache.shape[0], d.k_cache.shape[1],
+        d.indices.data_ptr(), d.indices.stride(0), d.indices.stride(1), d.indices.shape[-1],
+        ptr(d.topk_length),
+        ptr(ek), ek.stride(0) if ek is not None else 0, ek.shape[0] if ek is not None else 0,
+        ek.shape[1] if ek is not None else 1,
+        ptr(ei), ei.stride(0) if ei is not None else 0, ei.stride(1) if ei is not None else 0, etopk,
+        ptr(d.extra_topk_length), ptr(d.attn_sink), 512 ** -0.5,
+        out.data_ptr(), out.stride(0), out.stride(1), out.stride(2),
+        lse.data_ptr(), lse.stride(0), lse.stride(1), B, SQ, HQ,
+        ptr(ws), nbytes if workspace else 0, torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, rc
+    torch.cuda.synchronize()
+    return out.cpu(), lse.cpu(), nbytes
+
+
+def _split_case(name):
+    if name == "long":        # like the benchmark's extra8192 case, 24 rows
+        return W.make_mla_workload(batch=24, topk=128, num_pages=64, extra_topk=8192, extra_page=2,
+                                   extra_pages=512, seed=31, q_scale=0.1)
+    if name == "edges":       # empty rows, 128 heads, two query positions
+        w = W.make_mla_workload(batch=5, topk=2048, num_pages=40, heads=128, seq_q=2, seed=33)
+        w.topk_length = torch.tensor([0, 2048, 1, 0, 1500], dtype=torch.int32)
+        return w
+    if name == "tiny":        # fewer chunks than workgroups: most split ranges are empty
+        w = W.make_mla_workload(batch=3, topk=2048, num_pages=40, seed=35)
+        w.topk_length = torch.tensor([5, 0, 40], dtype=torch.int32)
+        return w
+    raise KeyError(name)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", ["long", "edges", "tiny"])
+def test_gpu_split_grid_against_oracle(case):
+    print(f"\n[case] sparse MLA split grid {case}", flush=True)
+    w = _split_case(case)
+    out, lse, nbytes = _gpu_raw(w, workspace=True)
+    assert nbytes > 0, "the case must take the split path"
+    o64, l64 = _oracle(w)
+    _assert_within_bound(out, o64, _vmax(w), case)
+    fin = torch.isfinite(l64)
+    assert torch.equal(torch.isfinite(lse), fin)
+    assert torch.allclose(lse.double()[fin], l64[fin], rtol=1e-5, atol=1e-5)
+    # the same call without a workspace (one workgroup per item) agrees
+    out1, lse1, _ = _gpu_raw(w, workspace=False)
+    _assert_within_bound(out1, o64, _vmax(w), case + " unsplit")
+    assert torch.allclose(lse1.double()[fin], lse.double()[fin], rtol=1e-6, atol=1e-6)
