@@ -592,7 +592,8 @@ sparse_mla_decode_split_kernel(MlaArgs a) {
 
 // Merges the partial slots of every item that crosses a split range
 // boundary, and writes the items that attend nothing.  One workgroup per
-// item; thread t handles head t/4, dims 128 (t%4) .. +127.
+// item; wave w merges head rows w, w+4, ..., lane l dims 8l..8l+7, so every
+// read of a 2 KiB partial row and every 1 KiB output row is contiguous.
 __global__ void __launch_bounds__(kThreads)
 sparse_mla_combine_kernel(MlaArgs a) {
     const int item = blockIdx.x;
@@ -611,56 +612,44 @@ sparse_mla_combine_kernel(MlaArgs a) {
         if (k_lo == k_hi)
             return;  // finished by its workgroup
     }
-    const int tid = threadIdx.x, h = tid >> 2, q4 = tid & 3;
-    const float* mbase = nullptr;
-    float M = -INFINITY;
-    for (int k = k_lo; k <= k_hi; ++k) {
-        if (start_of(k) == start_of(k + 1))
-            continue;  // empty range
-        const float* ws = a.partials + (int64_t)(k == k_lo ? 2 * k + 1 : 2 * k) * kSlotFloats;
-        M = fmaxf(M, ws[kBlockHeads * kHeadDim + h]);
-        mbase = ws;
-    }
-    (void)mbase;
-    const float M_use = M == -INFINITY ? 0.f : M;
-    float o[128];
-#pragma unroll
-    for (int i = 0; i < 128; ++i)
-        o[i] = 0.f;
-    float L = 0.f;
-    for (int k = k_lo; k <= k_hi; ++k) {
-        if (start_of(k) == start_of(k + 1))
-            continue;
-        const float* ws = a.partials + (int64_t)(k == k_lo ? 2 * k + 1 : 2 * k) * kSlotFloats;
-        const float l = ws[kBlockHeads * kHeadDim + kBlockHeads + h];
-        if (!(l > 0.f))
-            continue;
-        const float w = __builtin_amdgcn_exp2f(ws[kBlockHeads * kHeadDim + h] - M_use);
-        L += l * w;
-        const float* row = ws + h * kHeadDim + 128 * q4;
-#pragma unroll
-        for (int i = 0; i < 128; i += 4) {
-            const f32x4_t v = *reinterpret_cast<const f32x4_t*>(row + i);
-            o[i] += v[0] * w;
-            o[i + 1] += v[1] * w;
-            o[i + 2] += v[2] * w;
-            o[i + 3] += v[3] * w;
+    auto slot_of = [&](int k) {
+        return a.partials + (int64_t)(k == k_lo ? 2 * k + 1 : 2 * k) * kSlotFloats;
+    };
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    for (int h = wave; h < kBlockHeads; h += kThreads / 64) {
+        float M = -INFINITY;
+        for (int k = k_lo; k <= k_hi; ++k)
+            if (start_of(k) != start_of(k + 1))  // skip empty ranges
+                M = fmaxf(M, slot_of(k)[kBlockHeads * kHeadDim + h]);
+        const float M_use = M == -INFINITY ? 0.f : M;
+        f32x4_t o0 = {0.f, 0.f, 0.f, 0.f}, o1 = {0.f, 0.f, 0.f, 0.f};
+        float L = 0.f;
+        for (int k = k_lo; k <= k_hi; ++k) {
+            if (start_of(k) == start_of(k + 1))
+                continue;
+            const float* ws = slot_of(k);
+            const float l = ws[kBlockHeads * kHeadDim + kBlockHeads + h];
+            if (!(l > 0.f))
+                continue;
+            const float w = __builtin_amdgcn_exp2f(ws[kBlockHeads * kHeadDim + h] - M_use);
+            L += l * w;
+            const f32x4_t* row = reinterpret_cast<const f32x4_t*>(ws + h * kHeadDim + 8 * lane);
+            o0 += row[0] * w;
+            o1 += row[1] * w;
         }
+        const int head = hb * kBlockHeads + h;
+        const bool any = L > 0.f;
+        float factor = 0.f;
+        if (any)
+            factor = a.sink ? 1.f / (L + expf(a.sink[head] - M_use * kLn2)) : 1.f / L;
+        o0 *= factor;
+        o1 *= factor;
+        store16(a.out + b * a.o_sb + sq * a.o_ss + head * a.o_sh + 8 * lane,
+                make_uint4(pack_bf16x2(o0[0], o0[1]), pack_bf16x2(o0[2], o0[3]), pack_bf16x2(o1[0], o1[1]),
+                           pack_bf16x2(o1[2], o1[3])));
+        if (lane == 0)
+            a.lse[b * a.l_sb + head * a.l_sh + sq] = any ? M_use * kLn2 + logf(L) : INFINITY;
     }
-    const int head = hb * kBlockHeads + h;
-    const bool any = L > 0.f;
-    float factor = 0.f;
-    if (any)
-        factor = a.sink ? 1.f / (L + expf(a.sink[head] - M_use * kLn2)) : 1.f / L;
-    uint16_t* orow = a.out + b * a.o_sb + sq * a.o_ss + head * a.o_sh + 128 * q4;
-#pragma unroll
-    for (int i = 0; i < 128; i += 8)
-        store16(orow + i, make_uint4(pack_bf16x2(o[i] * factor, o[i + 1] * factor),
-                                     pack_bf16x2(o[i + 2] * factor, o[i + 3] * factor),
-                                     pack_bf16x2(o[i + 4] * factor, o[i + 5] * factor),
-                                     pack_bf16x2(o[i + 6] * factor, o[i + 7] * factor)));
-    if (q4 == 0)
-        a.lse[b * a.l_sb + head * a.l_sh + sq] = any ? M_use * kLn2 + logf(L) : INFINITY;
 }
 
 void fill_list(CacheList& L, const void* cache, int64_t block_stride, int64_t num_blocks, int64_t page_size,
