@@ -286,7 +286,13 @@ def main():
                                                  is_fp8_kvcache=True, indices=w.indices, out=out,
                                                  **kw)
 
-        kernel, workload = "sparse_mla_decode_kernel", f"mla_{args.mla_case}"
+        from flaggems_vllm import _native
+
+        split = _native.lib().fgv_sparse_mla_decode_workspace_bytes(
+            B, SQ, HQ, w.indices.shape[-1],
+            w.extra_indices.shape[-1] if w.extra_indices is not None else 0) > 0
+        kernel = "sparse_mla_decode_split_kernel" if split else "sparse_mla_decode_kernel"
+        workload = f"mla_{args.mla_case}"
         case = W.MLA_CASES[args.mla_case]
         config = {"workload": f"flash_mla_with_kvcache sparse MODEL1 decode '{args.mla_case}': "
                               f"batch {B}, seq_q {SQ}, {HQ} heads, top-k {case['topk']} over "
@@ -294,7 +300,9 @@ def main():
                               + (f", extra top-k {case['extra_topk']} over {case['extra_pages']} pages "
                                  f"of {case['extra_page']}" if "extra_topk" in case else ""),
                   "batch": B, "seq_q": SQ, "num_heads": HQ, "attended_entries": w_cpu.used_tokens(),
-                  "flops_per_call": flops_call}
+                  "flops_per_call": flops_call,
+                  "schedule": "balanced split grid + combine kernel" if split
+                              else "one workgroup per (row, 64-head block)"}
     elif args.op == "copy":
         n = 512 << 20
         src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
