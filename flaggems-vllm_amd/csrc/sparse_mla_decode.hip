@@ -21,7 +21,7 @@
 //     power of two, exact) and attended:
 //       S^T = K q^T on v_mfma_f32_16x16x32_bf16 (A = K rows, B = q), giving
 //         each lane one head and 8 entries of the chunk;
-//       online softmax in base 2 per head (two cross-lane shuffles) against
+//       online softmax in base 2 per head (row-swapping permutes) against
 //         a reference maximum that is only raised, and O rescaled, when a
 //         score exceeds it by more than 2^8 (so probabilities stay below
 //         256); the probabilities, rounded to bf16, are the B operand of
@@ -33,8 +33,7 @@
 // all free of LDS bank conflicts (256 bytes per LDS cycle), while each
 // lane's QK and PV addresses stay one base plus constant offsets.  Entries that are
 // not attended (past the top-k length, negative, or past the cache) are
-// gathered from a harmless address and zeroed, and their scores masked to
-// -inf.
+// gathered from a zero page, and their scores masked to -inf.
 #include <math.h>
 
 #include "fgv_device.h"
@@ -120,15 +119,25 @@ __device__ __forceinline__ int kbuf_byte(int row, int block) {
 // byte 0 converts at scale 1 and keeps only the sign bits (+-0, exact for
 // finite codes).  Byte 255 is an infinite scale, which the cache writer
 // cannot produce; like other non-finite inputs it is out of scope.
+template <bool kExact>
 __device__ __forceinline__ uint4 dequant8(uint2 codes, uint32_t byte) {
-    const float scale = __uint_as_float((byte ? byte : 127u) << 23);
-    const uint32_t keep = byte ? 0xffffffffu : 0x80008000u;
-    return make_uint4(
-        keep & __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)codes.x, scale, false)),
-        keep & __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)codes.x, scale, true)),
-        keep & __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)codes.y, scale, false)),
-        keep & __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)codes.y, scale, true)));
+    const float scale = __uint_as_float((kExact && !byte ? 127u : byte) << 23);
+    const uint32_t keep = kExact && !byte ? 0x80008000u : 0xffffffffu;
+    const uint4 v = make_uint4(
+        __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)codes.x, scale, false)),
+        __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)codes.x, scale, true)),
+        __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)codes.y, scale, false)),
+        __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)codes.y, scale, true)));
+    if (!kExact)
+        return v;
+    return make_uint4(keep & v.x, keep & v.y, keep & v.z, keep & v.w);
 }
+
+// A zero-filled stand-in for the entries a chunk does not attend (past the
+// length, negative, past the cache): gathering them from here makes their
+// K rows exactly zero without any select in the dequantisation (e4m3 code 0
+// gives 0 at any scale), and keeps every lane of a gather active.
+__device__ __align__(256) uint8_t mla_zero_entry[1024];
 
 // One list (main or extra) as one (batch row, query position) sees it.
 struct ListView {
@@ -233,11 +242,11 @@ __device__ __forceinline__ void issue_gather(const ListView& v, int t0, const ui
 // conversion: each lane reads its whole 16-byte piece.
 // (Selects are written per component: a select of whole HIP vector structs
 // is lowered through private memory.)
-__device__ __forceinline__ uint4 dequant_piece(uint4 piece, uint32_t byte, bool nope, bool hi, bool valid) {
+template <bool kExact>
+__device__ __forceinline__ uint4 dequant_piece(uint4 piece, uint32_t byte, bool nope, bool hi) {
     const uint2 codes = make_uint2(hi ? piece.z : piece.x, hi ? piece.w : piece.y);
-    const uint4 d = dequant8(codes, byte);
-    return make_uint4(valid ? (nope ? d.x : piece.x) : 0u, valid ? (nope ? d.y : piece.y) : 0u,
-                      valid ? (nope ? d.z : piece.z) : 0u, valid ? (nope ? d.w : piece.w) : 0u);
+    const uint4 d = dequant8<kExact>(codes, byte);
+    return make_uint4(nope ? d.x : piece.x, nope ? d.y : piece.y, nope ? d.z : piece.z, nope ? d.w : piece.w);
 }
 
 __device__ __forceinline__ void dequantize(const uint8_t* raw, const float* mask, uint8_t* kbuf, int wave,
@@ -256,11 +265,22 @@ __device__ __forceinline__ void dequantize(const uint8_t* raw, const float* mask
         const uint4 p3 = *reinterpret_cast<const uint4*>(raw + piece_off + 128 * e3);
         const uint32_t b0 = raw[scale_off + 32 * e0], b1 = raw[scale_off + 32 * e1];
         const uint32_t b2 = raw[scale_off + 32 * e2], b3 = raw[scale_off + 32 * e3];
-        const bool k0 = mask[e0] == 0.f, k1 = mask[e1] == 0.f, k2 = mask[e2] == 0.f, k3 = mask[e3] == 0.f;
-        *reinterpret_cast<uint4*>(kbuf + kbuf_byte(e0, lane)) = dequant_piece(p0, b0, nope, hi, k0);
-        *reinterpret_cast<uint4*>(kbuf + kbuf_byte(e1, lane)) = dequant_piece(p1, b1, nope, hi, k1);
-        *reinterpret_cast<uint4*>(kbuf + kbuf_byte(e2, lane)) = dequant_piece(p2, b2, nope, hi, k2);
-        *reinterpret_cast<uint4*>(kbuf + kbuf_byte(e3, lane)) = dequant_piece(p3, b3, nope, hi, k3);
+        // scale byte 0 in an attended entry (never written by the cache
+        // writer) takes the exact route for the whole wave; unattended entries
+        // are zero bytes and convert to zero either way
+        const bool odd = nope && ((b0 == 0 && mask[e0] == 0.f) || (b1 == 0 && mask[e1] == 0.f) ||
+                                  (b2 == 0 && mask[e2] == 0.f) || (b3 == 0 && mask[e3] == 0.f));
+        if (__builtin_expect(__any(odd), 0)) {
+            *reinterpret_cast<uint4*>(kbuf + kbuf_byte(e0, lane)) = dequant_piece<true>(p0, b0, nope, hi);
+            *reinterpret_cast<uint4*>(kbuf + kbuf_byte(e1, lane)) = dequant_piece<true>(p1, b1, nope, hi);
+            *reinterpret_cast<uint4*>(kbuf + kbuf_byte(e2, lane)) = dequant_piece<true>(p2, b2, nope, hi);
+            *reinterpret_cast<uint4*>(kbuf + kbuf_byte(e3, lane)) = dequant_piece<true>(p3, b3, nope, hi);
+        } else {
+            *reinterpret_cast<uint4*>(kbuf + kbuf_byte(e0, lane)) = dequant_piece<false>(p0, b0, nope, hi);
+            *reinterpret_cast<uint4*>(kbuf + kbuf_byte(e1, lane)) = dequant_piece<false>(p1, b1, nope, hi);
+            *reinterpret_cast<uint4*>(kbuf + kbuf_byte(e2, lane)) = dequant_piece<false>(p2, b2, nope, hi);
+            *reinterpret_cast<uint4*>(kbuf + kbuf_byte(e3, lane)) = dequant_piece<false>(p3, b3, nope, hi);
+        }
     }
 }
 
@@ -274,6 +294,29 @@ __device__ __forceinline__ void dequantize(const uint8_t* raw, const float* mask
     __shared__ __align__(16) uint8_t lds_kbuf[kChunk * kKRowBytes]; \
     __shared__ __align__(16) int32_t lds_ids[2][64];             \
     __shared__ float lds_mask[2][kChunk]
+
+// Max / sum over the four lanes l, l^16, l^32, l^48 (one head's lane
+// groups g) with gfx950's row-swapping permutes: with both operands x,
+// v_permlane16_swap returns {x[l], x[l^16]} (in row order) and
+// v_permlane32_swap {x[l], x[l^32]}, so each step is two VALU operations and
+// every lane of the four gets the same result (no LDS round trip).
+__device__ __forceinline__ float group4_max(float v) {
+    const uint32_t u = __float_as_uint(v);
+    const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const uint32_t w = __float_as_uint(v);
+    const auto b = __builtin_amdgcn_permlane32_swap(w, w, false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+__device__ __forceinline__ float group4_sum(float v) {
+    const uint32_t u = __float_as_uint(v);
+    const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const uint32_t w = __float_as_uint(v);
+    const auto b = __builtin_amdgcn_permlane32_swap(w, w, false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
 
 __device__ __forceinline__ uint2 read_tr(const uint8_t* kbuf, int byte) {
     const short4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -294,7 +337,7 @@ __device__ __forceinline__ void run_segment(const MlaArgs& a, uint8_t (&raw)[2][
     const ListView v0 = make_view(a.list[0], true, b, sq);
     const ListView v1 = make_view(a.list[1], a.num_lists > 1, b, sq);
     const int n0 = (v0.len + kChunk - 1) / kChunk;
-    const uint8_t* dummy = reinterpret_cast<const uint8_t*>(a.q);
+    const uint8_t* dummy = mla_zero_entry;
 
     // indices of the first two chunks, then the first chunk's bytes, in
     // flight before q
@@ -382,8 +425,7 @@ __device__ __forceinline__ void run_segment(const MlaArgs& a, uint8_t (&raw)[2][
 #pragma unroll
         for (int i = 1; i < 8; ++i)
             cmax = fmaxf(cmax, sv[i]);
-        cmax = fmaxf(cmax, __shfl_xor(cmax, 16));
-        cmax = fmaxf(cmax, __shfl_xor(cmax, 32));
+        cmax = group4_max(cmax);
         // Raise the reference maximum (and rescale O and the sum) only when a
         // score of this wave's heads exceeds it by more than kRescaleSlack.
         if (__any(cmax > m_run + kRescaleSlack)) {
@@ -402,8 +444,7 @@ __device__ __forceinline__ void run_segment(const MlaArgs& a, uint8_t (&raw)[2][
             p[i] = __builtin_amdgcn_exp2f(sv[i] - m_use);
             psum += p[i];
         }
-        psum += __shfl_xor(psum, 16);
-        psum += __shfl_xor(psum, 32);
+        psum = group4_sum(psum);
         l_run += psum;
         // k = 8g+i of the PV product is entry 4g+i (i < 4) or 16+4g+i-4
         const uint4 pw = make_uint4(pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]),
