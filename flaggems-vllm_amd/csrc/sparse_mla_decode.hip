@@ -11,7 +11,7 @@
 // wave w owns heads 16w..16w+15 and keeps their q (B operand) and fp32 O^T
 // accumulators in registers.  The selected entries of the main list, then of
 // the extra list, stream through in chunks of 32 with a three-stage pipeline:
-//   - indices of chunk c+2 are loaded into registers,
+//   - the index each lane needs for chunk c+2 is loaded into a register,
 //   - the raw 576 token bytes and 8 scale bytes of each entry of chunk c+1 are
 //     gathered straight into LDS (global_load_lds_dwordx4: no registers, no
 //     wait), into the other half of a double buffer; 8 lanes move one entry,
@@ -181,12 +181,13 @@ __device__ __forceinline__ ListView select(const ListView& v0, const ListView& v
     return v;
 }
 
-// The chunk's 32 indices are themselves gathered into LDS (lanes 0..31 of
-// wave 0; entries past the list's length read the row's first index and are
-// masked where they are used).
-__device__ __forceinline__ void issue_ids(const ListView& v, int t0, int lane, int32_t* ids_lds) {
-    const int32_t* src = (lane < kChunk && t0 + lane < v.len) ? v.row + t0 + lane : v.row;
-    __builtin_amdgcn_global_load_lds((global_u32_t*)src, (lds_u32_t*)ids_lds, 4, 0, 0);
+// The index of this lane's gather entry (8 * wave + lane / 8) of the chunk
+// starting at t0, or -1 past the list's length: one plain load per lane, a
+// chunk ahead of its use, so the compiler's own wait on the register is the
+// only synchronisation it needs.
+__device__ __forceinline__ int load_id(const ListView& v, int t0, int wave, int lane) {
+    const int t = t0 + 8 * wave + (lane >> 3);
+    return t < v.len ? v.row[t] : -1;
 }
 
 // Byte offset of entry `id` inside the cache (page * block stride + `unit` *
@@ -210,16 +211,15 @@ __device__ __forceinline__ int64_t entry_offset(const ListView& v, int id, int64
 
 // Raw bytes of the chunk's 32 entries -> LDS.  Lane `lane` of wave `wave`
 // moves pieces sub, sub+8, ..., sub+32 (sub = lane % 8, pieces past 35 repeat
-// piece 35 into padding) of entry 8 * wave + lane / 8, then a 4-byte scale
-// word (word lane % 2 of that entry's 8 scale bytes), and lanes with sub 0
-// write the entry's score mask (0 or -inf).  The mask lives in its own LDS
-// array: LDS written by these gathers is only read after the wait at the top
-// of the next chunk.
-__device__ __forceinline__ void issue_gather(const ListView& v, int t0, const uint8_t* dummy, int wave, int lane,
-                                             const int32_t* ids_lds, uint8_t* raw, float* mask) {
+// piece 35 into padding) of entry 8 * wave + lane / 8 (index `id`, from
+// load_id), then a 4-byte scale word (word lane % 2 of that entry's 8 scale
+// bytes), and lanes with sub 0 write the entry's score mask (0 or -inf).  The
+// mask lives in its own LDS array: LDS written by these gathers is only read
+// after the wait at the top of the next chunk.
+__device__ __forceinline__ void issue_gather(const ListView& v, const uint8_t* dummy, int wave, int lane, int id,
+                                             uint8_t* raw, float* mask) {
     __attribute__((address_space(3))) uint8_t* dst = (__attribute__((address_space(3))) uint8_t*)raw;
     const int e = 8 * wave + (lane >> 3), sub = lane & 7;
-    const int id = t0 + e < v.len ? ids_lds[e] : -1;
     const int64_t off = entry_offset(v, id, kTokenDataBytes);
     const uint8_t* tok = off >= 0 ? v.cache + off : dummy;
 #pragma unroll
@@ -292,7 +292,6 @@ __device__ __forceinline__ void dequantize(const uint8_t* raw, const float* mask
 #define FGV_MLA_LDS                                              \
     __shared__ __align__(16) uint8_t lds_raw[2][kRawBytes];      \
     __shared__ __align__(16) uint8_t lds_kbuf[kChunk * kKRowBytes]; \
-    __shared__ __align__(16) int32_t lds_ids[2][64];             \
     __shared__ float lds_mask[2][kChunk]
 
 // Max / sum over the four lanes l, l^16, l^32, l^48 (one head's lane
@@ -329,7 +328,7 @@ __device__ __forceinline__ uint2 read_tr(const uint8_t* kbuf, int byte) {
 // written; otherwise the unnormalised O, the reference maximum and the sum go
 // to partial slot `slot` of the workspace for the combine kernel.
 __device__ __forceinline__ void run_segment(const MlaArgs& a, uint8_t (&raw)[2][kRawBytes], uint8_t* kbuf,
-                                            int32_t (&ids_lds)[2][64], float (&mask_lds)[2][kChunk], int b,
+                                            float (&mask_lds)[2][kChunk], int b,
                                             int sq, int hb, int c_lo, int c_hi, int slot, int wave, int lane) {
     const int m16 = lane & 15, g = lane >> 4;
     const int head = hb * kBlockHeads + wave * 16 + m16;
@@ -339,20 +338,12 @@ __device__ __forceinline__ void run_segment(const MlaArgs& a, uint8_t (&raw)[2][
     const int n0 = (v0.len + kChunk - 1) / kChunk;
     const uint8_t* dummy = mla_zero_entry;
 
-    // indices of the first two chunks, then the first chunk's bytes, in
-    // flight before q
+    // The first two chunks' indices go first, then q's 16 loads (the largest
+    // transfer) overlap their round trip; the first chunk's bytes are gathered
+    // as soon as its index has arrived.
     auto first_of = [&](int c) { return (c >= n0 ? c - n0 : c) * kChunk; };
-    if (wave == 0) {
-        if (c_lo < c_hi)
-            issue_ids(select(v0, v1, c_lo >= n0), first_of(c_lo), lane, ids_lds[c_lo & 1]);
-        if (c_lo + 1 < c_hi)
-            issue_ids(select(v0, v1, c_lo + 1 >= n0), first_of(c_lo + 1), lane, ids_lds[(c_lo + 1) & 1]);
-    }
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (c_lo < c_hi)
-        issue_gather(select(v0, v1, c_lo >= n0), first_of(c_lo), dummy, wave, lane, ids_lds[c_lo & 1],
-                     raw[c_lo & 1], mask_lds[c_lo & 1]);
+    int id_cur = c_lo < c_hi ? load_id(select(v0, v1, c_lo >= n0), first_of(c_lo), wave, lane) : -1;
+    int id_next = c_lo + 1 < c_hi ? load_id(select(v0, v1, c_lo + 1 >= n0), first_of(c_lo + 1), wave, lane) : -1;
 
     // q as the B operand of S^T = K q^T: step s covers dims 32s..32s+31, lane
     // group g dims 32s+8g..32s+8g+7 of head m16.
@@ -361,6 +352,8 @@ __device__ __forceinline__ void run_segment(const MlaArgs& a, uint8_t (&raw)[2][
 #pragma unroll
     for (int s = 0; s < 16; ++s)
         qf[s] = __builtin_bit_cast(bf16x8_t, load16(qrow + 32 * s + 8 * g));
+    if (c_lo < c_hi)
+        issue_gather(select(v0, v1, c_lo >= n0), dummy, wave, lane, id_cur, raw[c_lo & 1], mask_lds[c_lo & 1]);
 
     f32x4_t acc[32];
 #pragma unroll
@@ -384,15 +377,15 @@ __device__ __forceinline__ void run_segment(const MlaArgs& a, uint8_t (&raw)[2][
         // across the MFMA loops, which need every register.
         int ln = lane;
         asm volatile("" : "+v"(ln));
-        __builtin_amdgcn_s_waitcnt(0);  // this wave's gathers of chunk c (and chunk c+1's indices)
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's gathers of chunk c (and chunk c+1's index)
         __syncthreads();                // everyone's gathers landed; K tile no longer read
         dequantize(cur, mask_lds[c & 1], kbuf, wave, ln);
         __syncthreads();
         if (c + 1 < c_hi)
-            issue_gather(select(v0, v1, c + 1 >= n0), first_of(c + 1), dummy, wave, ln, ids_lds[(c + 1) & 1],
-                         raw[(c + 1) & 1], mask_lds[(c + 1) & 1]);
-        if (wave == 0 && c + 2 < c_hi)
-            issue_ids(select(v0, v1, c + 2 >= n0), first_of(c + 2), ln, ids_lds[c & 1]);
+            issue_gather(select(v0, v1, c + 1 >= n0), dummy, wave, ln, id_next, raw[(c + 1) & 1],
+                         mask_lds[(c + 1) & 1]);
+        if (c + 2 < c_hi)
+            id_next = load_id(select(v0, v1, c + 2 >= n0), first_of(c + 2), wave, ln);
 
         // ---- S^T = K q^T for the chunk's two 16-entry tiles
         // K operands read two steps ahead of the MFMAs that consume them
@@ -532,7 +525,7 @@ sparse_mla_decode_kernel(MlaArgs a) {
     const ListView v0 = make_view(a.list[0], true, b, sq);
     const ListView v1 = make_view(a.list[1], a.num_lists > 1, b, sq);
     const int nchunks = (v0.len + kChunk - 1) / kChunk + (v1.len + kChunk - 1) / kChunk;
-    run_segment(a, lds_raw, lds_kbuf, lds_ids, lds_mask, b, sq, hb, 0, nchunks, -1, wave, lane);
+    run_segment(a, lds_raw, lds_kbuf, lds_mask, b, sq, hb, 0, nchunks, -1, wave, lane);
 }
 
 // Chunks a batch row's items have (the same for every query position and
@@ -617,7 +610,7 @@ sparse_mla_decode_split_kernel(MlaArgs a) {
         // addresses from being held (and spilled) across the segment loop
         int ln = lane;
         asm volatile("" : "+v"(ln));
-        run_segment(a, lds_raw, lds_kbuf, lds_ids, lds_mask, b, j / a.head_blocks, j % a.head_blocks, c, c_hi,
+        run_segment(a, lds_raw, lds_kbuf, lds_mask, b, j / a.head_blocks, j % a.head_blocks, c, c_hi,
                     slot, wave, ln);
         pos += c_hi - c;
         c = 0;
