@@ -7,10 +7,11 @@
 // torch oracle does (the Triton kernel keeps them in fp32); this makes codes
 // and scales equal to the oracle's bit for bit.
 //
-// Workgroups of 256 threads own kRowsPerBlock (token, head) rows; each row is
-// one 16-lane DPP row holding four 128-element chunks, one per 16-byte piece k
-// (see fgv_device.h), so a chunk's amax is one 16-lane DPP max.  One extra
-// workgroup zeroes the scales of the padding tokens T..Tpad-1.
+// Workgroups of 256 threads own 16 (token, head) rows: 16 consecutive tokens
+// of one head.  Each row is one 16-lane DPP row holding four 128-element
+// chunks, one per 16-byte piece k (see fgv_device.h), so a chunk's amax is one
+// 16-lane DPP max.  One extra workgroup zeroes the scales of the padding
+// tokens T..Tpad-1.
 #include "fgv_device.h"
 #include "fgv_host.h"
 
@@ -18,9 +19,7 @@ namespace fgv {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kRowsPerPass = kThreads / 16;
-constexpr int kPasses = 1;
-constexpr int kRowsPerBlock = kRowsPerPass * kPasses;
+constexpr int kTokensPerBlock = kThreads / 16;
 
 struct InvRopeArgs {
     const uint16_t* o;
@@ -32,7 +31,6 @@ struct InvRopeArgs {
     int64_t cs_stride, max_pos;
     int64_t fp8_sg, fp8_st;
     int64_t sc_sg, sc_sk;
-    uint32_t num_rows;     // num_tokens * num_heads
     uint32_t num_heads, heads_per_group;
     uint32_t num_tokens, padded_tokens, n_groups;
     uint32_t row_blocks;
@@ -79,106 +77,93 @@ __device__ __forceinline__ float div_by_scale(float x, float s, float y) {
     return __builtin_fmaf(-rn, y, q0);
 }
 
-// Position first (the cos/sin loads depend on it; vmcnt counts in issue
-// order), then the row, then cos/sin.  kOneToken (num_heads a multiple of 16):
-// the block's rows share one token and the position is a scalar load.
-template <bool kOneToken>
-__device__ void row_block(const InvRopeArgs& a, uint32_t rb, int lane16, int row_in_pass) {
-    uint4 v[kPasses][4];
-    float4 cs_c[kPasses], cs_s[kPasses];
-    uint32_t tok[kPasses], head[kPasses];
-    bool valid[kPasses];
-    int64_t praw[kPasses];
+// One workgroup owns kTokensPerBlock consecutive tokens of one head (16-lane
+// DPP row r: token t0 + r), so that the scales of a chunk, token-fastest in
+// the (G, K, Tpad) layout, come out as one contiguous 64-byte run: they are
+// collected in LDS and written by one wave.  Position first (the cos/sin
+// loads depend on it; vmcnt counts in issue order), then the row, then
+// cos/sin.
+__device__ void row_block(const InvRopeArgs& a, uint32_t rb, int lane16, int row_in_block) {
+    __shared__ uint32_t scales_lds[4][kTokensPerBlock];
     const bool rope_lane = lane16 >= 8;
-    const uint32_t row0 = rb * kRowsPerBlock;
-    const int64_t pos_block = kOneToken ? a.positions[row0 / a.num_heads] : 0;
-
-#pragma unroll
-    for (int p = 0; p < kPasses; ++p) {
-        const uint32_t row = row0 + p * kRowsPerPass + row_in_pass;
-        valid[p] = row < a.num_rows;
-        tok[p] = (valid[p] ? row : row0) / a.num_heads;
-        head[p] = (valid[p] ? row : row0) - tok[p] * a.num_heads;
-        praw[p] = kOneToken ? pos_block : a.positions[tok[p]];
-    }
+    const uint32_t head = rb % a.num_heads, t0 = (rb / a.num_heads) * kTokensPerBlock;
+    const uint32_t t = t0 + row_in_block;
+    const bool valid = t < a.num_tokens;
+    const int64_t praw = a.positions[valid ? t : t0];
     __builtin_amdgcn_sched_barrier(0);
+    uint4 v[4];
+    const uint16_t* x_row = a.o + (int64_t)(valid ? t : t0) * a.o_st + (int64_t)head * a.o_sh;
 #pragma unroll
-    for (int p = 0; p < kPasses; ++p) {
-        const uint16_t* x = a.o + (int64_t)tok[p] * a.o_st + (int64_t)head[p] * a.o_sh;
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-            v[p][k] = valid[p] ? load16(x + (lane16 + 16 * k) * 8) : make_uint4(0, 0, 0, 0);
-    }
+    for (int k = 0; k < 4; ++k)
+        v[k] = load16(x_row + (lane16 + 16 * k) * 8);
     __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int p = 0; p < kPasses; ++p) {
-        cs_c[p] = cs_s[p] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (rope_lane) {
-            const int64_t pos = clamp_position(praw[p], a.max_pos);
-            const float* cs = a.cos_sin + pos * a.cs_stride + (lane16 - 8) * 4;
-            cs_c[p] = *reinterpret_cast<const float4*>(cs);
-            cs_s[p] = *reinterpret_cast<const float4*>(cs + kHalfRope);
-        }
+    float4 cs_c = make_float4(0.f, 0.f, 0.f, 0.f), cs_s = cs_c;
+    if (rope_lane) {
+        const int64_t pos = clamp_position(praw, a.max_pos);
+        const float* cs = a.cos_sin + pos * a.cs_stride + (lane16 - 8) * 4;
+        cs_c = *reinterpret_cast<const float4*>(cs);
+        cs_s = *reinterpret_cast<const float4*>(cs + kHalfRope);
     }
 
     const float inv_max = (float)(1.0 / 448.0);
     const uint32_t eps_bits = __float_as_uint(a.eps);
+    const uint32_t g = head / a.heads_per_group;
+    const uint32_t hig = head - g * a.heads_per_group;
+    uint8_t* out = a.fp8 + (int64_t)g * a.fp8_sg + (int64_t)t * a.fp8_st + hig * kHeadDim;
+    uint32_t packed = 0;
+    float my_scale = 0.0f;  // lane k (k < 4) keeps chunk k's fp32 scale
 #pragma unroll
-    for (int p = 0; p < kPasses; ++p) {
-        if (!valid[p])
-            continue;
-        const uint32_t t = tok[p];
-        const uint32_t g = head[p] / a.heads_per_group;
-        const uint32_t hig = head[p] - g * a.heads_per_group;
-        uint8_t* out = a.fp8 + (int64_t)g * a.fp8_sg + (int64_t)t * a.fp8_st + hig * kHeadDim;
-        uint32_t packed = 0;
-        float my_scale = 0.0f;  // lane k (k < 4) keeps chunk k's fp32 scale
+    for (int k = 0; k < 4; ++k) {
+        float x[8];
+        unpack8(v[k], x);
+        if (k == 3 && rope_lane)
+            inv_rope_piece(x, cs_c, cs_s);
+        uint32_t m = 0;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            float x[8];
-            unpack8(v[p][k], x);
-            if (k == 3 && rope_lane)
-                inv_rope_piece(x, cs_c[p], cs_s[p]);
-            uint32_t m = 0;
+        for (int i = 0; i < 8; ++i)
+            m = max(m, __float_as_uint(x[i]) & 0x7fffffffu);
+        m = row16_max(m);
+        m = m > eps_bits ? m : eps_bits;  // max(amax, eps), eps > 0
+        float sc = __uint_as_float(m) * inv_max;
+        uint32_t lo, hi;
+        if (a.tma) {
+            // 2^ceil(log2(max(sc, 1e-10))) from the binary32 fields.
+            uint32_t b = __float_as_uint(sc);
+            b = b > 0x2EDBE6FFu ? b : 0x2EDBE6FFu;  // 1e-10f
+            int e = (int)(b >> 23) - 127 + ((b & 0x7fffffu) ? 1 : 0);
+            packed |= (uint32_t)(e + 127) << (8 * k);
+            const float inv = exp2_neg_int(e);
+            lo = pack_fp8x4(clamp_fp8(x[0] * inv), clamp_fp8(x[1] * inv),
+                            clamp_fp8(x[2] * inv), clamp_fp8(x[3] * inv));
+            hi = pack_fp8x4(clamp_fp8(x[4] * inv), clamp_fp8(x[5] * inv),
+                            clamp_fp8(x[6] * inv), clamp_fp8(x[7] * inv));
+        } else {
+            if (lane16 == k)
+                my_scale = sc;
+            const float y = 1.0f / sc;
+            float qv[8];
 #pragma unroll
             for (int i = 0; i < 8; ++i)
-                m = max(m, __float_as_uint(x[i]) & 0x7fffffffu);
-            m = row16_max(m);
-            m = m > eps_bits ? m : eps_bits;  // max(amax, eps), eps > 0
-            float sc = __uint_as_float(m) * inv_max;
-            uint32_t lo, hi;
-            if (a.tma) {
-                // 2^ceil(log2(max(sc, 1e-10))) from the binary32 fields.
-                uint32_t b = __float_as_uint(sc);
-                b = b > 0x2EDBE6FFu ? b : 0x2EDBE6FFu;  // 1e-10f
-                int e = (int)(b >> 23) - 127 + ((b & 0x7fffffu) ? 1 : 0);
-                packed |= (uint32_t)(e + 127) << (8 * k);
-                const float inv = exp2_neg_int(e);
-                lo = pack_fp8x4(clamp_fp8(x[0] * inv), clamp_fp8(x[1] * inv),
-                                clamp_fp8(x[2] * inv), clamp_fp8(x[3] * inv));
-                hi = pack_fp8x4(clamp_fp8(x[4] * inv), clamp_fp8(x[5] * inv),
-                                clamp_fp8(x[6] * inv), clamp_fp8(x[7] * inv));
-            } else {
-                if (lane16 == k)
-                    my_scale = sc;
-                const float y = 1.0f / sc;
-                float qv[8];
-#pragma unroll
-                for (int i = 0; i < 8; ++i)
-                    qv[i] = clamp_fp8(div_by_scale(x[i], sc, y));
-                lo = pack_fp8x4(qv[0], qv[1], qv[2], qv[3]);
-                hi = pack_fp8x4(qv[4], qv[5], qv[6], qv[7]);
-            }
+                qv[i] = clamp_fp8(div_by_scale(x[i], sc, y));
+            lo = pack_fp8x4(qv[0], qv[1], qv[2], qv[3]);
+            hi = pack_fp8x4(qv[4], qv[5], qv[6], qv[7]);
+        }
+        if (valid)
             store8(out + (lane16 + 16 * k) * 8, lo, hi);
-        }
-        if (a.tma) {
-            if (lane16 == 0)
-                static_cast<int32_t*>(a.scale)[(int64_t)g * a.sc_sg + (int64_t)hig * a.sc_sk + t] =
-                    (int32_t)packed;
-        } else if (lane16 < 4) {
-            static_cast<float*>(a.scale)[(int64_t)g * a.sc_sg +
-                                         (int64_t)(hig * 4 + lane16) * a.sc_sk + t] = my_scale;
-        }
+    }
+    if (a.tma) {
+        if (lane16 == 0)
+            scales_lds[0][row_in_block] = packed;
+    } else if (lane16 < 4) {
+        scales_lds[lane16][row_in_block] = __float_as_uint(my_scale);
+    }
+    __syncthreads();
+    // thread 16 k + r writes chunk k's scale of token t0 + r
+    const int k = threadIdx.x >> 4, r = threadIdx.x & 15;
+    const bool write = t0 + r < a.num_tokens && k < (a.tma ? 1 : 4);
+    if (write) {
+        const int64_t off = (int64_t)g * a.sc_sg + (int64_t)(a.tma ? hig : hig * 4 + k) * a.sc_sk + t0 + r;
+        static_cast<uint32_t*>(a.scale)[off] = scales_lds[k][r];
     }
 }
 
@@ -195,11 +180,10 @@ __device__ void pad_block(const InvRopeArgs& a) {
     }
 }
 
-template <bool kOneToken>
 __global__ void __launch_bounds__(kThreads)
 inv_rope_fp8_quant_kernel(InvRopeArgs a) {
     if (blockIdx.x < a.row_blocks)
-        row_block<kOneToken>(a, blockIdx.x, threadIdx.x & 15, threadIdx.x >> 4);
+        row_block(a, blockIdx.x, threadIdx.x & 15, threadIdx.x >> 4);
     else
         pad_block(a);
 }
@@ -254,21 +238,15 @@ extern "C" int fgv_inv_rope_fp8_quant(
     a.fp8_st = fp8_stride_token;
     a.sc_sg = scale_stride_group;
     a.sc_sk = scale_stride_k;
-    a.num_rows = (uint32_t)rows;
     a.num_heads = (uint32_t)num_heads;
     a.heads_per_group = (uint32_t)heads_per_group;
     a.num_tokens = (uint32_t)num_tokens;
     a.padded_tokens = (uint32_t)padded_tokens;
     a.n_groups = (uint32_t)n_groups;
-    a.row_blocks = (uint32_t)((rows + kRowsPerBlock - 1) / kRowsPerBlock);
+    a.row_blocks = (uint32_t)((num_tokens + kTokensPerBlock - 1) / kTokensPerBlock * num_heads);
     a.eps = eps;
     a.tma = tma_aligned_scales ? 1 : 0;
     const uint32_t grid = a.row_blocks + (padded_tokens > num_tokens ? 1u : 0u);
-    if (num_heads % kRowsPerBlock == 0)
-        hipLaunchKernelGGL(inv_rope_fp8_quant_kernel<true>, dim3(grid), dim3(kThreads), 0,
-                           static_cast<hipStream_t>(stream), a);
-    else
-        hipLaunchKernelGGL(inv_rope_fp8_quant_kernel<false>, dim3(grid), dim3(kThreads), 0,
-                           static_cast<hipStream_t>(stream), a);
+    hipLaunchKernelGGL(inv_rope_fp8_quant_kernel, dim3(grid), dim3(kThreads), 0, static_cast<hipStream_t>(stream), a);
     return launch_status();
 }
