@@ -30,7 +30,10 @@ constexpr int kDppQuadXor1 = 0xB1;   // quad_perm:[1,0,3,2]
 constexpr int kDppQuadXor2 = 0x4E;   // quad_perm:[2,3,0,1]
 constexpr int kDppHalfMirror = 0x141;  // lane i <-> 7-i inside each 8 lanes
 constexpr int kDppMirror = 0x140;      // lane i <-> 15-i inside each 16 lanes
+// row_ror:n rotates right inside each 16 lanes: lane i reads lane (i - n) mod 16
+constexpr int kDppRowRor4 = 0x124;     // lane i reads lane (i+12) mod 16
 constexpr int kDppRowRor8 = 0x128;     // lane i reads lane (i+8) mod 16
+constexpr int kDppRowRor12 = 0x12C;    // lane i reads lane (i+4) mod 16
 
 template <int CTRL>
 __device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {

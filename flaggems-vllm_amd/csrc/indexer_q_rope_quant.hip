@@ -154,8 +154,13 @@ __device__ __forceinline__ void indexer_row(const IndexerArgs& a, uint32_t t, ui
             y[i] = xf[p][i] * inv;
         const uint32_t nib = pack_fp4x8(y);
         *reinterpret_cast<uint32_t*>(qo + (lane16 + 16 * p) * 4) = nib;
-        if ((lane16 & 3) == 0)
-            so[(lane16 + 16 * p) >> 2] = (uint8_t)(k + 127);
+        // the piece's four block exponents (lanes 0, 4, 8, 12) leave as one
+        // 32-bit word from lane 0 instead of four byte stores
+        const uint32_t e = (uint32_t)(k + 127) & 0xffu;
+        const uint32_t word = e | dpp_u32<kDppRowRor12>(e) << 8 | dpp_u32<kDppRowRor8>(e) << 16 |
+                              dpp_u32<kDppRowRor4>(e) << 24;
+        if (lane16 == 0)
+            *reinterpret_cast<uint32_t*>(so + 4 * p) = word;
     }
     if (lane16 == 0) {
         float w = w_in * a.softmax_scale;
@@ -210,7 +215,10 @@ indexer_q_rope_quant_kernel(IndexerArgs a) {
 #pragma unroll
     for (int rr = 0; rr < kRows; ++rr) {
         c[rr] = s[rr] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (rope_lane) {
+        if (kOneToken && rr > 0) {  // one token: the first row's cos/sin serve every row
+            c[rr] = c[0];
+            s[rr] = s[0];
+        } else if (rope_lane) {
             const int64_t pos = clamp_position(praw[rr], a.max_pos);
             const int64_t off = pos * a.cs_stride + (lane16 - 8) * 4;
             c[rr] = load_cs4(a.cos_sin, off, kCsBf16);
@@ -277,6 +285,8 @@ extern "C" int fgv_fused_indexer_q_rope_quant(
     if (use_fp4) {
         if (!aligned(q_out, 4) || q_out_stride_token % 4 || q_out_stride_head % 4)
             return fail(FGV_E_MISALIGNED, "packed MXFP4 output must be 4-byte aligned");
+        if (!aligned(scale_out, 4) || scale_out_stride_token % 4 || scale_out_stride_head % 4)
+            return fail(FGV_E_MISALIGNED, "MXFP4 scales must be 4-byte aligned, strides multiples of 4");
     } else if (!aligned(q_out, 8) || q_out_stride_token % 8 || q_out_stride_head % 8) {
         return fail(FGV_E_MISALIGNED, "FP8 output must be 8-byte aligned, strides multiple of 8");
     }

@@ -168,7 +168,8 @@ int fgv_fused_q_kv_rmsnorm(
  *                k = ceil(log2(max(amax, 1e-4) / 448));
  *                weights_out = ((w * 2^k) * softmax_scale) * head_scale.
  *   use_fp4 != 0: q_out = packed E2M1 nibbles [.., head_dim/2] (even element
- *                in the low nibble), scale_out = UE8M0 byte per 32 elements,
+ *                in the low nibble), scale_out = UE8M0 byte per 32 elements
+ *                (4-byte aligned, strides multiples of 4),
  *                k = ceil(log2(max(amax, 6*2^-126) / 6));
  *                weights_out = (w * softmax_scale) * head_scale.
  */
