@@ -447,18 +447,21 @@ __device__ __forceinline__ void run_segment(const MlaArgs& a, uint8_t (&raw)[2][
         // ---- O^T = alpha * O^T + V^T P^T over the 32 16-dim tiles: the
         // transposing read hands lane j of group g dim 16dt+j of rows
         // 4g..4g+3 (then 16+4g..16+4g+3), the A operand of k = 8g..8g+7.
-        uint2 vlo[3], vhi[3];
+        // (four steps ahead: one MFMA per step covers less LDS latency than
+        // the two per step of the QK loop)
+        uint2 vlo[5], vhi[5];
         auto read_v = [&](int dt, uint2& x, uint2& y) {
             x = read_tr(kbuf, tr_base + 32 * dt);
             y = read_tr(kbuf, tr_base + 32 * dt + 16 * kKRowBytes);
         };
-        read_v(0, vlo[0], vhi[0]);
-        read_v(1, vlo[1], vhi[1]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            read_v(i, vlo[i], vhi[i]);
 #pragma unroll
         for (int dt = 0; dt < 32; ++dt) {
-            if (dt + 2 < 32)
-                read_v(dt + 2, vlo[(dt + 2) % 3], vhi[(dt + 2) % 3]);
-            const uint2 lo = vlo[dt % 3], hi = vhi[dt % 3];
+            if (dt + 4 < 32)
+                read_v(dt + 4, vlo[(dt + 4) % 5], vhi[(dt + 4) % 5]);
+            const uint2 lo = vlo[dt % 5], hi = vhi[dt % 5];
             const bf16x8_t av = __builtin_bit_cast(bf16x8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
             acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pb, acc[dt], 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
