@@ -22,6 +22,8 @@ from .ops import (  # noqa: F401
     get_mla_metadata,
 )
 
+from . import library  # noqa: F401,E402  (torch.ops.flaggems_vllm.* registrations)
+
 device = "cuda"
 vendor_name = "amd"
 __version__ = "0.1.0"

@@ -1,0 +1,148 @@
+"""torch.library registrations of the path's ops (``torch.ops.flaggems_vllm.*``).
+
+The public API stays the plain Python functions the reference package exports
+(src/flaggems_vllm/__init__.py:21-46); vllm-plugin-fl calls those directly.
+These registrations expose the same ops to torch.compile and graph capture as
+opaque custom ops: the schemas declare what each op writes, namely ``q`` and
+``k_cache`` for the main op (alias-annotated ``Tensor(a0!) q``, ``Tensor(a2!) k_cache``), ``out``
+for the gather and ``slot_mapping`` for the slot mapping.  The fake (meta)
+implementations give the output shapes and strides the real ops return.
+Each registered op calls the same wrapper, so argument checks and errors are
+the wrapper's.
+
+``fused_indexer_q_rope_quant`` returns ``(q, q_scale, weights)`` here, with an
+empty ``q_scale`` for FP8, because an op schema cannot return the nested tuple
+the Python function returns for MXFP4.  ``flash_mla_with_kvcache`` takes a
+scheduler-metadata object and is not registered.
+"""
+from typing import List, Optional, Tuple
+
+import torch
+
+from .ops import (
+    compute_slot_mapping_parallel,
+    dequantize_and_gather_k_cache,
+    fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert,
+    fused_indexer_q_rope_quant,
+    fused_inv_rope_fp8_quant,
+    fused_q_kv_rmsnorm,
+)
+
+NAMESPACE = "flaggems_vllm"
+
+
+def _op(name: str, mutates: Tuple[str, ...] = ()):
+    return torch.library.custom_op(f"{NAMESPACE}::{name}", mutates_args=mutates, device_types="cuda")
+
+
+@_op("fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert", ("q", "k_cache"))
+def _qnorm_rope_kv_insert(q: torch.Tensor, kv: torch.Tensor, k_cache: torch.Tensor, slot_mapping: torch.Tensor,
+                          position_ids: torch.Tensor, cos_sin_cache: torch.Tensor, eps: float,
+                          cache_block_size: int) -> None:
+    fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert(q, kv, k_cache, slot_mapping, position_ids, cos_sin_cache,
+                                                      eps, cache_block_size)
+
+
+@_qnorm_rope_kv_insert.register_fake
+def _(q, kv, k_cache, slot_mapping, position_ids, cos_sin_cache, eps, cache_block_size):
+    return None
+
+
+@_op("fused_inv_rope_fp8_quant")
+def _inv_rope_fp8_quant(o: torch.Tensor, positions: torch.Tensor, cos_sin_cache: torch.Tensor, n_groups: int,
+                        heads_per_group: int, nope_dim: int = 448, rope_dim: int = 64,
+                        quant_group_size: int = 128, eps: float = 1e-10,
+                        tma_aligned_scales: bool = False) -> Tuple[torch.Tensor, torch.Tensor]:
+    return fused_inv_rope_fp8_quant(o, positions, cos_sin_cache, n_groups, heads_per_group, nope_dim, rope_dim,
+                                    quant_group_size, eps, None, tma_aligned_scales)
+
+
+@_inv_rope_fp8_quant.register_fake
+def _(o, positions, cos_sin_cache, n_groups, heads_per_group, nope_dim=448, rope_dim=64, quant_group_size=128,
+      eps=1e-10, tma_aligned_scales=False):
+    # the real op's layout: fp8 (G, T, d) and scales (G, K, Tpad), both
+    # returned transposed to token-major views
+    t = o.shape[0]
+    d = heads_per_group * o.shape[-1]
+    blocks = d // quant_group_size
+    tpad = (t + 3) // 4 * 4
+    inner = (blocks + 3) // 4 if tma_aligned_scales else blocks
+    fp8 = o.new_empty((n_groups, t, d), dtype=torch.float8_e4m3fn).transpose(0, 1)
+    scale = o.new_empty(n_groups * inner * tpad, dtype=torch.int32 if tma_aligned_scales else torch.float32)
+    scale = scale.as_strided((n_groups, t, inner), (inner * tpad, 1, tpad)).transpose(0, 1)
+    return fp8, scale
+
+
+@_op("fused_q_kv_rmsnorm")
+def _q_kv_rmsnorm(qr: torch.Tensor, kv: torch.Tensor, q_weight: torch.Tensor, kv_weight: torch.Tensor,
+                  eps: float) -> Tuple[torch.Tensor, torch.Tensor]:
+    return fused_q_kv_rmsnorm(qr, kv, q_weight, kv_weight, eps)
+
+
+@_q_kv_rmsnorm.register_fake
+def _(qr, kv, q_weight, kv_weight, eps):
+    return torch.empty_like(qr), torch.empty_like(kv)
+
+
+@_op("dequantize_and_gather_k_cache", ("out",))
+def _dequantize_and_gather(out: torch.Tensor, k_cache: torch.Tensor, seq_lens: torch.Tensor,
+                           gather_lens: Optional[torch.Tensor], block_table: torch.Tensor, block_size: int,
+                           offset: int = 0, rope_dim: int = 64, nope_dim: Optional[int] = None,
+                           scale_slots: Optional[int] = None) -> None:
+    dequantize_and_gather_k_cache(out, k_cache, seq_lens, gather_lens, block_table, block_size, offset, rope_dim,
+                                  nope_dim, scale_slots)
+
+
+@_dequantize_and_gather.register_fake
+def _(out, k_cache, seq_lens, gather_lens, block_table, block_size, offset=0, rope_dim=64, nope_dim=None,
+      scale_slots=None):
+    return None
+
+
+@_op("fused_indexer_q_rope_quant")
+def _indexer_q_rope_quant(positions: torch.Tensor, index_q: torch.Tensor, index_q_cos_sin_cache: torch.Tensor,
+                          index_weights: torch.Tensor, index_weights_softmax_scale: float,
+                          index_weights_head_scale: float,
+                          use_fp4: bool = False) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    q, w = fused_indexer_q_rope_quant(positions, index_q, index_q_cos_sin_cache, index_weights,
+                                      index_weights_softmax_scale, index_weights_head_scale, use_fp4=use_fp4)
+    if use_fp4:
+        return q[0], q[1], w
+    return q, q.new_empty((0,), dtype=torch.uint8), w
+
+
+@_indexer_q_rope_quant.register_fake
+def _(positions, index_q, index_q_cos_sin_cache, index_weights, index_weights_softmax_scale,
+      index_weights_head_scale, use_fp4=False):
+    t, h, d = positions.shape[0], index_q.shape[1], index_q.shape[2]
+    w = index_weights.new_empty((t, h), dtype=torch.float32)
+    if use_fp4:
+        return (index_q.new_empty((t, h, d // 2), dtype=torch.uint8),
+                index_q.new_empty((t, h, d // 32), dtype=torch.uint8), w)
+    return index_q.new_empty((t, h, d), dtype=torch.float8_e4m3fn), index_q.new_empty((0,), dtype=torch.uint8), w
+
+
+@_op("compute_slot_mapping_parallel", ("slot_mapping",))
+def _slot_mapping(num_tokens: int, max_num_tokens: int, query_start_loc: torch.Tensor, num_reqs: int,
+                  positions: torch.Tensor, block_table: torch.Tensor, slot_mapping: torch.Tensor, block_size: int,
+                  cp_world_size: int = 1, cp_rank: int = 0, cp_kv_cache_interleave_size: int = 1,
+                  pad_id: int = -1) -> None:
+    compute_slot_mapping_parallel(num_tokens, max_num_tokens, query_start_loc, num_reqs, positions, block_table,
+                                  slot_mapping, block_size, cp_world_size, cp_rank, cp_kv_cache_interleave_size,
+                                  pad_id)
+
+
+@_slot_mapping.register_fake
+def _(num_tokens, max_num_tokens, query_start_loc, num_reqs, positions, block_table, slot_mapping, block_size,
+      cp_world_size=1, cp_rank=0, cp_kv_cache_interleave_size=1, pad_id=-1):
+    return None
+
+
+REGISTERED: List[str] = [
+    "fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert",
+    "fused_inv_rope_fp8_quant",
+    "fused_q_kv_rmsnorm",
+    "dequantize_and_gather_k_cache",
+    "fused_indexer_q_rope_quant",
+    "compute_slot_mapping_parallel",
+]

@@ -1,0 +1,156 @@
+"""torch.ops.flaggems_vllm registrations: schemas, fake shapes, and identity
+with the plain functions on the GPU.
+
+The plain Python functions are the reference API; these tests check that the
+registered custom ops declare exactly the tensors each op writes (the main op
+writes q and k_cache, as vLLM's op schema marks them) and that they compute
+the same bytes as the functions they wrap.
+"""
+import pytest
+import torch
+
+import flaggems_vllm
+from flaggems_vllm import library
+from flaggems_vllm import testing as W
+
+from .test_gather import _ref_fixture
+from .test_indexer import _case as _indexer_case
+from .test_rmsnorm import _inputs as _rmsnorm_inputs
+from .test_slot_mapping import _ragged_inputs
+
+DEV = torch.device("cuda:0")
+
+WRITES = {
+    "fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert": {"q", "k_cache"},
+    "fused_inv_rope_fp8_quant": set(),
+    "fused_q_kv_rmsnorm": set(),
+    "dequantize_and_gather_k_cache": {"out"},
+    "fused_indexer_q_rope_quant": set(),
+    "compute_slot_mapping_parallel": {"slot_mapping"},
+}
+
+
+def _op(name):
+    return getattr(torch.ops.flaggems_vllm, name).default
+
+
+# ------------------------------------------------------------------- CPU ----
+
+@pytest.mark.parametrize("name", library.REGISTERED)
+def test_schema_declares_exactly_the_written_tensors(name):
+    schema = _op(name)._schema
+    written = {a.name for a in schema.arguments if a.alias_info is not None and a.alias_info.is_write}
+    assert written == WRITES[name]
+    # the main op keeps the reference's positional order
+    if name == "fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert":
+        assert [a.name for a in schema.arguments] == ["q", "kv", "k_cache", "slot_mapping", "position_ids",
+                                                       "cos_sin_cache", "eps", "cache_block_size"]
+        assert len(schema.returns) == 0
+
+
+@pytest.mark.parametrize("tma", [False, True])
+@pytest.mark.parametrize("T", [1, 6, 8])
+def test_sibling_fake_layout(T, tma):
+    """Shapes, dtypes and strides of the fake outputs: fp8 [T, G, d] with
+    strides (d, T*d, 1); scales [T, G, K] token-fastest with Tpad = T rounded up to 4."""
+    H, G = 16, 4
+    o = torch.empty(T, H, 512, dtype=torch.bfloat16, device="meta")
+    pos = torch.empty(T, dtype=torch.int64, device="meta")
+    cs = torch.empty(4096, 64, dtype=torch.float32, device="meta")
+    fp8, scale = _op("fused_inv_rope_fp8_quant")(o, pos, cs, G, H // G, tma_aligned_scales=tma)
+    d = (H // G) * 512
+    tpad = (T + 3) // 4 * 4
+    k = d // 128
+    inner = (k + 3) // 4 if tma else k
+    assert fp8.shape == (T, G, d) and fp8.dtype == torch.float8_e4m3fn and fp8.stride() == (d, T * d, 1)
+    assert scale.shape == (T, G, inner) and scale.stride() == (1, inner * tpad, tpad)
+    assert scale.dtype == (torch.int32 if tma else torch.float32)
+
+
+@pytest.mark.parametrize("fp4", [False, True])
+def test_indexer_fake_layout(fp4):
+    pos = torch.empty(5, dtype=torch.int64, device="meta")
+    q = torch.empty(5, 8, 128, dtype=torch.bfloat16, device="meta")
+    cs = torch.empty(64, 64, dtype=torch.float32, device="meta")
+    w = torch.empty(5, 8, dtype=torch.bfloat16, device="meta")
+    qo, sc, wo = _op("fused_indexer_q_rope_quant")(pos, q, cs, w, 0.1, 0.2, fp4)
+    assert wo.shape == (5, 8) and wo.dtype == torch.float32
+    if fp4:
+        assert qo.shape == (5, 8, 64) and qo.dtype == torch.uint8 and sc.shape == (5, 8, 4)
+    else:
+        assert qo.shape == (5, 8, 128) and qo.dtype == torch.float8_e4m3fn and sc.numel() == 0
+
+
+# ------------------------------------------------------------------- GPU ----
+
+def _say(msg):
+    print(f"\n[case] {msg}", flush=True)
+
+
+@pytest.mark.gpu
+def test_gpu_main_op_matches_function_and_opcheck():
+    _say("torch.ops main op, config 0")
+    w = W.make_workload(0).to(DEV)
+    a, b = w.clone(), w.clone()
+    flaggems_vllm.fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert(*a.args())
+    _op("fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert")(*b.args())
+    torch.cuda.synchronize()
+    assert torch.equal(a.q.view(torch.int16), b.q.view(torch.int16))
+    assert torch.equal(a.k_cache, b.k_cache)
+    c = w.clone()
+    torch.library.opcheck(_op("fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert"), tuple(c.args()),
+                          test_utils=("test_schema", "test_faketensor"))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("tma", [False, True])
+def test_gpu_sibling_matches_function_and_fake_layout(tma):
+    _say(f"torch.ops sibling tma={tma}")
+    w = W.make_inv_rope_workload(37, 16, 4, seed=3).to(DEV)
+    args = (w.o, w.positions, w.cos_sin_cache, w.n_groups, w.heads_per_group)
+    f8, fs = flaggems_vllm.fused_inv_rope_fp8_quant(*args, tma_aligned_scales=tma)
+    o8, os_ = _op("fused_inv_rope_fp8_quant")(*args, tma_aligned_scales=tma)
+    torch.cuda.synchronize()
+    assert o8.stride() == f8.stride() and os_.stride() == fs.stride()
+    assert torch.equal(o8.view(torch.uint8), f8.view(torch.uint8))
+    assert torch.equal(os_.view(torch.int32), fs.view(torch.int32))
+    torch.library.opcheck(_op("fused_inv_rope_fp8_quant"), args, {"tma_aligned_scales": tma},
+                          test_utils=("test_schema", "test_faketensor"))
+
+
+@pytest.mark.gpu
+def test_gpu_rmsnorm_indexer_gather_slot_match_functions():
+    _say("torch.ops rmsnorm / indexer / gather / slot mapping")
+    qr, kv, qw, kw = (t.to(DEV) for t in _rmsnorm_inputs(9, 1536, 512, 4))
+    a = flaggems_vllm.fused_q_kv_rmsnorm(qr, kv, qw, kw, 1e-6)
+    b = _op("fused_q_kv_rmsnorm")(qr, kv, qw, kw, 1e-6)
+    assert all(torch.equal(x.view(torch.int16), y.view(torch.int16)) for x, y in zip(a, b))
+
+    pos, q, cs, wt, sm, hs = _indexer_case(11, seed=5)
+    pos, q, cs, wt = pos.to(DEV), q.to(DEV), cs.to(DEV), wt.to(DEV)
+    for fp4 in (False, True):
+        fq, fw = flaggems_vllm.fused_indexer_q_rope_quant(pos, q, cs, wt, sm, hs, use_fp4=fp4)
+        oq, osc, ow = _op("fused_indexer_q_rope_quant")(pos, q, cs, wt, sm, hs, fp4)
+        assert torch.equal(fw, ow)
+        if fp4:
+            assert torch.equal(fq[0], oq) and torch.equal(fq[1], osc)
+        else:
+            assert torch.equal(fq.view(torch.uint8), oq.view(torch.uint8)) and osc.numel() == 0
+
+    cache, expected, seq_lens, gather_lens, bt, slots = _ref_fixture(2, 12, 5, 64, 448, 64)
+    out_f = torch.zeros_like(expected, device=DEV)
+    out_o = torch.zeros_like(expected, device=DEV)
+    gargs = (cache.to(DEV), seq_lens.to(DEV), gather_lens.to(DEV), bt.to(DEV), 64)
+    flaggems_vllm.dequantize_and_gather_k_cache(out_f, *gargs)
+    _op("dequantize_and_gather_k_cache")(out_o, *gargs)
+    assert torch.equal(out_f.cpu(), expected) and torch.equal(out_o.cpu(), expected)
+
+    qsl, p, table = _ragged_inputs(2)
+    n = int(qsl[-1])
+    sl_f = torch.full((n + 5,), -7, dtype=torch.int64, device=DEV)
+    sl_o = sl_f.clone()
+    sargs = (n, n + 5, qsl.to(DEV), qsl.numel() - 1, p.to(DEV), table.to(DEV))
+    flaggems_vllm.compute_slot_mapping_parallel(*sargs, sl_f, 16)
+    _op("compute_slot_mapping_parallel")(*sargs, sl_o, 16)
+    torch.cuda.synchronize()
+    assert torch.equal(sl_f, sl_o)
