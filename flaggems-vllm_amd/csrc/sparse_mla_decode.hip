@@ -628,12 +628,17 @@ sparse_mla_decode_split_kernel(MlaArgs a) {
 }
 
 // Merges the partial slots of every item that crosses a split range
-// boundary, and writes the items that attend nothing.  One workgroup per
-// item; wave w merges head rows w, w+4, ..., lane l dims 8l..8l+7, so every
-// read of a 2 KiB partial row and every 1 KiB output row is contiguous.
+// boundary, and writes the items that attend nothing.  Four workgroups per
+// item, one per quarter of its 64 heads; wave w of a workgroup merges 4 head
+// rows, lane l dims 8l..8l+7 of each, so every read of a 2 KiB partial row and
+// every 1 KiB output row is contiguous.  Each slot's reads for the wave's four
+// heads (reference maxima and sums, then the rows) are issued together and
+// unconditionally: a slot whose segment attended nothing holds zero rows and
+// a zero sum, and takes weight 0.
 __global__ void __launch_bounds__(kThreads)
 sparse_mla_combine_kernel(MlaArgs a) {
-    const int item = blockIdx.x;
+    constexpr int kHeadsPerWave = kBlockHeads / 4 / (kThreads / 64);
+    const int item = blockIdx.x >> 2, quarter = blockIdx.x & 3;
     const int R = a.seq_q * a.head_blocks, G = a.split_grid;
     const int b = item / R, jr = item % R;
     const int sq = jr / a.head_blocks, hb = jr % a.head_blocks;
@@ -653,39 +658,63 @@ sparse_mla_combine_kernel(MlaArgs a) {
         return a.partials + (int64_t)(k == k_lo ? 2 * k + 1 : 2 * k) * kSlotFloats;
     };
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    for (int h = wave; h < kBlockHeads; h += kThreads / 64) {
-        float M = -INFINITY;
-        for (int k = k_lo; k <= k_hi; ++k)
-            if (start_of(k) != start_of(k + 1))  // skip empty ranges
-                M = fmaxf(M, slot_of(k)[kBlockHeads * kHeadDim + h]);
-        const float M_use = M == -INFINITY ? 0.f : M;
-        f32x4_t o0 = {0.f, 0.f, 0.f, 0.f}, o1 = {0.f, 0.f, 0.f, 0.f};
-        float L = 0.f;
-        for (int k = k_lo; k <= k_hi; ++k) {
-            if (start_of(k) == start_of(k + 1))
-                continue;
-            const float* ws = slot_of(k);
-            const float l = ws[kBlockHeads * kHeadDim + kBlockHeads + h];
-            if (!(l > 0.f))
-                continue;
-            const float w = __builtin_amdgcn_exp2f(ws[kBlockHeads * kHeadDim + h] - M_use);
-            L += l * w;
-            const f32x4_t* row = reinterpret_cast<const f32x4_t*>(ws + h * kHeadDim + 8 * lane);
-            o0 += row[0] * w;
-            o1 += row[1] * w;
+    const int h0 = quarter * (kBlockHeads / 4) + wave * kHeadsPerWave;
+
+    float M[kHeadsPerWave];
+#pragma unroll
+    for (int i = 0; i < kHeadsPerWave; ++i)
+        M[i] = -INFINITY;
+    for (int k = k_lo; k <= k_hi; ++k) {
+        if (start_of(k) == start_of(k + 1))  // skip empty ranges
+            continue;
+        const float* mk = slot_of(k) + kBlockHeads * kHeadDim + h0;
+#pragma unroll
+        for (int i = 0; i < kHeadsPerWave; ++i)
+            M[i] = fmaxf(M[i], mk[i]);
+    }
+    float M_use[kHeadsPerWave], L[kHeadsPerWave];
+    f32x4_t o[kHeadsPerWave][2];
+#pragma unroll
+    for (int i = 0; i < kHeadsPerWave; ++i) {
+        M_use[i] = M[i] == -INFINITY ? 0.f : M[i];
+        L[i] = 0.f;
+        o[i][0] = o[i][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
+    for (int k = k_lo; k <= k_hi; ++k) {
+        if (start_of(k) == start_of(k + 1))
+            continue;
+        const float* ws = slot_of(k);
+        float m[kHeadsPerWave], l[kHeadsPerWave];
+        f32x4_t r0[kHeadsPerWave], r1[kHeadsPerWave];
+#pragma unroll
+        for (int i = 0; i < kHeadsPerWave; ++i) {
+            m[i] = ws[kBlockHeads * kHeadDim + h0 + i];
+            l[i] = ws[kBlockHeads * kHeadDim + kBlockHeads + h0 + i];
+            const f32x4_t* row = reinterpret_cast<const f32x4_t*>(ws + (h0 + i) * kHeadDim + 8 * lane);
+            r0[i] = row[0];
+            r1[i] = row[1];
         }
-        const int head = hb * kBlockHeads + h;
-        const bool any = L > 0.f;
+#pragma unroll
+        for (int i = 0; i < kHeadsPerWave; ++i) {
+            const float w = l[i] > 0.f ? __builtin_amdgcn_exp2f(m[i] - M_use[i]) : 0.f;
+            L[i] += l[i] * w;
+            o[i][0] += r0[i] * w;
+            o[i][1] += r1[i] * w;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < kHeadsPerWave; ++i) {
+        const int head = hb * kBlockHeads + h0 + i;
+        const bool any = L[i] > 0.f;
         float factor = 0.f;
         if (any)
-            factor = a.sink ? 1.f / (L + expf(a.sink[head] - M_use * kLn2)) : 1.f / L;
-        o0 *= factor;
-        o1 *= factor;
+            factor = a.sink ? 1.f / (L[i] + expf(a.sink[head] - M_use[i] * kLn2)) : 1.f / L[i];
+        const f32x4_t v0 = o[i][0] * factor, v1 = o[i][1] * factor;
         store16(a.out + b * a.o_sb + sq * a.o_ss + head * a.o_sh + 8 * lane,
-                make_uint4(pack_bf16x2(o0[0], o0[1]), pack_bf16x2(o0[2], o0[3]), pack_bf16x2(o1[0], o1[1]),
-                           pack_bf16x2(o1[2], o1[3])));
+                make_uint4(pack_bf16x2(v0[0], v0[1]), pack_bf16x2(v0[2], v0[3]), pack_bf16x2(v1[0], v1[1]),
+                           pack_bf16x2(v1[2], v1[3])));
         if (lane == 0)
-            a.lse[b * a.l_sb + head * a.l_sh + sq] = any ? M_use * kLn2 + logf(L) : INFINITY;
+            a.lse[b * a.l_sb + head * a.l_sh + sq] = any ? M_use[i] * kLn2 + logf(L[i]) : INFINITY;
     }
 }
 
@@ -828,7 +857,8 @@ extern "C" int fgv_sparse_mla_decode_model1(
     const int64_t items = batch * seq_q * a.head_blocks;
     hipStream_t st = static_cast<hipStream_t>(stream);
     const int64_t need = split_bytes(batch, topk, extra_k_cache ? extra_topk : 0);
-    if (need > 0 && workspace && workspace_bytes >= need) {
+    // (the combine kernel runs four workgroups per item)
+    if (need > 0 && workspace && workspace_bytes >= need && 4 * items <= 0x7fffffffLL) {
         if (!aligned(workspace, 256))
             return fail(FGV_E_MISALIGNED, "workspace must be 256-byte aligned");
         a.split_grid = split_grid();
@@ -839,7 +869,7 @@ extern "C" int fgv_sparse_mla_decode_model1(
         rc = launch_status();
         if (rc)
             return rc;
-        hipLaunchKernelGGL(sparse_mla_combine_kernel, dim3((unsigned)items), dim3(kThreads), 0, st, a);
+        hipLaunchKernelGGL(sparse_mla_combine_kernel, dim3((unsigned)(4 * items)), dim3(kThreads), 0, st, a);
         return launch_status();
     }
     hipLaunchKernelGGL(sparse_mla_decode_kernel, dim3((unsigned)items), dim3(kThreads), 0, st, a);
