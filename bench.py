@@ -188,6 +188,19 @@ def cpu_baseline_mla(w, sample_rows, seconds):
                       f"median of {reps} runs, {t:.3f} s per run"}
 
 
+def cpu_baseline_port(run, units, unit, sample, seconds):
+    """Median wall time of a torch CPU restatement (oracle.torch_ref) run on a
+    bounded sample; `units` of the metric per run."""
+    import torch
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    t, reps = _repeat(run, seconds)
+    return {"value": units / t, "unit": unit, "cores": cores, "kind": "port",
+            "sample": f"{sample}: torch CPU restatement (oracle/torch_ref.py), median of {reps} runs, "
+                      f"{t:.3f} s per run"}
+
+
 def main():
     args = parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -203,6 +216,9 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    from oracle import torch_ref
+
+    cpu_case = None  # (run, units per run, unit, sample) for ops timed by cpu_baseline_port
 
     if args.op == "main":
         w_cpu = W.make_workload(args.config)
@@ -242,7 +258,12 @@ def main():
         config = {"workload": f"dequantize_and_gather_k_cache: all positions of c{args.config}'s "
                               f"{bt.shape[0]} sequences ({T} rows) from its 584 B/token FP8 cache",
                   "rows": T, "num_reqs": int(bt.shape[0])}
-        args.no_cpu_baseline = True
+        cache_cpu = w.k_cache.cpu()
+        n0 = int(m["seq_lens"][0])
+        out_cpu = torch.empty(1, n0, 512, dtype=torch.bfloat16)
+        cpu_case = (lambda: torch_ref.dequantize_and_gather_k_cache(
+                        out_cpu, cache_cpu, m["seq_lens"][:1], None, m["block_table"][:1], w.block_size),
+                    n0, "tokens/s", f"the first of {bt.shape[0]} sequences ({n0} rows)")
     elif args.op == "rmsnorm":
         # DeepSeek-V4 q LoRA rank 1536 and kv latent 512 for c2's 8192 tokens
         g = torch.Generator().manual_seed(0)
@@ -259,7 +280,10 @@ def main():
         kernel, workload = "fused_q_kv_rmsnorm_kernel", "T8192_q1536_kv512"
         config = {"workload": "fused_q_kv_rmsnorm T=8192, q 1536, kv 512, bf16 weights",
                   "num_tokens": T}
-        args.no_cpu_baseline = True
+        nc = min(args.cpu_sample_tokens, T)
+        cq, ck, cqw, ckw = qr[:nc].cpu(), kvr[:nc].cpu(), qw.cpu(), kw.cpu()
+        cpu_case = (lambda: torch_ref.fused_q_kv_rmsnorm(cq, ck, cqw, ckw, 1e-6), nc, "tokens/s",
+                    f"first {nc} of {T} tokens")
     elif args.op == "indexer":
         # DeepSeek-V4 sparse indexer: 64 index heads of 128 dims for c2's 8192 tokens
         g = torch.Generator().manual_seed(0)
@@ -278,7 +302,11 @@ def main():
         workload = "T8192_H64_D128" + ("_mxfp4" if args.fp4 else "_fp8")
         config = {"workload": f"fused_indexer_q_rope_quant T=8192, H=64, D=128, "
                               f"{'MXFP4' if args.fp4 else 'FP8'}", "num_tokens": T}
-        args.no_cpu_baseline = True
+        nc = min(args.cpu_sample_tokens, 1024, T)  # ~1 s per run on 8 cores
+        cpos, ciq, ccs, ciw = pos[:nc].cpu(), iq[:nc].cpu(), cs.cpu(), iw[:nc].cpu()
+        cpu_case = (lambda: torch_ref.fused_indexer_q_rope_quant(cpos, ciq, ccs, ciw, 128 ** -0.5, H ** -0.5,
+                                                                 use_fp4=args.fp4),
+                    nc, "tokens/s", f"first {nc} of {T} tokens, all {H} heads")
     elif args.op == "slot_mapping":
         # slots of c4's ragged batch (64 requests) from its block tables
         w_cpu = W.make_workload(4 if args.config == 2 else args.config)
@@ -298,7 +326,11 @@ def main():
         kernel, workload = "slot_mapping_kernel", f"{w_cpu.name}"
         config = {"workload": f"compute_slot_mapping_parallel over {w_cpu.name}: {T} tokens, "
                               f"{qsl.numel() - 1} requests", "num_tokens": T}
-        args.no_cpu_baseline = True
+        nreq = min(8, qsl.numel() - 1)
+        ns = int(qsl[nreq])
+        cpu_case = (lambda: torch_ref.slot_mapping(ns, qsl[:nreq + 1], w_cpu.position_ids, m["block_table"], 64),
+                    ns, "tokens/s", f"the first {nreq} of {qsl.numel() - 1} requests ({ns} tokens; "
+                                    f"the reference test's per-request loop)")
     elif args.op == "mla":
         # the reference benchmark's MODEL1 sparse decode (batch 512, 64 heads, top-k 128)
         w_cpu = W.make_mla_case(args.mla_case)
@@ -378,7 +410,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16" if args.op == "mla" else "f32",
+        "dtype": {"mla": "bf16", "slot_mapping": "int64", "copy": "u8"}.get(args.op, "f32"),
         "data": ("synthetic: seeded q ~ N(0,1)/10 bf16, cache NoPE ~ N(0,0.1) quantised to e4m3 + "
                  "E8M0 per 64, RoPE ~ N(0,0.1) bf16, uniform indices and top-k lengths, sink ~ N(0,1)"
                  if args.op == "mla" else
@@ -399,6 +431,8 @@ def main():
                                                        args.cpu_seconds)
         elif args.op == "mla":
             result["cpu_baseline"] = cpu_baseline_mla(w_cpu, 64, args.cpu_seconds)
+        elif cpu_case is not None:
+            result["cpu_baseline"] = cpu_baseline_port(*cpu_case, args.cpu_seconds)
         else:
             result["cpu_baseline"] = cpu_baseline_inv(w_cpu, args.tma, args.cpu_sample_tokens,
                                                       args.cpu_seconds)
