@@ -181,3 +181,50 @@ def test_combined(T, H, bs):
         assert torch.equal(g.k_cache.cpu(), ref.k_cache)
     else:
         _check_ref_case(w)
+
+
+# (T, H, gap units between tokens, 1 KiB units from the 16 KiB boundary below q).
+# These place q so that its rows do not tile 16 KiB-aligned chunks, which the
+# kernel then walks chunk by chunk of address space: gaps smaller and larger
+# than a chunk, q starting mid-chunk, head counts below / not a multiple of 16,
+# one token, and the contiguous-but-misaligned case.
+LAYOUTS = [
+    (37, 64, 1, 0),    # c4: q = buf[:, :H*512] of a [T, H*512 + 512] buffer
+    (37, 64, 1, 3),
+    (50, 7, 0, 5),     # contiguous rows, misaligned start
+    (20, 16, 0, 1),
+    (9, 3, 40, 2),     # gap wider than a chunk: whole chunks hold no q row
+    (1, 64, 0, 9),
+    (33, 128, 5, 15),
+    (200, 1, 2, 7),
+    (64, 64, 0, 0),    # aligned and contiguous: the row-order mapping
+]
+
+
+@pytest.mark.parametrize("T,H,gap,lead", LAYOUTS)
+def test_q_layouts(T, H, gap, lead):
+    """q as a strided view at a chosen address: every q element bit-exact vs the
+    oracle, the cache exact, and every element of the buffer outside q (pitch
+    gaps, before and after) left as it was."""
+    _say(f"q layout T={T} H={H} gap={gap} lead={lead}")
+    w = _ref_style(T, H, 16, kv_random=True, q_random=True,
+                   slots=torch.arange(T, dtype=torch.int64), seed=4)
+    ref = oracle_main(w)
+    pitch = (H + gap) * 512
+    n = T * pitch + 16 * 1024  # elements, with room for the alignment shift
+    sentinel = torch.randint(-32768, 32767, (n,), generator=torch.Generator().manual_seed(9),
+                             dtype=torch.int16).to(DEV)
+    buf = sentinel.clone().view(torch.bfloat16)
+    # element offset putting q at `lead` KiB past a 16 KiB boundary
+    start = ((16384 - buf.data_ptr() % 16384) % 16384 + lead * 1024) // 2
+    q = torch.as_strided(buf, (T, H, 512), (pitch, 512, 1), start)
+    assert (q.data_ptr() % 16384) == lead * 1024
+    q.copy_(w.q.to(DEV))
+    g = w.to(DEV)
+    OP(q, g.kv, g.k_cache, g.slot_mapping, g.position_ids, g.cos_sin_cache, g.eps, g.block_size)
+    torch.cuda.synchronize()
+    assert_q_exact(q.cpu(), ref.q, f"layout {T, H, gap, lead}")
+    assert torch.equal(g.k_cache.cpu(), ref.k_cache)
+    outside = torch.ones(n, dtype=torch.bool, device=DEV)
+    torch.as_strided(outside, (T, H, 512), (pitch, 512, 1), start).fill_(False)
+    assert torch.equal(buf.view(torch.int16)[outside], sentinel[outside]), "elements outside q written"
