@@ -298,7 +298,7 @@ def main():
             flaggems_vllm.fused_indexer_q_rope_quant(pos, iq, cs, iw, 128 ** -0.5, H ** -0.5,
                                                      use_fp4=args.fp4)
 
-        kernel = "indexer_q_rope_quant_kernel"
+        kernel = "indexer_token_kernel"  # one token per workgroup (H = 64)
         workload = "T8192_H64_D128" + ("_mxfp4" if args.fp4 else "_fp8")
         config = {"workload": f"fused_indexer_q_rope_quant T=8192, H=64, D=128, "
                               f"{'MXFP4' if args.fp4 else 'FP8'}", "num_tokens": T}

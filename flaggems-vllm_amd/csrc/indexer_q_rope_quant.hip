@@ -75,13 +75,13 @@ __device__ __forceinline__ uint32_t pack_fp4x8(const float (&x)[8]) {
     return w;
 }
 
-// One (token, head) row: rotate, quantise, store codes, scales and weight.
+// bf16 pieces of one row -> binary32, with the GPT-J rotation applied on
+// lanes 8..15 of the last piece: x_even*cos - x_odd*sin, x_odd*cos +
+// x_even*sin, each rounded to binary32 and the result to bf16 (reference
+// kernel :113-123).
 template <int kPieces>
-__device__ __forceinline__ void indexer_row(const IndexerArgs& a, uint32_t t, uint32_t h,
-                                            const uint4 (&v)[kPieces], float4 c, float4 s,
-                                            float w_in, int lane16) {
-    const bool rope_lane = lane16 >= 8;
-    float xf[kPieces][8];
+__device__ __forceinline__ void unpack_rope(const uint4 (&v)[kPieces], float4 c, float4 s, int lane16,
+                                            float (&xf)[kPieces][8]) {
 #pragma unroll
     for (int p = 0; p < kPieces; ++p) {
         const uint32_t w4[4] = {v[p].x, v[p].y, v[p].z, v[p].w};
@@ -91,9 +91,7 @@ __device__ __forceinline__ void indexer_row(const IndexerArgs& a, uint32_t t, ui
             xf[p][2 * i + 1] = bf16_hi(w4[i]);
         }
     }
-    if (rope_lane) {
-        // x_even*cos - x_odd*sin, x_odd*cos + x_even*sin, each rounded to
-        // binary32 and the result to bf16 (reference kernel :113-123).
+    if (lane16 >= 8) {
         float* r = xf[kPieces - 1];
         const float cc[4] = {c.x, c.y, c.z, c.w}, ss[4] = {s.x, s.y, s.z, s.w};
 #pragma unroll
@@ -105,39 +103,48 @@ __device__ __forceinline__ void indexer_row(const IndexerArgs& a, uint32_t t, ui
             r[2 * i + 1] = bf16_hi(w);
         }
     }
+}
 
-    uint8_t* qo = a.q_out + (int64_t)t * a.qo_st + (int64_t)h * a.qo_sh;
-    if (!a.fp4) {
-        uint32_t m = 0;
+// FP8: the row's UE8M0 exponent k (one 16-lane max) and each piece's eight
+// e4m3 codes as two words.
+template <int kPieces>
+__device__ __forceinline__ int fp8_codes(const float (&xf)[kPieces][8], uint32_t (&lo)[kPieces],
+                                         uint32_t (&hi)[kPieces]) {
+    uint32_t m = 0;
 #pragma unroll
-        for (int p = 0; p < kPieces; ++p)
+    for (int p = 0; p < kPieces; ++p)
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
-                m = max(m, __float_as_uint(xf[p][i]) & 0x7fffffffu);
-        m = row16_max(m);
-        const int k = fp8_row_exponent(m);
-        const float inv = exp2_neg_int(k);
+        for (int i = 0; i < 8; ++i)
+            m = max(m, __float_as_uint(xf[p][i]) & 0x7fffffffu);
+    m = row16_max(m);
+    const int k = fp8_row_exponent(m);
+    const float inv = exp2_neg_int(k);
 #pragma unroll
-        for (int p = 0; p < kPieces; ++p) {
-            const float* y = xf[p];
-            const uint32_t lo = pack_fp8x4(clamp_fp8(y[0] * inv), clamp_fp8(y[1] * inv),
-                                           clamp_fp8(y[2] * inv), clamp_fp8(y[3] * inv));
-            const uint32_t hi = pack_fp8x4(clamp_fp8(y[4] * inv), clamp_fp8(y[5] * inv),
-                                           clamp_fp8(y[6] * inv), clamp_fp8(y[7] * inv));
-            store8(qo + (lane16 + 16 * p) * 8, lo, hi);
-        }
-        if (lane16 == 0) {
-            const float q_scale = __uint_as_float((uint32_t)(k + 127) << 23);
-            float w = w_in * q_scale;
-            w = w * a.softmax_scale;
-            w = w * a.head_scale;
-            a.weights_out[(int64_t)t * a.wo_st + h] = w;
-        }
-        return;
+    for (int p = 0; p < kPieces; ++p) {
+        const float* y = xf[p];
+        lo[p] = pack_fp8x4(clamp_fp8(y[0] * inv), clamp_fp8(y[1] * inv), clamp_fp8(y[2] * inv),
+                           clamp_fp8(y[3] * inv));
+        hi[p] = pack_fp8x4(clamp_fp8(y[4] * inv), clamp_fp8(y[5] * inv), clamp_fp8(y[6] * inv),
+                           clamp_fp8(y[7] * inv));
     }
+    return k;
+}
 
-    // MXFP4: 32-element blocks are lane quads (4 lanes x 8 elements).
-    uint8_t* so = a.scale_out + (int64_t)t * a.so_st + (int64_t)h * a.so_sh;
+// The FP8 weight ((w * 2^k) * softmax_scale) * head_scale.
+__device__ __forceinline__ float fp8_weight(float w_in, int k, const IndexerArgs& a) {
+    const float q_scale = __uint_as_float((uint32_t)(k + 127) << 23);
+    float w = w_in * q_scale;
+    w = w * a.softmax_scale;
+    return w * a.head_scale;
+}
+
+// MXFP4: 32-element blocks are lane quads (4 lanes x 8 elements).  Per piece,
+// this lane's eight E2M1 nibbles and, on lane 0 of the row, the piece's four
+// block exponents (lanes 0, 4, 8, 12) as one word, so they leave in one 32-bit
+// store instead of four byte stores.
+template <int kPieces>
+__device__ __forceinline__ void fp4_codes(const float (&xf)[kPieces][8], uint32_t (&nib)[kPieces],
+                                          uint32_t (&word)[kPieces]) {
 #pragma unroll
     for (int p = 0; p < kPieces; ++p) {
         uint32_t m = 0;
@@ -152,21 +159,48 @@ __device__ __forceinline__ void indexer_row(const IndexerArgs& a, uint32_t t, ui
 #pragma unroll
         for (int i = 0; i < 8; ++i)
             y[i] = xf[p][i] * inv;
-        const uint32_t nib = pack_fp4x8(y);
-        *reinterpret_cast<uint32_t*>(qo + (lane16 + 16 * p) * 4) = nib;
-        // the piece's four block exponents (lanes 0, 4, 8, 12) leave as one
-        // 32-bit word from lane 0 instead of four byte stores
+        nib[p] = pack_fp4x8(y);
         const uint32_t e = (uint32_t)(k + 127) & 0xffu;
-        const uint32_t word = e | dpp_u32<kDppRowRor12>(e) << 8 | dpp_u32<kDppRowRor8>(e) << 16 |
-                              dpp_u32<kDppRowRor4>(e) << 24;
+        word[p] = e | dpp_u32<kDppRowRor12>(e) << 8 | dpp_u32<kDppRowRor8>(e) << 16 | dpp_u32<kDppRowRor4>(e) << 24;
+    }
+}
+
+// The MXFP4 weight (w * softmax_scale) * head_scale.
+__device__ __forceinline__ float fp4_weight(float w_in, const IndexerArgs& a) {
+    const float w = w_in * a.softmax_scale;
+    return w * a.head_scale;
+}
+
+// One (token, head) row with 64-bit addressing: rotate, quantise, store codes,
+// scales and weight.
+template <int kPieces>
+__device__ __forceinline__ void indexer_row(const IndexerArgs& a, uint32_t t, uint32_t h,
+                                            const uint4 (&v)[kPieces], float4 c, float4 s,
+                                            float w_in, int lane16) {
+    float xf[kPieces][8];
+    unpack_rope<kPieces>(v, c, s, lane16, xf);
+    uint8_t* qo = a.q_out + (int64_t)t * a.qo_st + (int64_t)h * a.qo_sh;
+    if (!a.fp4) {
+        uint32_t lo[kPieces], hi[kPieces];
+        const int k = fp8_codes<kPieces>(xf, lo, hi);
+#pragma unroll
+        for (int p = 0; p < kPieces; ++p)
+            store8(qo + (lane16 + 16 * p) * 8, lo[p], hi[p]);
         if (lane16 == 0)
-            *reinterpret_cast<uint32_t*>(so + 4 * p) = word;
+            a.weights_out[(int64_t)t * a.wo_st + h] = fp8_weight(w_in, k, a);
+        return;
     }
-    if (lane16 == 0) {
-        float w = w_in * a.softmax_scale;
-        w = w * a.head_scale;
-        a.weights_out[(int64_t)t * a.wo_st + h] = w;
+    uint8_t* so = a.scale_out + (int64_t)t * a.so_st + (int64_t)h * a.so_sh;
+    uint32_t nib[kPieces], word[kPieces];
+    fp4_codes<kPieces>(xf, nib, word);
+#pragma unroll
+    for (int p = 0; p < kPieces; ++p) {
+        *reinterpret_cast<uint32_t*>(qo + (lane16 + 16 * p) * 4) = nib[p];
+        if (lane16 == 0)
+            *reinterpret_cast<uint32_t*>(so + 4 * p) = word[p];
     }
+    if (lane16 == 0)
+        a.weights_out[(int64_t)t * a.wo_st + h] = fp4_weight(w_in, a);
 }
 
 // Each 16-lane group owns kRows rows, 16 rows apart inside the block, so a
@@ -231,6 +265,94 @@ indexer_q_rope_quant_kernel(IndexerArgs a) {
         if (valid[rr])
             indexer_row<kPieces>(a, tt[rr], hh[rr], v[rr], c[rr], s[rr], w_in, lane16);
     }
+}
+
+// One token per block (num_heads a multiple of the block's rows) and every
+// per-head offset below 2^31 bytes: the token, its position and the base
+// pointers of its rows are uniform (scalar registers) and each lane addresses
+// its rows with 32-bit offsets.  The general kernel's per-row division by
+// num_heads and 64-bit address products made it VALU-bound (about 650 VALU
+// instructions per wave against ~330 here for the same math).
+template <int kPieces, int kRows, bool kCsBf16>
+__global__ void __launch_bounds__(kThreads)
+indexer_token_kernel(IndexerArgs a) {
+    const int lane16 = threadIdx.x & 15;
+    const uint32_t row0 = blockIdx.x * (kRowsPerBlock * kRows);
+    const uint32_t t = row0 / a.num_heads;
+    const uint32_t h = row0 - t * a.num_heads + (threadIdx.x >> 4);  // rows h + 16 * rr
+    const int64_t pos_raw = a.positions[t];
+    uint32_t w_bits[kRows];
+    if (a.w_f32) {
+        const uint32_t* wb = static_cast<const uint32_t*>(a.weights) + (int64_t)t * a.w_st;
+#pragma unroll
+        for (int rr = 0; rr < kRows; ++rr)
+            w_bits[rr] = wb[h + 16 * rr];
+    } else {
+        const uint16_t* wb = static_cast<const uint16_t*>(a.weights) + (int64_t)t * a.w_st;
+#pragma unroll
+        for (int rr = 0; rr < kRows; ++rr)
+            w_bits[rr] = wb[h + 16 * rr];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    const uint8_t* qb = reinterpret_cast<const uint8_t*>(a.q + (int64_t)t * a.q_st);
+    const uint32_t q_row = (uint32_t)a.q_sh * 2;  // bytes between heads
+    const uint32_t q_off = h * q_row + lane16 * 16;
+    uint4 v[kRows][kPieces];
+#pragma unroll
+    for (int rr = 0; rr < kRows; ++rr)
+#pragma unroll
+        for (int p = 0; p < kPieces; ++p)
+            v[rr][p] = load16(qb + (q_off + rr * 16 * q_row + p * 256));
+    __builtin_amdgcn_sched_barrier(0);
+    float4 c = make_float4(0.f, 0.f, 0.f, 0.f), s = c;
+    if (lane16 >= 8) {
+        const int64_t off = clamp_position(pos_raw, a.max_pos) * a.cs_stride + (lane16 - 8) * 4;
+        c = load_cs4(a.cos_sin, off, kCsBf16);
+        s = load_cs4(a.cos_sin, off + kHalfRope, kCsBf16);
+    }
+    uint8_t* qo = a.q_out + (int64_t)t * a.qo_st;
+    float* wo = a.weights_out + (int64_t)t * a.wo_st;
+    const uint32_t qo_row = (uint32_t)a.qo_sh;
+#pragma unroll
+    for (int rr = 0; rr < kRows; ++rr) {
+        const uint32_t hr = h + 16 * rr;
+        const float w_in = __uint_as_float(a.w_f32 ? w_bits[rr] : w_bits[rr] << 16);
+        float xf[kPieces][8];
+        unpack_rope<kPieces>(v[rr], c, s, lane16, xf);
+        if (!a.fp4) {
+            uint32_t lo[kPieces], hi[kPieces];
+            const int k = fp8_codes<kPieces>(xf, lo, hi);
+#pragma unroll
+            for (int p = 0; p < kPieces; ++p)
+                store8(qo + (hr * qo_row + lane16 * 8 + p * 128), lo[p], hi[p]);
+            if (lane16 == 0)
+                wo[hr] = fp8_weight(w_in, k, a);
+        } else {
+            uint8_t* so = a.scale_out + (int64_t)t * a.so_st;
+            uint32_t nib[kPieces], word[kPieces];
+            fp4_codes<kPieces>(xf, nib, word);
+#pragma unroll
+            for (int p = 0; p < kPieces; ++p) {
+                *reinterpret_cast<uint32_t*>(qo + (hr * qo_row + lane16 * 4 + p * 64)) = nib[p];
+                if (lane16 == 0)
+                    *reinterpret_cast<uint32_t*>(so + (hr * (uint32_t)a.so_sh + p * 4)) = word[p];
+            }
+            if (lane16 == 0)
+                wo[hr] = fp4_weight(w_in, a);
+        }
+    }
+}
+
+// Rows per 16-lane group in the one-token kernel, for head_dim 128, 256, 512.
+constexpr int kTokenRows[3] = {4, 2, 1};
+
+template <int kPieces>
+void launch_token(const IndexerArgs& a, bool cs_bf16, dim3 grid, hipStream_t s) {
+    constexpr int kRows = kTokenRows[kPieces == 1 ? 0 : kPieces == 2 ? 1 : 2];
+    if (cs_bf16)
+        hipLaunchKernelGGL((indexer_token_kernel<kPieces, kRows, true>), grid, dim3(kThreads), 0, s, a);
+    else
+        hipLaunchKernelGGL((indexer_token_kernel<kPieces, kRows, false>), grid, dim3(kThreads), 0, s, a);
 }
 
 template <int kPieces>
@@ -319,6 +441,23 @@ extern "C" int fgv_fused_indexer_q_rope_quant(
     const dim3 grid((unsigned)((rows + rows_per_block - 1) / rows_per_block));
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool one_token = num_heads % rows_per_block == 0;
+    // the one-token kernel's 32-bit per-head offsets (bytes) must stay below 2^31
+    const auto fits = [&](int64_t stride_bytes, int64_t row_bytes) {
+        return stride_bytes >= 0 && (num_heads - 1) * stride_bytes + row_bytes < (1LL << 31);
+    };
+    const int token_rows = kRowsPerBlock * kTokenRows[head_dim == 128 ? 0 : head_dim == 256 ? 1 : 2];
+    const dim3 token_grid((unsigned)(rows / token_rows));
+    if (num_heads % token_rows == 0 && fits(q_stride_head * 2, head_dim * 2) &&
+        fits(q_out_stride_head, use_fp4 ? head_dim / 2 : head_dim) &&
+        (!use_fp4 || fits(scale_out_stride_head, head_dim / 32))) {
+        if (head_dim == 128)
+            launch_token<1>(a, cos_sin_is_bf16, token_grid, s);
+        else if (head_dim == 256)
+            launch_token<2>(a, cos_sin_is_bf16, token_grid, s);
+        else
+            launch_token<4>(a, cos_sin_is_bf16, token_grid, s);
+        return launch_status();
+    }
     if (head_dim == 128)
         launch_indexer<1>(a, cos_sin_is_bf16, one_token, grid, s);
     else if (head_dim == 256)

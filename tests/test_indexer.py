@@ -170,3 +170,35 @@ def test_gpu_converter_exhaustive(use_fp4, limit):
     cs = W.make_cos_sin_cache(16)
     w = torch.ones(T, 1, dtype=torch.bfloat16)
     _check((pos, q, cs, w, 1.0, 1.0), use_fp4)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("D,H", [(128, 64), (128, 128), (256, 32), (512, 16)])
+@pytest.mark.parametrize("use_fp4", [False, True])
+@pytest.mark.parametrize("w_f32", [False, True])
+def test_gpu_one_token_blocks(D, H, use_fp4, w_f32):
+    """Head counts that fill whole blocks with one token's rows, so the kernel
+    with per-block token and 32-bit row offsets runs (including two blocks per
+    token at H=128), on a strided q view (head stride D + 64) with bf16 or fp32
+    weights."""
+    import flaggems_vllm
+
+    print(f"\n[case] indexer one-token D={D} H={H} fp4={use_fp4} w_f32={w_f32}", flush=True)
+    T = 37
+    pos, q, cs, w, sm, hs = _case(T, H=H, D=D, seed=11)
+    if w_f32:
+        w = (w.float() * 1.0009765625).contiguous()  # not representable in bf16
+    wide = torch.zeros(T, H, D + 64, dtype=torch.bfloat16, device=DEV)
+    wide[..., :D] = q.to(DEV)
+    qv = wide[..., :D]
+    assert qv.stride() == (H * (D + 64), D + 64, 1)
+    out, wo = flaggems_vllm.fused_indexer_q_rope_quant(pos.to(DEV), qv, cs.to(DEV), w.to(DEV), sm, hs,
+                                                       use_fp4=use_fp4)
+    torch.cuda.synchronize()
+    (oq, ow) = oracle.fused_indexer_q_rope_quant(pos, q, cs, w, sm, hs, use_fp4=use_fp4)
+    if use_fp4:
+        assert torch.equal(out[0].cpu(), oq[0])
+        assert torch.equal(out[1].cpu(), oq[1].contiguous().view(torch.int32).reshape(T, H, -1).squeeze(-1))
+    else:
+        assert torch.equal(out.cpu().view(torch.uint8), oq)
+    assert torch.equal(wo.cpu(), ow)
