@@ -350,9 +350,12 @@ def main():
 
         from flaggems_vllm import _native
 
-        split = _native.lib().fgv_sparse_mla_decode_workspace_bytes(
-            B, SQ, HQ, w.indices.shape[-1],
-            w.extra_indices.shape[-1] if w.extra_indices is not None else 0) > 0
+        query = _native.lib().fgv_sparse_mla_decode_workspace_bytes
+        etopk = w.extra_indices.shape[-1] if w.extra_indices is not None else 0
+        entries = w.extra_k_cache.shape[0] * w.extra_k_cache.shape[1] if w.extra_k_cache is not None else 0
+        split = query(B, SQ, HQ, w.indices.shape[-1], etopk, 0) > 0
+        expanded = query(B, SQ, HQ, w.indices.shape[-1], etopk, entries) > query(B, SQ, HQ, w.indices.shape[-1],
+                                                                                  etopk, 0)
         kernel = "sparse_mla_decode_split_kernel" if split else "sparse_mla_decode_kernel"
         workload = f"mla_{args.mla_case}"
         case = W.MLA_CASES[args.mla_case]
@@ -363,8 +366,9 @@ def main():
                                  f"of {case['extra_page']}" if "extra_topk" in case else ""),
                   "batch": B, "seq_q": SQ, "num_heads": HQ, "attended_entries": w_cpu.used_tokens(),
                   "flops_per_call": flops_call,
-                  "schedule": "balanced split grid + combine kernel" if split
-                              else "one workgroup per (row, 64-head block)"}
+                  "schedule": ("balanced split grid + combine kernel" if split
+                               else "one workgroup per (row, 64-head block)")
+                              + ("; extra cache expanded to bf16 once per call" if expanded else "")}
     elif args.op == "copy":
         n = 512 << 20
         src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)

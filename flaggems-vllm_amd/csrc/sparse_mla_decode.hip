@@ -74,8 +74,10 @@ struct CacheList {
     const uint8_t* cache;
     const int32_t* indices;
     const int32_t* lengths;  // [batch] or null
+    const uint8_t* expanded; // bf16 rows [num_entries][512] of the whole cache, or null
     int64_t block_stride;    // bytes
     int64_t idx_stride_b, idx_stride_s;
+    int64_t num_entries;     // num_blocks * page_size
     double inv_page;         // 1 / page_size
     int32_t num_blocks, page_size, topk, pad;
 };
@@ -143,7 +145,8 @@ __device__ __align__(256) uint8_t mla_zero_entry[1024];
 struct ListView {
     const uint8_t* cache;
     const int32_t* row;     // this query's index row
-    int64_t block_stride;
+    const uint8_t* expanded;
+    int64_t block_stride, num_entries;
     double inv_page;
     int page_size, num_blocks, len;
 };
@@ -152,6 +155,8 @@ __device__ __forceinline__ ListView make_view(const CacheList& L, bool present, 
     ListView v;
     v.cache = L.cache;
     v.row = L.indices + b * L.idx_stride_b + sq * L.idx_stride_s;
+    v.expanded = L.expanded;
+    v.num_entries = L.num_entries;
     v.block_stride = L.block_stride;
     v.inv_page = L.inv_page;
     v.page_size = L.page_size;
@@ -173,6 +178,8 @@ __device__ __forceinline__ ListView select(const ListView& v0, const ListView& v
     ListView v;
     v.cache = second ? v1.cache : v0.cache;
     v.row = second ? v1.row : v0.row;
+    v.expanded = second ? v1.expanded : v0.expanded;
+    v.num_entries = second ? v1.num_entries : v0.num_entries;
     v.block_stride = second ? v1.block_stride : v0.block_stride;
     v.inv_page = second ? v1.inv_page : v0.inv_page;
     v.page_size = second ? v1.page_size : v0.page_size;
@@ -234,6 +241,29 @@ __device__ __forceinline__ void issue_gather(const ListView& v, const uint8_t* d
     __builtin_amdgcn_global_load_lds((global_u32_t*)scl, (lds_u32_t*)(dst + kRawScaleOff + 256 * wave), 4, 0, 0);
     if (sub == 0)
         mask[e] = off >= 0 ? 0.f : -INFINITY;
+}
+
+// A chunk of an expanded list (bf16 rows, 1 KiB per entry) straight into a K
+// tile, with no dequantisation: wave w moves entries 8w..8w+7, one row per
+// wave-wide 16-byte LDS DMA (64 lanes x 16 bytes land contiguously at the row's
+// start).  The tile's block swizzle is applied on the source side: lane l
+// fetches block l ^ x of the entry, x = bit 3 of the row = bit 0 of w.  Each
+// row's index comes from lane 8j (load_id's layout); entries that are not
+// attended come from the zero page, and the mask is written as for a gather.
+__device__ __forceinline__ void issue_rows(const ListView& v, int wave, int lane, int id, uint8_t* tile,
+                                           float* mask) {
+    __attribute__((address_space(3))) uint8_t* dst = (__attribute__((address_space(3))) uint8_t*)tile;
+    const int src_off = 16 * (lane ^ (wave & 1));
+#pragma unroll
+    for (int j = 0; j < kChunk / 4; ++j) {
+        const int idj = __builtin_amdgcn_readlane(id, 8 * j);
+        const uint8_t* row = idj >= 0 && idj < v.num_entries ? v.expanded + (int64_t)idj * (2 * kHeadDim)
+                                                             : mla_zero_entry;
+        __builtin_amdgcn_global_load_lds((global_u32_t*)(row + src_off),
+                                         (lds_u32_t*)(dst + (8 * wave + j) * kKRowBytes), 16, 0, 0);
+    }
+    if ((lane & 7) == 0)
+        mask[8 * wave + (lane >> 3)] = id >= 0 && id < v.num_entries ? 0.f : -INFINITY;
 }
 
 // Chunk in `raw` -> bf16 K tile: wave w converts entries w, w+4, ..., lane l
@@ -352,8 +382,19 @@ __device__ __forceinline__ void run_segment(const MlaArgs& a, uint8_t (&raw)[2][
 #pragma unroll
     for (int s = 0; s < 16; ++s)
         qf[s] = __builtin_bit_cast(bf16x8_t, load16(qrow + 32 * s + 8 * g));
-    if (c_lo < c_hi)
-        issue_gather(select(v0, v1, c_lo >= n0), dummy, wave, lane, id_cur, raw[c_lo & 1], mask_lds[c_lo & 1]);
+    // Chunks [c_lo, c_mid) come from the FP8 cache through the raw gather and
+    // the dequantisation; with an expanded extra list, its chunks [c_mid, c_hi)
+    // come as bf16 rows, alternating between two K tiles: the raw gather
+    // buffers (free then; extra chunk n0 + 2i) and the K tile (n0 + 2i + 1).
+    static_assert(kChunk * kKRowBytes <= 2 * kRawBytes, "the raw gather buffers hold a K tile");
+    uint8_t* const raw_tile = &raw[0][0];
+    const int c_mid = v1.expanded ? max(c_lo, min(c_hi, n0)) : c_hi;
+    if (c_lo < c_hi) {
+        if (c_lo < c_mid)
+            issue_gather(select(v0, v1, c_lo >= n0), dummy, wave, lane, id_cur, raw[c_lo & 1], mask_lds[c_lo & 1]);
+        else
+            issue_rows(v1, wave, lane, id_cur, ((c_lo - n0) & 1) ? kbuf : raw_tile, mask_lds[c_lo & 1]);
+    }
 
     f32x4_t acc[32];
 #pragma unroll
@@ -370,30 +411,17 @@ __device__ __forceinline__ void run_segment(const MlaArgs& a, uint8_t (&raw)[2][
     const int tr_row = 4 * g + (m16 >> 2);
     const int tr_base = kbuf_byte(tr_row, (m16 & 3) >> 1) + 8 * (m16 & 1);
 
-    for (int c = c_lo; c < c_hi; ++c) {
-        uint8_t* cur = raw[c & 1];
-        // The gather and dequantisation addresses derive from the lane id; an
-        // opaque copy per chunk keeps them from being held (and spilled)
-        // across the MFMA loops, which need every register.
-        int ln = lane;
-        asm volatile("" : "+v"(ln));
-        __builtin_amdgcn_s_waitcnt(0);  // this wave's gathers of chunk c (and chunk c+1's index)
-        __syncthreads();                // everyone's gathers landed; K tile no longer read
-        dequantize(cur, mask_lds[c & 1], kbuf, wave, ln);
-        __syncthreads();
-        if (c + 1 < c_hi)
-            issue_gather(select(v0, v1, c + 1 >= n0), dummy, wave, ln, id_next, raw[(c + 1) & 1],
-                         mask_lds[(c + 1) & 1]);
-        if (c + 2 < c_hi)
-            id_next = load_id(select(v0, v1, c + 2 >= n0), first_of(c + 2), wave, ln);
-
+    // Attends one chunk whose bf16 K tile is at `kt` and score mask at `mask`.
+    // (Each call site passes one fixed LDS array, so the compiler can tell the
+    // tile read from the tile the LDS DMA is filling.)
+    auto attend = [&](const uint8_t* kt, const float* mask) __attribute__((always_inline)) {
         // ---- S^T = K q^T for the chunk's two 16-entry tiles
         // K operands read two steps ahead of the MFMAs that consume them
         f32x4_t s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
         bf16x8_t ka[3], kb[3];
         auto read_k = [&](int s, bf16x8_t& x, bf16x8_t& y) {
-            x = *reinterpret_cast<const bf16x8_t*>(kbuf + qk_base + 64 * s);
-            y = *reinterpret_cast<const bf16x8_t*>(kbuf + qk_base + 64 * s + 16 * kKRowBytes);
+            x = *reinterpret_cast<const bf16x8_t*>(kt + qk_base + 64 * s);
+            y = *reinterpret_cast<const bf16x8_t*>(kt + qk_base + 64 * s + 16 * kKRowBytes);
         };
         read_k(0, ka[0], kb[0]);
         read_k(1, ka[1], kb[1]);
@@ -407,7 +435,6 @@ __device__ __forceinline__ void run_segment(const MlaArgs& a, uint8_t (&raw)[2][
         }
 
         // ---- online softmax (base 2) for head m16 over entries 4g+r, 16+4g+r
-        const float* mask = mask_lds[c & 1];
         float sv[8];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -451,8 +478,8 @@ __device__ __forceinline__ void run_segment(const MlaArgs& a, uint8_t (&raw)[2][
         // the two per step of the QK loop)
         uint2 vlo[5], vhi[5];
         auto read_v = [&](int dt, uint2& x, uint2& y) {
-            x = read_tr(kbuf, tr_base + 32 * dt);
-            y = read_tr(kbuf, tr_base + 32 * dt + 16 * kKRowBytes);
+            x = read_tr(kt, tr_base + 32 * dt);
+            y = read_tr(kt, tr_base + 32 * dt + 16 * kKRowBytes);
         };
 #pragma unroll
         for (int i = 0; i < 4; ++i)
@@ -466,6 +493,50 @@ __device__ __forceinline__ void run_segment(const MlaArgs& a, uint8_t (&raw)[2][
             acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pb, acc[dt], 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
         }
+    };
+
+    for (int c = c_lo; c < c_mid; ++c) {
+        uint8_t* cur = raw[c & 1];
+        // The gather and dequantisation addresses derive from the lane id; an
+        // opaque copy per chunk keeps them from being held (and spilled)
+        // across the MFMA loops, which need every register.
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's gathers of chunk c (and chunk c+1's index)
+        __syncthreads();                // everyone's gathers landed; K tile no longer read
+        dequantize(cur, mask_lds[c & 1], kbuf, wave, ln);
+        __syncthreads();
+        if (c + 1 < c_mid)
+            issue_gather(select(v0, v1, c + 1 >= n0), dummy, wave, ln, id_next, raw[(c + 1) & 1],
+                         mask_lds[(c + 1) & 1]);
+        else if (c + 1 < c_hi)  // the first expanded chunk (n0) goes to the raw buffers
+            issue_rows(v1, wave, ln, id_next, raw_tile, mask_lds[(c + 1) & 1]);
+        if (c + 2 < c_hi)
+            id_next = load_id(select(v0, v1, c + 2 >= n0), first_of(c + 2), wave, ln);
+        attend(kbuf, mask_lds[c & 1]);
+    }
+    // One expanded chunk: its rows are read from `tile` while the next chunk's
+    // rows stream into `other`.  The loop below runs these in (raw, K tile)
+    // pairs, so that each step reads one fixed array (two steps under an
+    // if / else would merge every accumulator register at the join).
+    auto expanded_step = [&](int c, uint8_t* tile, uint8_t* other) __attribute__((always_inline)) {
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's rows of chunk c (and chunk c+1's index)
+        __syncthreads();                // everyone's rows landed; `other` no longer read
+        if (c + 1 < c_hi)
+            issue_rows(v1, wave, ln, id_next, other, mask_lds[(c + 1) & 1]);
+        if (c + 2 < c_hi)
+            id_next = load_id(v1, first_of(c + 2), wave, ln);
+        attend(tile, mask_lds[c & 1]);
+    };
+    int c = c_mid;
+    if (c < c_hi && ((c - n0) & 1))  // a segment that starts on an odd extra chunk
+        expanded_step(c++, kbuf, raw_tile);
+    for (; c < c_hi; c += 2) {
+        expanded_step(c, raw_tile, kbuf);
+        if (c + 1 < c_hi)
+            expanded_step(c + 1, kbuf, raw_tile);
     }
 
     if (slot >= 0) {
@@ -718,11 +789,62 @@ sparse_mla_combine_kernel(MlaArgs a) {
     }
 }
 
+// Dequantises every entry of a list's cache into bf16 rows [num_entries][512]
+// (the expanded copy the chunk loop then DMAs without converting), with the
+// conversion the chunk loop uses (scale byte 0 included), so either route
+// gives the same K rows.  Each 32-lane half of a wave does kExpandPerHalf
+// entries, all loads first (the kernel is short, and latency-bound with fewer
+// bytes in flight); lane k makes output blocks k and k + 32, so each store
+// instruction writes two whole 512-byte halves: blocks below 56 from 8 code
+// bytes and their scale byte, blocks 56..63 from 16 RoPE bytes.
+constexpr int kExpandPerHalf = 2;
+constexpr int kExpandPerBlock = kThreads / 32 * kExpandPerHalf;
+
+__global__ void __launch_bounds__(kThreads)
+mla_expand_cache_kernel(CacheList L, uint8_t* out) {
+    const int k = threadIdx.x & 31, k2 = k + 32;
+    const int64_t e0 = (int64_t)blockIdx.x * kExpandPerBlock + (threadIdx.x >> 5) * kExpandPerHalf;
+    uint2 c0[kExpandPerHalf];
+    uint4 c1[kExpandPerHalf];  // codes of block k2 in .x/.y, or its RoPE bytes
+    uint32_t b0[kExpandPerHalf], b1[kExpandPerHalf];
+#pragma unroll
+    for (int i = 0; i < kExpandPerHalf; ++i) {
+        // (entries < 2^16 here: the copy is at most 64 MiB of 1 KiB rows)
+        const uint32_t e = (uint32_t)(e0 + i < L.num_entries ? e0 + i : L.num_entries - 1);
+        const uint32_t page = e / (uint32_t)L.page_size, rel = e - page * (uint32_t)L.page_size;
+        const uint8_t* base = L.cache + (int64_t)page * L.block_stride;
+        const uint8_t* tok = base + rel * kTokenDataBytes;
+        const uint8_t* scl = base + (int64_t)L.page_size * kTokenDataBytes + rel * kScaleBytesPerToken;
+        c0[i] = *reinterpret_cast<const uint2*>(tok + 8 * k);
+        b0[i] = scl[k >> 3];
+        if (k2 < kNopeDim / 8) {
+            const uint2 c = *reinterpret_cast<const uint2*>(tok + 8 * k2);
+            c1[i] = make_uint4(c.x, c.y, 0u, 0u);
+            b1[i] = scl[k2 >> 3];
+        } else {
+            c1[i] = *reinterpret_cast<const uint4*>(tok + kNopeDim + 16 * (k2 - kNopeDim / 8));
+            b1[i] = 0;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < kExpandPerHalf; ++i) {
+        if (e0 + i >= L.num_entries)
+            break;
+        const uint4 r0 = dequant8<true>(c0[i], b0[i]);
+        const uint4 r1 = k2 < kNopeDim / 8 ? dequant8<true>(make_uint2(c1[i].x, c1[i].y), b1[i]) : c1[i];
+        uint8_t* row = out + (e0 + i) * (2 * kHeadDim);
+        store16(row + 16 * k, r0);
+        store16(row + 16 * k2, r1);
+    }
+}
+
 void fill_list(CacheList& L, const void* cache, int64_t block_stride, int64_t num_blocks, int64_t page_size,
                const int32_t* indices, int64_t idx_sb, int64_t idx_ss, int64_t topk, const int32_t* lengths) {
     L.cache = static_cast<const uint8_t*>(cache);
     L.indices = indices;
     L.lengths = lengths;
+    L.expanded = nullptr;
+    L.num_entries = num_blocks * page_size;
     L.block_stride = block_stride;
     L.idx_stride_b = idx_sb;
     L.idx_stride_s = idx_ss;
@@ -766,6 +888,22 @@ int split_grid() {
     return 2 * cus;
 }
 
+// An extra list gathered at least this many times per cache entry (counting
+// every row, query position and head block at its full top-k) is dequantised
+// once per call into a bf16 copy in the workspace, up to this size; its chunks
+// then skip the dequantisation (2.0 bytes of L2 -> LDS per byte of K instead
+// of 1.14, no conversion, one barrier per chunk instead of two).
+constexpr int64_t kExpandMinReuse = 8;
+constexpr int64_t kExpandMaxBytes = 64LL << 20;
+static_assert(kExpandMaxBytes / (2 * kHeadDim) <= (1LL << 31), "the expand kernel counts entries in 32 bits");
+
+int64_t expand_bytes(int64_t batch, int64_t seq_q, int64_t num_heads, int64_t extra_topk, int64_t extra_entries) {
+    if (extra_entries <= 0 || extra_topk <= 0 || extra_entries * 2 * kHeadDim > kExpandMaxBytes)
+        return 0;
+    const int64_t gathers = batch * seq_q * (num_heads / kBlockHeads) * extra_topk;
+    return gathers >= kExpandMinReuse * extra_entries ? extra_entries * 2 * kHeadDim : 0;
+}
+
 int64_t split_bytes(int64_t batch, int64_t topk, int64_t extra_topk) {
     if (chunks_of(topk) + chunks_of(extra_topk) < kSplitMinChunks || batch > kMaxSplitRows)
         return 0;
@@ -777,12 +915,13 @@ int64_t split_bytes(int64_t batch, int64_t topk, int64_t extra_topk) {
 }  // namespace fgv
 
 extern "C" int64_t fgv_sparse_mla_decode_workspace_bytes(int64_t batch, int64_t seq_q, int64_t num_heads,
-                                                         int64_t topk, int64_t extra_topk) {
-    (void)seq_q;
-    (void)num_heads;
-    if (batch <= 0 || topk < 0 || extra_topk < 0)
+                                                         int64_t topk, int64_t extra_topk,
+                                                         int64_t extra_num_entries) {
+    if (batch <= 0 || seq_q <= 0 || num_heads <= 0 || num_heads % fgv::kBlockHeads || topk < 0 || extra_topk < 0 ||
+        extra_num_entries < 0)
         return 0;
-    return fgv::split_bytes(batch, topk, extra_topk);
+    return fgv::expand_bytes(batch, seq_q, num_heads, extra_topk, extra_num_entries) +
+           fgv::split_bytes(batch, topk, extra_topk);
 }
 
 extern "C" int fgv_sparse_mla_decode_model1(
@@ -856,15 +995,33 @@ extern "C" int fgv_sparse_mla_decode_model1(
     a.split_grid = 0;
     const int64_t items = batch * seq_q * a.head_blocks;
     hipStream_t st = static_cast<hipStream_t>(stream);
-    const int64_t need = split_bytes(batch, topk, extra_k_cache ? extra_topk : 0);
+    // Workspace: [expanded extra cache][split slots][row prefix sums].  A
+    // workspace too small for both drops the expansion first, then the split.
     // (the combine kernel runs four workgroups per item)
-    if (need > 0 && workspace && workspace_bytes >= need && 4 * items <= 0x7fffffffLL) {
-        if (!aligned(workspace, 256))
-            return fail(FGV_E_MISALIGNED, "workspace must be 256-byte aligned");
+    const int64_t need_split = 4 * items <= 0x7fffffffLL ? split_bytes(batch, topk, extra_k_cache ? extra_topk : 0) : 0;
+    const int64_t need_expand =
+        extra_k_cache ? expand_bytes(batch, seq_q, num_heads, extra_topk, a.list[1].num_entries) : 0;
+    const int64_t have = workspace ? workspace_bytes : 0;
+    const bool use_expand = need_expand > 0 && have >= need_expand + need_split;
+    const bool use_split = need_split > 0 && have >= need_split + (use_expand ? need_expand : 0);
+    if ((use_expand || use_split) && !aligned(workspace, 256))
+        return fail(FGV_E_MISALIGNED, "workspace must be 256-byte aligned");
+    uint8_t* ws = static_cast<uint8_t*>(workspace);
+    if (use_expand) {
+        a.list[1].expanded = ws;
+        const int64_t per_block = kExpandPerBlock;
+        hipLaunchKernelGGL(mla_expand_cache_kernel,
+                           dim3((unsigned)((a.list[1].num_entries + per_block - 1) / per_block)), dim3(kThreads), 0,
+                           st, a.list[1], ws);
+        rc = launch_status();
+        if (rc)
+            return rc;
+        ws += need_expand;
+    }
+    if (use_split) {
         a.split_grid = split_grid();
-        a.partials = static_cast<float*>(workspace);
-        a.row_prefix = reinterpret_cast<int32_t*>(static_cast<uint8_t*>(workspace) +
-                                                  2 * (int64_t)a.split_grid * kSlotFloats * 4);
+        a.partials = reinterpret_cast<float*>(ws);
+        a.row_prefix = reinterpret_cast<int32_t*>(ws + 2 * (int64_t)a.split_grid * kSlotFloats * 4);
         hipLaunchKernelGGL(sparse_mla_decode_split_kernel, dim3((unsigned)a.split_grid), dim3(kThreads), 0, st, a);
         rc = launch_status();
         if (rc)

@@ -145,7 +145,7 @@ def lib():
         _P,  # stream
     ]
     L.fgv_sparse_mla_decode_workspace_bytes.restype = ctypes.c_int64
-    L.fgv_sparse_mla_decode_workspace_bytes.argtypes = [_I64, _I64, _I64, _I64, _I64]
+    L.fgv_sparse_mla_decode_workspace_bytes.argtypes = [_I64, _I64, _I64, _I64, _I64, _I64]
     _lib = L
     return _lib
 

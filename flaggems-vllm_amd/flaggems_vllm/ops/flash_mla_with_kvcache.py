@@ -213,10 +213,12 @@ def flash_mla_with_kvcache(
     ei = extra_indices_in_kvcache
     ptr = lambda t: t.data_ptr() if t is not None else None
     with on_device_of(q):
-        # long lists: a workspace for the balanced split schedule (cf. the
+        # a workspace for the balanced split schedule of long lists (cf. the
         # reference's lse_part / o_part, flash_mla_with_kvcache_model1.py:1588-1595)
+        # and for a bf16 copy of an extra cache that is gathered many times over
         ws_bytes = _native.lib().fgv_sparse_mla_decode_workspace_bytes(
-            batch, seq_q, num_heads_q, topk, extra_topk or 0)
+            batch, seq_q, num_heads_q, topk, extra_topk or 0,
+            ek.shape[0] * ek.shape[1] if ek is not None else 0)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes > 0 else None
         rc = _native.lib().fgv_sparse_mla_decode_model1(
             q.data_ptr(), q.stride(0), q.stride(1), q.stride(2),

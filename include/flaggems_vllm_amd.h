@@ -254,19 +254,26 @@ int fgv_sparse_mla_decode_model1(
     void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
- * Bytes of device workspace (256-byte aligned) with which
- * fgv_sparse_mla_decode_model1 balances long lists across the GPU: a grid of
- * two workgroups per CU splits all (row, head block) items' chunks evenly,
- * and a combine kernel merges the items that cross a split (the reference's
- * split-KV schedule and combine, ops/flash_mla_with_kvcache_model1.py:1212-1395).
- * 0 when the lists are short enough (topk + extra_topk below 2048 entries) or
- * the batch too large (above 8000 rows) for the split schedule: then the
- * workspace argument is ignored.  Passing no workspace (NULL or too small)
- * always works, with one workgroup per item.  The value depends on the
- * current device's CU count.
+ * Bytes of device workspace (256-byte aligned) that fgv_sparse_mla_decode_model1
+ * can use, the sum of two optional parts:
+ *   - an expanded extra cache: when the extra list is gathered at least 8 times
+ *     per cache entry (batch * seq_q * num_heads/64 * extra_topk >=
+ *     8 * extra_num_entries) and the copy is at most 64 MiB, the extra cache is
+ *     dequantised once per call into bf16 rows (1 KiB per entry) that the
+ *     attention reads without converting.  The results are the same bits.
+ *   - the split schedule: for long lists (topk + extra_topk at least 2048
+ *     entries, batch at most 8000 rows) a grid of two workgroups per CU splits
+ *     all (row, head block) items' chunks evenly, and a combine kernel merges
+ *     the items that cross a split (the reference's split-KV schedule and
+ *     combine, ops/flash_mla_with_kvcache_model1.py:1212-1395).  Its size
+ *     depends on the current device's CU count.
+ * extra_num_entries is extra_num_blocks * extra_page_size (0 without an extra
+ * cache).  0 means the workspace argument is ignored.  Passing no workspace
+ * (NULL or too small) always works: a workspace too small for both parts drops
+ * the expansion first, then the split (one workgroup per item).
  */
 int64_t fgv_sparse_mla_decode_workspace_bytes(int64_t batch, int64_t seq_q, int64_t num_heads,
-                                              int64_t topk, int64_t extra_topk);
+                                              int64_t topk, int64_t extra_topk, int64_t extra_num_entries);
 
 #ifdef __cplusplus
 }

@@ -348,18 +348,27 @@ def test_c_abi_rejects_bad_arguments():
 
 def test_workspace_query():
     """The balanced split schedule is used for long lists only, and then needs
-    two partial slots per workgroup of the grid plus the row prefix sums."""
+    two partial slots per workgroup of the grid plus the row prefix sums; an
+    extra cache gathered at least 8 times per entry gets a bf16 copy of
+    1 KiB per entry (at most 64 MiB)."""
     from flaggems_vllm import _native
 
     f = _native.lib().fgv_sparse_mla_decode_workspace_bytes
-    assert f(512, 1, 64, 128, 0) == 0            # decode: one workgroup per item
-    assert f(512, 1, 64, 128, 512) == 0          # 20 chunks: still unsplit
-    big = f(512, 1, 64, 128, 8192)
+    assert f(512, 1, 64, 128, 0, 0) == 0            # decode: one workgroup per item
+    assert f(512, 1, 64, 128, 512, 0) == 0          # 20 chunks: still unsplit
+    big = f(512, 1, 64, 128, 8192, 0)
     slot = (64 * 512 + 128) * 4
     prefix = (513 * 4 + 255) // 256 * 256
     assert big > 0 and (big - prefix) % (2 * slot) == 0 and big % 256 == 0
-    assert f(9000, 1, 64, 128, 8192) == 0        # prefix sums must fit in LDS
-    assert f(0, 1, 64, 128, 8192) == 0
+    assert f(9000, 1, 64, 128, 8192, 0) == 0        # prefix sums must fit in LDS
+    assert f(0, 1, 64, 128, 8192, 0) == 0
+    # the benchmark's extra caches: 512 rows x 512 over 32768 entries is 8 per entry
+    assert f(512, 1, 64, 128, 512, 32768) == 32768 * 1024
+    assert f(511, 1, 64, 128, 512, 32768) == 0      # just below 8 per entry
+    assert f(256, 1, 128, 128, 512, 32768) == 32768 * 1024   # two head blocks gather twice
+    assert f(256, 2, 64, 128, 512, 32768) == 32768 * 1024    # so do two query positions
+    assert f(512, 1, 64, 128, 8192, 1024) == big + 1024 * 1024
+    assert f(512, 1, 64, 128, 8192, 65537) == big   # a copy above 64 MiB is not made
 
 
 # --------------------------------------------------------------- GPU ----
@@ -485,8 +494,9 @@ def test_gpu_deterministic():
 
 # ------------------------------------------------------- GPU: split grid ----
 
-def _gpu_raw(w, workspace):
-    """Calls the C ABI directly, with or without a workspace."""
+def _gpu_raw(w, workspace, ws_bytes=None):
+    """Calls the C ABI directly, with or without a workspace (of the queried
+    size, or `ws_bytes`)."""
     from flaggems_vllm import _native
 
     d = w.to(DEV)
@@ -495,10 +505,13 @@ def _gpu_raw(w, workspace):
     lse = torch.empty(B, HQ, SQ, dtype=torch.float32, device=DEV)
     L = _native.lib()
     etopk = d.extra_indices.shape[-1] if d.extra_indices is not None else 0
-    nbytes = L.fgv_sparse_mla_decode_workspace_bytes(B, SQ, HQ, d.indices.shape[-1], etopk)
+    ek, ei = d.extra_k_cache, d.extra_indices
+    entries = ek.shape[0] * ek.shape[1] if ek is not None else 0
+    nbytes = L.fgv_sparse_mla_decode_workspace_bytes(B, SQ, HQ, d.indices.shape[-1], etopk, entries)
+    if ws_bytes is not None:
+        nbytes = ws_bytes
     ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=DEV) if workspace else None
     ptr = lambda t: t.data_ptr() if t is not None else None
-    ek, ei = d.extra_k_cache, d.extra_indices
     rc = L.fgv_sparse_mla_decode_model1(
         d.q.data_ptr(), d.q.stride(0), d.q.stride(1), d.q.stride(2),
         d.k_cache.data_ptr(), d.k_cache.stride(0), d.k_cache.shape[0], d.k_cache.shape[1],
@@ -547,3 +560,63 @@ def test_gpu_split_grid_against_oracle(case):
     out1, lse1, _ = _gpu_raw(w, workspace=False)
     _assert_within_bound(out1, o64, _vmax(w), case + " unsplit")
     assert torch.allclose(lse1.double()[fin], lse.double()[fin], rtol=1e-6, atol=1e-6)
+
+
+# ------------------------------------------------- GPU: expanded extra cache ----
+
+def _expanded_case():
+    """An extra cache of 256 entries gathered 16 x 512 times (32 per entry), with
+    per-row lengths, repeated entries and entries that are not attended
+    (negative, past the cache): short enough to stay unsplit."""
+    w = W.make_mla_workload(batch=16, topk=64, num_pages=8, extra_topk=512, extra_page=64, extra_pages=4,
+                            seed=41, q_scale=0.1)
+    g = torch.Generator().manual_seed(7)
+    ei = w.extra_indices.clone()
+    flat = ei.view(-1)
+    pick = torch.randperm(flat.numel(), generator=g)[:400]
+    flat[pick[:200]] = -1
+    flat[pick[200:300]] = 256 + torch.randint(0, 1000, (100,), generator=g, dtype=torch.int32)
+    flat[pick[300:]] = 5  # a repeated entry
+    w.extra_indices = ei
+    return w
+
+
+@pytest.mark.gpu
+def test_gpu_expanded_extra_cache_bit_exact():
+    """The extra cache dequantised once into bf16 rows gives the same bits as
+    dequantising each gathered chunk: same K rows, same order of operations."""
+    from flaggems_vllm import _native
+
+    print("\n[case] sparse MLA expanded extra cache vs in-chunk dequantisation", flush=True)
+    w = _expanded_case()
+    B, SQ, HQ, _ = w.q.shape
+    need = _native.lib().fgv_sparse_mla_decode_workspace_bytes(B, SQ, HQ, w.indices.shape[-1],
+                                                               w.extra_indices.shape[-1], 256)
+    assert need == 256 * 1024, "the case must take the expanded route and no split"
+    out_x, lse_x, _ = _gpu_raw(w, workspace=True)
+    out_d, lse_d, _ = _gpu_raw(w, workspace=False)
+    assert torch.equal(out_x.view(torch.int16), out_d.view(torch.int16))
+    assert torch.equal(lse_x, lse_d)
+    o64, l64 = _oracle(w)
+    _assert_within_bound(out_x, o64, _vmax(w), "expanded")
+
+
+@pytest.mark.gpu
+def test_gpu_split_grid_expanded_matches_split_alone():
+    """The split schedule over an expanded extra cache (segments starting on
+    even and odd extra chunks) gives the same bits as the split schedule with a
+    workspace too small for the copy, which dequantises in the chunk loop."""
+    from flaggems_vllm import _native
+
+    print("\n[case] sparse MLA split grid, expanded vs not", flush=True)
+    w = _split_case("long")
+    B, SQ, HQ, _ = w.q.shape
+    f = _native.lib().fgv_sparse_mla_decode_workspace_bytes
+    entries = w.extra_k_cache.shape[0] * w.extra_k_cache.shape[1]
+    split_only = f(B, SQ, HQ, w.indices.shape[-1], w.extra_indices.shape[-1], 0)
+    both = f(B, SQ, HQ, w.indices.shape[-1], w.extra_indices.shape[-1], entries)
+    assert both == split_only + entries * 1024 and split_only > 0
+    out_x, lse_x, _ = _gpu_raw(w, workspace=True)
+    out_s, lse_s, _ = _gpu_raw(w, workspace=True, ws_bytes=split_only)
+    assert torch.equal(out_x.view(torch.int16), out_s.view(torch.int16))
+    assert torch.equal(lse_x, lse_s)
