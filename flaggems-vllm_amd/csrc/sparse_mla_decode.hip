@@ -27,11 +27,10 @@
 //         256); the probabilities, rounded to bf16, are the B operand of
 //       O^T += V^T P^T, whose A operand (V^T = K^T) is read from the same K
 //         tile with ds_read_b64_tr_b16 transposing loads.
-// K tile rows are 1056 bytes apart (1024 + 32) and bit 0 of the 16-byte block
-// index is flipped in rows 8..15 of every 16, so that the 16-lane row reads
-// of QK, the 32-lane transposing reads of PV and the dequantising writes are
-// all free of LDS bank conflicts (256 bytes per LDS cycle), while each
-// lane's QK and PV addresses stay one base plus constant offsets.  Entries that are
+// K tile rows are 1056 bytes apart (1024 + 32), so that the row reads of QK,
+// the transposing reads of PV and the row writes are all free of LDS bank
+// conflicts (measured), while each lane's QK and PV addresses stay one base
+// plus constant offsets.  Entries that are
 // not attended (past the top-k length, negative, or past the cache) are
 // gathered from a zero page, and their scores masked to -inf.
 #include <math.h>
@@ -100,18 +99,19 @@ struct MlaArgs {
     int32_t split_grid;
 };
 
-// K tile addressing: 16-byte block b of row r at r * kKRowBytes + 16 (b ^ x(r)),
-// x(r) = bit 3 of r.  In 16-byte bank groups (mod 16) row r starts at 2r, so
-//   - QK, 16 lanes reading block c of rows 0..15: groups 2r + (c ^ x(r)) are
-//     16 distinct values (rows r and r+8 differ in x, hence in parity);
-//   - PV, 32 lanes reading blocks {2d, 2d+1} of rows 0..7 (or 8..15): the
-//     pairs {2r + 2d, 2r + 2d + 1} are 8 disjoint pairs;
-//   - dequantisation, 16 lanes writing 16 consecutive blocks of one row:
-//     distinct.
+// K tile addressing: 16-byte block b of row r at r * kKRowBytes + 16 b, rows
+// 1056 bytes apart.  Measured with the LDS bank-conflict counter on gfx950
+// (one wave, each access pattern alone): QK's ds_read_b128 (lane (m, g) reads
+// block 4s+g of row m) and PV's ds_read_b64_tr_b16 (lane j of group g reads
+// row 4g + j/4) are both conflict-free at this pitch.  Flipping block bit 0 in
+// rows 8..15 (a swizzle meant for 16-lane ds_read_b128 passes) made half of
+// QK's LDS cycles conflicts; pitches of 1040, 1072, 1088 or 1152 bytes
+// conflict in both.  The dequantising writes and the row DMAs write whole
+// rows, which is conflict-free at any pitch.
 constexpr int kKRowBytes = kHeadDim * 2 + 32;
 
 __device__ __forceinline__ int kbuf_byte(int row, int block) {
-    return row * kKRowBytes + ((block ^ ((row >> 3) & 1)) << 4);
+    return row * kKRowBytes + (block << 4);
 }
 
 // 8 e4m3 codes times 2^(byte - 127) -> 8 bf16, as the reference computes
@@ -246,14 +246,13 @@ __device__ __forceinline__ void issue_gather(const ListView& v, const uint8_t* d
 // A chunk of an expanded list (bf16 rows, 1 KiB per entry) straight into a K
 // tile, with no dequantisation: wave w moves entries 8w..8w+7, one row per
 // wave-wide 16-byte LDS DMA (64 lanes x 16 bytes land contiguously at the row's
-// start).  The tile's block swizzle is applied on the source side: lane l
-// fetches block l ^ x of the entry, x = bit 3 of the row = bit 0 of w.  Each
-// row's index comes from lane 8j (load_id's layout); entries that are not
-// attended come from the zero page, and the mask is written as for a gather.
+// start, lane l's block l).  Each row's index comes from lane 8j (load_id's
+// layout); entries that are not attended come from the zero page, and the
+// mask is written as for a gather.
 __device__ __forceinline__ void issue_rows(const ListView& v, int wave, int lane, int id, uint8_t* tile,
                                            float* mask) {
     __attribute__((address_space(3))) uint8_t* dst = (__attribute__((address_space(3))) uint8_t*)tile;
-    const int src_off = 16 * (lane ^ (wave & 1));
+    const int src_off = 16 * lane;
 #pragma unroll
     for (int j = 0; j < kChunk / 4; ++j) {
         const int idj = __builtin_amdgcn_readlane(id, 8 * j);
@@ -405,8 +404,7 @@ __device__ __forceinline__ void run_segment(const MlaArgs& a, uint8_t (&raw)[2][
     // LDS byte offsets of this lane's K-tile reads.  QK: block 4s+g of row
     // m16 (then row 16+m16).  PV: lane j of group g points at row 4g + j/4,
     // dims 16dt + 4(j%4), i.e. block 2dt + (j%4)/2, byte 8(j%2) (then row
-    // 16 + 4g + j/4).  The flip touches only block bit 0, so s and dt enter as
-    // constant offsets 64 s and 32 dt.
+    // 16 + 4g + j/4).  s and dt enter as constant offsets 64 s and 32 dt.
     const int qk_base = kbuf_byte(m16, g);
     const int tr_row = 4 * g + (m16 >> 2);
     const int tr_base = kbuf_byte(tr_row, (m16 & 3) >> 1) + 8 * (m16 & 1);
