@@ -27,6 +27,11 @@
 //         256); the probabilities, rounded to bf16, are the B operand of
 //       O^T += V^T P^T, whose A operand (V^T = K^T) is read from the same K
 //         tile with ds_read_b64_tr_b16 transposing loads.
+// An extra list that is gathered many times per cache entry can instead be
+// dequantised once per call into bf16 rows in the workspace
+// (mla_expand_cache_kernel); its chunks are then DMA'd straight into a K tile,
+// alternating between the K tile and the (then idle) raw gather buffers, with
+// no conversion and one barrier per chunk.
 // K tile rows are 1056 bytes apart (1024 + 32), so that the row reads of QK,
 // the transposing reads of PV and the row writes are all free of LDS bank
 // conflicts (measured), while each lane's QK and PV addresses stay one base
