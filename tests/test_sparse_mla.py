@@ -564,12 +564,12 @@ def test_gpu_split_grid_against_oracle(case):
 
 # ------------------------------------------------- GPU: expanded extra cache ----
 
-def _expanded_case():
+def _expanded_case(heads=64, seq_q=1):
     """An extra cache of 256 entries gathered 16 x 512 times (32 per entry), with
     per-row lengths, repeated entries and entries that are not attended
     (negative, past the cache): short enough to stay unsplit."""
     w = W.make_mla_workload(batch=16, topk=64, num_pages=8, extra_topk=512, extra_page=64, extra_pages=4,
-                            seed=41, q_scale=0.1)
+                            heads=heads, seq_q=seq_q, seed=41, q_scale=0.1)
     g = torch.Generator().manual_seed(7)
     ei = w.extra_indices.clone()
     flat = ei.view(-1)
@@ -582,13 +582,15 @@ def _expanded_case():
 
 
 @pytest.mark.gpu
-def test_gpu_expanded_extra_cache_bit_exact():
+@pytest.mark.parametrize("heads,seq_q", [(64, 1), (128, 2)])
+def test_gpu_expanded_extra_cache_bit_exact(heads, seq_q):
     """The extra cache dequantised once into bf16 rows gives the same bits as
     dequantising each gathered chunk: same K rows, same order of operations."""
     from flaggems_vllm import _native
 
-    print("\n[case] sparse MLA expanded extra cache vs in-chunk dequantisation", flush=True)
-    w = _expanded_case()
+    print(f"\n[case] sparse MLA expanded extra cache vs in-chunk dequantisation H={heads} SQ={seq_q}",
+          flush=True)
+    w = _expanded_case(heads, seq_q)
     B, SQ, HQ, _ = w.q.shape
     need = _native.lib().fgv_sparse_mla_decode_workspace_bytes(B, SQ, HQ, w.indices.shape[-1],
                                                                w.extra_indices.shape[-1], 256)
