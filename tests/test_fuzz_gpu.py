@@ -203,3 +203,58 @@ def test_fuzz_dequantize_and_gather(case):
                                                 offset)
     torch.cuda.synchronize()
     assert torch.equal(od.cpu().view(torch.int16), ref.view(torch.int16))
+
+
+# ------------------------------------------------------------- sparse MLA ----
+
+@pytest.mark.parametrize("case", range(12))
+def test_fuzz_sparse_mla(case):
+    """Random MODEL1 decode cases (rows, heads, query positions, top-k and its
+    lengths, an extra list of another page size, the sink, entries that are not
+    attended), with and without a workspace: both within the bound of the
+    binary64 oracle, and when the extra cache is expanded without a split, the
+    two routes agree bit for bit."""
+    from flaggems_vllm import _native
+
+    from .test_sparse_mla import _assert_within_bound, _gpu_raw, _oracle, _vmax
+
+    g = torch.Generator().manual_seed(6000 + case)
+    batch = _rand(g, 1, 6)
+    heads = _pick(g, [64, 64, 128])
+    seq_q = _pick(g, [1, 1, 2])
+    topk = _pick(g, [1, 7, 64, 130, 300])
+    num_pages = _pick(g, [1, 4, 16])
+    extra = _pick(g, [False, True, True])
+    extra_topk = _pick(g, [1, 40, 256, 600, 2100]) if extra else 0   # 2100: the split schedule
+    extra_page = _pick(g, [2, 16, 64])
+    extra_pages = _rand(g, 1, 40)
+    lengths = _pick(g, [False, True])
+    sink = _pick(g, [False, True])
+    q_scale = _pick(g, [0.1, 1.0])
+    _say(f"fuzz MLA {case}: B={batch} H={heads} SQ={seq_q} topk={topk} pages={num_pages} extra={extra_topk}"
+         f"x{extra_page}/{extra_pages} lengths={lengths} sink={sink} q_scale={q_scale}")
+    w = W.make_mla_workload(batch=batch, topk=topk, num_pages=num_pages, heads=heads, seq_q=seq_q,
+                            extra_topk=extra_topk, extra_page=extra_page, extra_pages=extra_pages,
+                            topk_length=lengths, sink=sink, seed=7000 + case, q_scale=q_scale)
+    # entries that are not attended: negative, or past the cache
+    for idx, entries in ((w.indices, num_pages * 64),
+                         (w.extra_indices, extra_pages * extra_page if extra else 0)):
+        if idx is None:
+            continue
+        flat = idx.view(-1)
+        pick = torch.rand(flat.numel(), generator=g)
+        flat[pick < 0.05] = -1
+        flat[(pick >= 0.05) & (pick < 0.08)] = entries + 3
+    o64, l64 = _oracle(w)
+    vm = _vmax(w)
+    out_w, lse_w, nbytes = _gpu_raw(w, workspace=True)
+    out_n, lse_n, _ = _gpu_raw(w, workspace=False)
+    for out, lse, what in ((out_w, lse_w, "workspace"), (out_n, lse_n, "no workspace")):
+        _assert_within_bound(out, o64, vm, what)
+        fin = torch.isfinite(l64)
+        assert torch.equal(torch.isfinite(lse), fin), what
+        assert torch.allclose(lse.double()[fin], l64[fin], rtol=1e-5, atol=1e-5), what
+    split_only = _native.lib().fgv_sparse_mla_decode_workspace_bytes(batch, seq_q, heads, topk, extra_topk, 0)
+    if nbytes > 0 and split_only == 0:  # expanded, not split: the same order of operations
+        assert torch.equal(out_w.view(torch.int16), out_n.view(torch.int16))
+        assert torch.equal(lse_w, lse_n)
