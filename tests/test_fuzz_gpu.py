@@ -258,3 +258,63 @@ def test_fuzz_sparse_mla(case):
     if nbytes > 0 and split_only == 0:  # expanded, not split: the same order of operations
         assert torch.equal(out_w.view(torch.int16), out_n.view(torch.int16))
         assert torch.equal(lse_w, lse_n)
+
+
+# ---------------------------------------------------------------- rmsnorm ----
+
+@pytest.mark.parametrize("case", CASES)
+def test_fuzz_q_kv_rmsnorm(case):
+    import flaggems_vllm
+
+    g = torch.Generator().manual_seed(8000 + case)
+    T = _pick(g, [1, 2, 17, 300, 1025])
+    qd, kd = 8 * _rand(g, 1, 512), 8 * _rand(g, 1, 512)   # row sizes: multiples of 8 up to 4096
+    wdtype = _pick(g, [torch.bfloat16, torch.float32])
+    q_gap, k_gap = 8 * _pick(g, [0, 0, 3]), 8 * _pick(g, [0, 0, 5])
+    eps = _pick(g, [1e-6, 1e-5])
+    scale = _pick(g, [1.0, 1e-3, 200.0])
+    _say(f"fuzz rmsnorm {case}: T={T} q={qd} kv={kd} w={wdtype} gaps={q_gap},{k_gap} scale={scale}")
+    qr = (W.randn_bf16((T, qd), g).float() * scale).to(torch.bfloat16)
+    kv = W.randn_bf16((T, kd), g)
+    qw, kw = W.randn_bf16((qd,), g).to(wdtype), W.randn_bf16((kd,), g).to(wdtype)
+    rq, rk = oracle.fused_q_kv_rmsnorm(qr, kv, qw, kw, eps)
+    qrd, _, _ = _placed(qr, (qd + q_gap, 1), 0, 12 + case)
+    kvd, _, _ = _placed(kv, (kd + k_gap, 1), 0, 13 + case)
+    qo, ko = flaggems_vllm.fused_q_kv_rmsnorm(qrd, kvd, qw.to(DEV), kw.to(DEV), eps)
+    torch.cuda.synchronize()
+    assert torch.equal(qo.cpu().view(torch.int16), rq.view(torch.int16))
+    assert torch.equal(ko.cpu().view(torch.int16), rk.view(torch.int16))
+
+
+# ----------------------------------------------------------- slot mapping ----
+
+@pytest.mark.parametrize("case", CASES)
+def test_fuzz_slot_mapping(case):
+    import flaggems_vllm
+
+    g = torch.Generator().manual_seed(9000 + case)
+    nreq = _rand(g, 1, 40)
+    bs = _pick(g, [1, 16, 64, 128])
+    cpw = _pick(g, [1, 1, 2, 4])
+    rank = _rand(g, 0, cpw - 1)
+    il = _pick(g, [1, 1, 2, 16])
+    lens = torch.randint(0, 120, (nreq,), generator=g)
+    qsl = torch.zeros(nreq + 1, dtype=torch.int32)
+    qsl[1:] = torch.cumsum(lens, 0).to(torch.int32)
+    n = int(qsl[-1])
+    starts = torch.randint(0, 5000, (nreq,), generator=g)
+    pos = torch.cat([s + torch.arange(int(k)) for s, k in zip(starts.tolist(), lens.tolist())] +
+                    [torch.zeros(0, dtype=torch.int64)]).to(_pick(g, [torch.int32, torch.int64]))
+    maxb = (5200 + bs * cpw - 1) // (bs * cpw)
+    bt = torch.randint(0, 1 << 20, (nreq, maxb), generator=g, dtype=torch.int32)
+    max_tokens = n + _pick(g, [0, 1, 37])
+    pad = _pick(g, [-1, 0, -7])
+    _say(f"fuzz slot mapping {case}: reqs={nreq} tokens={n} bs={bs} cp={cpw}/{rank} il={il} pad={pad}")
+    kw = dict(cp_world_size=cpw, cp_rank=rank, cp_kv_cache_interleave_size=il, pad_id=pad)
+    want = torch.full((max_tokens + 3,), -99, dtype=torch.int64)
+    oracle.compute_slot_mapping(n, max_tokens, qsl, nreq, pos, bt, want, bs, **kw)
+    got = torch.full((max_tokens + 3,), -99, dtype=torch.int64, device=DEV)
+    flaggems_vllm.compute_slot_mapping_parallel(n, max_tokens, qsl.to(DEV), nreq, pos.to(DEV), bt.to(DEV), got, bs,
+                                                **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(got.cpu(), want)
