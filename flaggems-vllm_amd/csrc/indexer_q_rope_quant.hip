@@ -64,68 +64,71 @@ __device__ __forceinline__ int fp8_row_exponent(uint32_t amax_bits) {
     return (int)(a >> 23) - 127 - 8 + ((a & 0x7fffffu) > 0x600000u ? 1 : 0);
 }
 
-// Eight values (already scaled into [-6, 6]) -> eight E2M1 nibbles, element i
-// in bits 4i..4i+3 (even element in the low nibble of each byte), RNE.
-__device__ __forceinline__ uint32_t pack_fp4x8(const float (&x)[8]) {
-    uint32_t w = 0;
-    w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, x[0], x[1], 1.0f, 0);
-    w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, x[2], x[3], 1.0f, 1);
-    w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, x[4], x[5], 1.0f, 2);
-    w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, x[6], x[7], 1.0f, 3);
-    return w;
-}
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef short short2_t __attribute__((ext_vector_type(2)));
+typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
 
-// bf16 pieces of one row -> binary32, with the GPT-J rotation applied on
-// lanes 8..15 of the last piece: x_even*cos - x_odd*sin, x_odd*cos +
-// x_even*sin, each rounded to binary32 and the result to bf16 (reference
-// kernel :113-123).
+// One row's values stay packed bf16 words (element 2i in the low half of word
+// i): lanes 8..15 rotate the 4 (even, odd) pairs of their last piece with
+// GPT-J RoPE, x_even*cos - x_odd*sin, x_odd*cos + x_even*sin, each product and
+// sum rounded to binary32 and the result to bf16 (reference kernel :113-123),
+// and the other lanes keep the loaded words.
 template <int kPieces>
-__device__ __forceinline__ void unpack_rope(const uint4 (&v)[kPieces], float4 c, float4 s, int lane16,
-                                            float (&xf)[kPieces][8]) {
+__device__ __forceinline__ void rope_words(const uint4 (&v)[kPieces], float4 c, float4 s, int lane16,
+                                           uint32_t (&w)[kPieces][4]) {
 #pragma unroll
     for (int p = 0; p < kPieces; ++p) {
-        const uint32_t w4[4] = {v[p].x, v[p].y, v[p].z, v[p].w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            xf[p][2 * i] = bf16_lo(w4[i]);
-            xf[p][2 * i + 1] = bf16_hi(w4[i]);
-        }
+        w[p][0] = v[p].x; w[p][1] = v[p].y; w[p][2] = v[p].z; w[p][3] = v[p].w;
     }
     if (lane16 >= 8) {
-        float* r = xf[kPieces - 1];
+        uint32_t* r = w[kPieces - 1];
         const float cc[4] = {c.x, c.y, c.z, c.w}, ss[4] = {s.x, s.y, s.z, s.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const float e = r[2 * i], o = r[2 * i + 1];
+            const float e = bf16_lo(r[i]), o = bf16_hi(r[i]);
             const float ec = e * cc[i], os = o * ss[i], oc = o * cc[i], es = e * ss[i];
-            const uint32_t w = pack_bf16x2(ec - os, oc + es);
-            r[2 * i] = bf16_lo(w);
-            r[2 * i + 1] = bf16_hi(w);
+            r[i] = pack_bf16x2(ec - os, oc + es);
         }
     }
+}
+
+// Binary32 bits of the largest |value| among `n` packed bf16 words: the bf16
+// magnitudes compare as integers (two per v_pk_max_u16) and, shifted up 16
+// bits, are the binary32 patterns of the same values.
+template <int n>
+__device__ __forceinline__ uint32_t absmax_bits(const uint32_t* w) {
+    u16x2_t m = {0, 0};
+#pragma unroll
+    for (int i = 0; i < n; ++i)
+        m = __builtin_elementwise_max(m, __builtin_bit_cast(u16x2_t, w[i] & 0x7fff7fffu));
+    return (uint32_t)(m.x > m.y ? m.x : m.y) << 16;
+}
+
+// Two bf16 pairs -> four e4m3 codes, each value divided by `scale` (2^k) inside
+// v_cvt_scalef32_pk_fp8_bf16.  For every bf16 value and every k the row
+// exponent takes (-22..120) with |x / 2^k| <= 448, this gives the same code as
+// e4m3(med3(f32(x) * 2^-k, -448, 448)) (checked exhaustively on gfx950), and
+// k makes every value of the row that small.
+__device__ __forceinline__ uint32_t fp8x4_scaled(uint32_t a, uint32_t b, float scale) {
+    short2_t r = {0, 0};
+    r = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(r, __builtin_bit_cast(bf16x2_t, a), scale, false);
+    r = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(r, __builtin_bit_cast(bf16x2_t, b), scale, true);
+    return __builtin_bit_cast(uint32_t, r);
 }
 
 // FP8: the row's UE8M0 exponent k (one 16-lane max) and each piece's eight
 // e4m3 codes as two words.
 template <int kPieces>
-__device__ __forceinline__ int fp8_codes(const float (&xf)[kPieces][8], uint32_t (&lo)[kPieces],
+__device__ __forceinline__ int fp8_codes(const uint32_t (&w)[kPieces][4], uint32_t (&lo)[kPieces],
                                          uint32_t (&hi)[kPieces]) {
-    uint32_t m = 0;
-#pragma unroll
-    for (int p = 0; p < kPieces; ++p)
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-            m = max(m, __float_as_uint(xf[p][i]) & 0x7fffffffu);
+    uint32_t m = absmax_bits<4 * kPieces>(&w[0][0]);
     m = row16_max(m);
     const int k = fp8_row_exponent(m);
-    const float inv = exp2_neg_int(k);
+    const float scale = __uint_as_float((uint32_t)(k + 127) << 23);
 #pragma unroll
     for (int p = 0; p < kPieces; ++p) {
-        const float* y = xf[p];
-        lo[p] = pack_fp8x4(clamp_fp8(y[0] * inv), clamp_fp8(y[1] * inv), clamp_fp8(y[2] * inv),
-                           clamp_fp8(y[3] * inv));
-        hi[p] = pack_fp8x4(clamp_fp8(y[4] * inv), clamp_fp8(y[5] * inv), clamp_fp8(y[6] * inv),
-                           clamp_fp8(y[7] * inv));
+        lo[p] = fp8x4_scaled(w[p][0], w[p][1], scale);
+        hi[p] = fp8x4_scaled(w[p][2], w[p][3], scale);
     }
     return k;
 }
@@ -139,27 +142,28 @@ __device__ __forceinline__ float fp8_weight(float w_in, int k, const IndexerArgs
 }
 
 // MXFP4: 32-element blocks are lane quads (4 lanes x 8 elements).  Per piece,
-// this lane's eight E2M1 nibbles and, on lane 0 of the row, the piece's four
-// block exponents (lanes 0, 4, 8, 12) as one word, so they leave in one 32-bit
-// store instead of four byte stores.
+// this lane's eight E2M1 nibbles, each value divided by the block's 2^k inside
+// v_cvt_scalef32_pk_fp4_bf16 (the same nibble as converting f32(x) * 2^-k at
+// scale 1, for every bf16 value and every k -124..125: checked exhaustively
+// on gfx950), and, on lane 0 of the row, the piece's four block exponents
+// (lanes 0, 4, 8, 12) as one word, so they leave in one 32-bit store instead
+// of four byte stores.
 template <int kPieces>
-__device__ __forceinline__ void fp4_codes(const float (&xf)[kPieces][8], uint32_t (&nib)[kPieces],
+__device__ __forceinline__ void fp4_codes(const uint32_t (&w)[kPieces][4], uint32_t (&nib)[kPieces],
                                           uint32_t (&word)[kPieces]) {
 #pragma unroll
     for (int p = 0; p < kPieces; ++p) {
-        uint32_t m = 0;
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-            m = max(m, __float_as_uint(xf[p][i]) & 0x7fffffffu);
+        uint32_t m = absmax_bits<4>(w[p]);
         m = max(m, dpp_u32<kDppQuadXor1>(m));
         m = max(m, dpp_u32<kDppQuadXor2>(m));
         const int k = mxfp4_exponent(m);
-        const float inv = exp2_neg_int(k);
-        float y[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-            y[i] = xf[p][i] * inv;
-        nib[p] = pack_fp4x8(y);
+        const float scale = __uint_as_float((uint32_t)(k + 127) << 23);
+        uint32_t r = 0;
+        r = __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(r, __builtin_bit_cast(bf16x2_t, w[p][0]), scale, 0);
+        r = __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(r, __builtin_bit_cast(bf16x2_t, w[p][1]), scale, 1);
+        r = __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(r, __builtin_bit_cast(bf16x2_t, w[p][2]), scale, 2);
+        r = __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(r, __builtin_bit_cast(bf16x2_t, w[p][3]), scale, 3);
+        nib[p] = r;
         const uint32_t e = (uint32_t)(k + 127) & 0xffu;
         word[p] = e | dpp_u32<kDppRowRor12>(e) << 8 | dpp_u32<kDppRowRor8>(e) << 16 | dpp_u32<kDppRowRor4>(e) << 24;
     }
@@ -177,12 +181,12 @@ template <int kPieces>
 __device__ __forceinline__ void indexer_row(const IndexerArgs& a, uint32_t t, uint32_t h,
                                             const uint4 (&v)[kPieces], float4 c, float4 s,
                                             float w_in, int lane16) {
-    float xf[kPieces][8];
-    unpack_rope<kPieces>(v, c, s, lane16, xf);
+    uint32_t xw[kPieces][4];
+    rope_words<kPieces>(v, c, s, lane16, xw);
     uint8_t* qo = a.q_out + (int64_t)t * a.qo_st + (int64_t)h * a.qo_sh;
     if (!a.fp4) {
         uint32_t lo[kPieces], hi[kPieces];
-        const int k = fp8_codes<kPieces>(xf, lo, hi);
+        const int k = fp8_codes<kPieces>(xw, lo, hi);
 #pragma unroll
         for (int p = 0; p < kPieces; ++p)
             store8(qo + (lane16 + 16 * p) * 8, lo[p], hi[p]);
@@ -192,7 +196,7 @@ __device__ __forceinline__ void indexer_row(const IndexerArgs& a, uint32_t t, ui
     }
     uint8_t* so = a.scale_out + (int64_t)t * a.so_st + (int64_t)h * a.so_sh;
     uint32_t nib[kPieces], word[kPieces];
-    fp4_codes<kPieces>(xf, nib, word);
+    fp4_codes<kPieces>(xw, nib, word);
 #pragma unroll
     for (int p = 0; p < kPieces; ++p) {
         *reinterpret_cast<uint32_t*>(qo + (lane16 + 16 * p) * 4) = nib[p];
@@ -317,11 +321,11 @@ indexer_token_kernel(IndexerArgs a) {
     for (int rr = 0; rr < kRows; ++rr) {
         const uint32_t hr = h + 16 * rr;
         const float w_in = __uint_as_float(a.w_f32 ? w_bits[rr] : w_bits[rr] << 16);
-        float xf[kPieces][8];
-        unpack_rope<kPieces>(v[rr], c, s, lane16, xf);
+        uint32_t xw[kPieces][4];
+        rope_words<kPieces>(v[rr], c, s, lane16, xw);
         if (!a.fp4) {
             uint32_t lo[kPieces], hi[kPieces];
-            const int k = fp8_codes<kPieces>(xf, lo, hi);
+            const int k = fp8_codes<kPieces>(xw, lo, hi);
 #pragma unroll
             for (int p = 0; p < kPieces; ++p)
                 store8(qo + (hr * qo_row + lane16 * 8 + p * 128), lo[p], hi[p]);
@@ -330,7 +334,7 @@ indexer_token_kernel(IndexerArgs a) {
         } else {
             uint8_t* so = a.scale_out + (int64_t)t * a.so_st;
             uint32_t nib[kPieces], word[kPieces];
-            fp4_codes<kPieces>(xf, nib, word);
+            fp4_codes<kPieces>(xw, nib, word);
 #pragma unroll
             for (int p = 0; p < kPieces; ++p) {
                 *reinterpret_cast<uint32_t*>(qo + (hr * qo_row + lane16 * 4 + p * 64)) = nib[p];
