@@ -157,14 +157,38 @@ def _exhaustive_rows(limit):
     return rows.view(nrow, 1, 128).to(torch.bfloat16)
 
 
+def _exhaustive_rows_at(limit, k):
+    """Like _exhaustive_rows at block exponent k: every bf16 value with
+    |v| <= limit * 2^k, 31 per 32-element block after one entry of exactly
+    limit * 2^k, so the row (FP8) or block (MXFP4) exponent is k."""
+    v = _all_bf16_finite()
+    top = limit * 2.0 ** k
+    v = v[v.abs() <= top]
+    per = 31
+    nblk = (v.numel() + per - 1) // per
+    vals = torch.zeros(nblk * per, dtype=torch.float64)
+    vals[:v.numel()] = v.double()
+    blocks = torch.cat([torch.full((nblk, 1), top, dtype=torch.float64), vals.view(nblk, per)], dim=1)
+    nrow = (nblk + 3) // 4
+    rows = torch.zeros(nrow * 4, 32, dtype=torch.float64)
+    rows[:nblk] = blocks
+    rows[nblk:, 0] = top
+    return rows.view(nrow, 1, 128).to(torch.bfloat16)
+
+
 @pytest.mark.gpu
-@pytest.mark.parametrize("use_fp4,limit", [(False, 448.0), (True, 6.0)])
-def test_gpu_converter_exhaustive(use_fp4, limit):
-    """Every bf16 value within range goes through the hardware e4m3 / E2M1
-    conversion at scale 1 (position 0: cos 1, sin 0, so RoPE is the
-    identity); codes must equal the oracle's software encoders."""
-    print(f"\n[case] indexer converter exhaustive fp4={use_fp4}", flush=True)
-    q = _exhaustive_rows(limit)
+@pytest.mark.parametrize("use_fp4,limit,k", [(False, 448.0, 0), (True, 6.0, 0),
+                                             (False, 448.0, -22), (False, 448.0, -7), (False, 448.0, 9),
+                                             (False, 448.0, 100), (True, 6.0, -124), (True, 6.0, -60),
+                                             (True, 6.0, 13), (True, 6.0, 125)])
+def test_gpu_converter_exhaustive(use_fp4, limit, k):
+    """Every bf16 value within range of block exponent k goes through the
+    hardware's scaled e4m3 / E2M1 conversion (position 0: cos 1, sin 0, so
+    RoPE is the identity); codes must equal the oracle's software encoders of
+    x * 2^-k, at the ends of the exponent ranges the quantisers produce
+    (FP8 -22..120, MXFP4 -124..125) and between."""
+    print(f"\n[case] indexer converter exhaustive fp4={use_fp4} k={k}", flush=True)
+    q = _exhaustive_rows(limit) if k == 0 else _exhaustive_rows_at(limit, k)
     T = q.shape[0]
     pos = torch.zeros(T, dtype=torch.int64)
     cs = W.make_cos_sin_cache(16)
