@@ -40,12 +40,19 @@ struct IndexerArgs {
     int w_f32, fp4;
 };
 
-__device__ __forceinline__ float4 load_cs4(const void* base, int64_t off, bool bf16) {
+// Two consecutive cos (or sin) values at element offset `off` (even).
+__device__ __forceinline__ float2 load_cs2(const void* base, int64_t off, bool bf16) {
     if (bf16) {
-        const uint2 v = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(base) + off);
-        return make_float4(bf16_lo(v.x), bf16_hi(v.x), bf16_lo(v.y), bf16_hi(v.y));
+        const uint32_t v = *reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(base) + off);
+        return make_float2(bf16_lo(v), bf16_hi(v));
     }
-    return *reinterpret_cast<const float4*>(static_cast<const float*>(base) + off);
+    return *reinterpret_cast<const float2*>(static_cast<const float*>(base) + off);
+}
+
+// The first of the two RoPE pairs this lane rotates (see rope_words): pairs
+// 4(l-8) and 4(l-8)+1 on lanes l = 8..15, pairs 4l+2 and 4l+3 on lanes l < 8.
+__device__ __forceinline__ int rope_pair0(int lane16) {
+    return lane16 >= 8 ? 4 * (lane16 - 8) : 4 * lane16 + 2;
 }
 
 // MXFP4 block exponent k = ceil(log2(max(amax, 6*2^-126) / 6)) from the
@@ -68,27 +75,38 @@ typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef short short2_t __attribute__((ext_vector_type(2)));
 typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
 
+// GPT-J rotation of one (even, odd) pair held as a packed bf16 word:
+// x_even*cos - x_odd*sin, x_odd*cos + x_even*sin, each product and sum rounded
+// to binary32 and the result to bf16 (reference kernel :113-123).
+__device__ __forceinline__ uint32_t rotate_pair(uint32_t word, float c, float s) {
+    const float e = bf16_lo(word), o = bf16_hi(word);
+    const float ec = e * c, os = o * s, oc = o * c, es = e * s;
+    return pack_bf16x2(ec - os, oc + es);
+}
+
 // One row's values stay packed bf16 words (element 2i in the low half of word
-// i): lanes 8..15 rotate the 4 (even, odd) pairs of their last piece with
-// GPT-J RoPE, x_even*cos - x_odd*sin, x_odd*cos + x_even*sin, each product and
-// sum rounded to binary32 and the result to bf16 (reference kernel :113-123),
-// and the other lanes keep the loaded words.
+// i).  The RoPE half is the last piece of lanes 8..15 (word i of lane l: pair
+// 4(l-8)+i).  All 16 lanes rotate two pairs each: lane l >= 8 its words 0 and
+// 1; lane j < 8 words 2 and 3 of lane j+8, fetched and returned with a row
+// rotation by 8.  c and s hold the lane's two pairs' cos and sin (rope_pair0).
 template <int kPieces>
-__device__ __forceinline__ void rope_words(const uint4 (&v)[kPieces], float4 c, float4 s, int lane16,
+__device__ __forceinline__ void rope_words(const uint4 (&v)[kPieces], float2 c, float2 s, int lane16,
                                            uint32_t (&w)[kPieces][4]) {
 #pragma unroll
     for (int p = 0; p < kPieces; ++p) {
         w[p][0] = v[p].x; w[p][1] = v[p].y; w[p][2] = v[p].z; w[p][3] = v[p].w;
     }
-    if (lane16 >= 8) {
-        uint32_t* r = w[kPieces - 1];
-        const float cc[4] = {c.x, c.y, c.z, c.w}, ss[4] = {s.x, s.y, s.z, s.w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float e = bf16_lo(r[i]), o = bf16_hi(r[i]);
-            const float ec = e * cc[i], os = o * ss[i], oc = o * cc[i], es = e * ss[i];
-            r[i] = pack_bf16x2(ec - os, oc + es);
-        }
+    uint32_t* r = w[kPieces - 1];
+    const bool rope_lane = lane16 >= 8;
+    const uint32_t f2 = dpp_u32<kDppRowRor8>(r[2]), f3 = dpp_u32<kDppRowRor8>(r[3]);
+    const uint32_t o0 = rotate_pair(rope_lane ? r[0] : f2, c.x, s.x);
+    const uint32_t o1 = rotate_pair(rope_lane ? r[1] : f3, c.y, s.y);
+    const uint32_t b0 = dpp_u32<kDppRowRor8>(o0), b1 = dpp_u32<kDppRowRor8>(o1);
+    if (rope_lane) {
+        r[0] = o0;
+        r[1] = o1;
+        r[2] = b0;
+        r[3] = b1;
     }
 }
 
@@ -179,7 +197,7 @@ __device__ __forceinline__ float fp4_weight(float w_in, const IndexerArgs& a) {
 // scales and weight.
 template <int kPieces>
 __device__ __forceinline__ void indexer_row(const IndexerArgs& a, uint32_t t, uint32_t h,
-                                            const uint4 (&v)[kPieces], float4 c, float4 s,
+                                            const uint4 (&v)[kPieces], float2 c, float2 s,
                                             float w_in, int lane16) {
     uint32_t xw[kPieces][4];
     rope_words<kPieces>(v, c, s, lane16, xw);
@@ -218,7 +236,6 @@ __global__ void __launch_bounds__(kThreads)
 indexer_q_rope_quant_kernel(IndexerArgs a) {
     constexpr int kRows = 4 / kPieces;
     const int lane16 = threadIdx.x & 15;
-    const bool rope_lane = lane16 >= 8;
     const uint32_t row0 = blockIdx.x * (kRowsPerBlock * kRows);
     uint32_t tt[kRows], hh[kRows];
     bool valid[kRows];
@@ -249,18 +266,17 @@ indexer_q_rope_quant_kernel(IndexerArgs a) {
             v[rr][p] = valid[rr] ? load16(x + (lane16 + 16 * p) * 8) : make_uint4(0, 0, 0, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
-    float4 c[kRows], s[kRows];
+    float2 c[kRows], s[kRows];
 #pragma unroll
     for (int rr = 0; rr < kRows; ++rr) {
-        c[rr] = s[rr] = make_float4(0.f, 0.f, 0.f, 0.f);
         if (kOneToken && rr > 0) {  // one token: the first row's cos/sin serve every row
             c[rr] = c[0];
             s[rr] = s[0];
-        } else if (rope_lane) {
+        } else {
             const int64_t pos = clamp_position(praw[rr], a.max_pos);
-            const int64_t off = pos * a.cs_stride + (lane16 - 8) * 4;
-            c[rr] = load_cs4(a.cos_sin, off, kCsBf16);
-            s[rr] = load_cs4(a.cos_sin, off + kHalfRope, kCsBf16);
+            const int64_t off = pos * a.cs_stride + rope_pair0(lane16);
+            c[rr] = load_cs2(a.cos_sin, off, kCsBf16);
+            s[rr] = load_cs2(a.cos_sin, off + kHalfRope, kCsBf16);
         }
     }
 #pragma unroll
@@ -308,12 +324,9 @@ indexer_token_kernel(IndexerArgs a) {
         for (int p = 0; p < kPieces; ++p)
             v[rr][p] = load16(qb + (q_off + rr * 16 * q_row + p * 256));
     __builtin_amdgcn_sched_barrier(0);
-    float4 c = make_float4(0.f, 0.f, 0.f, 0.f), s = c;
-    if (lane16 >= 8) {
-        const int64_t off = clamp_position(pos_raw, a.max_pos) * a.cs_stride + (lane16 - 8) * 4;
-        c = load_cs4(a.cos_sin, off, kCsBf16);
-        s = load_cs4(a.cos_sin, off + kHalfRope, kCsBf16);
-    }
+    const int64_t cs_off = clamp_position(pos_raw, a.max_pos) * a.cs_stride + rope_pair0(lane16);
+    const float2 c = load_cs2(a.cos_sin, cs_off, kCsBf16);
+    const float2 s = load_cs2(a.cos_sin, cs_off + kHalfRope, kCsBf16);
     uint8_t* qo = a.q_out + (int64_t)t * a.qo_st;
     float* wo = a.weights_out + (int64_t)t * a.wo_st;
     const uint32_t qo_row = (uint32_t)a.qo_sh;
