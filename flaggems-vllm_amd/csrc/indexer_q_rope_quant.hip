@@ -163,12 +163,10 @@ __device__ __forceinline__ float fp8_weight(float w_in, int k, const IndexerArgs
 // this lane's eight E2M1 nibbles, each value divided by the block's 2^k inside
 // v_cvt_scalef32_pk_fp4_bf16 (the same nibble as converting f32(x) * 2^-k at
 // scale 1, for every bf16 value and every k -124..125: checked exhaustively
-// on gfx950), and, on lane 0 of the row, the piece's four block exponents
-// (lanes 0, 4, 8, 12) as one word, so they leave in one 32-bit store instead
-// of four byte stores.
+// on gfx950), and its quad's UE8M0 byte k + 127.
 template <int kPieces>
 __device__ __forceinline__ void fp4_codes(const uint32_t (&w)[kPieces][4], uint32_t (&nib)[kPieces],
-                                          uint32_t (&word)[kPieces]) {
+                                          uint32_t (&ebyte)[kPieces]) {
 #pragma unroll
     for (int p = 0; p < kPieces; ++p) {
         uint32_t m = absmax_bits<4>(w[p]);
@@ -182,9 +180,14 @@ __device__ __forceinline__ void fp4_codes(const uint32_t (&w)[kPieces][4], uint3
         r = __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(r, __builtin_bit_cast(bf16x2_t, w[p][2]), scale, 2);
         r = __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(r, __builtin_bit_cast(bf16x2_t, w[p][3]), scale, 3);
         nib[p] = r;
-        const uint32_t e = (uint32_t)(k + 127) & 0xffu;
-        word[p] = e | dpp_u32<kDppRowRor12>(e) << 8 | dpp_u32<kDppRowRor8>(e) << 16 | dpp_u32<kDppRowRor4>(e) << 24;
+        ebyte[p] = (uint32_t)(k + 127) & 0xffu;
     }
+}
+
+// The four block bytes of a piece (lanes 0, 4, 8, 12) as one word on lane 0 of
+// the row, so they leave in one 32-bit store instead of four byte stores.
+__device__ __forceinline__ uint32_t exponent_word(uint32_t e) {
+    return e | dpp_u32<kDppRowRor12>(e) << 8 | dpp_u32<kDppRowRor8>(e) << 16 | dpp_u32<kDppRowRor4>(e) << 24;
 }
 
 // The MXFP4 weight (w * softmax_scale) * head_scale.
@@ -213,13 +216,14 @@ __device__ __forceinline__ void indexer_row(const IndexerArgs& a, uint32_t t, ui
         return;
     }
     uint8_t* so = a.scale_out + (int64_t)t * a.so_st + (int64_t)h * a.so_sh;
-    uint32_t nib[kPieces], word[kPieces];
-    fp4_codes<kPieces>(xw, nib, word);
+    uint32_t nib[kPieces], ebyte[kPieces];
+    fp4_codes<kPieces>(xw, nib, ebyte);
 #pragma unroll
     for (int p = 0; p < kPieces; ++p) {
         *reinterpret_cast<uint32_t*>(qo + (lane16 + 16 * p) * 4) = nib[p];
+        const uint32_t word = exponent_word(ebyte[p]);
         if (lane16 == 0)
-            *reinterpret_cast<uint32_t*>(so + 4 * p) = word[p];
+            *reinterpret_cast<uint32_t*>(so + 4 * p) = word;
     }
     if (lane16 == 0)
         a.weights_out[(int64_t)t * a.wo_st + h] = fp4_weight(w_in, a);
@@ -296,10 +300,18 @@ indexer_q_rope_quant_kernel(IndexerArgs a) {
 template <int kPieces, int kRows, bool kCsBf16>
 __global__ void __launch_bounds__(kThreads)
 indexer_token_kernel(IndexerArgs a) {
+    // The block's per-head weights (and MXFP4 exponent words) gather in LDS and
+    // leave as one contiguous run per block: from lane 0 of each row they would
+    // be 16-byte pieces per store instruction, which measured ~2 us on the
+    // DeepSeek-V4 shape for 2 MB of scales.
+    constexpr int kBlockRows = kRowsPerBlock * kRows;
+    __shared__ float w_lds[kBlockRows];
+    __shared__ uint32_t s_lds[kBlockRows * kPieces];  // byte 4 (row * kPieces + p) + quad
     const int lane16 = threadIdx.x & 15;
-    const uint32_t row0 = blockIdx.x * (kRowsPerBlock * kRows);
+    const uint32_t row0 = blockIdx.x * kBlockRows;
     const uint32_t t = row0 / a.num_heads;
-    const uint32_t h = row0 - t * a.num_heads + (threadIdx.x >> 4);  // rows h + 16 * rr
+    const uint32_t hb = row0 - t * a.num_heads;                  // the block's first head
+    const uint32_t h = hb + (threadIdx.x >> 4);                  // rows h + 16 * rr
     const int64_t pos_raw = a.positions[t];
     uint32_t w_bits[kRows];
     if (a.w_f32) {
@@ -328,11 +340,11 @@ indexer_token_kernel(IndexerArgs a) {
     const float2 c = load_cs2(a.cos_sin, cs_off, kCsBf16);
     const float2 s = load_cs2(a.cos_sin, cs_off + kHalfRope, kCsBf16);
     uint8_t* qo = a.q_out + (int64_t)t * a.qo_st;
-    float* wo = a.weights_out + (int64_t)t * a.wo_st;
     const uint32_t qo_row = (uint32_t)a.qo_sh;
 #pragma unroll
     for (int rr = 0; rr < kRows; ++rr) {
         const uint32_t hr = h + 16 * rr;
+        const int local = (threadIdx.x >> 4) + 16 * rr;
         const float w_in = __uint_as_float(a.w_f32 ? w_bits[rr] : w_bits[rr] << 16);
         uint32_t xw[kPieces][4];
         rope_words<kPieces>(v[rr], c, s, lane16, xw);
@@ -343,20 +355,30 @@ indexer_token_kernel(IndexerArgs a) {
             for (int p = 0; p < kPieces; ++p)
                 store8(qo + (hr * qo_row + lane16 * 8 + p * 128), lo[p], hi[p]);
             if (lane16 == 0)
-                wo[hr] = fp8_weight(w_in, k, a);
+                w_lds[local] = fp8_weight(w_in, k, a);
         } else {
-            uint8_t* so = a.scale_out + (int64_t)t * a.so_st;
-            uint32_t nib[kPieces], word[kPieces];
-            fp4_codes<kPieces>(xw, nib, word);
+            uint32_t nib[kPieces], ebyte[kPieces];
+            fp4_codes<kPieces>(xw, nib, ebyte);
 #pragma unroll
-            for (int p = 0; p < kPieces; ++p) {
+            for (int p = 0; p < kPieces; ++p)
                 *reinterpret_cast<uint32_t*>(qo + (hr * qo_row + lane16 * 4 + p * 64)) = nib[p];
-                if (lane16 == 0)
-                    *reinterpret_cast<uint32_t*>(so + (hr * (uint32_t)a.so_sh + p * 4)) = word[p];
+            if ((lane16 & 3) == 0) {
+                uint8_t* sb = reinterpret_cast<uint8_t*>(s_lds);
+#pragma unroll
+                for (int p = 0; p < kPieces; ++p)
+                    sb[4 * (local * kPieces + p) + (lane16 >> 2)] = (uint8_t)ebyte[p];
             }
             if (lane16 == 0)
-                wo[hr] = fp4_weight(w_in, a);
+                w_lds[local] = fp4_weight(w_in, a);
         }
+    }
+    __syncthreads();
+    if (threadIdx.x < kBlockRows)
+        a.weights_out[(int64_t)t * a.wo_st + hb + threadIdx.x] = w_lds[threadIdx.x];
+    if (a.fp4 && threadIdx.x < kBlockRows * kPieces) {
+        const uint32_t r = threadIdx.x / kPieces, p = threadIdx.x % kPieces;
+        uint8_t* so = a.scale_out + (int64_t)t * a.so_st;
+        *reinterpret_cast<uint32_t*>(so + ((hb + r) * (uint32_t)a.so_sh + p * 4)) = s_lds[threadIdx.x];
     }
 }
 
