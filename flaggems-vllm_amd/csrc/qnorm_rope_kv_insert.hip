@@ -34,6 +34,14 @@ constexpr int kRowsPerPass = kThreads / 16;   // 16 rows per pass
 // block (more loads per wave, fewer waves) measured slower.
 constexpr int kQRowsPerBlock = kRowsPerPass;
 constexpr int kKvTokensPerBlock = kRowsPerPass;
+// Dynamic LDS reserved per workgroup (the kernel uses none) to cap the launch
+// at four workgroups, 16 waves, per CU (160 KiB of LDS).  Each wave keeps 4 KiB
+// of loads in flight; with all 32 wave slots of a CU filled the GPU has ~32 MB
+// of rows in flight, which measured slower than ~16 MB (c2 168.7 -> 165.5 us,
+// c4 1266 -> 1225 us; five per CU the same, three slower).  An in-place stream
+// probe with four loads per lane showed the same, and the one-load-per-lane
+// stream the probe peaks with fills every slot.
+constexpr size_t kOccupancyLds = 40 * 1024;
 
 struct QnormArgs {
     uint16_t* q;
@@ -374,13 +382,13 @@ extern "C" int fgv_qnorm_rope_kv_rope_quant_insert(
         return fail(FGV_E_TOO_LARGE, "grid exceeds 2^31 - 1 workgroups");
     const hipStream_t st = static_cast<hipStream_t>(stream);
     if (map == kMapAligned)
-        hipLaunchKernelGGL(qnorm_rope_kv_insert_kernel<kMapAligned>, dim3((uint32_t)grid), dim3(kThreads), 0,
-                           st, a);
+        hipLaunchKernelGGL(qnorm_rope_kv_insert_kernel<kMapAligned>, dim3((uint32_t)grid), dim3(kThreads),
+                           kOccupancyLds, st, a);
     else if (map == kMapRowsOneToken)
         hipLaunchKernelGGL(qnorm_rope_kv_insert_kernel<kMapRowsOneToken>, dim3((uint32_t)grid),
-                           dim3(kThreads), 0, st, a);
+                           dim3(kThreads), kOccupancyLds, st, a);
     else
-        hipLaunchKernelGGL(qnorm_rope_kv_insert_kernel<kMapRows>, dim3((uint32_t)grid), dim3(kThreads), 0,
-                           st, a);
+        hipLaunchKernelGGL(qnorm_rope_kv_insert_kernel<kMapRows>, dim3((uint32_t)grid), dim3(kThreads),
+                           kOccupancyLds, st, a);
     return launch_status();
 }
