@@ -23,6 +23,11 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kRowsPerBlock = kThreads / 16;
+// Dynamic LDS reserved per workgroup (the kernel uses none) to cap the launch
+// at four workgroups, 16 waves, per CU (160 KiB of LDS).  On c2's 114,967
+// whole-sequence rows: none 34.0 us, 24 KiB 33.3, 32-40 KiB 32.5, 52 KiB 34.4,
+// 64 KiB and above 39.6.
+constexpr size_t kOccupancyLds = 40 * 1024;
 
 struct GatherArgs {
     uint16_t* out;
@@ -189,10 +194,10 @@ extern "C" int fgv_dequantize_and_gather_k_cache(
                       scale_slots == kScaleBytesPerToken;
     const dim3 grid((unsigned)((rows_bound + kRowsPerBlock - 1) / kRowsPerBlock), (unsigned)num_reqs);
     if (dsv4)
-        hipLaunchKernelGGL(dequantize_gather_kernel<true>, grid, dim3(kThreads), 0,
+        hipLaunchKernelGGL(dequantize_gather_kernel<true>, grid, dim3(kThreads), kOccupancyLds,
                            static_cast<hipStream_t>(stream), a);
     else
-        hipLaunchKernelGGL(dequantize_gather_kernel<false>, grid, dim3(kThreads), 0,
+        hipLaunchKernelGGL(dequantize_gather_kernel<false>, grid, dim3(kThreads), kOccupancyLds,
                            static_cast<hipStream_t>(stream), a);
     return launch_status();
 }

@@ -5,9 +5,9 @@
 //   y = (x * rsqrt(mean(x^2) + eps)) * w, stored in x's dtype (bf16).
 //
 // Layout: a row of up to 512 elements is one 16-lane DPP row (fgv_device.h),
-// a longer one a whole wave; lane l owns the 16-byte pieces l + L*j of its
-// row, so DeepSeek-V4's 1536-wide q row is 3 pieces on each of 64 lanes and
-// its 512-wide kv row 4 pieces on each of 16 lanes, keeping 8 waves per SIMD.
+// one of up to 1536 a half wave, a longer one a whole wave; lane l owns the
+// 16-byte pieces l + L*j of its row, so DeepSeek-V4's 1536-wide q row is 6
+// pieces on each of 32 lanes and its 512-wide kv row 4 pieces on each of 16.
 // Workgroups [0, q_blocks) take q rows, the rest kv rows.  As in the main op
 // the sum of squares is exact in binary64 and mean and rsqrt are correctly
 // rounded, so results do not depend on the reduction order.
@@ -55,8 +55,15 @@ __device__ __forceinline__ double wave_sum(double v) {
     return v;
 }
 
+// Sum over each 32-lane half of the wave.
+__device__ __forceinline__ double half_wave_sum(double v) {
+    v = row16_sum(v);
+    v += __shfl_xor(v, 16);
+    return v;
+}
+
 // One row of kPieces * 16-byte pieces per lane over kLanes lanes (16: a DPP
-// row, 64: the whole wave).
+// row, 32: a half wave, 64: the whole wave).
 template <int kPieces, int kLanes>
 __device__ __forceinline__ void rms_row(const RmsArgs& a, int which, uint32_t row, int lane) {
     if (row >= a.num_rows)
@@ -83,7 +90,7 @@ __device__ __forceinline__ void rms_row(const RmsArgs& a, int which, uint32_t ro
             s = __builtin_fma(hi, hi, s);
         }
     }
-    s = kLanes == 64 ? wave_sum(s) : row16_sum(s);
+    s = kLanes == 64 ? wave_sum(s) : kLanes == 32 ? half_wave_sum(s) : row16_sum(s);
     float var = (float)(s / (double)size);
     var = var + a.eps;
     const float r = (float)(1.0 / __builtin_sqrt((double)var));
@@ -121,16 +128,23 @@ fused_q_kv_rmsnorm_kernel(RmsArgs a) {
     }
 }
 
-// Row shapes: up to 512 elements -> 16 lanes x 4 pieces; up to 2048 -> 64
-// lanes x 4 pieces; up to 4096 -> 64 lanes x 8 pieces.
-inline int shape_of(int64_t size) { return size <= 512 ? 0 : size <= 2048 ? 1 : 2; }
-inline int lanes_of(int shape) { return shape == 0 ? 16 : 64; }
+// Row shapes (pieces per lane x lanes per row): up to 512 elements -> 4 x 16;
+// up to 1536 -> 6 x 32; up to 2048 -> 4 x 64; up to 4096 -> 8 x 64.  The
+// 32-lane shape keeps DeepSeek-V4's T = 8192 launch (q 1536, kv 512) inside one
+// round of waves, 24 per CU: with a whole wave per 1536-wide row it took 10,240
+// waves, 1.25 rounds of the 32 slots per CU, and 13.6 us against 9.8 us.
+inline int shape_of(int64_t size) {
+    return size <= 512 ? 0 : size <= 1536 ? 1 : size <= 2048 ? 2 : 3;
+}
+inline int lanes_of(int shape) { return shape == 0 ? 16 : shape == 1 ? 32 : 64; }
 
 template <int kQP, int kQL>
 void launch_kv_shape(const RmsArgs& a, int kv_shape, dim3 grid, hipStream_t st) {
     if (kv_shape == 0)
         hipLaunchKernelGGL((fused_q_kv_rmsnorm_kernel<kQP, kQL, 4, 16>), grid, dim3(kThreads), 0, st, a);
     else if (kv_shape == 1)
+        hipLaunchKernelGGL((fused_q_kv_rmsnorm_kernel<kQP, kQL, 6, 32>), grid, dim3(kThreads), 0, st, a);
+    else if (kv_shape == 2)
         hipLaunchKernelGGL((fused_q_kv_rmsnorm_kernel<kQP, kQL, 4, 64>), grid, dim3(kThreads), 0, st, a);
     else
         hipLaunchKernelGGL((fused_q_kv_rmsnorm_kernel<kQP, kQL, 8, 64>), grid, dim3(kThreads), 0, st, a);
@@ -189,6 +203,8 @@ extern "C" int fgv_fused_q_kv_rmsnorm(
     if (qs == 0)
         launch_kv_shape<4, 16>(a, ks, grid, st);
     else if (qs == 1)
+        launch_kv_shape<6, 32>(a, ks, grid, st);
+    else if (qs == 2)
         launch_kv_shape<4, 64>(a, ks, grid, st);
     else
         launch_kv_shape<8, 64>(a, ks, grid, st);

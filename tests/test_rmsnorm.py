@@ -71,7 +71,9 @@ def _gpu(qr, kv, qw, kw, eps):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("T,qdim,kvdim", [(4, 256, 128), (8, 1536, 512), (1, 1536, 512),
-                                          (8192, 1536, 512), (33, 4096, 64)])
+                                          (8192, 1536, 512), (33, 4096, 64),
+                                          # either side of each row-shape boundary (512, 1536, 2048)
+                                          (17, 520, 1536), (9, 1544, 1024), (5, 2048, 2056)])
 @pytest.mark.parametrize("wdtype", [torch.bfloat16, torch.float32])
 def test_gpu_matches_oracle(T, qdim, kvdim, wdtype):
     print(f"\n[case] rmsnorm T={T} q={qdim} kv={kvdim} w={wdtype}", flush=True)
