@@ -12,6 +12,7 @@ tests/test_slot_mapping.py:53-66): slot = block_table[seq][pos // bs] * bs
 + pos % bs, with block tables drawn from a random permutation of the cache's
 blocks.
 """
+import math
 import os
 from concurrent.futures import ThreadPoolExecutor
 from dataclasses import dataclass, field
@@ -35,6 +36,42 @@ def make_cos_sin_cache(max_pos: int, rope_dim: int = ROPE_DIM, base: float = 100
     exps = torch.arange(0, rope_dim, 2, dtype=torch.float32) / rope_dim
     theta = 1.0 / (base ** exps)
     ang = torch.outer(torch.arange(max_pos, dtype=torch.float32), theta)
+    return torch.cat((ang.cos(), ang.sin()), dim=-1).contiguous()
+
+
+def yarn_correction_range(beta_fast: float, beta_slow: float, rope_dim: int, base: float,
+                          max_pos: int):
+    """YaRN's blend band (Peng et al. 2023, "YaRN: Efficient Context Window
+    Extension of Large Language Models", eq. 17-18): the rotary dimension at
+    which a frequency completes r turns over max_pos positions is
+    d(r) = rope_dim * ln(max_pos / (2 pi r)) / (2 ln base); the band runs from
+    floor(d(beta_fast)) to ceil(d(beta_slow)), clipped to [0, rope_dim - 1]."""
+    def dim_of(turns):
+        return rope_dim * math.log(max_pos / (turns * 2 * math.pi)) / (2 * math.log(base))
+
+    return max(math.floor(dim_of(beta_fast)), 0), min(math.ceil(dim_of(beta_slow)), rope_dim - 1)
+
+
+def make_yarn_cos_sin_cache(max_pos: int = 65536, rope_dim: int = ROPE_DIM, scaling_factor: float = 16,
+                            base: float = 10000.0, beta_fast: float = 32, beta_slow: float = 1,
+                            rows: int = None):
+    """DeepSeek-V4's YaRN-scaled rotary table as the reference test builds it
+    (tests/test_fused_inv_rope_fp8_quant.py:246-264): frequency j is
+    theta_j = base^(-2j/rope_dim) below the blend band, theta_j / scaling_factor
+    above it, and a linear blend inside it; row p holds cos(p theta) | sin(p
+    theta) in float32.  The full table has max_pos * scaling_factor rows; `rows`
+    keeps only its first rows (each row depends on p alone)."""
+    half = rope_dim // 2
+    extra = 1.0 / (base ** (torch.arange(0, rope_dim, 2, dtype=torch.float32) / rope_dim))
+    interp = extra / scaling_factor
+    lo, hi = yarn_correction_range(beta_fast, beta_slow, rope_dim, base, max_pos)
+    if lo == hi:
+        hi += 0.001
+    ramp = ((torch.arange(half, dtype=torch.float32) - lo) / (hi - lo)).clamp(0, 1)
+    keep = 1.0 - ramp  # 1: extrapolated frequency, 0: interpolated
+    theta = interp * (1 - keep) + extra * keep
+    n = int(max_pos * scaling_factor) if rows is None else rows
+    ang = torch.outer(torch.arange(n, dtype=torch.float32), theta)
     return torch.cat((ang.cos(), ang.sin()), dim=-1).contiguous()
 
 

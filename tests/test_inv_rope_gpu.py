@@ -5,7 +5,8 @@ Reference tests mirrored: tests/test_fused_inv_rope_fp8_quant.py
   test_fused_inv_rope_fp8_quant :324-361, test_output_layout :364-391,
   test_per_group_contiguity :394-408, test_scales_are_power_of_two :411-430,
   test_large_values :433-448, test_nope_dims_unchanged :451-496,
-  test_zero_positions :499-515, test_dequant_numerical_accuracy :518-545;
+  test_zero_positions :499-515, test_dequant_numerical_accuracy :518-545,
+  test_with_real_deepseek_v4_rope :586-620;
   shapes from tests/accuracy_utils.py:104-115.
 """
 import pytest
@@ -149,3 +150,25 @@ def test_zero_positions_and_accuracy(tma):
     x = w.o.float().view(32, 8, 4096)
     rel = (deq - x).abs() / x.abs().clamp(min=1e-6)
     assert float(rel.mean()) < 0.15
+
+
+@pytest.mark.parametrize("tma", [False, True])
+@pytest.mark.parametrize("T", [1, 32, 256])
+def test_real_deepseek_v4_rope(T, tma):
+    """DeepSeek-V4's YaRN-scaled cos/sin table (scaling 16, 65536 original
+    positions; the first 65536 of its rows) at positions in [0, 4096), H=64,
+    G=8: codes and scales bit for bit, and the reference's dequantised check."""
+    _say(f"real DeepSeek-V4 rope T={T} tma={tma}")
+    w = W.make_inv_rope_workload(T, 64, 8, seed=0, max_pos=4096)
+    w = W.InvRopeWorkload(w.o, w.positions, W.make_yarn_cos_sin_cache(65536, rows=65536), 8, 8)
+    out, scale, r8, rs = run_case(w, tma)
+    assert torch.equal(out.cpu().view(torch.uint8), r8) and torch.equal(scale.cpu(), rs)
+    # the dequantised output against the rotated input, as the reference compares them
+    deq = dequant(out, scale, 8).cpu().reshape(T, 64, 512)
+    x = w.o.float().view(T, 64, 512).clone()
+    cs = w.cos_sin_cache[w.positions]
+    c, s_ = cs[:, None, :32], cs[:, None, 32:]
+    e, o = x[..., 448::2].clone(), x[..., 449::2].clone()
+    x[..., 448::2], x[..., 449::2] = e * c + o * s_, o * c - e * s_
+    cos = torch.nn.functional.cosine_similarity(deq.flatten(), x.flatten(), dim=0)
+    assert float(1 - cos) < 1e-3

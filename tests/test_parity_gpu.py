@@ -228,3 +228,21 @@ def test_q_layouts(T, H, gap, lead):
     outside = torch.ones(n, dtype=torch.bool, device=DEV)
     torch.as_strided(outside, (T, H, 512), (pitch, 512, 1), start).fill_(False)
     assert torch.equal(buf.view(torch.int16)[outside], sentinel[outside]), "elements outside q written"
+
+
+@pytest.mark.parametrize("T", [1, 32, 256])
+@pytest.mark.parametrize("H", [64, 128])
+def test_real_deepseek_v4_rope(T, H):
+    """DeepSeek-V4's YaRN-scaled cos/sin table (scaling 16, 65536 original
+    positions; the first 65536 of its 1,048,576 rows) at random positions in
+    [0, 4096), as the reference's sibling test draws them
+    (tests/test_fused_inv_rope_fp8_quant.py:586-620): q, rope and cache bytes bit
+    for bit against the oracle."""
+    _say(f"real DeepSeek-V4 rope T={T} H={H}")
+    g = torch.Generator().manual_seed(5)
+    w = W.Workload(f"yarn T{T} H{H}", W.randn_bf16((T, H, 512), g), W.randn_bf16((T, 512), g),
+                   torch.zeros((T + 63) // 64 + 1, 64 * W.HEAD_BYTES, dtype=torch.uint8),
+                   torch.randperm(((T + 63) // 64 + 1) * 64, generator=g)[:T].to(torch.int64),
+                   torch.randint(0, 4096, (T,), generator=g, dtype=torch.int64),
+                   W.make_yarn_cos_sin_cache(65536, rows=65536), 1e-6, 64)
+    _check_ref_case(w)
