@@ -42,6 +42,11 @@ constexpr int kKvTokensPerBlock = kRowsPerPass;
 // probe with four loads per lane showed the same, and the one-load-per-lane
 // stream the probe peaks with fills every slot.
 constexpr size_t kOccupancyLds = 40 * 1024;
+// The cap applies to grids of more than one uncapped round of workgroups (8 per
+// CU on MI355X's 256 CUs).  A smaller grid fits the GPU at once without it,
+// while the cap would split it: c1 (T = 256, H = 64) is 1040 workgroups, one
+// round uncapped, but 1024 + 16 with four per CU.
+constexpr int64_t kUncappedRound = 8 * 256;
 
 struct QnormArgs {
     uint16_t* q;
@@ -381,14 +386,15 @@ extern "C" int fgv_qnorm_rope_kv_rope_quant_insert(
     if (grid > 0x7fffffffLL)
         return fail(FGV_E_TOO_LARGE, "grid exceeds 2^31 - 1 workgroups");
     const hipStream_t st = static_cast<hipStream_t>(stream);
+    const size_t lds = grid > kUncappedRound ? kOccupancyLds : 0;
     if (map == kMapAligned)
         hipLaunchKernelGGL(qnorm_rope_kv_insert_kernel<kMapAligned>, dim3((uint32_t)grid), dim3(kThreads),
-                           kOccupancyLds, st, a);
+                           lds, st, a);
     else if (map == kMapRowsOneToken)
         hipLaunchKernelGGL(qnorm_rope_kv_insert_kernel<kMapRowsOneToken>, dim3((uint32_t)grid),
-                           dim3(kThreads), kOccupancyLds, st, a);
+                           dim3(kThreads), lds, st, a);
     else
         hipLaunchKernelGGL(qnorm_rope_kv_insert_kernel<kMapRows>, dim3((uint32_t)grid), dim3(kThreads),
-                           kOccupancyLds, st, a);
+                           lds, st, a);
     return launch_status();
 }
