@@ -469,6 +469,10 @@ def main():
         "gbps": achieved,
         "bytes_per_call": bytes_call,
         "bytes_per_token": bytes_call / T,
+        # HBM read + write bytes from the committed rocprofv3 PMC summary (FETCH_SIZE + WRITE_SIZE,
+        # calibrated), per token and over the kernel time measured here
+        "traffic_bytes_per_token": traffic / T if traffic else None,
+        "traffic_gbps": traffic / t_kernel / 1e9 if traffic else None,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic,
                      "kernel": kernel},
