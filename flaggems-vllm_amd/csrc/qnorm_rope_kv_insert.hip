@@ -11,7 +11,8 @@
 // is HBM bound (about 98.6% of its bytes are the in-place q read and write):
 // every global access is a non-temporal 16-byte (8-byte for the cache) access,
 // the per-row math uses DPP reductions only, and q blocks hold one pass of 16
-// rows (16 KiB in, 16 KiB out) so that 8 waves per SIMD keep loads in flight.
+// rows (16 KiB in, 16 KiB out); large grids run four workgroups per CU
+// (kOccupancyLds below), 4 waves per SIMD with 4 KiB of loads in flight each.
 //
 // Which 16 rows a q block takes (QMap):
 //   kMapRows / kMapRowsOneToken: rows 16b .. 16b+15 in (token, head) order.
@@ -30,8 +31,8 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kRowsPerPass = kThreads / 16;   // 16 rows per pass
-// One pass of four 16-byte loads per lane (8 waves per SIMD); more rows per
-// block (more loads per wave, fewer waves) measured slower.
+// One pass of four 16-byte loads per lane; more rows per block (more loads per
+// wave, fewer waves) measured slower.
 constexpr int kQRowsPerBlock = kRowsPerPass;
 constexpr int kKvTokensPerBlock = kRowsPerPass;
 // Dynamic LDS reserved per workgroup (the kernel uses none) to cap the launch
