@@ -133,6 +133,25 @@ def time_gpu(fn, steps, warmup):
         return wall / steps, eager, "events around the eager loop"
 
 
+def median_call_us(fn, calls):
+    """Median over `calls` eager calls of the time between HIP events recorded
+    on the launch stream before and after each call (one event chain, so the
+    intervals tile the loop).  It is the kernel's duration where the kernel
+    outlasts the wrapper's host cost (the main op's c2-c4); for shorter kernels
+    the intervals also hold the GPU's wait for the next launch."""
+    import torch
+
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(calls + 1)]
+    fn()
+    torch.cuda.synchronize()
+    ev[0].record()
+    for i in range(calls):
+        fn()
+        ev[i + 1].record()
+    torch.cuda.synchronize()
+    return statistics.median(ev[i].elapsed_time(ev[i + 1]) * 1000.0 for i in range(calls))
+
+
 def _repeat(run, seconds):
     """Median wall time of run(), repeated until `seconds` are spent (3..200 runs)."""
     times = []
@@ -442,6 +461,7 @@ def main():
                                 + ("in turn > 2 x 256 MB MALL)" if span > 2 * MALL_BYTES
                                    else "in turn, within the 256 MB MALL: cache-warm)"))
     ms_step, t_kernel, timing = time_gpu(step, args.steps, args.warmup)
+    median_us = median_call_us(step, max(20, args.steps))
     achieved = bytes_call / t_kernel / 1e9
     if args.op == "mla":
         config["mfma_tflops"] = flops_call / t_kernel / 1e12
@@ -466,6 +486,7 @@ def main():
         "config": config,
         "kernel_us": t_kernel * 1e6,
         "kernel_timing": timing,
+        "kernel_us_median_per_call": median_us,
         "gbps": achieved,
         "bytes_per_call": bytes_call,
         "bytes_per_token": bytes_call / T,
