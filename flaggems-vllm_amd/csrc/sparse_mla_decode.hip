@@ -361,6 +361,28 @@ __device__ __forceinline__ uint2 read_tr(const uint8_t* kbuf, int byte) {
 // extra) chunk sequence.  With slot < 0 the item is complete and out/lse are
 // written; otherwise the unnormalised O, the reference maximum and the sum go
 // to partial slot `slot` of the workspace for the combine kernel.
+// q's loads per lane: 16 steps of 32 dims, one 16-byte load each.
+constexpr int kQLoads = 16;
+// s_waitcnt operand "vmcnt(kQLoads)", expcnt and lgkmcnt not waited for
+// (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+constexpr int kWaitAllButQ = (kQLoads & 15) | ((kQLoads >> 4) << 14) | (7 << 4) | (15 << 8);
+static_assert(kQLoads < 64, "vmcnt holds 6 bits");
+
+// s_waitcnt operand "lgkmcnt(0)" alone.
+constexpr int kWaitLds = 15 | (3 << 14) | (7 << 4);
+
+// Workgroup barrier over LDS work only.  __syncthreads' fence (even one
+// scoped to LDS) waits for every outstanding global load, q's included, since
+// LDS-DMA writes count there too; the callers wait for their LDS-DMA gathers
+// explicitly before this.  The empty asm statements keep the compiler from
+// moving memory accesses across the barrier.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(kWaitLds);  // this wave's LDS reads and writes done
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 __device__ __forceinline__ void run_segment(const MlaArgs& a, uint8_t (&raw)[2][kRawBytes], uint8_t* kbuf,
                                             float (&mask_lds)[2][kChunk], int b,
                                             int sq, int hb, int c_lo, int c_hi, int slot, int wave, int lane) {
@@ -372,20 +394,24 @@ __device__ __forceinline__ void run_segment(const MlaArgs& a, uint8_t (&raw)[2][
     const int n0 = (v0.len + kChunk - 1) / kChunk;
     const uint8_t* dummy = mla_zero_entry;
 
-    // The first two chunks' indices go first, then q's 16 loads (the largest
-    // transfer) overlap their round trip; the first chunk's bytes are gathered
-    // as soon as its index has arrived.
+    // The first two chunks' indices go first, then the first chunk's gather,
+    // then q's 16 loads (the largest transfer), in the same branch: the first
+    // chunk waits for its gather alone (vmcnt counts in issue order), so q's
+    // loads overlap that chunk's dequantisation.
     auto first_of = [&](int c) { return (c >= n0 ? c - n0 : c) * kChunk; };
-    int id_cur = c_lo < c_hi ? load_id(select(v0, v1, c_lo >= n0), first_of(c_lo), wave, lane) : -1;
-    int id_next = c_lo + 1 < c_hi ? load_id(select(v0, v1, c_lo + 1 >= n0), first_of(c_lo + 1), wave, lane) : -1;
+    int id_next = -1;
 
     // q as the B operand of S^T = K q^T: step s covers dims 32s..32s+31, lane
     // group g dims 32s+8g..32s+8g+7 of head m16.
     const uint16_t* qrow = a.q + b * a.q_sb + sq * a.q_ss + head * a.q_sh;
-    bf16x8_t qf[16];
+    bf16x8_t qf[kQLoads];
+    auto load_q = [&]() __attribute__((always_inline)) {
+        asm volatile("" ::: "memory");  // q's loads stay behind the gather
 #pragma unroll
-    for (int s = 0; s < 16; ++s)
-        qf[s] = __builtin_bit_cast(bf16x8_t, load16(qrow + 32 * s + 8 * g));
+        for (int s = 0; s < kQLoads; ++s)
+            qf[s] = __builtin_bit_cast(bf16x8_t, load16(qrow + 32 * s + 8 * g));
+        asm volatile("" ::: "memory");
+    };
     // Chunks [c_lo, c_mid) come from the FP8 cache through the raw gather and
     // the dequantisation; with an expanded extra list, its chunks [c_mid, c_hi)
     // come as bf16 rows, alternating between two K tiles: the raw gather
@@ -394,10 +420,18 @@ __device__ __forceinline__ void run_segment(const MlaArgs& a, uint8_t (&raw)[2][
     uint8_t* const raw_tile = &raw[0][0];
     const int c_mid = v1.expanded ? max(c_lo, min(c_hi, n0)) : c_hi;
     if (c_lo < c_hi) {
-        if (c_lo < c_mid)
+        const int id_cur = load_id(select(v0, v1, c_lo >= n0), first_of(c_lo), wave, lane);
+        if (c_lo + 1 < c_hi)
+            id_next = load_id(select(v0, v1, c_lo + 1 >= n0), first_of(c_lo + 1), wave, lane);
+        if (c_lo < c_mid) {
             issue_gather(select(v0, v1, c_lo >= n0), dummy, wave, lane, id_cur, raw[c_lo & 1], mask_lds[c_lo & 1]);
-        else
+            load_q();
+        } else {
             issue_rows(v1, wave, lane, id_cur, ((c_lo - n0) & 1) ? kbuf : raw_tile, mask_lds[c_lo & 1]);
+            load_q();
+        }
+    } else {
+        load_q();
     }
 
     f32x4_t acc[32];
@@ -505,10 +539,15 @@ __device__ __forceinline__ void run_segment(const MlaArgs& a, uint8_t (&raw)[2][
         // across the MFMA loops, which need every register.
         int ln = lane;
         asm volatile("" : "+v"(ln));
-        __builtin_amdgcn_s_waitcnt(0);  // this wave's gathers of chunk c (and chunk c+1's index)
-        __syncthreads();                // everyone's gathers landed; K tile no longer read
+        // This wave's gathers of chunk c (and chunk c+1's index); on the first
+        // chunk, all but q's loads, which are issued last.
+        if (c == c_lo)
+            __builtin_amdgcn_s_waitcnt(kWaitAllButQ);
+        else
+            __builtin_amdgcn_s_waitcnt(0);
+        lds_barrier();  // everyone's gathers landed; K tile no longer read
         dequantize(cur, mask_lds[c & 1], kbuf, wave, ln);
-        __syncthreads();
+        lds_barrier();
         if (c + 1 < c_mid)
             issue_gather(select(v0, v1, c + 1 >= n0), dummy, wave, ln, id_next, raw[(c + 1) & 1],
                          mask_lds[(c + 1) & 1]);
