@@ -46,6 +46,10 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="repeat the CPU sample until this much CPU time is spent (min 3 runs)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--grid", action="store_true",
+                    help="main op over the reference benchmark's grid (T x H); one JSON line per point "
+                         "and a markdown table, instead of the single headline line")
+    ap.add_argument("--grid-max-tokens", type=int, default=131072)
     return ap.parse_args()
 
 
@@ -245,6 +249,70 @@ def cpu_baseline_port(run, units, unit, sample, seconds):
                       f"{t:.3f} s per run"}
 
 
+# The reference benchmark's shapes for the main op
+# (benchmark/test_fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert.py:137-163):
+# positions = arange(T), slot_mapping = arange(T), 64-slot blocks, max_pos =
+# max(4096, T) with the rope base chosen by max_pos (:170-192).
+GRID_TOKENS = [1, 4, 17, 64, 1024, 2048, 8192, 32768, 65536, 98304, 131072]
+GRID_HEADS = [64, 128]
+
+
+def run_grid(args):
+    """Times the main op at every point of the reference benchmark's grid with
+    inputs drawn on the device like the reference benchmark's, rotating device
+    copies for calls under 512 MB (mall_sets), graph-replay kernel time."""
+    import torch
+
+    import flaggems_vllm
+    from flaggems_vllm import testing as W
+
+    dev = torch.device("cuda:0")
+    op = flaggems_vllm.fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert
+    rows = []
+    for T in [t for t in GRID_TOKENS if t <= args.grid_max_tokens]:
+        for H in GRID_HEADS:
+            max_pos = max(4096, T)
+            base = 10000.0 if max_pos <= 8192 else 20000.0 if max_pos <= 32768 else 40000.0 \
+                if max_pos <= 65536 else 60000.0 if max_pos <= 98304 else 100000.0
+            cs = W.make_cos_sin_cache(max_pos, base=base).to(dev)
+            pos = torch.arange(T, dtype=torch.int64, device=dev)
+            slots = torch.arange(T, dtype=torch.int64, device=dev)
+            nblk = (T + 63) // 64 + 1
+            bytes_call = W.main_op_bytes(T, H, T)
+            gen = torch.Generator(device=dev).manual_seed(T * 1000 + H)
+
+            def make_step(i):
+                q = torch.randn(T, H, 512, generator=gen, device=dev, dtype=torch.bfloat16)
+                kv = torch.randn(T, 512, generator=gen, device=dev, dtype=torch.bfloat16)
+                cache = torch.zeros(nblk, 64 * W.HEAD_BYTES, dtype=torch.uint8, device=dev)
+                return lambda: op(q, kv, cache, slots, pos, cs, 1e-6, 64)
+
+            step, n_sets = rotating(make_step, bytes_call)
+            steps = args.steps if T >= 8192 else max(args.steps, 200)
+            _, t_kernel, timing = time_gpu(step, steps, args.warmup)
+            median_us = median_call_us(step, max(20, min(steps, 200)))
+            gbps = bytes_call / t_kernel / 1e9
+            span = n_sets * bytes_call
+            row = {"op": "fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert", "num_tokens": T, "num_heads": H,
+                   "kernel_us": t_kernel * 1e6, "kernel_us_median_per_call": median_us,
+                   "bytes_per_call": bytes_call, "gbps": gbps, "frac_of_8tbps": gbps / HBM_PEAK_GBPS,
+                   "tokens_per_s": T / t_kernel, "input_sets": n_sets,
+                   "mall": "cold" if n_sets == 1 or span > 2 * MALL_BYTES else "warm", "steps": steps,
+                   "kernel_timing": timing}
+            print(json.dumps(row), flush=True)
+            rows.append(row)
+            del step
+            torch.cuda.empty_cache()
+    print("\n| T | H | MB per call | input sets | µs per call (graph) | µs median per eager call "
+          "| GB/s | % of 8 TB/s | tokens/s |")
+    print("|---|---|---|---|---|---|---|---|---|")
+    for r in rows:
+        sets = f"{r['input_sets']}" + (" (MALL-warm)" if r["mall"] == "warm" else "")
+        print(f"| {r['num_tokens']} | {r['num_heads']} | {r['bytes_per_call'] / 1e6:.2f} | {sets} "
+              f"| {r['kernel_us']:.2f} | {r['kernel_us_median_per_call']:.2f} | {r['gbps']:.0f} "
+              f"| {100 * r['frac_of_8tbps']:.1f} | {r['tokens_per_s']:.3g} |", flush=True)
+
+
 def main():
     args = parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -260,6 +328,9 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.grid:
+        run_grid(args)
+        return
     from oracle import torch_ref
 
     cpu_case = None  # (run, units per run, unit, sample) for ops timed by cpu_baseline_port

@@ -114,12 +114,15 @@ def _indexer_q_rope_quant(positions: torch.Tensor, index_q: torch.Tensor, index_
 @_indexer_q_rope_quant.register_fake
 def _(positions, index_q, index_q_cos_sin_cache, index_weights, index_weights_softmax_scale,
       index_weights_head_scale, use_fp4=False):
+    # the real op's outputs: weights like index_weights in float32; FP8 codes
+    # like index_q; MXFP4 nibbles [T, H, D/2] and the UE8M0 bytes [T, H, D/32]
+    # viewed as int32 [T, H, D/128], squeezed to [T, H] when D == 128
     t, h, d = positions.shape[0], index_q.shape[1], index_q.shape[2]
-    w = index_weights.new_empty((t, h), dtype=torch.float32)
+    w = torch.empty_like(index_weights, dtype=torch.float32)
     if use_fp4:
-        return (index_q.new_empty((t, h, d // 2), dtype=torch.uint8),
-                index_q.new_empty((t, h, d // 32), dtype=torch.uint8), w)
-    return index_q.new_empty((t, h, d), dtype=torch.float8_e4m3fn), index_q.new_empty((0,), dtype=torch.uint8), w
+        scale = index_q.new_empty((t, h, d // 128), dtype=torch.int32)
+        return index_q.new_empty((t, h, d // 2), dtype=torch.uint8), scale.squeeze(-1), w
+    return torch.empty_like(index_q, dtype=torch.float8_e4m3fn), index_q.new_empty((0,), dtype=torch.uint8), w
 
 
 @_op("compute_slot_mapping_parallel", ("slot_mapping",))

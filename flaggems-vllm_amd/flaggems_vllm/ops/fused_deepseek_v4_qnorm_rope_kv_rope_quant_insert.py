@@ -23,6 +23,19 @@ HEAD_DIM = 512
 ROPE_DIM = 64
 
 
+def cache_geometry(k_cache: torch.Tensor):
+    """(num_blocks, block stride in bytes) the kernel addresses k_cache with.
+
+    A [num_blocks, block_bytes] cache (or any cache with more dimensions)
+    has k_cache.shape[0] blocks, stride(0) bytes apart.  A 1-D cache is one
+    block of numel bytes: slots past cache_block_size then fall in block >= 1,
+    which the kernel's block bound skips, so nothing is written past its end.
+    """
+    if k_cache.dim() > 1:
+        return k_cache.shape[0], k_cache.stride(0)
+    return 1, k_cache.numel()
+
+
 def fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert(
     q: torch.Tensor,
     kv: torch.Tensor,
@@ -76,8 +89,7 @@ def fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert(
 
     if num_tokens == 0:
         return
-    num_blocks = k_cache.shape[0]
-    block_stride = k_cache.stride(0) if k_cache.dim() > 1 else k_cache.numel()
+    num_blocks, block_stride = cache_geometry(k_cache)
     with on_device_of(q):
         rc = _native.lib().fgv_qnorm_rope_kv_rope_quant_insert(
             q.data_ptr(), q.stride(0), q.stride(1),

@@ -72,8 +72,10 @@ def fused_indexer_q_rope_quant(
         scale = torch.empty((num_tokens, num_index_q_heads, num_scale_blocks),
                             dtype=torch.uint8, device=index_q.device)
     else:
-        q_out = torch.empty((num_tokens, num_index_q_heads, index_q_head_dim),
-                            dtype=torch.float8_e4m3fn, device=index_q.device)
+        # as the reference allocates it: index_q's shape (its rows may exceed
+        # num_tokens; only the first num_tokens are written) and layout
+        q_out = torch.empty_like(index_q, dtype=torch.float8_e4m3fn)
+        assert q_out.stride(-1) == 1
         scale = None
 
     with on_device_of(index_q):

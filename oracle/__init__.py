@@ -24,7 +24,9 @@ import os
 import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_LIB_PATH = os.path.join(_HERE, "liboracle_dsv4.so")
+# FGV_ORACLE_LIB selects another build of the same source, e.g. the
+# AddressSanitizer/UBSan one from `make -C oracle sanitize`.
+_LIB_PATH = os.environ.get("FGV_ORACLE_LIB") or os.path.join(_HERE, "liboracle_dsv4.so")
 _lib = None
 
 _P = ctypes.c_void_p

@@ -162,3 +162,21 @@ def test_product_never_imports_the_oracle():
                 text = open(os.path.join(dirpath, f)).read()
                 assert "import oracle" not in text and "from oracle" not in text, f
                 assert "liboracle" not in text, f
+
+
+@pytest.mark.parametrize("shape,expected", [
+    ((4, 64 * 584), (4, 64 * 584)),
+    ((3, 16, 1, 584), (3, 16 * 584)),
+    ((64 * 584 * 2,), (1, 64 * 584 * 2)),   # 1-D: one block of numel bytes
+    ((100,), (1, 100)),
+])
+def test_main_cache_geometry(shape, expected):
+    """Block count and stride handed to the C ABI.  A 1-D cache is one block,
+    so the kernel's block bound (blk < num_blocks) skips every slot past
+    cache_block_size instead of writing past the allocation."""
+    from flaggems_vllm.ops.fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert import cache_geometry
+
+    assert cache_geometry(torch.zeros(shape, dtype=torch.uint8)) == expected
+    # a padded 2-D view keeps its row stride
+    padded = torch.zeros(4, 64 * 584 + 256, dtype=torch.uint8)[:, :64 * 584]
+    assert cache_geometry(padded) == (4, 64 * 584 + 256)

@@ -38,21 +38,41 @@ def assert_q_exact(q_gpu_cpu, q_ref, what):
     assert n_bad == 0, f"{what}: {n_bad} q elements differ from the oracle (max {int(d.max())} ulp)"
 
 
+# Rope elements of q allowed beyond 1 bf16 ulp of the reference's torch
+# formulation, as a fraction of all rope elements.  The torch path's float32
+# RMS factor differs from the correctly rounded one by a few float32 ulps;
+# where the rotation e*c - o*s (or e*s + o*c) cancels, that moves the result
+# by more than one of its own ulps.  Measured (the GPU equals the C oracle bit
+# for bit): c2 13 of 33,554,432 (max 16 ulps), c3's 2048 sampled tokens 9 of
+# 16,777,216, c4's 7 of 8,388,608; none at c0 and c1.
+ROPE_BEYOND_1ULP_CEILING = 1e-6
+
+
 def assert_q_within_torch_ref(q_gpu_cpu, w_in: W.Workload, what):
-    """North-star bar against the reference's torch formulation: nope elements
-    within 1 bf16 ulp; rope elements within 1 ulp plus the cancellation term of
-    rope_cancellation_bound."""
+    """North-star bar against the reference's torch formulation: every nope
+    element within 1 bf16 ulp; rope elements within 1 ulp except at most
+    ROPE_BEYOND_1ULP_CEILING of them, and each of those within 1 ulp plus the
+    cancellation term of rope_cancellation_bound.  Prints the counts and the
+    largest distances."""
     r = w_in.clone()
     torch_ref.qnorm_rope_kv_insert(*r.args())
     d = bf16_ulp_distance(q_gpu_cpu, r.q)
-    assert int(d[..., :448].max()) <= 1, f"{what}: nope beyond 1 ulp"
-    rope_d = d[..., 448:]
-    if int(rope_d.max()) > 1:
-        xf = w_in.q.float()
+    nope_d, rope_d = d[..., :448], d[..., 448:]
+    beyond = rope_d > 1
+    n_beyond = int(beyond.sum())
+    print(f"[q vs torch ref] {what}: nope elements at 1 ulp {int((nope_d == 1).sum())} of "
+          f"{nope_d.numel()} (max {int(nope_d.max())} ulp); rope elements beyond 1 ulp {n_beyond} of "
+          f"{rope_d.numel()} (max {int(rope_d.max())} ulp)", flush=True)
+    assert int(nope_d.max()) <= 1, f"{what}: nope beyond 1 ulp"
+    assert n_beyond <= ROPE_BEYOND_1ULP_CEILING * rope_d.numel(), (
+        f"{what}: {n_beyond} rope elements beyond 1 ulp, above the ceiling")
+    if n_beyond:
+        tok = torch.nonzero(beyond.flatten(1).any(1)).flatten()  # only tokens with an exceedance
+        xf = w_in.q[tok].float()
         y = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + w_in.eps)
-        cs = w_in.cos_sin_cache[w_in.position_ids][:, None, :]
-        bound = rope_cancellation_bound(y[..., 448:], cs) + bf16_ulp_size(r.q[..., 448:])
-        diff = (q_gpu_cpu[..., 448:].float() - r.q[..., 448:].float()).abs()
+        cs = w_in.cos_sin_cache[w_in.position_ids[tok]][:, None, :]
+        bound = rope_cancellation_bound(y[..., 448:], cs) + bf16_ulp_size(r.q[tok][..., 448:])
+        diff = (q_gpu_cpu[tok][..., 448:].float() - r.q[tok][..., 448:].float()).abs()
         assert bool((diff <= bound).all()), f"{what}: rope beyond the cancellation bound"
 
 
@@ -66,8 +86,7 @@ def test_benchmark_configs_full(config):
     assert_q_exact(g.q.cpu(), ref.q, f"c{config}")
     assert torch.equal(g.k_cache.cpu(), ref.k_cache), f"c{config}: k_cache differs"
     assert torch.equal(g.kv.cpu(), w.kv), f"c{config}: kv modified"
-    if config < 2:
-        assert_q_within_torch_ref(g.q.cpu(), w, f"c{config}")
+    assert_q_within_torch_ref(g.q.cpu(), w, f"c{config}")
 
 
 @pytest.mark.parametrize("config", [3, 4])
@@ -84,7 +103,9 @@ def test_benchmark_configs_sampled(config):
     toks = torch.randperm(w.num_tokens, generator=gen)[:2048].sort().values
     sub = sub_workload(w, toks)
     ref = oracle_main(sub)
-    assert_q_exact(g.q[toks.to(DEV)].cpu(), ref.q, f"c{config} sampled q")
+    q_sampled = g.q[toks.to(DEV)].cpu()
+    assert_q_exact(q_sampled, ref.q, f"c{config} sampled q")
+    assert_q_within_torch_ref(q_sampled, sub, f"c{config} sampled")
     keep = sub.slot_mapping >= 0
     idx = slot_byte_index(sub.slot_mapping[keep], w.block_size, w.k_cache.stride(0))
     flat_g = g.k_cache.view(-1)
@@ -246,3 +267,84 @@ def test_real_deepseek_v4_rope(T, H):
                    torch.randint(0, 4096, (T,), generator=g, dtype=torch.int64),
                    W.make_yarn_cos_sin_cache(65536, rows=65536), 1e-6, 64)
     _check_ref_case(w)
+
+
+def test_one_dimensional_cache():
+    """A 1-D k_cache (one block of numel bytes) carved from a larger buffer:
+    slots inside the block are written as the oracle writes them, slots past
+    cache_block_size are skipped, and no byte after the cache changes."""
+    _say("main op 1-D k_cache")
+    bs, T = 16, 12
+    g = torch.Generator().manual_seed(12)
+    slots = torch.tensor([0, 3, 15, 16, 17, 40, -1, 5, 31, 2, 100, 9], dtype=torch.int64)
+    w = W.Workload("1-D cache", W.randn_bf16((T, 8, 512), g), W.randn_bf16((T, 512), g),
+                   torch.zeros(1, bs * W.HEAD_BYTES, dtype=torch.uint8), slots,
+                   torch.randint(0, 4096, (T,), generator=g, dtype=torch.int64),
+                   W.make_cos_sin_cache(4096), 1e-6, bs)
+    ref_in = w.clone()
+    ref_in.slot_mapping = torch.where(slots < bs, slots, torch.full_like(slots, -1))
+    ref = oracle_main(ref_in)
+    sentinel = torch.randint(0, 256, (3 * bs * W.HEAD_BYTES,), generator=g, dtype=torch.int32).to(torch.uint8)
+    buf = sentinel.clone().to(DEV)
+    cache = buf[:bs * W.HEAD_BYTES]
+    cache.zero_()
+    assert cache.dim() == 1
+    d = w.to(DEV)
+    OP(d.q, d.kv, cache, d.slot_mapping, d.position_ids, d.cos_sin_cache, d.eps, bs)
+    torch.cuda.synchronize()
+    assert torch.equal(cache.cpu(), ref.k_cache.view(-1))
+    assert torch.equal(buf[bs * W.HEAD_BYTES:].cpu(), sentinel[bs * W.HEAD_BYTES:]), "bytes past the cache written"
+    assert_q_exact(d.q.cpu(), ref.q, "1-D cache")
+
+
+# The reference's largest combined shapes
+# (tests/test_fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert.py:525-531):
+# up to 131072 tokens x 128 heads = 2^33 q elements (16 GiB), where any 32-bit
+# element or byte offset would wrap.
+@pytest.mark.parametrize("T", [65536, 131072])
+@pytest.mark.parametrize("H", [64, 128])
+@pytest.mark.parametrize("bs", [16, 64])
+def test_combined_largest(T, H, bs):
+    """q and kv drawn on the device (seeded), positions = arange, the rope
+    base chosen by max_pos as the reference test does.  Before the call,
+    2048 sampled tokens of q are copied to the host (the first and last
+    tokens and those on either side of the 2^31-element and 2^32- and
+    2^33-byte offsets included); afterwards their q rows are compared bit for
+    bit with the C oracle, and the whole cache with the oracle's kv insert
+    over all T tokens."""
+    _say(f"combined largest T={T} H={H} bs={bs}")
+    gen = torch.Generator(device=DEV).manual_seed(7 + T + H + bs)
+    q = torch.randn(T, H, 512, generator=gen, device=DEV, dtype=torch.bfloat16)
+    kv = torch.randn(T, 512, generator=gen, device=DEV, dtype=torch.bfloat16)
+    row_bytes = H * 1024
+    edges = set([0, 1, T - 2, T - 1])
+    for off in (1 << 31, 1 << 32, 1 << 33):   # bytes; 2^31 elements = 2^32 bytes
+        t = off // row_bytes
+        edges.update(x for x in (t - 1, t, t + 1) if 0 <= x < T)
+    hsel = torch.Generator().manual_seed(T * 3 + H)
+    toks = torch.randperm(T, generator=hsel)[:2048 - len(edges)]
+    toks = torch.unique(torch.cat([toks, torch.tensor(sorted(edges))]))
+    q_in = q[toks.to(DEV)].cpu()
+    kv_cpu = kv.cpu()
+    positions = torch.arange(T, dtype=torch.int64)
+    base = 10000.0 if T <= 8192 else 20000.0 if T <= 32768 else 40000.0 if T <= 65536 \
+        else 60000.0 if T <= 98304 else 100000.0
+    cos_sin = W.make_cos_sin_cache(T, base=base)
+    slots = torch.arange(T, dtype=torch.int64)
+    nblk = (T + bs - 1) // bs + 1
+    cache = torch.zeros(nblk, bs * W.HEAD_BYTES, dtype=torch.uint8, device=DEV)
+    OP(q, kv, cache, slots.to(DEV), positions.to(DEV), cos_sin.to(DEV), 1e-6, bs)
+    torch.cuda.synchronize()
+    q_out = q[toks.to(DEV)].cpu()
+    cache_out = cache.cpu()
+    del q, kv, cache
+    torch.cuda.empty_cache()
+
+    sub = W.Workload("sampled", q_in, kv_cpu[toks].clone(), torch.zeros(1, bs * W.HEAD_BYTES, dtype=torch.uint8),
+                     torch.full((toks.numel(),), -1, dtype=torch.int64), positions[toks].clone(), cos_sin, 1e-6, bs)
+    ref = oracle_main(sub)
+    assert_q_exact(q_out, ref.q, f"T={T} H={H} sampled q")
+    full = W.Workload("kv", torch.zeros(T, 0, 512, dtype=torch.bfloat16), kv_cpu,
+                      torch.zeros(nblk, bs * W.HEAD_BYTES, dtype=torch.uint8), slots, positions, cos_sin, 1e-6, bs)
+    ref_kv = oracle_main(full)
+    assert torch.equal(cache_out, ref_kv.k_cache), f"T={T} H={H} bs={bs}: cache differs"

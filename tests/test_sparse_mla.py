@@ -471,6 +471,101 @@ def test_gpu_extreme_scales():
         assert torch.equal(out[i, 0], row.expand(64, 512)), int(choices[i])
 
 
+_FINITE_E4M3 = [c for c in range(256) if c not in (0x7F, 0xFF)]
+
+
+def _scale_sweep_cache(finite_rows_only):
+    """A [4, 64, 1, 584] MODEL1 cache whose entry b (b = 0..254) has all seven
+    scale bytes b and NoPE codes cycling through the 254 finite e4m3 codes
+    (starting at code index 7b, so each code meets every group); entry 255
+    repeats byte 127.  With finite_rows_only, codes whose dequantised value
+    overflows bf16 (bytes 247..254 only) are replaced by the finite-valued
+    codes in turn, so every row is finite and attention over it stays finite.
+    RoPE bytes are seeded bf16 N(0, 0.1)."""
+    g = torch.Generator().manual_seed(41)
+    cache = W.make_model1_cache(4, 64, g)
+    pages = cache.view(4, -1)
+    data = pages[:, :64 * 576].view(4, 64, 576)   # views into the cache
+    scl = pages[:, 64 * 576:].view(4, 64, 8)
+    for b in range(256):
+        byte = b if b < 255 else 127
+        scl[b // 64, b % 64, :7] = byte
+        codes = [_FINITE_E4M3[(7 * b + i) % 254] for i in range(448)]
+        if finite_rows_only:
+            ok = [c for c in _FINITE_E4M3
+                  if torch.isfinite(oracle.e4m3fn_decode(torch.tensor([c], dtype=torch.uint8)).double()
+                                    * 2.0 ** (byte - 127)).all()
+                  and abs(float(oracle.e4m3fn_decode(torch.tensor([c], dtype=torch.uint8)))) * 2.0 ** (byte - 127)
+                  < 3.3895e38]
+            codes = [c if c in ok else ok[i % len(ok)] for i, c in enumerate(codes)]
+        data[b // 64, b % 64, :448] = torch.tensor(codes, dtype=torch.uint8)
+    return cache
+
+
+def test_scale_sweep_cache_rows():
+    """The sweep cache's rows (oracle dequantisation): every byte 0..254 and
+    all 254 finite codes occur in every entry; with finite_rows_only every row
+    is finite, without it bytes 247..254 hold infinite values."""
+    full = _scale_sweep_cache(False)
+    fin = _scale_sweep_cache(True)
+    for b in range(255):
+        codes = set(full.view(4, -1)[b // 64, (b % 64) * 576:(b % 64) * 576 + 448].tolist())
+        assert codes == set(_FINITE_E4M3)
+        assert bool(torch.isfinite(oracle.model1_token_row(fin, b).float()).all())
+        assert bool(torch.isfinite(oracle.model1_token_row(full, b).float()).all()) == (b < 247)
+
+
+@pytest.mark.gpu
+def test_gpu_scaled_dequant_every_scale_byte():
+    """v_cvt_scalef32_pk_bf16_fp8 in the chunk loop, for every scale byte
+    0..254 and every finite code: batch row b attends entry b alone
+    (topk_length 1, no sink), so its softmax weight is exactly 1 and every
+    head's output is that entry's bf16 row, which must equal the oracle's
+    bf16(f32(code) * 2^(byte - 127)) (byte 0: scale 0) bit for bit.  q row b
+    is scaled down for large bytes so the score stays finite in fp32."""
+    print("\n[case] sparse MLA scaled dequant, scale bytes 0..254", flush=True)
+    cache = _scale_sweep_cache(True)
+    g = torch.Generator().manual_seed(42)
+    B = 255
+    q = torch.randn(B, 1, 64, 512, generator=g)
+    for b in range(B):
+        q[b] *= 2.0 ** -max(0, b - 200)
+    idx = torch.randint(0, 256, (B, 1, 64), generator=g, dtype=torch.int32)
+    idx[:, 0, 0] = torch.arange(B, dtype=torch.int32)
+    w = W.MlaWorkload("scale sweep", q.to(torch.bfloat16), cache, idx,
+                      torch.ones(B, dtype=torch.int32), None)
+    out, lse = _gpu(w)
+    out = out.cpu()
+    bad = []
+    for b in range(B):
+        row = oracle.model1_token_row(cache, b)
+        if not torch.equal(out[b, 0].view(torch.int16), row.expand(64, 512).view(torch.int16)):
+            bad.append(b)
+    assert not bad, f"scale bytes whose attended row differs from the oracle's: {bad[:16]}"
+
+
+@pytest.mark.gpu
+def test_gpu_expanded_copy_every_scale_byte():
+    """The expanded-cache copy (mla_expand_cache_kernel, the conversion the
+    chunk loop uses, scale byte 0 included) for every scale byte 0..254 and
+    every finite code, overflowing ones included: the bf16 rows it leaves at
+    the start of the workspace equal the oracle's rows bit for bit (values
+    past the bf16 maximum become +-inf in both)."""
+    print("\n[case] sparse MLA expanded copy, scale bytes 0..254", flush=True)
+    w = W.make_mla_workload(batch=8, topk=64, num_pages=2, sink=False, seed=43)
+    w.extra_k_cache = _scale_sweep_cache(False)
+    g = torch.Generator().manual_seed(44)
+    w.extra_indices = torch.randint(0, 256, (8, 1, 256), generator=g, dtype=torch.int32)
+    # 8 rows x 256 extra entries gather the 256-entry cache 8 times: expanded
+    _, _, nbytes, ws = _gpu_raw(w, workspace=True, keep_ws=True)
+    assert nbytes >= 256 * 1024
+    rows = ws[:256 * 1024].cpu().view(torch.bfloat16).view(256, 512)
+    bad = [b for b in range(256)
+           if not torch.equal(rows[b].view(torch.int16),
+                              oracle.model1_token_row(w.extra_k_cache, b).view(torch.int16))]
+    assert not bad, f"expanded rows that differ from the oracle's: {bad[:16]}"
+
+
 @pytest.mark.gpu
 def test_gpu_bench_case_against_oracle():
     """The benchmark's decode case at full size (batch 512, top-k 128 over 512
@@ -494,9 +589,9 @@ def test_gpu_deterministic():
 
 # ------------------------------------------------------- GPU: split grid ----
 
-def _gpu_raw(w, workspace, ws_bytes=None):
+def _gpu_raw(w, workspace, ws_bytes=None, keep_ws=False):
     """Calls the C ABI directly, with or without a workspace (of the queried
-    size, or `ws_bytes`)."""
+    size, or `ws_bytes`); with keep_ws the workspace tensor is returned too."""
     from flaggems_vllm import _native
 
     d = w.to(DEV)
@@ -526,6 +621,8 @@ def _gpu_raw(w, workspace, ws_bytes=None):
         ptr(ws), nbytes if workspace else 0, torch.cuda.current_stream().cuda_stream)
     assert rc == 0, rc
     torch.cuda.synchronize()
+    if keep_ws:
+        return out.cpu(), lse.cpu(), nbytes, ws
     return out.cpu(), lse.cpu(), nbytes
 
 

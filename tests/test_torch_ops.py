@@ -68,17 +68,25 @@ def test_sibling_fake_layout(T, tma):
 
 
 @pytest.mark.parametrize("fp4", [False, True])
-def test_indexer_fake_layout(fp4):
+@pytest.mark.parametrize("D", [128, 256, 512])
+def test_indexer_fake_layout(fp4, D):
+    """The fake outputs have the real op's layouts: FP8 codes like index_q
+    (its rows, which may exceed the token count); MXFP4 nibbles [T, H, D/2]
+    and the UE8M0 bytes as the int32 view [T, H, D/128], squeezed to [T, H]
+    at D = 128 (reference ops/fused_indexer_q_rope_quant.py:378-391); weights
+    like index_weights in float32."""
     pos = torch.empty(5, dtype=torch.int64, device="meta")
-    q = torch.empty(5, 8, 128, dtype=torch.bfloat16, device="meta")
+    q = torch.empty(7, 8, D, dtype=torch.bfloat16, device="meta")
     cs = torch.empty(64, 64, dtype=torch.float32, device="meta")
-    w = torch.empty(5, 8, dtype=torch.bfloat16, device="meta")
+    w = torch.empty(6, 8, dtype=torch.bfloat16, device="meta")
     qo, sc, wo = _op("fused_indexer_q_rope_quant")(pos, q, cs, w, 0.1, 0.2, fp4)
-    assert wo.shape == (5, 8) and wo.dtype == torch.float32
+    assert wo.shape == (6, 8) and wo.dtype == torch.float32
     if fp4:
-        assert qo.shape == (5, 8, 64) and qo.dtype == torch.uint8 and sc.shape == (5, 8, 4)
+        assert qo.shape == (5, 8, D // 2) and qo.dtype == torch.uint8
+        assert sc.dtype == torch.int32
+        assert sc.shape == ((5, 8) if D == 128 else (5, 8, D // 128))
     else:
-        assert qo.shape == (5, 8, 128) and qo.dtype == torch.float8_e4m3fn and sc.numel() == 0
+        assert qo.shape == (7, 8, D) and qo.dtype == torch.float8_e4m3fn and sc.numel() == 0
 
 
 # ------------------------------------------------------------------- GPU ----
@@ -154,3 +162,25 @@ def test_gpu_rmsnorm_indexer_gather_slot_match_functions():
     _op("compute_slot_mapping_parallel")(*sargs, sl_o, 16)
     torch.cuda.synchronize()
     assert torch.equal(sl_f, sl_o)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("fp4", [False, True])
+@pytest.mark.parametrize("D", [128, 256])
+def test_gpu_indexer_opcheck(fp4, D):
+    """Schema and fake-tensor checks of the indexer op in both modes: the
+    fake's dtypes, shapes and strides equal the real outputs' (int32 UE8M0
+    view, squeezed at D = 128), with index_q holding more rows than there are
+    positions, as the reference's assert allows."""
+    _say(f"torch.ops indexer opcheck fp4={fp4} D={D}")
+    pos, q, cs, wt, sm, hs = _indexer_case(9, H=16, D=D, seed=6)
+    qbig = torch.cat([q, q[:3]]).to(DEV)  # 12 rows for 9 positions
+    args = (pos.to(DEV), qbig, cs.to(DEV), wt.to(DEV), sm, hs, fp4)
+    oq, osc, ow = _op("fused_indexer_q_rope_quant")(*args)
+    torch.cuda.synchronize()
+    if fp4:
+        assert osc.dtype == torch.int32 and osc.shape == ((9, 16) if D == 128 else (9, 16, D // 128))
+    else:
+        assert oq.shape == qbig.shape and oq.stride() == qbig.stride()
+    torch.library.opcheck(_op("fused_indexer_q_rope_quant"), args,
+                          test_utils=("test_schema", "test_faketensor"))
