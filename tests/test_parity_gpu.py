@@ -39,19 +39,21 @@ def assert_q_exact(q_gpu_cpu, q_ref, what):
 
 
 # Rope elements of q allowed beyond 1 bf16 ulp of the reference's torch
-# formulation, as a fraction of all rope elements.  The torch path's float32
-# RMS factor differs from the correctly rounded one by a few float32 ulps;
-# where the rotation e*c - o*s (or e*s + o*c) cancels, that moves the result
-# by more than one of its own ulps.  Measured (the GPU equals the C oracle bit
-# for bit): c2 13 of 33,554,432 (max 16 ulps), c3's 2048 sampled tokens 9 of
-# 16,777,216, c4's 7 of 8,388,608; none at c0 and c1.
+# formulation: this fraction of all rope elements, plus one (a shape of a few
+# hundred thousand rope elements is too small for the rate to mean anything).
+# The torch path's float32 RMS factor differs from the correctly rounded one
+# by a few float32 ulps; where the rotation e*c - o*s (or e*s + o*c) cancels,
+# that moves the result by more than one of its own ulps.  Measured (the GPU
+# equals the C oracle bit for bit): c2 13 of 33,554,432 (max 16 ulps), c3's
+# 2048 sampled tokens 9 of 16,777,216, c4's 7 of 8,388,608, the reference's
+# T=1000 H=128 shape 4 of 8,192,000, T=64 H=64 1 of 262,144; none at c0, c1.
 ROPE_BEYOND_1ULP_CEILING = 1e-6
 
 
 def assert_q_within_torch_ref(q_gpu_cpu, w_in: W.Workload, what):
     """North-star bar against the reference's torch formulation: every nope
     element within 1 bf16 ulp; rope elements within 1 ulp except at most
-    ROPE_BEYOND_1ULP_CEILING of them, and each of those within 1 ulp plus the
+    ROPE_BEYOND_1ULP_CEILING of them plus one, and each of those within 1 ulp plus the
     cancellation term of rope_cancellation_bound.  Prints the counts and the
     largest distances."""
     r = w_in.clone()
@@ -64,7 +66,7 @@ def assert_q_within_torch_ref(q_gpu_cpu, w_in: W.Workload, what):
           f"{nope_d.numel()} (max {int(nope_d.max())} ulp); rope elements beyond 1 ulp {n_beyond} of "
           f"{rope_d.numel()} (max {int(rope_d.max())} ulp)", flush=True)
     assert int(nope_d.max()) <= 1, f"{what}: nope beyond 1 ulp"
-    assert n_beyond <= ROPE_BEYOND_1ULP_CEILING * rope_d.numel(), (
+    assert n_beyond <= ROPE_BEYOND_1ULP_CEILING * rope_d.numel() + 1, (
         f"{what}: {n_beyond} rope elements beyond 1 ulp, above the ceiling")
     if n_beyond:
         tok = torch.nonzero(beyond.flatten(1).any(1)).flatten()  # only tokens with an exceedance
