@@ -536,12 +536,19 @@ def test_gpu_scaled_dequant_every_scale_byte():
                       torch.ones(B, dtype=torch.int32), None)
     out, lse = _gpu(w)
     out = out.cpu()
-    bad = []
+    bad, detail = [], ""
     for b in range(B):
         row = oracle.model1_token_row(cache, b)
-        if not torch.equal(out[b, 0].view(torch.int16), row.expand(64, 512).view(torch.int16)):
+        got = out[b, 0].view(torch.int16)
+        want = row.expand(64, 512).view(torch.int16)
+        if not torch.equal(got, want):
+            if not bad:
+                diff = torch.nonzero(got != want)
+                detail = "; first byte's differences (head, dim, gpu bits, oracle bits): " + ", ".join(
+                    f"({h}, {d}, {int(got[h, d]) & 0xFFFF:#06x}, {int(want[h, d]) & 0xFFFF:#06x})"
+                    for h, d in diff[:12].tolist()) + f" of {diff.shape[0]}"
             bad.append(b)
-    assert not bad, f"scale bytes whose attended row differs from the oracle's: {bad[:16]}"
+    assert not bad, f"{len(bad)} scale bytes whose attended row differs from the oracle's: {bad}{detail}"
 
 
 @pytest.mark.gpu
