@@ -522,7 +522,9 @@ def test_gpu_scaled_dequant_every_scale_byte():
     (topk_length 1, no sink), so its softmax weight is exactly 1 and every
     head's output is that entry's bf16 row, which must equal the oracle's
     bf16(f32(code) * 2^(byte - 127)) (byte 0: scale 0) bit for bit.  q row b
-    is scaled down for large bytes so the score stays finite in fp32."""
+    is scaled down for large bytes so the score stays finite in fp32.  The
+    sign of zero is not compared: the output is the fp32 sum 0 + 1 * V, in
+    which a -0 of V becomes +0, as in the reference's accumulation."""
     print("\n[case] sparse MLA scaled dequant, scale bytes 0..254", flush=True)
     cache = _scale_sweep_cache(True)
     g = torch.Generator().manual_seed(42)
@@ -539,8 +541,9 @@ def test_gpu_scaled_dequant_every_scale_byte():
     bad, detail = [], ""
     for b in range(B):
         row = oracle.model1_token_row(cache, b)
-        got = out[b, 0].view(torch.int16)
-        want = row.expand(64, 512).view(torch.int16)
+        zero_as_pos = lambda x: torch.where((x & 0x7FFF) == 0, torch.zeros_like(x), x)
+        got = zero_as_pos(out[b, 0].view(torch.int16))
+        want = zero_as_pos(row.expand(64, 512).view(torch.int16))
         if not torch.equal(got, want):
             if not bad:
                 diff = torch.nonzero(got != want)
