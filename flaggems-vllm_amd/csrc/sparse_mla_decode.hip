@@ -121,8 +121,9 @@ __device__ __forceinline__ int kbuf_byte(int row, int block) {
 
 // 8 e4m3 codes times 2^(byte - 127) -> 8 bf16, as the reference computes
 // it: bf16(f32(code) * f32 bits (byte << 23)).  v_cvt_scalef32_pk_bf16_fp8
-// gives exactly that for bytes 1..254 (checked on the GPU for all 256 x 254
-// code/byte pairs).  It reads byte 0 as 2^-127 where the bit cast gives 0, so
+// gives exactly that for bytes 1..254 (tests/test_sparse_mla.py sweeps every
+// byte 0..254 with all 254 finite codes through the attention and through
+// the expanded copy).  It reads byte 0 as 2^-127 where the bit cast gives 0, so
 // byte 0 converts at scale 1 and keeps only the sign bits (+-0, exact for
 // finite codes).  Byte 255 is an infinite scale, which the cache writer
 // cannot produce; like other non-finite inputs it is out of scope.
