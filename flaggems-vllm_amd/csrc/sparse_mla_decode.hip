@@ -40,6 +40,8 @@
 // gathered from a zero page, and their scores masked to -inf.
 #include <math.h>
 
+#include <mutex>
+
 #include "fgv_device.h"
 #include "fgv_host.h"
 
@@ -967,20 +969,28 @@ extern "C" int64_t fgv_sparse_mla_decode_workspace_bytes(int64_t batch, int64_t 
            fgv::split_bytes(batch, topk, extra_topk);
 }
 
-extern "C" int fgv_sparse_mla_decode_model1(
-    const void* q, int64_t q_stride_b, int64_t q_stride_s, int64_t q_stride_h,
-    const void* k_cache, int64_t cache_block_stride, int64_t num_blocks, int64_t page_size,
-    const int32_t* indices, int64_t idx_stride_b, int64_t idx_stride_s, int64_t topk,
-    const int32_t* topk_length,
-    const void* extra_k_cache, int64_t extra_block_stride, int64_t extra_num_blocks, int64_t extra_page_size,
-    const int32_t* extra_indices, int64_t extra_idx_stride_b, int64_t extra_idx_stride_s, int64_t extra_topk,
-    const int32_t* extra_topk_length,
-    const float* attn_sink, float softmax_scale,
-    void* out, int64_t out_stride_b, int64_t out_stride_s, int64_t out_stride_h,
-    float* lse, int64_t lse_stride_b, int64_t lse_stride_h,
-    int64_t batch, int64_t seq_q, int64_t num_heads,
-    void* workspace, int64_t workspace_bytes, void* stream) {
-    using namespace fgv;
+// The argument list of fgv_sparse_mla_decode_model1 up to (not including) the
+// workspace, shared by both entry points.
+#define FGV_MLA_PARAMS                                                                                           \
+    const void *q, int64_t q_stride_b, int64_t q_stride_s, int64_t q_stride_h, const void *k_cache,             \
+        int64_t cache_block_stride, int64_t num_blocks, int64_t page_size, const int32_t *indices,               \
+        int64_t idx_stride_b, int64_t idx_stride_s, int64_t topk, const int32_t *topk_length,                    \
+        const void *extra_k_cache, int64_t extra_block_stride, int64_t extra_num_blocks, int64_t extra_page_size, \
+        const int32_t *extra_indices, int64_t extra_idx_stride_b, int64_t extra_idx_stride_s, int64_t extra_topk, \
+        const int32_t *extra_topk_length, const float *attn_sink, float softmax_scale, void *out,                \
+        int64_t out_stride_b, int64_t out_stride_s, int64_t out_stride_h, float *lse, int64_t lse_stride_b,      \
+        int64_t lse_stride_h, int64_t batch, int64_t seq_q, int64_t num_heads
+#define FGV_MLA_ARGS                                                                                        \
+    q, q_stride_b, q_stride_s, q_stride_h, k_cache, cache_block_stride, num_blocks, page_size, indices,     \
+        idx_stride_b, idx_stride_s, topk, topk_length, extra_k_cache, extra_block_stride, extra_num_blocks, \
+        extra_page_size, extra_indices, extra_idx_stride_b, extra_idx_stride_s, extra_topk,                 \
+        extra_topk_length, attn_sink, softmax_scale, out, out_stride_b, out_stride_s, out_stride_h, lse,    \
+        lse_stride_b, lse_stride_h, batch, seq_q, num_heads
+
+namespace fgv {
+namespace {
+
+int mla_decode(FGV_MLA_PARAMS, void* workspace, int64_t workspace_bytes, void* stream) {
     if (batch < 0 || seq_q < 0 || num_heads < 0)
         return fail(FGV_E_BAD_SHAPE, "negative size");
     if (num_heads % kBlockHeads)
@@ -1074,4 +1084,69 @@ extern "C" int fgv_sparse_mla_decode_model1(
     }
     hipLaunchKernelGGL(sparse_mla_decode_kernel, dim3((unsigned)items), dim3(kThreads), 0, st, a);
     return launch_status();
+}
+
+// ---- the no-allocation entry point's scratch: a fixed device array in
+// place of the caller's workspace.  Each device that loads the library holds
+// its own copy until the process ends.  Nothing in it needs clearing between
+// calls: every byte a call reads (the expanded cache, the split partial
+// slots, the row prefix sums) is written earlier in the same call.
+constexpr int64_t kScratchBytes = FGV_MLA_NO_ALLOC_SCRATCH_BYTES;
+__device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices];
+
+// Device address of `scratch` on the current device, looked up once per
+// device with that device current (the array's name in host code is only a
+// host-side stand-in).
+int scratch_of_current_device(void** ptr) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess)
+        return static_cast<int>(e);
+    if (dev < 0 || dev >= kMaxScratchDevices)
+        return fail(FGV_E_BAD_SHAPE, "device index beyond the 64 devices the scratch table holds");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess)
+            return static_cast<int>(e);
+        if (!p)
+            return fail(FGV_E_NULL_POINTER, "hipGetSymbolAddress gave no address for the scratch array");
+        g_scratch_ptr[dev] = p;
+    }
+    *ptr = g_scratch_ptr[dev];
+    return FGV_OK;
+}
+
+}  // namespace
+}  // namespace fgv
+
+extern "C" int fgv_sparse_mla_decode_model1(FGV_MLA_PARAMS, void* workspace, int64_t workspace_bytes,
+                                            void* stream) {
+    return fgv::mla_decode(FGV_MLA_ARGS, workspace, workspace_bytes, stream);
+}
+
+extern "C" int fgv_sparse_mla_decode_model1_no_alloc(FGV_MLA_PARAMS, void* stream) {
+    using namespace fgv;
+    // the schedule fgv_sparse_mla_decode_model1 runs with the workspace the
+    // query asks for, or an error when that does not fit the scratch
+    const int64_t extra_entries = extra_k_cache ? extra_num_blocks * extra_page_size : 0;
+    const int64_t need = fgv_sparse_mla_decode_workspace_bytes(batch, seq_q, num_heads, topk,
+                                                               extra_k_cache ? extra_topk : 0, extra_entries);
+    if (need > kScratchBytes)
+        return fail(FGV_E_TOO_LARGE,
+                    "fgv_sparse_mla_decode_model1_no_alloc: this call's schedule needs more workspace than the "
+                    "64 MiB scratch (fgv_sparse_mla_decode_workspace_bytes); call "
+                    "fgv_sparse_mla_decode_model1 with a workspace instead");
+    void* ws = nullptr;
+    if (need > 0) {
+        const int rc = scratch_of_current_device(&ws);
+        if (rc)
+            return rc;
+    }
+    return mla_decode(FGV_MLA_ARGS, ws, need, stream);
 }

@@ -144,6 +144,8 @@ def lib():
         _P, _I64,  # workspace, workspace_bytes
         _P,  # stream
     ]
+    L.fgv_sparse_mla_decode_model1_no_alloc.restype = ctypes.c_int
+    L.fgv_sparse_mla_decode_model1_no_alloc.argtypes = L.fgv_sparse_mla_decode_model1.argtypes[:-3] + [_P]
     L.fgv_sparse_mla_decode_workspace_bytes.restype = ctypes.c_int64
     L.fgv_sparse_mla_decode_workspace_bytes.argtypes = [_I64, _I64, _I64, _I64, _I64, _I64]
     _lib = L
@@ -172,4 +174,5 @@ EXPORTED_SYMBOLS = (
     "fgv_compute_slot_mapping",
     "fgv_sparse_mla_decode_model1",
     "fgv_sparse_mla_decode_workspace_bytes",
+    "fgv_sparse_mla_decode_model1_no_alloc",
 )

@@ -275,6 +275,46 @@ int fgv_sparse_mla_decode_model1(
 int64_t fgv_sparse_mla_decode_workspace_bytes(int64_t batch, int64_t seq_q, int64_t num_heads,
                                               int64_t topk, int64_t extra_topk, int64_t extra_num_entries);
 
+/* Size of the fixed device scratch of fgv_sparse_mla_decode_model1_no_alloc. */
+#define FGV_MLA_NO_ALLOC_SCRATCH_BYTES (64LL << 20)
+
+/*
+ * Sparse MLA decode exactly as fgv_sparse_mla_decode_model1 with the workspace
+ * fgv_sparse_mla_decode_workspace_bytes asks for (same arguments, same
+ * schedule, same output bits), but with no workspace argument and no
+ * allocation of any kind: the workspace is a fixed device array of
+ * FGV_MLA_NO_ALLOC_SCRATCH_BYTES (64 MiB) inside the library, one per device,
+ * held from the library's first use on that device until the process ends.
+ *
+ * No counterpart in the reference.  It is for callers that cannot allocate
+ * device memory: code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc.
+ *
+ * Limit: a call whose workspace query exceeds 64 MiB returns FGV_E_TOO_LARGE
+ * and launches nothing (with today's schedule: expanded extra caches above
+ * 64 MiB, and every call long enough for the split grid, whose partial slots
+ * take ~135 MB); call fgv_sparse_mla_decode_model1 with a workspace for those.
+ * Calls on one device share its scratch: calls that overlap in time on one
+ * device (concurrent streams, other host threads) race and must be serialised
+ * by the caller.  The scratch of the device current at the call is used; the
+ * stream must belong to that device.
+ */
+int fgv_sparse_mla_decode_model1_no_alloc(
+    const void* q, int64_t q_stride_b, int64_t q_stride_s, int64_t q_stride_h,
+    const void* k_cache, int64_t cache_block_stride, int64_t num_blocks, int64_t page_size,
+    const int32_t* indices, int64_t idx_stride_b, int64_t idx_stride_s, int64_t topk,
+    const int32_t* topk_length,
+    const void* extra_k_cache, int64_t extra_block_stride, int64_t extra_num_blocks,
+    int64_t extra_page_size,
+    const int32_t* extra_indices, int64_t extra_idx_stride_b, int64_t extra_idx_stride_s,
+    int64_t extra_topk,
+    const int32_t* extra_topk_length,
+    const float* attn_sink, float softmax_scale,
+    void* out, int64_t out_stride_b, int64_t out_stride_s, int64_t out_stride_h,
+    float* lse, int64_t lse_stride_b, int64_t lse_stride_h,
+    int64_t batch, int64_t seq_q, int64_t num_heads,
+    void* stream);
+
 #ifdef __cplusplus
 }
 #endif
