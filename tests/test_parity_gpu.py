@@ -350,3 +350,24 @@ def test_combined_largest(T, H, bs):
                       torch.zeros(nblk, bs * W.HEAD_BYTES, dtype=torch.uint8), slots, positions, cos_sin, 1e-6, bs)
     ref_kv = oracle_main(full)
     assert torch.equal(cache_out, ref_kv.k_cache), f"T={T} H={H} bs={bs}: cache differs"
+
+
+# Grids around one round of workgroups (T * H from 8192 to 32769 rows, 512 to
+# 2049 blocks): head counts that are and are not multiples of the 16-row block
+# (one token per block or not), ragged last blocks, H = 1.
+@pytest.mark.parametrize("T,H", [(8193, 1), (600, 16), (257, 37), (300, 48), (256, 64), (129, 128),
+                                 (512, 64), (8192, 1), (32769, 1)])
+def test_mid_size_grids(T, H):
+    _say(f"mid-size grid T={T} H={H}")
+    g = torch.Generator().manual_seed(T + H)
+    nblk = (T + 63) // 64 + 2
+    slots = torch.randperm(nblk * 64, generator=g)[:T].to(torch.int64)
+    slots[::11] = -1
+    w = W.Workload(f"R2 T{T} H{H}", W.randn_bf16((T, H, 512), g), W.randn_bf16((T, 512), g),
+                   torch.zeros(nblk, 64 * W.HEAD_BYTES, dtype=torch.uint8), slots,
+                   torch.randint(0, 4096, (T,), generator=g, dtype=torch.int64),
+                   W.make_cos_sin_cache(4096), 1e-6, 64)
+    gw = run_gpu(w)
+    ref = oracle_main(w)
+    assert_q_exact(gw.q.cpu(), ref.q, w.name)
+    assert torch.equal(gw.k_cache.cpu(), ref.k_cache), f"{w.name}: cache differs"
