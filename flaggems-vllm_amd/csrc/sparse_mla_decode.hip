@@ -148,6 +148,11 @@ __device__ __forceinline__ uint4 dequant8(uint2 codes, uint32_t byte) {
 // K rows exactly zero without any select in the dequantisation (e4m3 code 0
 // gives 0 at any scale), and keeps every lane of a gather active.
 __device__ __align__(256) uint8_t mla_zero_entry[1024];
+// The scale bytes gathered for entries that are not attended: 127 (2^0), so
+// that a zero scale byte in a gathered chunk always belongs to an attended
+// entry (dequantize's exact-route test needs no score mask).
+__device__ __align__(16) uint8_t mla_unit_scales[16] = {127, 127, 127, 127, 127, 127, 127, 127,
+                                                        127, 127, 127, 127, 127, 127, 127, 127};
 
 // One list (main or extra) as one (batch row, query position) sees it.
 struct ListView {
@@ -244,7 +249,7 @@ __device__ __forceinline__ void issue_gather(const ListView& v, const uint8_t* d
                                          (lds_u32_t*)(dst + n * kRegion + 1024 * wave), 16, 0, 0);
     }
     const int64_t soff = entry_offset(v, id, kScaleBytesPerToken);
-    const uint8_t* scl = (soff >= 0 ? v.cache + (int64_t)v.page_size * kTokenDataBytes + soff : dummy) +
+    const uint8_t* scl = (soff >= 0 ? v.cache + (int64_t)v.page_size * kTokenDataBytes + soff : mla_unit_scales) +
                          4 * (lane & 1);
     __builtin_amdgcn_global_load_lds((global_u32_t*)scl, (lds_u32_t*)(dst + kRawScaleOff + 256 * wave), 4, 0, 0);
     if (sub == 0)
@@ -286,8 +291,7 @@ __device__ __forceinline__ uint4 dequant_piece(uint4 piece, uint32_t byte, bool 
     return make_uint4(nope ? d.x : piece.x, nope ? d.y : piece.y, nope ? d.z : piece.z, nope ? d.w : piece.w);
 }
 
-__device__ __forceinline__ void dequantize(const uint8_t* raw, const float* mask, uint8_t* kbuf, int wave,
-                                           int lane) {
+__device__ __forceinline__ void dequantize(const uint8_t* raw, uint8_t* kbuf, int wave, int lane) {
     const bool nope = lane < kNopeDim / 8, hi = lane & 1;
     const int k = nope ? lane >> 1 : lane - (kNopeDim / 8 - kNopeDim / 16);
     const int piece_off = (k >> 3) * kRegion + 16 * (k & 7);
@@ -302,11 +306,10 @@ __device__ __forceinline__ void dequantize(const uint8_t* raw, const float* mask
         const uint4 p3 = *reinterpret_cast<const uint4*>(raw + piece_off + 128 * e3);
         const uint32_t b0 = raw[scale_off + 32 * e0], b1 = raw[scale_off + 32 * e1];
         const uint32_t b2 = raw[scale_off + 32 * e2], b3 = raw[scale_off + 32 * e3];
-        // scale byte 0 in an attended entry (never written by the cache
-        // writer) takes the exact route for the whole wave; unattended entries
-        // are zero bytes and convert to zero either way
-        const bool odd = nope && ((b0 == 0 && mask[e0] == 0.f) || (b1 == 0 && mask[e1] == 0.f) ||
-                                  (b2 == 0 && mask[e2] == 0.f) || (b3 == 0 && mask[e3] == 0.f));
+        // a zero scale byte (never written by the cache writer) takes the
+        // exact route for the whole wave; entries that are not attended carry
+        // scale byte 127 and zero codes (issue_gather), so they never ask for it
+        const bool odd = nope && (b0 == 0 || b1 == 0 || b2 == 0 || b3 == 0);
         if (__builtin_expect(__any(odd), 0)) {
             *reinterpret_cast<uint4*>(kbuf + kbuf_byte(e0, lane)) = dequant_piece<true>(p0, b0, nope, hi);
             *reinterpret_cast<uint4*>(kbuf + kbuf_byte(e1, lane)) = dequant_piece<true>(p1, b1, nope, hi);
@@ -549,7 +552,7 @@ __device__ __forceinline__ void run_segment(const MlaArgs& a, uint8_t (&raw)[2][
         else
             __builtin_amdgcn_s_waitcnt(0);
         lds_barrier();  // everyone's gathers landed; K tile no longer read
-        dequantize(cur, mask_lds[c & 1], kbuf, wave, ln);
+        dequantize(cur, kbuf, wave, ln);
         lds_barrier();
         if (c + 1 < c_mid)
             issue_gather(select(v0, v1, c + 1 >= n0), dummy, wave, ln, id_next, raw[(c + 1) & 1],
