@@ -35,13 +35,17 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", type=int, default=2, help="main-op workload c0..c4 (default c2)")
     ap.add_argument("--op", choices=["main", "inv_rope", "gather", "rmsnorm", "indexer",
-                                     "slot_mapping", "mla", "copy"],
+                                     "slot_mapping", "mla", "indexer_k", "indexer_k_gather", "copy"],
                     default="main",
                     help="copy: torch device copy of 512 MiB, the HBM calibration kernel")
     ap.add_argument("--tma", action="store_true", help="inv_rope: packed UE8M0 scales")
     ap.add_argument("--fp4", action="store_true", help="indexer: MXFP4 instead of FP8")
     ap.add_argument("--mla-case", choices=["decode", "extra512", "extra8192"], default="decode",
                     help="mla: the reference benchmark's MODEL1 sparse-decode case")
+    ap.add_argument("--indexer-case", choices=["0", "1", "2", "3", "large"], default="3",
+                    help="indexer_k / indexer_k_gather: the reference benchmark's shape 0..3 (default its "
+                         "largest) or 'large' (65536 tokens, head_dim 512)")
+    ap.add_argument("--fp16", action="store_true", help="indexer_k: float16 keys instead of bfloat16")
     ap.add_argument("--cpu-sample-tokens", type=int, default=8192)
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="repeat the CPU sample until this much CPU time is spent (min 3 runs)")
@@ -491,6 +495,57 @@ def main():
                   "schedule": ("balanced split grid + combine kernel" if split
                                else "one workgroup per (row, 64-head block)")
                               + ("; extra cache expanded to bf16 once per call" if expanded else "")}
+    elif args.op == "indexer_k":
+        # indexer key quantise + insert at the reference benchmark's shapes
+        # (benchmark/test_indexer_k_quant_and_cache.py:97-102)
+        if args.indexer_case == "large":
+            T, nblk, bs, hd = 65536, 4096, 16, 512
+        else:
+            T, nblk, bs, hd = W.INDEXER_K_INSERT_CASES[int(args.indexer_case)]
+        dtype = torch.float16 if args.fp16 else torch.bfloat16
+        k_cpu, cache_cpu, slots_cpu = W.make_indexer_k_insert(T, nblk, bs, hd, dtype)
+        bytes_call = W.indexer_k_insert_bytes(T - 1, hd)  # the last token is padding (slot -1)
+        k_d, slots_d = k_cpu.to(dev), slots_cpu.to(dev)
+
+        def make_step(i):
+            x = (k_d, cache_cpu.to(dev), slots_d) if i == 0 else (k_d.clone(), cache_cpu.to(dev), slots_d.clone())
+            return lambda: flaggems_vllm.indexer_k_quant_and_cache(x[0], x[1], x[2], 128, "ue8m0")
+
+        kernel = "indexer_k_quant_kernel"
+        workload = f"T{T}_hd{hd}_bs{bs}" + ("_fp16" if args.fp16 else "_bf16")
+        config = {"workload": f"indexer_k_quant_and_cache T={T}, head_dim={hd}, {nblk} blocks x {bs} slots, "
+                              f"{'fp16' if args.fp16 else 'bf16'} keys, UE8M0 scales", "num_tokens": T,
+                  "head_dim": hd, "block_size": bs}
+        nc = min(T, 8192)
+        ck, cc, cs_ = k_cpu[:nc], cache_cpu.clone(), slots_cpu[:nc]
+        cpu_case = (lambda: torch_ref.indexer_k_quant_and_cache(ck, cc, cs_, 128, "ue8m0"), nc, "tokens/s",
+                    f"first {nc} of {T} tokens")
+    elif args.op == "indexer_k_gather":
+        # gather of a batch's cached indexer keys at the reference benchmark's
+        # shapes (benchmark/test_cp_gather_indexer_k_quant_cache.py:125-131)
+        if args.indexer_case == "large":
+            B, L, bs, hd = 64, 1024, 16, 512
+        else:
+            B, L, bs, hd = W.INDEXER_K_GATHER_CASES[int(args.indexer_case)]
+        cache_cpu, kf_cpu, ks_cpu, bt_cpu, cu_cpu = W.make_indexer_k_gather([L] * B, bs, hd)
+        T = B * L
+        bytes_call = W.indexer_k_gather_bytes(T, hd)
+        bt_d, cu_d = bt_cpu.to(dev), cu_cpu.to(dev)
+
+        def make_step(i):
+            c, kf, ks = cache_cpu.to(dev), kf_cpu.to(dev), ks_cpu.to(dev)
+            return lambda: flaggems_vllm.cp_gather_indexer_k_quant_cache(c, kf, ks, bt_d, cu_d)
+
+        kernel = "indexer_k_gather_kernel"
+        workload = f"B{B}_L{L}_hd{hd}_bs{bs}"
+        config = {"workload": f"cp_gather_indexer_k_quant_cache batch={B} x {L} tokens, head_dim={hd}, "
+                              f"block {bs}", "num_tokens": T, "batch": B, "head_dim": hd, "block_size": bs}
+        nb = max(1, min(B, 8192 // L))
+        ck2, cs2 = kf_cpu[:nb * L].clone(), ks_cpu[:nb * L].clone()
+        cpu_case = (lambda: torch_ref.cp_gather_indexer_k_quant_cache(cache_cpu, ck2, cs2, bt_cpu[:nb],
+                                                                      cu_cpu[:nb + 1]),
+                    nb * L, "tokens/s", f"first {nb} of {B} requests ({nb * L} tokens; the reference "
+                                        f"test's per-token loop)")
     elif args.op == "copy":
         n = 512 << 20
         src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
@@ -522,7 +577,7 @@ def main():
                   "num_tokens": T, "num_heads": H, "n_groups": 8}
 
     n_sets = 1
-    if args.op in ("main", "gather", "rmsnorm", "indexer", "mla", "inv_rope"):
+    if args.op in ("main", "gather", "rmsnorm", "indexer", "mla", "inv_rope", "indexer_k", "indexer_k_gather"):
         step, n_sets = rotating(make_step, bytes_call)
     if n_sets == 1:
         config["input_sets"] = "one input set"
@@ -549,10 +604,14 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": {"mla": "bf16", "slot_mapping": "int64", "copy": "u8"}.get(args.op, "f32"),
+        "dtype": {"mla": "bf16", "slot_mapping": "int64", "copy": "u8",
+                  "indexer_k_gather": "u8"}.get(args.op, "f32"),
         "data": ("synthetic: seeded q ~ N(0,1)/10 bf16, cache NoPE ~ N(0,0.1) quantised to e4m3 + "
                  "E8M0 per 64, RoPE ~ N(0,0.1) bf16, uniform indices and top-k lengths, sink ~ N(0,1)"
                  if args.op == "mla" else
+                 "synthetic: seeded N(0,1) keys, distinct random slots (last one -1), cache pre-filled with "
+                 "e4m3 codes of N(0,1) and scales U[0.01, 1.01) as the reference's tests fill it"
+                 if args.op in ("indexer_k", "indexer_k_gather") else
                  "synthetic: seeded N(0,1) bf16 q/kv, fp32 cos/sin (theta 1e4), vLLM-style paged slots"),
         "config": config,
         "kernel_us": t_kernel * 1e6,

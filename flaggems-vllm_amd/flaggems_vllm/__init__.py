@@ -3,8 +3,10 @@
 Public names follow the reference package (src/flaggems_vllm/__init__.py:21-46):
 ``fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert``, ``fused_inv_rope_fp8_quant``,
 their compatibility aliases ``ops_deepseek_v4_qnorm_rope_kv_rope_quant_insert`` and
-``ops_inv_rope_fp8_quant``, ``SUPPORTED_FP8_DTYPE``, ``device`` and ``vendor_name``.
-Both ops run hand-written HIP kernels through the C ABI declared in
+``ops_inv_rope_fp8_quant``, ``SUPPORTED_FP8_DTYPE``, ``device`` and ``vendor_name``;
+and the ops either side of that path (src/flaggems_vllm/ops/__init__.py): the
+K-cache gather, q/kv RMSNorm, indexer q and key-cache ops, slot mapping and
+sparse MLA decode.  Every op runs hand-written HIP kernels through the C ABI declared in
 include/flaggems_vllm_amd.h; there is no Triton, no vendor dispatch and no
 CPU fallback.
 """
@@ -13,6 +15,7 @@ from .ops import (  # noqa: F401
     SUPPORTED_FP8_DTYPE,
     FlashMLASchedMeta,
     compute_slot_mapping_parallel,
+    cp_gather_indexer_k_quant_cache,
     dequantize_and_gather_k_cache,
     flash_mla_with_kvcache,
     fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert,
@@ -20,6 +23,7 @@ from .ops import (  # noqa: F401
     fused_inv_rope_fp8_quant,
     fused_q_kv_rmsnorm,
     get_mla_metadata,
+    indexer_k_quant_and_cache,
 )
 
 from . import library  # noqa: F401,E402  (torch.ops.flaggems_vllm.* registrations)
@@ -34,6 +38,7 @@ ops_inv_rope_fp8_quant = fused_inv_rope_fp8_quant
 __all__ = [
     "FlashMLASchedMeta",
     "compute_slot_mapping_parallel",
+    "cp_gather_indexer_k_quant_cache",
     "flash_mla_with_kvcache",
     "get_mla_metadata",
     "dequantize_and_gather_k_cache",
@@ -41,6 +46,7 @@ __all__ = [
     "fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert",
     "fused_indexer_q_rope_quant",
     "fused_inv_rope_fp8_quant",
+    "indexer_k_quant_and_cache",
     "ops_deepseek_v4_qnorm_rope_kv_rope_quant_insert",
     "ops_inv_rope_fp8_quant",
     "SUPPORTED_FP8_DTYPE",

@@ -148,6 +148,23 @@ def lib():
     L.fgv_sparse_mla_decode_model1_no_alloc.argtypes = L.fgv_sparse_mla_decode_model1.argtypes[:-3] + [_P]
     L.fgv_sparse_mla_decode_workspace_bytes.restype = ctypes.c_int64
     L.fgv_sparse_mla_decode_workspace_bytes.argtypes = [_I64, _I64, _I64, _I64, _I64, _I64]
+    L.fgv_indexer_k_quant_and_cache.restype = ctypes.c_int
+    L.fgv_indexer_k_quant_and_cache.argtypes = [
+        _P, _I64, ctypes.c_int,  # k, k_stride_token, k_is_fp16
+        _I64, _I64, _I64,  # num_tokens, head_dim, quant_block_size
+        _P, _I64, _I64, _I64,  # kv_cache, cache_block_stride, num_blocks, block_size
+        _P, ctypes.c_int,  # slot_mapping, use_ue8m0
+        _P,  # stream
+    ]
+    L.fgv_cp_gather_indexer_k_quant_cache.restype = ctypes.c_int
+    L.fgv_cp_gather_indexer_k_quant_cache.argtypes = [
+        _P, _I64, _I64, _I64,  # kv_cache, cache_block_stride, num_blocks, block_size
+        _I64, _I64,  # head_dim, quant_block_size
+        _P, _I64, _P, _I64,  # k_out, stride, scale_out, stride (bytes)
+        _P, _I64, _I64,  # block_table, stride, max_blocks_per_seq
+        _P, _I64, _I64,  # cu_seqlen, batch_size, num_tokens
+        _P,  # stream
+    ]
     _lib = L
     return _lib
 
@@ -175,4 +192,6 @@ EXPORTED_SYMBOLS = (
     "fgv_sparse_mla_decode_model1",
     "fgv_sparse_mla_decode_workspace_bytes",
     "fgv_sparse_mla_decode_model1_no_alloc",
+    "fgv_indexer_k_quant_and_cache",
+    "fgv_cp_gather_indexer_k_quant_cache",
 )

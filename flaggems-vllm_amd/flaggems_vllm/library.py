@@ -5,7 +5,8 @@ The public API stays the plain Python functions the reference package exports
 These registrations expose the same ops to torch.compile and graph capture as
 opaque custom ops: the schemas declare what each op writes, namely ``q`` and
 ``k_cache`` for the main op (alias-annotated ``Tensor(a0!) q``, ``Tensor(a2!) k_cache``), ``out``
-for the gather and ``slot_mapping`` for the slot mapping.  The fake (meta)
+for the gather, ``slot_mapping`` for the slot mapping, ``kv_cache`` for the
+indexer key insert and ``k_fp8`` / ``k_fp8_scale`` for its gather.  The fake (meta)
 implementations give the output shapes and strides the real ops return.
 Each registered op calls the same wrapper, so argument checks and errors are
 the wrapper's.
@@ -21,11 +22,13 @@ import torch
 
 from .ops import (
     compute_slot_mapping_parallel,
+    cp_gather_indexer_k_quant_cache,
     dequantize_and_gather_k_cache,
     fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert,
     fused_indexer_q_rope_quant,
     fused_inv_rope_fp8_quant,
     fused_q_kv_rmsnorm,
+    indexer_k_quant_and_cache,
 )
 
 NAMESPACE = "flaggems_vllm"
@@ -141,6 +144,28 @@ def _(num_tokens, max_num_tokens, query_start_loc, num_reqs, positions, block_ta
     return None
 
 
+@_op("indexer_k_quant_and_cache", ("kv_cache",))
+def _indexer_k_quant_and_cache(k: torch.Tensor, kv_cache: torch.Tensor, slot_mapping: torch.Tensor,
+                               quant_block_size: int, scale_fmt: Optional[str]) -> None:
+    indexer_k_quant_and_cache(k, kv_cache, slot_mapping, quant_block_size, scale_fmt)
+
+
+@_indexer_k_quant_and_cache.register_fake
+def _(k, kv_cache, slot_mapping, quant_block_size, scale_fmt):
+    return None
+
+
+@_op("cp_gather_indexer_k_quant_cache", ("k_fp8", "k_fp8_scale"))
+def _cp_gather_indexer_k_quant_cache(k_cache: torch.Tensor, k_fp8: torch.Tensor, k_fp8_scale: torch.Tensor,
+                                     block_table: torch.Tensor, cu_seqlen: torch.Tensor) -> None:
+    cp_gather_indexer_k_quant_cache(k_cache, k_fp8, k_fp8_scale, block_table, cu_seqlen)
+
+
+@_cp_gather_indexer_k_quant_cache.register_fake
+def _(k_cache, k_fp8, k_fp8_scale, block_table, cu_seqlen):
+    return None
+
+
 REGISTERED: List[str] = [
     "fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert",
     "fused_inv_rope_fp8_quant",
@@ -148,4 +173,6 @@ REGISTERED: List[str] = [
     "dequantize_and_gather_k_cache",
     "fused_indexer_q_rope_quant",
     "compute_slot_mapping_parallel",
+    "indexer_k_quant_and_cache",
+    "cp_gather_indexer_k_quant_cache",
 ]

@@ -1,4 +1,5 @@
-"""DeepSeek-V4 attention pre-processing ops (reference: src/flaggems_vllm/ops/__init__.py:34-38, 55, 61-65)."""
+"""DeepSeek-V4 attention pre-processing ops (reference: src/flaggems_vllm/ops/__init__.py:23-24, 34-38, 55, 61-65, 78)."""
+from .cp_gather_indexer_k_quant_cache import cp_gather_indexer_k_quant_cache
 from .deepseek_v4_attention_dequantize_and_gather_k_cache import dequantize_and_gather_k_cache
 from .deepseek_v4_attention_fused_q_kv_rmsnorm import fused_q_kv_rmsnorm
 from .flash_mla_with_kvcache import FlashMLASchedMeta, flash_mla_with_kvcache, get_mla_metadata
@@ -7,11 +8,13 @@ from .fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert import (
 )
 from .fused_indexer_q_rope_quant import fused_indexer_q_rope_quant
 from .fused_inv_rope_fp8_quant import SUPPORTED_FP8_DTYPE, fused_inv_rope_fp8_quant
+from .indexer_k_quant_and_cache import indexer_k_quant_and_cache
 from .slot_mapping import compute_slot_mapping_parallel
 
 __all__ = [
     "FlashMLASchedMeta",
     "compute_slot_mapping_parallel",
+    "cp_gather_indexer_k_quant_cache",
     "flash_mla_with_kvcache",
     "get_mla_metadata",
     "dequantize_and_gather_k_cache",
@@ -19,5 +22,6 @@ __all__ = [
     "fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert",
     "fused_indexer_q_rope_quant",
     "fused_inv_rope_fp8_quant",
+    "indexer_k_quant_and_cache",
     "SUPPORTED_FP8_DTYPE",
 ]

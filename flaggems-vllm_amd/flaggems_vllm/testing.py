@@ -467,3 +467,83 @@ def mla_flops(w: MlaWorkload) -> int:
     (head, attended entry)."""
     HQ = w.q.shape[2]
     return 4 * HEAD_DIM * HQ * w.used_tokens()
+
+
+# ---------------------------------------------------------------------------
+# Sparse-indexer key cache (indexer_k_quant_and_cache / its gather).  Shapes of
+# the reference's tests (tests/test_indexer_k_quant_and_cache.py:177-185,
+# tests/test_cp_gather_indexer_k_quant_cache.py:168-175) and benchmarks
+# (benchmark/test_indexer_k_quant_and_cache.py:97-102,
+# benchmark/test_cp_gather_indexer_k_quant_cache.py:125-131).
+# ---------------------------------------------------------------------------
+
+INDEXER_QUANT_BLOCK = 128
+INDEXER_K_INSERT_CASES = [  # num_tokens, num_blocks, block_size, head_dim (reference benchmark)
+    (128, 16, 16, 128), (512, 64, 16, 128), (1024, 128, 16, 512), (2048, 256, 16, 512)]
+INDEXER_K_GATHER_CASES = [  # batch, seq_len, block_size, head_dim (reference benchmark)
+    (4, 256, 16, 128), (8, 512, 16, 128), (16, 1024, 16, 512), (32, 1024, 16, 512)]
+
+
+def indexer_k_row_bytes(head_dim: int) -> int:
+    """Cache bytes per token: head_dim e4m3fn codes + a float32 scale per 128."""
+    return head_dim + 4 * (head_dim // INDEXER_QUANT_BLOCK)
+
+
+def make_indexer_k_cache(num_blocks: int, block_size: int, head_dim: int, gen: torch.Generator) -> torch.Tensor:
+    """uint8 [num_blocks, block_size, row bytes] filled as the reference's tests
+    fill it: codes of N(0, 1) samples, scales uniform in [0.01, 1.01)."""
+    nqb = head_dim // INDEXER_QUANT_BLOCK
+    cache = torch.empty(num_blocks, block_size, indexer_k_row_bytes(head_dim), dtype=torch.uint8)
+    flat = cache.view(num_blocks, -1)
+    codes = torch.randn(num_blocks, block_size * head_dim, generator=gen).to(torch.float8_e4m3fn)
+    flat[:, :block_size * head_dim] = codes.view(torch.uint8)
+    flat[:, block_size * head_dim:].view(torch.float32)[:] = (
+        torch.rand(num_blocks, block_size * nqb, generator=gen) + 0.01)
+    return cache
+
+
+def make_indexer_k_insert(num_tokens: int, num_blocks: int, block_size: int, head_dim: int,
+                          dtype=torch.bfloat16, seed: int = 0):
+    """(k, kv_cache, slot_mapping): N(0, 1) keys, distinct random slots with the
+    last one -1, as the reference's test draws them."""
+    g = torch.Generator().manual_seed(seed)
+    k = torch.randn(num_tokens, head_dim, generator=g).to(dtype)
+    slots = torch.randperm(num_blocks * block_size, generator=g)[:num_tokens].to(torch.int64)
+    if num_tokens:
+        slots[-1] = -1
+    return k, make_indexer_k_cache(num_blocks, block_size, head_dim, g), slots
+
+
+def make_indexer_k_gather(seq_lens, block_size: int, head_dim: int, extra_tokens: int = 0, seed: int = 1,
+                          sentinel: int = 0x7B):
+    """(k_cache, k_fp8, k_fp8_scale, block_table, cu_seqlen) with the reference
+    test's metadata: consecutive blocks per request, -1 past each request's
+    blocks, outputs pre-filled with a sentinel byte, extra_tokens rows past
+    the last request."""
+    g = torch.Generator().manual_seed(seed)
+    lens = torch.tensor(seq_lens, dtype=torch.int32)
+    cu = torch.zeros(len(seq_lens) + 1, dtype=torch.int32)
+    cu[1:] = torch.cumsum(lens, 0)
+    per = [(n + block_size - 1) // block_size for n in seq_lens]
+    table = torch.full((len(seq_lens), max(1, max(per))), -1, dtype=torch.int32)
+    nxt = 0
+    for b, n in enumerate(per):
+        table[b, :n] = torch.arange(nxt, nxt + n, dtype=torch.int32)
+        nxt += n
+    cache = make_indexer_k_cache(max(1, nxt), block_size, head_dim, g)
+    rows = int(cu[-1]) + extra_tokens
+    k_fp8 = torch.full((rows, head_dim), sentinel, dtype=torch.uint8).view(torch.float8_e4m3fn)
+    k_scale = torch.full((rows, 4 * (head_dim // INDEXER_QUANT_BLOCK)), sentinel, dtype=torch.uint8)
+    return cache, k_fp8, k_scale, table, cu
+
+
+def indexer_k_insert_bytes(num_tokens: int, head_dim: int, key_bytes: int = 2) -> int:
+    """Algorithmic HBM bytes of one insert: key row read, slot read, codes and
+    scales written."""
+    return num_tokens * (key_bytes * head_dim + 8 + indexer_k_row_bytes(head_dim))
+
+
+def indexer_k_gather_bytes(num_tokens: int, head_dim: int) -> int:
+    """Algorithmic HBM bytes of one gather: per token the cached row read and
+    written out, and its 4-byte block-table entry."""
+    return num_tokens * (2 * indexer_k_row_bytes(head_dim) + 4)

@@ -211,6 +211,57 @@ int fgv_compute_slot_mapping(
     int64_t pad_id, void* stream);
 
 /*
+ * Sparse-indexer key quantise + paged insert.
+ *
+ * Replaces flaggems_vllm.ops.indexer_k_quant_and_cache
+ * (reference: src/flaggems_vllm/ops/indexer_k_quant_and_cache.py:100-132,
+ * kernel :44-96; torch oracle tests/test_indexer_k_quant_and_cache.py:99-142).
+ *
+ *   k         bf16 (or fp16 if k_is_fp16) [num_tokens, head_dim], row stride
+ *             k_stride_token elements (multiple of 8), 16-byte aligned
+ *   kv_cache  uint8 blocks cache_block_stride bytes apart; block b holds
+ *             block_size x head_dim e4m3fn codes, then block_size x
+ *             (head_dim / 128) float32 scales
+ *   slot_mapping  int64 [num_tokens]; < 0 skips the token
+ *
+ * For token t with slot s >= 0 (block s / block_size < num_blocks) and quant
+ * block j of 128 elements:
+ *   scale = max(amax_j, 1e-4) / 448 (IEEE binary32 division);
+ *           use_ue8m0: 2^ceil(log2(scale))
+ *   codes = e4m3fn(k / scale), scale stored as float32
+ * at row s % block_size of block s / block_size.  quant_block_size must be
+ * 128; head_dim a multiple of 128, at most 2048.
+ */
+int fgv_indexer_k_quant_and_cache(
+    const void* k, int64_t k_stride_token, int k_is_fp16,
+    int64_t num_tokens, int64_t head_dim, int64_t quant_block_size,
+    void* kv_cache, int64_t cache_block_stride, int64_t num_blocks, int64_t block_size,
+    const int64_t* slot_mapping, int use_ue8m0, void* stream);
+
+/*
+ * Gather of a batch's cached sparse-indexer keys.
+ *
+ * Replaces flaggems_vllm.ops.cp_gather_indexer_k_quant_cache
+ * (reference: src/flaggems_vllm/ops/cp_gather_indexer_k_quant_cache.py:114-176,
+ * kernel :23-111; torch oracle tests/test_cp_gather_indexer_k_quant_cache.py:83-114).
+ * Cache layout as fgv_indexer_k_quant_and_cache writes it.  Token
+ * t < num_tokens of request b (cu_seqlen[b] <= t < cu_seqlen[b + 1]) at
+ * position p = t - cu_seqlen[b] copies the head_dim code bytes and
+ * head_dim / 128 float32 scales of row p % block_size of block
+ * block_table[b, p / block_size] to k_out + t * k_out_stride and
+ * scale_out + t * scale_out_stride (byte strides; multiples of 8 and 4).
+ * Tokens outside every request, and tokens whose block-table index or block
+ * is out of range, are left untouched.  cu_seqlen has batch_size + 1 entries,
+ * non-decreasing.
+ */
+int fgv_cp_gather_indexer_k_quant_cache(
+    const void* kv_cache, int64_t cache_block_stride, int64_t num_blocks, int64_t block_size,
+    int64_t head_dim, int64_t quant_block_size,
+    void* k_out, int64_t k_out_stride, void* scale_out, int64_t scale_out_stride,
+    const int32_t* block_table, int64_t block_table_stride, int64_t max_blocks_per_seq,
+    const int32_t* cu_seqlen, int64_t batch_size, int64_t num_tokens, void* stream);
+
+/*
  * Sparse MLA decode over the 584-byte MODEL1 cache.
  *
  * Replaces the sparse MODEL1 branch of flaggems_vllm.flash_mla_with_kvcache

@@ -115,6 +115,21 @@ def lib():
             _I64, _I64, _P, _I64, _P, ctypes.c_int, _P, _I64, _I64, _P, _I64,
             _I64, _I64, _I64, _I64,
         ]
+        L.oracle_f16_to_f32.restype = ctypes.c_float
+        L.oracle_f16_to_f32.argtypes = [ctypes.c_uint16]
+        L.oracle_indexer_k_quant_and_cache.restype = None
+        L.oracle_indexer_k_quant_and_cache.argtypes = [
+            _P, _I64, ctypes.c_int, _I64, _I64, _I64,  # k, k_st, fp16, T, head_dim, qbs
+            _P, _I64, _I64, _I64,  # cache, block_stride, num_blocks, block_size
+            _P, ctypes.c_int,  # slots, ue8m0
+        ]
+        L.oracle_cp_gather_indexer_k_quant_cache.restype = None
+        L.oracle_cp_gather_indexer_k_quant_cache.argtypes = [
+            _P, _I64, _I64, _I64, _I64, _I64,  # cache, block_stride, num_blocks, block_size, head_dim, qbs
+            _P, _I64, _P, _I64,  # k_out, stride, scale_out, stride (bytes)
+            _P, _I64, _I64,  # block_table, stride, max_blocks
+            _P, _I64, _I64,  # cu, batch, T
+        ]
         L.oracle_model1_token_row.restype = None
         L.oracle_model1_token_row.argtypes = [_P, _I64, _I64, _I64, _P]
         L.oracle_sparse_mla_decode_model1.restype = None
@@ -364,3 +379,43 @@ def sparse_mla_decode_model1(q, k_cache, indices, topk_length=None, attn_sink=No
         out.data_ptr(), lse.data_ptr())
     del keep0, keep1
     return out, lse
+
+
+def _cache_bytes(kv_cache):
+    """(flat uint8 view, block stride bytes, num_blocks, block_size) of a
+    [num_blocks, block_size, head_dim + 4 * head_dim / 128] uint8 cache."""
+    _cpu(kv_cache, torch.uint8)
+    assert kv_cache.dim() == 3 and kv_cache[0].is_contiguous()
+    return kv_cache, kv_cache.stride(0), kv_cache.shape[0], kv_cache.shape[1]
+
+
+def indexer_k_quant_and_cache(k, kv_cache, slot_mapping, quant_block_size, scale_fmt):
+    """CPU restatement, in place on ``kv_cache`` (same arguments as
+    flaggems_vllm.ops.indexer_k_quant_and_cache; k bf16 or fp16)."""
+    _cpu(k)
+    assert k.dtype in (torch.bfloat16, torch.float16) and k.stride(-1) == 1
+    cache, bstride, nblk, bs = _cache_bytes(kv_cache)
+    slots = _cpu(slot_mapping, torch.int64).contiguous()
+    lib().oracle_indexer_k_quant_and_cache(
+        k.data_ptr(), k.stride(0), int(k.dtype == torch.float16), slots.shape[0], k.shape[-1],
+        int(quant_block_size), cache.data_ptr(), bstride, nblk, bs, slots.data_ptr(),
+        int(scale_fmt == "ue8m0"))
+
+
+def cp_gather_indexer_k_quant_cache(k_cache, k_fp8, k_fp8_scale, block_table, cu_seqlen):
+    """CPU restatement, in place on ``k_fp8`` / ``k_fp8_scale`` (same arguments
+    as flaggems_vllm.ops.cp_gather_indexer_k_quant_cache; k_fp8_scale holds
+    4 * head_dim / quant_block_size bytes per row).  Positions whose table
+    index or block is out of range are skipped."""
+    cache, bstride, nblk, bs = _cache_bytes(k_cache)
+    head_dim = k_fp8.shape[-1]
+    qbs = head_dim * 4 // (k_fp8_scale.shape[1] * k_fp8_scale.element_size())
+    kb = _cpu(k_fp8).view(torch.uint8)
+    sb = _cpu(k_fp8_scale).view(torch.uint8)
+    bt = _cpu(block_table, torch.int32)
+    cu = _cpu(cu_seqlen, torch.int32).contiguous()
+    assert kb.stride(-1) == 1 and sb.stride(-1) == 1 and bt.stride(-1) == 1
+    assert cu.numel() >= bt.shape[0] + 1
+    lib().oracle_cp_gather_indexer_k_quant_cache(
+        cache.data_ptr(), bstride, nblk, bs, head_dim, qbs, kb.data_ptr(), kb.stride(0), sb.data_ptr(),
+        sb.stride(0), bt.data_ptr(), bt.stride(0), bt.shape[1], cu.data_ptr(), bt.shape[0], kb.shape[0])

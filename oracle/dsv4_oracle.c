@@ -26,6 +26,11 @@
  *   oracle_dequantize_and_gather_k_cache
  *     reference op   src/flaggems_vllm/ops/deepseek_v4_attention_dequantize_and_gather_k_cache.py:38-172
  *     reference test tests/test_deepseek_v4_attention_dequantize_and_gather_k_cache.py:42-119
+ *   oracle_indexer_k_quant_and_cache, oracle_cp_gather_indexer_k_quant_cache
+ *     reference ops  src/flaggems_vllm/ops/indexer_k_quant_and_cache.py:44-132
+ *                    src/flaggems_vllm/ops/cp_gather_indexer_k_quant_cache.py:23-176
+ *     reference test tests/test_indexer_k_quant_and_cache.py:99-142 (torch_indexer)
+ *                    tests/test_cp_gather_indexer_k_quant_cache.py:83-114 (torch_gather)
  *   oracle_sparse_mla_decode_model1 (binary64 attention, see its comment)
  *     reference op   src/flaggems_vllm/ops/flash_mla_with_kvcache.py:489-688, 852-1073
  *                    src/flaggems_vllm/ops/flash_mla_with_kvcache_model1.py:389-470, 699-720
@@ -72,6 +77,17 @@ static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
 static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
 
 float oracle_bf16_to_f32(uint16_t h) { return u2f((uint32_t)h << 16); }
+
+/* IEEE binary16 -> binary32 (exact; subnormals kept). */
+float oracle_f16_to_f32(uint16_t h)
+{
+    uint32_t sign = (uint32_t)(h >> 15) << 31, e = (h >> 10) & 0x1f, m = h & 0x3ff;
+    if (e == 0x1f)
+        return u2f(sign | 0x7f800000u | (m << 13));
+    if (e == 0)
+        return (sign ? -1.0f : 1.0f) * ldexpf((float)m, -24);
+    return u2f(sign | ((e + 112) << 23) | (m << 13));
+}
 
 /* binary32 -> bfloat16, round to nearest, ties to even. NaN -> quiet NaN. */
 uint16_t oracle_f32_to_bf16(float f)
@@ -686,6 +702,83 @@ void oracle_sparse_mla_decode_model1(const uint16_t* q, int64_t B, int64_t SQ, i
             free(kv);
             free(which);
             free(ids);
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------
+ * Sparse indexer key cache (reference test torch_indexer / torch_gather).
+ * Cache block b at cache + b * block_stride: block_size x head_dim e4m3fn
+ * codes, then block_size x (head_dim / qbs) float32 scales.
+ * ------------------------------------------------------------------------ */
+
+/* k: [T, head_dim] bf16 (k_fp16 = 0) or fp16 (k_fp16 = 1), row stride k_st
+ * elements.  For token t with slot s >= 0 and quant block j:
+ *   scale = fl32(max(amax_j, 1e-4) / 448), ue8m0: 2^ceil(log2(scale))
+ *   code  = e4m3fn(fl32(k / scale)) (division IEEE; |k / scale| <= 448(1+eps)
+ *           rounds to 448 at most, so no clamp is needed)
+ * exactly as the torch oracle writes them (tests/test_indexer_k_quant_and_cache.py:118-142). */
+void oracle_indexer_k_quant_and_cache(const uint16_t* k, int64_t k_st, int k_fp16, int64_t T, int64_t head_dim,
+                                      int64_t qbs, uint8_t* cache, int64_t block_stride, int64_t num_blocks,
+                                      int64_t block_size, const int64_t* slots, int ue8m0)
+{
+    if (qbs <= 0 || qbs > 1024)
+        return; /* v[] below holds one quant block */
+    int64_t nqb = head_dim / qbs;
+    for (int64_t t = 0; t < T; ++t) {
+        int64_t slot = slots[t];
+        if (slot < 0)
+            continue;
+        int64_t blk = slot / block_size, row = slot % block_size;
+        if (blk >= num_blocks)
+            continue;
+        uint8_t* base = cache + blk * block_stride;
+        for (int64_t j = 0; j < nqb; ++j) {
+            float v[1024];
+            float amax = 0.0f;
+            for (int64_t i = 0; i < qbs; ++i) {
+                uint16_t h = k[t * k_st + j * qbs + i];
+                v[i] = k_fp16 ? oracle_f16_to_f32(h) : oracle_bf16_to_f32(h);
+                float a = fabsf(v[i]);
+                amax = a > amax ? a : amax;
+            }
+            float scale = (amax > 1e-4f ? amax : 1e-4f) / 448.0f;
+            if (ue8m0)
+                scale = exp2f(ceilf(log2f(scale)));
+            for (int64_t i = 0; i < qbs; ++i)
+                base[row * head_dim + j * qbs + i] = oracle_e4m3fn(v[i] / scale);
+            memcpy(base + block_size * head_dim + (row * nqb + j) * 4, &scale, 4);
+        }
+    }
+}
+
+/* Token t of request b (cu[b] <= t < cu[b + 1], t < T) takes position
+ * pos = t - cu[b] from block block_table[b, pos / block_size], row
+ * pos % block_size: head_dim code bytes into k_out + t * k_out_st and
+ * nqb float32 scales into scale_out + t * scale_out_st (byte strides).
+ * A position whose table index is >= max_blocks, or whose block is outside
+ * [0, num_blocks), is skipped (its rows keep their contents): the product's
+ * documented contract where the reference's behaviour is undefined. */
+void oracle_cp_gather_indexer_k_quant_cache(const uint8_t* cache, int64_t block_stride, int64_t num_blocks,
+                                            int64_t block_size, int64_t head_dim, int64_t qbs, uint8_t* k_out,
+                                            int64_t k_out_st, uint8_t* scale_out, int64_t scale_out_st,
+                                            const int32_t* block_table, int64_t bt_stride, int64_t max_blocks,
+                                            const int32_t* cu, int64_t batch, int64_t T)
+{
+    int64_t nqb = head_dim / qbs;
+    for (int64_t b = 0; b < batch; ++b) {
+        for (int64_t t = cu[b]; t < cu[b + 1] && t < T; ++t) {
+            if (t < 0)
+                continue;
+            int64_t pos = t - cu[b];
+            if (pos / block_size >= max_blocks)
+                continue;
+            int64_t blk = block_table[b * bt_stride + pos / block_size], row = pos % block_size;
+            if (blk < 0 || blk >= num_blocks)
+                continue;
+            const uint8_t* base = cache + blk * block_stride;
+            memcpy(k_out + t * k_out_st, base + row * head_dim, (size_t)head_dim);
+            memcpy(scale_out + t * scale_out_st, base + block_size * head_dim + row * nqb * 4, (size_t)(nqb * 4));
         }
     }
 }

@@ -21,7 +21,10 @@ oracle that the reference's own tests compare its Triton kernels against:
   (ops/deepseek_v4_attention_dequantize_and_gather_k_cache.py:61-120) in torch
   index arithmetic, with torch's float8 -> float cast and exp2 scale;
 * sparse MLA decode over the MODEL1 cache: the portable kernel's chunked
-  online softmax (ops/flash_mla_with_kvcache.py:489-688).
+  online softmax (ops/flash_mla_with_kvcache.py:489-688);
+* indexer key cache: tests/test_indexer_k_quant_and_cache.py ``torch_indexer``
+  :99-142 and tests/test_cp_gather_indexer_k_quant_cache.py ``torch_gather``
+  :83-114, with float8_e4m3fn codes.
 
 Arithmetic is whatever torch's CPU kernels do in float32: the sum of squares
 and rsqrt are torch's, which is why q is compared against this restatement
@@ -291,3 +294,51 @@ def sparse_mla_decode_model1(q, k_cache, indices, topk_length=None, attn_sink=No
             o = acc / torch.where(empty, 1.0, denom)[:, None]
             out[b, s] = torch.where(empty[:, None], 0.0, o).to(torch.bfloat16)
     return out, lse
+
+
+def indexer_k_quant_and_cache(k, kv_cache, slot_mapping, quant_block_size, scale_fmt):
+    """Per token and quant block, in place on the uint8 cache: scale =
+    max(amax, 1e-4) / 448 (ue8m0: exp2(ceil(log2(scale)))), codes =
+    float8_e4m3fn(k / scale), float32 scales after the block's codes.  The
+    reference's per-token loop, batched over tokens (the same elementwise
+    float32 operations); slots are assumed distinct, as vLLM assigns them."""
+    num_blocks, block_size = kv_cache.shape[0], kv_cache.shape[1]
+    head_dim = k.shape[-1]
+    nqb = head_dim // quant_block_size
+    flat = kv_cache.view(num_blocks, -1)
+    values = flat[:, :block_size * head_dim]
+    scales = flat[:, block_size * head_dim:].view(torch.float32)
+    slots = slot_mapping.to(torch.int64)
+    keep = torch.nonzero(slots >= 0).flatten()
+    if keep.numel() == 0:
+        return
+    s = slots[keep]
+    b, r = s // block_size, s % block_size
+    v = k[keep].reshape(-1, nqb, quant_block_size)
+    amax = v.abs().to(torch.float32).amax(dim=-1)
+    scale = torch.maximum(amax, torch.tensor(1e-4, dtype=torch.float32)) / 448.0
+    if scale_fmt == "ue8m0":
+        scale = torch.exp2(torch.ceil(torch.log2(scale)))
+    codes = (v.to(torch.float32) / scale[..., None]).to(torch.float8_e4m3fn).view(torch.uint8)
+    codes = codes.reshape(-1, head_dim)
+    cols = r[:, None] * head_dim + torch.arange(head_dim)
+    values[b[:, None], cols] = codes
+    scales[b[:, None], r[:, None] * nqb + torch.arange(nqb)] = scale
+
+
+def cp_gather_indexer_k_quant_cache(k_cache, k_fp8, k_fp8_scale, block_table, cu_seqlen):
+    """Token t of request b copies the codes and scales of position
+    t - cu_seqlen[b] into row t of k_fp8 / k_fp8_scale (byte views)."""
+    block_size = k_cache.shape[1]
+    head_dim = k_fp8.shape[1]
+    nqb = head_dim // (head_dim * 4 // k_fp8_scale.shape[1])
+    flat = k_cache.view(k_cache.shape[0], -1)
+    values = flat[:, :block_size * head_dim]
+    scales = flat[:, block_size * head_dim:].view(torch.float32)
+    kb, sf = k_fp8.view(torch.uint8), k_fp8_scale.view(torch.float32)
+    for b in range(block_table.shape[0]):
+        for t in range(int(cu_seqlen[b]), int(cu_seqlen[b + 1])):
+            pos = t - int(cu_seqlen[b])
+            blk, r = int(block_table[b, pos // block_size]), pos % block_size
+            kb[t] = values[blk, r * head_dim:(r + 1) * head_dim]
+            sf[t] = scales[blk, r * nqb:(r + 1) * nqb]

@@ -27,6 +27,8 @@ WRITES = {
     "dequantize_and_gather_k_cache": {"out"},
     "fused_indexer_q_rope_quant": set(),
     "compute_slot_mapping_parallel": {"slot_mapping"},
+    "indexer_k_quant_and_cache": {"kv_cache"},
+    "cp_gather_indexer_k_quant_cache": {"k_fp8", "k_fp8_scale"},
 }
 
 
