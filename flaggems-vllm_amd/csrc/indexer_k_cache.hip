@@ -17,12 +17,15 @@
 //     block_table[b, pos / block_size], row pos % block_size) into row t of
 //     k_fp8 and k_fp8_scale.
 //
-// Layout: one quant block (128 elements, 256 bytes of bf16 / fp16 input) per
-// 16-lane DPP row for the insert, each lane one 16-byte piece; the block's
-// maximum is a DPP all-reduce (fgv_device.h), the codes one 8-byte store per
-// lane, the scale one 4-byte store.  The gather gives one token per 16-lane
-// row.  Both are bandwidth- and launch-bound: a DeepSeek-V4 index key is one
-// 128-element head, 256 bytes in and 132 bytes out per token.
+// Layout: the insert gives each 16-lane DPP row four consecutive (token,
+// quant block) units; a unit's 128 elements are one 16-byte piece per lane,
+// its maximum a DPP all-reduce (fgv_device.h), its codes one 8-byte store per
+// lane and its scale one 4-byte store.  The gather gives each wave 4R
+// consecutive tokens (R per 16-lane group) and finds their requests with one
+// 64-way ballot search plus one load of the following request boundaries.
+// Both kernels issue every load of a lane before its first store, so a lane
+// keeps 64-128 bytes in flight: both are HBM streams (DeepSeek-V4's index key
+// is one 128-element head: 256 bytes in and 132 bytes out per token).
 #include "fgv_device.h"
 #include "fgv_host.h"
 
@@ -30,8 +33,10 @@ namespace fgv {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kRows = kThreads / 16;
 constexpr int kQuantBlock = 128;
+constexpr int kLanes = 8;                      // lanes per quant block in the insert
+constexpr int kElems = kQuantBlock / kLanes;   // 16 elements (32 bytes) per lane
+constexpr int kGroups = kThreads / kLanes;     // quant blocks per workgroup
 
 struct IndexerKArgs {
     const uint16_t* k;
@@ -44,10 +49,11 @@ struct IndexerKArgs {
     int32_t nqb;             // quant blocks per token
     int32_t fp16;            // k is float16 (else bfloat16)
     int32_t ue8m0;
+    int32_t store_bytes;     // 16, 8 or 4: the widest the cache's block alignment allows
 };
 
 // Eight bf16 or fp16 values of a 16-byte piece as binary32 (exact).
-__device__ __forceinline__ void unpack8_any(uint4 v, bool fp16, float (&x)[8]) {
+__device__ __forceinline__ void unpack8_any(uint4 v, bool fp16, float* x) {
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -61,33 +67,47 @@ __device__ __forceinline__ void unpack8_any(uint4 v, bool fp16, float (&x)[8]) {
     }
 }
 
+// (block, row) of a slot; 32-bit division when both fit.
+__device__ __forceinline__ void split_slot(int64_t slot, int64_t block_size, int64_t& blk, int64_t& row) {
+    if (((uint64_t)slot | (uint64_t)block_size) >> 31)
+        blk = slot / block_size;
+    else
+        blk = (uint32_t)slot / (uint32_t)block_size;
+    row = slot - blk * block_size;
+}
+
+// One (token, quant block) unit per 8-lane group: two 16-byte key loads and
+// one 16-byte code store per lane, the block maximum a 3-step DPP reduction.
+// (Measured against 16 lanes x 16 bytes and 4 lanes x 64 bytes per block, and
+// against 2-4 units per group: this layout streams fastest.)
 __global__ void __launch_bounds__(kThreads)
 indexer_k_quant_kernel(IndexerKArgs a) {
-    const int lane16 = threadIdx.x & 15;
-    const int64_t u = (int64_t)blockIdx.x * kRows + (threadIdx.x >> 4);
+    const int ln = threadIdx.x & (kLanes - 1);
+    const int64_t u = (int64_t)blockIdx.x * kGroups + threadIdx.x / kLanes;
     if (u >= a.units)
         return;
     const int64_t t = u / a.nqb;
     const int j = (int)(u - t * a.nqb);
     const int64_t slot = a.slots[t];
-    __builtin_amdgcn_sched_barrier(0);  // the slot load ahead of the key load
-    const uint4 v = load16(a.k + t * a.k_stride + (int64_t)j * kQuantBlock + 8 * lane16);
+    const uint16_t* src = a.k + t * a.k_stride + (int64_t)j * kQuantBlock + kElems * ln;
+    const uint4 v0 = load16(src), v1 = load16(src + 8);
     if (slot < 0)
         return;
-    const int64_t blk = slot / a.block_size;
-    const int64_t row = slot - blk * a.block_size;
+    int64_t blk, row;
+    split_slot(slot, a.block_size, blk, row);
     if (blk >= a.num_blocks)
         return;
-    float x[8];
-    unpack8_any(v, a.fp16 != 0, x);
+    float x[kElems];
+    unpack8_any(v0, a.fp16 != 0, x);
+    unpack8_any(v1, a.fp16 != 0, x + 8);
     uint32_t m = 0;
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-        m = max(m, __float_as_uint(x[i]) & 0x7fffffffu);
-    const float amax = __uint_as_float(row16_max(m));
+    for (int e = 0; e < kElems; ++e)
+        m = max(m, __float_as_uint(x[e]) & 0x7fffffffu);
+    const float amax = __uint_as_float(row8_max(m));
     // max(amax, 1e-4) / 448, correctly rounded (HIP's binary32 division)
     float scale = fmaxf(amax, 1e-4f) / kFp8Max;
-    float q[8];
+    float q[kElems];
     if (a.ue8m0) {
         // 2^ceil(log2(scale)) from the binary32 fields (scale is a normal
         // number >= 1e-4 / 448): exponent, plus one if any mantissa bit is set
@@ -96,17 +116,30 @@ indexer_k_quant_kernel(IndexerKArgs a) {
         scale = __uint_as_float((uint32_t)(e + 127) << 23);
         const float inv = exp2_neg_int(e);  // x / 2^e == x * 2^-e exactly
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
-            q[i] = clamp_fp8(x[i] * inv);
+        for (int c = 0; c < kElems; ++c)
+            q[c] = clamp_fp8(x[c] * inv);
     } else {
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
-            q[i] = clamp_fp8(x[i] / scale);  // correctly rounded division
+        for (int c = 0; c < kElems; ++c)
+            q[c] = clamp_fp8(x[c] / scale);  // correctly rounded division
     }
     uint8_t* base = a.cache + blk * a.block_stride;
-    store8(base + row * a.head_dim + (int64_t)j * kQuantBlock + 8 * lane16, pack_fp8x4(q[0], q[1], q[2], q[3]),
-           pack_fp8x4(q[4], q[5], q[6], q[7]));
-    if (lane16 == 0)
+    uint8_t* dst = base + row * a.head_dim + (int64_t)j * kQuantBlock + kElems * ln;
+    const uint4 w = make_uint4(pack_fp8x4(q[0], q[1], q[2], q[3]), pack_fp8x4(q[4], q[5], q[6], q[7]),
+                               pack_fp8x4(q[8], q[9], q[10], q[11]), pack_fp8x4(q[12], q[13], q[14], q[15]));
+    if (a.store_bytes == 16) {
+        store16(dst, w);
+    } else if (a.store_bytes == 8) {
+        store8(dst, w.x, w.y);
+        store8(dst + 8, w.z, w.w);
+    } else {
+        uint32_t* d4 = reinterpret_cast<uint32_t*>(dst);
+        d4[0] = w.x;
+        d4[1] = w.y;
+        d4[2] = w.z;
+        d4[3] = w.w;
+    }
+    if (ln == 0)
         *reinterpret_cast<float*>(base + a.block_size * a.head_dim + (row * a.nqb + j) * 4) = scale;
 }
 
@@ -116,47 +149,160 @@ struct GatherArgs {
     uint8_t* scale_out;
     const int32_t* block_table;
     const int32_t* cu_seqlen;
-    int64_t block_stride, num_blocks, block_size;
+    int64_t block_stride, num_blocks;
     int64_t k_out_stride, scale_out_stride, bt_stride;  // bytes, bytes, elements
-    int64_t head_dim, num_tokens;
-    int32_t batch, max_blocks, nqb;
+    int64_t head_dim;
+    int32_t num_tokens, block_size;
+    int32_t batch, max_blocks, nqb, nch;
 };
 
+// #{j in [0, batch] : cu[j] <= t} for a wave-uniform t, by 64-way ballot
+// search (one load per lane per level: two levels cover 4096 requests).
+// Every lane of the wave must call it with the same t.
+__device__ __forceinline__ int count_le(const int32_t* cu, int batch, int32_t t, int lane) {
+    int base = 0, span = batch + 1;  // entries < base are <= t, entries >= base + span are > t
+    while (span > 64) {
+        const int stride = (span + 63) >> 6;
+        const int off = lane * stride;
+        const int k = __popcll(__ballot(off < span && cu[base + off] <= t));
+        if (k == 0)
+            return base;
+        const int end = k * stride < span ? base + k * stride : base + span;
+        base += (k - 1) * stride + 1;
+        span = end - base;
+    }
+    return base + __popcll(__ballot(lane < span && cu[base + lane] <= t));
+}
+
+template <int CB>
+struct Chunk;
+template <>
+struct Chunk<8> {
+    typedef u32x2_t T;
+};
+template <>
+struct Chunk<4> {
+    typedef uint32_t T;
+};
+template <>
+struct Chunk<16> {
+    typedef u32x4_t T;
+};
+
+// Each wave gathers 4 * R consecutive tokens, R per 16-lane group (token
+// t0 + 4 r + group).  The requests of all of them come from one ballot search
+// for t0 (one load of cu[0..batch] below 64 requests) and the few request
+// boundaries inside the wave's tokens; then every lane issues its R
+// block-table loads, then its R x nch chunk loads of CB bytes, and only then
+// stores.  NCH > 0 fixes the chunk count at compile time;
+// NCH < 0 means at most -NCH chunks, a.nch of them.
+template <int CB, int NCH, int R, int GL>
 __global__ void __launch_bounds__(kThreads)
 indexer_k_gather_kernel(GatherArgs a) {
-    const int lane16 = threadIdx.x & 15;
-    const int64_t t = (int64_t)blockIdx.x * kRows + (threadIdx.x >> 4);
-    if (t >= a.num_tokens || a.batch <= 0)
+    typedef typename Chunk<CB>::T V;
+    constexpr int MAXC = NCH > 0 ? NCH : -NCH;
+    constexpr int NG = 64 / GL;  // token groups per wave
+    const int nch = NCH > 0 ? NCH : a.nch;
+    const int lane = threadIdx.x & 63;
+    const int g = lane / GL, lg = lane % GL;
+    const int64_t t0l = ((int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6)) * (NG * R);
+    if (t0l >= a.num_tokens)
         return;
-    // largest b < batch with cu_seqlen[b] <= t
-    int32_t lo = 0, hi = a.batch - 1;
-    while (lo < hi) {
-        const int32_t mid = (lo + hi + 1) >> 1;
-        if (a.cu_seqlen[mid] <= t)
-            lo = mid;
-        else
-            hi = mid - 1;
+    const int32_t t0 = (int32_t)t0l;
+    const int32_t tl = t0 + NG * R - 1;  // the wave's last token
+    // c0 = #{cu <= t0}; the request boundaries after it sit in lanes j0, j0 + 1,
+    // ... of bnd, and K of them fall inside the wave's tokens.  With at most 63
+    // requests one load of cu[0..batch] gives all of it.
+    int c0, j0, K;
+    int32_t bnd, prev;
+    if (a.batch < 64) {
+        bnd = lane <= a.batch ? a.cu_seqlen[lane] : 0x7fffffff;
+        c0 = __popcll(__ballot(bnd <= t0));
+        j0 = c0;
+        K = __popcll(__ballot(bnd <= tl)) - c0;
+        prev = c0 >= 1 ? __builtin_amdgcn_readlane(bnd, c0 - 1) : 0;
+    } else {
+        c0 = count_le(a.cu_seqlen, a.batch, t0, lane);
+        bnd = c0 + lane <= a.batch ? a.cu_seqlen[c0 + lane] : 0x7fffffff;
+        prev = c0 >= 1 ? a.cu_seqlen[c0 - 1] : 0;
+        j0 = 0;
+        K = __popcll(__ballot(bnd <= tl));
     }
-    const int64_t start = a.cu_seqlen[lo];
-    if (t < start || t >= a.cu_seqlen[lo + 1])
-        return;  // not inside any request: left as it is
-    const int64_t pos = t - start;
-    const int64_t bt = pos / a.block_size;
-    if (bt >= a.max_blocks)
-        return;
-    const int64_t blk = a.block_table[lo * a.bt_stride + bt];
-    if (blk < 0 || blk >= a.num_blocks)
-        return;
-    const int64_t row = pos - bt * a.block_size;
-    const uint8_t* src = a.cache + blk * a.block_stride + row * a.head_dim;
-    uint8_t* dst = a.k_out + t * a.k_out_stride;
-    // head_dim is a multiple of 128: 8 bytes per lane per 128
-    for (int64_t off = 8 * lane16; off < a.head_dim; off += 128)
-        *reinterpret_cast<uint2*>(dst + off) = *reinterpret_cast<const uint2*>(src + off);
-    if (lane16 < a.nqb) {
-        const uint8_t* s = a.cache + blk * a.block_stride + a.block_size * a.head_dim + (row * a.nqb + lane16) * 4;
-        *reinterpret_cast<uint32_t*>(a.scale_out + t * a.scale_out_stride + 4 * lane16) =
-            *reinterpret_cast<const uint32_t*>(s);
+    int req[R];
+    int32_t start[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        req[r] = c0 - 1;
+        start[r] = prev;
+    }
+    if (K < 64 - j0 || a.batch < 64) {
+        // usually K is 0 or 1: step each token past the boundaries at or below it
+        for (int j = 0; j < K; ++j) {
+            const int32_t b = __builtin_amdgcn_readlane(bnd, j0 + j);
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                if (t0 + NG * r + g >= b) {
+                    ++req[r];
+                    start[r] = b;
+                }
+            }
+        }
+    } else {
+        // 64 or more requests start inside this wave's tokens (empty
+        // requests): search each token on its own
+#pragma unroll
+        for (int w = 0; w < NG * R; ++w) {
+            const int c = count_le(a.cu_seqlen, a.batch, t0 + w, lane);
+            const int32_t st = c >= 1 ? a.cu_seqlen[c - 1] : 0;
+            if (w % NG == g) {
+                req[w / NG] = c - 1;
+                start[w / NG] = st;
+            }
+        }
+    }
+    int64_t blk[R];
+    int32_t row[R];
+    bool ok[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int32_t t = t0 + NG * r + g;
+        const int b = req[r];
+        ok[r] = t < a.num_tokens && b >= 0 && b < a.batch;
+        const int32_t pos = t - start[r];
+        const int32_t bi = (int32_t)((uint32_t)pos / (uint32_t)a.block_size);
+        ok[r] = ok[r] && bi < a.max_blocks;
+        blk[r] = ok[r] ? (int64_t)a.block_table[(int64_t)b * a.bt_stride + bi] : -1;
+        ok[r] = ok[r] && blk[r] >= 0 && blk[r] < a.num_blocks;
+        row[r] = pos - bi * a.block_size;
+    }
+    V d[R][MAXC];
+    uint32_t s[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        if (!ok[r])
+            continue;
+        const uint8_t* base = a.cache + blk[r] * a.block_stride;
+        const uint8_t* p = base + (int64_t)row[r] * a.head_dim + CB * lg;
+#pragma unroll
+        for (int i = 0; i < MAXC; ++i)
+            if (i < nch)
+                d[r][i] = __builtin_nontemporal_load(reinterpret_cast<const V*>(p + i * GL * CB));
+        if (lg < a.nqb)
+            s[r] = *reinterpret_cast<const uint32_t*>(base + (int64_t)a.block_size * a.head_dim +
+                                                        ((int64_t)row[r] * a.nqb + lg) * 4);
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        if (!ok[r])
+            continue;
+        const int64_t t = t0 + NG * r + g;
+        uint8_t* q = a.k_out + t * a.k_out_stride + CB * lg;
+#pragma unroll
+        for (int i = 0; i < MAXC; ++i)
+            if (i < nch)
+                __builtin_nontemporal_store(d[r][i], reinterpret_cast<V*>(q + i * GL * CB));
+        if (lg < a.nqb)
+            *reinterpret_cast<uint32_t*>(a.scale_out + t * a.scale_out_stride + 4 * lg) = s[r];
     }
 }
 
@@ -193,8 +339,8 @@ extern "C" int fgv_indexer_k_quant_and_cache(
         return fail(FGV_E_BAD_STRIDE, "cache block stride is below block_size * (head_dim + 4 * head_dim / 128)");
     if (!aligned(k, 16) || k_stride_token % 8)
         return fail(FGV_E_MISALIGNED, "k must be 16-byte aligned with a token stride a multiple of 8 elements");
-    if (!aligned(kv_cache, 8) || cache_block_stride % 8)
-        return fail(FGV_E_MISALIGNED, "kv_cache and its block stride must be 8-byte aligned");
+    if (!aligned(kv_cache, 4) || cache_block_stride % 4)
+        return fail(FGV_E_MISALIGNED, "kv_cache and its block stride must be 4-byte aligned");
     if (num_tokens > (1LL << 40))
         return fail(FGV_E_TOO_LARGE, "too many tokens");
     IndexerKArgs a;
@@ -210,7 +356,12 @@ extern "C" int fgv_indexer_k_quant_and_cache(
     a.nqb = (int32_t)nqb;
     a.fp16 = k_is_fp16 != 0;
     a.ue8m0 = use_ue8m0 != 0;
-    const int64_t grid = (a.units + kRows - 1) / kRows;
+    // a block of block_size x (head_dim + head_dim / 32) bytes is 16-byte
+    // aligned when block_size is a multiple of 4, 8-byte aligned when even
+    a.store_bytes = aligned(kv_cache, 16) && cache_block_stride % 16 == 0  ? 16
+                    : aligned(kv_cache, 8) && cache_block_stride % 8 == 0 ? 8
+                                                                          : 4;
+    const int64_t grid = (a.units + kGroups - 1) / kGroups;
     if (grid > 0x7fffffffLL)
         return fail(FGV_E_TOO_LARGE, "grid exceeds 2^31 - 1 workgroups");
     hipLaunchKernelGGL(indexer_k_quant_kernel, dim3((uint32_t)grid), dim3(kThreads), 0,
@@ -239,12 +390,14 @@ extern "C" int fgv_cp_gather_indexer_k_quant_cache(
     const int64_t nqb = head_dim / kQuantBlock;
     if (cache_block_stride < block_size * (head_dim + 4 * nqb))
         return fail(FGV_E_BAD_STRIDE, "cache block stride is below block_size * (head_dim + 4 * head_dim / 128)");
-    if (!aligned(kv_cache, 8) || cache_block_stride % 8 || !aligned(k_out, 8) || k_out_stride % 8)
-        return fail(FGV_E_MISALIGNED, "kv_cache, k_fp8 and their strides must be 8-byte aligned");
+    if (!aligned(kv_cache, 4) || cache_block_stride % 4 || !aligned(k_out, 4) || k_out_stride % 4)
+        return fail(FGV_E_MISALIGNED, "kv_cache, k_fp8 and their strides must be 4-byte aligned");
     if (!aligned(scale_out, 4) || scale_out_stride % 4)
         return fail(FGV_E_MISALIGNED, "k_fp8_scale and its row stride must be 4-byte aligned");
-    if (batch_size > 0x7fffffffLL - 1 || max_blocks_per_seq > 0x7fffffffLL || num_tokens > 0x7fffffffLL)
-        return fail(FGV_E_TOO_LARGE, "batch, block table and token counts must fit in int32");
+    if (batch_size > (1LL << 30) || max_blocks_per_seq > 0x7fffffffLL || num_tokens > 0x7fffffffLL - 64)
+        return fail(FGV_E_TOO_LARGE, "batch must be at most 2^30, block table and token counts below 2^31 - 64");
+    if (block_size > 0x7fffffffLL)
+        return fail(FGV_E_TOO_LARGE, "block_size must fit in int32");
     GatherArgs a;
     a.cache = static_cast<const uint8_t*>(kv_cache);
     a.k_out = static_cast<uint8_t*>(k_out);
@@ -253,17 +406,46 @@ extern "C" int fgv_cp_gather_indexer_k_quant_cache(
     a.cu_seqlen = cu_seqlen;
     a.block_stride = cache_block_stride;
     a.num_blocks = num_blocks;
-    a.block_size = block_size;
     a.k_out_stride = k_out_stride;
     a.scale_out_stride = scale_out_stride;
     a.bt_stride = block_table_stride;
     a.head_dim = head_dim;
-    a.num_tokens = num_tokens;
+    a.num_tokens = (int32_t)num_tokens;
+    a.block_size = (int32_t)block_size;
     a.batch = (int32_t)batch_size;
     a.max_blocks = (int32_t)max_blocks_per_seq;
     a.nqb = (int32_t)nqb;
-    const int64_t grid = (num_tokens + kRows - 1) / kRows;
-    hipLaunchKernelGGL(indexer_k_gather_kernel, dim3((uint32_t)grid), dim3(kThreads), 0,
-                       static_cast<hipStream_t>(stream), a);
+    // 16-byte chunks where head_dim is 128, 256, 512, 1024 or 2048 and the
+    // code rows are 16-byte aligned on both sides, else 8-byte chunks, or
+    // 4-byte ones where a row is only 4-byte aligned (an odd block_size)
+    const bool wide = (head_dim & (head_dim - 1)) == 0 && aligned(kv_cache, 16) && cache_block_stride % 16 == 0 &&
+                      aligned(k_out, 16) && k_out_stride % 16 == 0;
+    const bool narrow = !(aligned(kv_cache, 8) && cache_block_stride % 8 == 0 && aligned(k_out, 8) &&
+                          k_out_stride % 8 == 0);
+    a.nch = (int32_t)(narrow ? head_dim / 64 : head_dim / 128);
+    // Below 16384 tokens the launch is latency-bound and one token per lane
+    // group is fastest; above, several tokens per group keep more loads in
+    // flight (measured on MI355X: 2 at head_dim 512, 4 at 128).
+    const bool big = num_tokens >= 16384;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    auto launch = [&](auto kernel, int tokens_per_wave) {
+        const int64_t per_block = (kThreads / 64) * tokens_per_wave;
+        const int64_t grid = (num_tokens + per_block - 1) / per_block;
+        hipLaunchKernelGGL(kernel, dim3((uint32_t)grid), dim3(kThreads), 0, st, a);
+    };
+    if (wide && head_dim == 128)
+        big ? launch(indexer_k_gather_kernel<16, 1, 4, 8>, 32) : launch(indexer_k_gather_kernel<16, 1, 1, 8>, 8);
+    else if (wide && head_dim == 256)
+        big ? launch(indexer_k_gather_kernel<16, 1, 4, 16>, 16) : launch(indexer_k_gather_kernel<16, 1, 1, 16>, 4);
+    else if (wide && head_dim == 512)
+        big ? launch(indexer_k_gather_kernel<16, 2, 2, 16>, 8) : launch(indexer_k_gather_kernel<16, 2, 1, 16>, 4);
+    else if (wide && head_dim == 1024)
+        launch(indexer_k_gather_kernel<16, 4, 1, 16>, 4);
+    else if (wide)
+        launch(indexer_k_gather_kernel<16, 8, 1, 16>, 4);
+    else if (narrow)
+        launch(indexer_k_gather_kernel<4, -32, 1, 16>, 4);
+    else
+        launch(indexer_k_gather_kernel<8, -16, 1, 16>, 4);
     return launch_status();
 }

@@ -219,8 +219,10 @@ int fgv_compute_slot_mapping(
  *
  *   k         bf16 (or fp16 if k_is_fp16) [num_tokens, head_dim], row stride
  *             k_stride_token elements (multiple of 8), 16-byte aligned
- *   kv_cache  uint8 blocks cache_block_stride bytes apart; block b holds
- *             block_size x head_dim e4m3fn codes, then block_size x
+ *   kv_cache  uint8 blocks cache_block_stride bytes apart (pointer and stride
+ *             4-byte aligned; 16-byte alignment, i.e. block_size a multiple
+ *             of 4 in a packed cache, gives 16-byte code stores); block b
+ *             holds block_size x head_dim e4m3fn codes, then block_size x
  *             (head_dim / 128) float32 scales
  *   slot_mapping  int64 [num_tokens]; < 0 skips the token
  *
@@ -249,7 +251,8 @@ int fgv_indexer_k_quant_and_cache(
  * position p = t - cu_seqlen[b] copies the head_dim code bytes and
  * head_dim / 128 float32 scales of row p % block_size of block
  * block_table[b, p / block_size] to k_out + t * k_out_stride and
- * scale_out + t * scale_out_stride (byte strides; multiples of 8 and 4).
+ * scale_out + t * scale_out_stride (byte strides; kv_cache, k_out, scale_out
+ * and their strides 4-byte aligned).
  * Tokens outside every request, and tokens whose block-table index or block
  * is out of range, are left untouched.  cu_seqlen has batch_size + 1 entries,
  * non-decreasing.

@@ -315,7 +315,7 @@ def _call_insert(**kw):
 @pytest.mark.parametrize("kw,code", [
     (dict(qbs=64), -2), (dict(hd=192), -2), (dict(hd=4096), -2), (dict(T=-1), -2), (dict(bs=0), -2),
     (dict(k=None), -1), (dict(slots=None), -1), (dict(k=264), -3), (dict(kst=132), -3),
-    (dict(cache=260), -3), (dict(cst=16 * 132 - 8), -4),
+    (dict(cache=258), -3), (dict(cst=16 * 132 - 8), -4), (dict(cst=16 * 132 + 2), -3),
 ])
 def test_insert_c_abi_rejects_bad_arguments(kw, code):
     assert _call_insert(**kw) == code
@@ -337,7 +337,8 @@ def _call_gather(**kw):
 
 @pytest.mark.parametrize("kw,code", [
     (dict(qbs=256), -2), (dict(hd=100), -2), (dict(B=-1), -2), (dict(bs=0), -2), (dict(cu=None), -1),
-    (dict(ko=None), -1), (dict(cst=100), -4), (dict(ko=260), -3), (dict(sst=6), -3), (dict(so=258), -3),
+    (dict(ko=None), -1), (dict(cst=100), -4), (dict(ko=258), -3), (dict(kst=130), -3), (dict(sst=6), -3),
+    (dict(so=258), -3),
 ])
 def test_gather_c_abi_rejects_bad_arguments(kw, code):
     assert _call_gather(**kw) == code
@@ -464,6 +465,83 @@ def test_gpu_gather_fuzz(seed):
     torch.cuda.synchronize()
     _first_diff(gkw.cpu(), wk, "k_fp8 (with the untouched stride padding)")
     _first_diff(gsw.cpu().view(torch.int32), ws.view(torch.int32), "scales")
+
+
+def _gather_case(lens, bs, hd, gen, nblk=None):
+    """Random block tables (distinct blocks per request) for the given lengths."""
+    B = len(lens)
+    cu = torch.zeros(B + 1, dtype=torch.int32)
+    cu[1:] = torch.cumsum(torch.tensor(lens, dtype=torch.int64), 0).to(torch.int32)
+    maxb = max(1, (max(lens) + bs - 1) // bs)
+    nblk = nblk or max(4, B * maxb)
+    bt = torch.randint(0, nblk, (B, maxb), generator=gen, dtype=torch.int32)
+    return W.make_indexer_k_cache(nblk, bs, hd, gen), bt, cu
+
+
+def _run_gather_pair(cache, bt, cu, T, hd, k_offset=0):
+    """GPU gather into sentinel-filled outputs (k_fp8 starting k_offset bytes
+    into its buffer) against the oracle on the same outputs."""
+    nqb = hd // 128
+    kbuf = torch.full((T * hd + k_offset,), SENTINEL, dtype=torch.uint8)
+    ks = torch.full((T, 4 * nqb), SENTINEL, dtype=torch.uint8)
+    wk, ws = kbuf.clone(), ks.clone()
+    oracle.cp_gather_indexer_k_quant_cache(cache, wk[k_offset:].view(T, hd), ws, bt, cu)
+    gk, gs = kbuf.to(DEV), ks.to(DEV)
+    flaggems_vllm.cp_gather_indexer_k_quant_cache(cache.to(DEV), gk[k_offset:].view(T, hd), gs, bt.to(DEV),
+                                                  cu.to(DEV))
+    torch.cuda.synchronize()
+    _first_diff(gk.cpu(), wk, "k_fp8 buffer")
+    _first_diff(gs.cpu(), ws, "k_fp8_scale")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("hd,k_offset", [(384, 0), (2048, 0), (512, 8), (256, 8), (1024, 0)])
+def test_gpu_gather_chunk_variants(hd, k_offset):
+    """Every chunk layout of the gather: 16-byte chunks at head_dim 256-2048,
+    8-byte chunks where head_dim is not a power-of-two multiple of 256 (384)
+    or where k_fp8 is only 8-byte aligned."""
+    gen = torch.Generator().manual_seed(hd + k_offset)
+    lens = torch.randint(1, 70, (9,), generator=gen).tolist()
+    cache, bt, cu = _gather_case(lens, 16, hd, gen)
+    T = int(cu[-1]) + 3
+    _say(f"indexer k gather chunks hd={hd} k_offset={k_offset} T={T}")
+    _run_gather_pair(cache, bt, cu, T, hd, k_offset)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("bs", [1, 2, 3, 6])
+def test_gpu_odd_block_sizes(bs):
+    """Block sizes whose packed blocks are only 4- or 8-byte aligned (132 *
+    block_size bytes at head_dim 128): the insert's narrower code stores and
+    the gather's narrower chunks, bit for bit against the oracle."""
+    for hd in (128, 512):
+        _say(f"indexer k odd block size bs={bs} hd={hd}")
+        T = 29
+        k, cache, slots = W.make_indexer_k_insert(T, (T + bs - 1) // bs + 2, bs, hd, torch.bfloat16, seed=bs)
+        want = _insert_oracle(k, cache, slots, "ue8m0")
+        g = cache.to(DEV)
+        flaggems_vllm.indexer_k_quant_and_cache(k.to(DEV), g, slots.to(DEV), QB, "ue8m0")
+        torch.cuda.synchronize()
+        _first_diff(g.cpu(), want, "cache")
+        gen = torch.Generator().manual_seed(bs)
+        lens = torch.randint(0, 20, (5,), generator=gen).tolist()
+        gcache, bt, cu = _gather_case(lens, bs, hd, gen)
+        _run_gather_pair(gcache, bt, cu, int(cu[-1]) + 2, hd)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("B", [70, 5000])
+def test_gpu_gather_many_short_requests(B):
+    """Thousands of requests of 0-2 tokens: more than 64 request starts inside
+    one wave's tokens (the per-token fallback search) and a request search
+    over more than 4096 boundaries (three ballot levels)."""
+    gen = torch.Generator().manual_seed(B)
+    lens = torch.tensor([0, 0, 0, 1, 2])[torch.randint(0, 5, (B,), generator=gen)].tolist()
+    lens[0] = 0
+    cache, bt, cu = _gather_case(lens, 16, 128, gen, nblk=64)
+    T = int(cu[-1]) + 5
+    _say(f"indexer k gather many requests B={B} T={T}")
+    _run_gather_pair(cache, bt, cu, T, 128)
 
 
 @pytest.mark.gpu
