@@ -35,17 +35,22 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", type=int, default=2, help="main-op workload c0..c4 (default c2)")
     ap.add_argument("--op", choices=["main", "inv_rope", "gather", "rmsnorm", "indexer",
-                                     "slot_mapping", "mla", "indexer_k", "indexer_k_gather", "copy"],
+                                     "slot_mapping", "mla", "indexer_k", "indexer_k_gather", "mqa_logits",
+                                     "paged_mqa_logits", "copy"],
                     default="main",
                     help="copy: torch device copy of 512 MiB, the HBM calibration kernel")
     ap.add_argument("--tma", action="store_true", help="inv_rope: packed UE8M0 scales")
-    ap.add_argument("--fp4", action="store_true", help="indexer: MXFP4 instead of FP8")
+    ap.add_argument("--fp4", action="store_true", help="indexer, mqa_logits, paged_mqa_logits: MXFP4 q instead of FP8")
     ap.add_argument("--mla-case", choices=["decode", "extra512", "extra8192"], default="decode",
                     help="mla: the reference benchmark's MODEL1 sparse-decode case")
     ap.add_argument("--indexer-case", choices=["0", "1", "2", "3", "large"], default="3",
                     help="indexer_k / indexer_k_gather: the reference benchmark's shape 0..3 (default its "
                          "largest) or 'large' (65536 tokens, head_dim 512)")
     ap.add_argument("--fp16", action="store_true", help="indexer_k: float16 keys instead of bfloat16")
+    ap.add_argument("--mqa-shape", default="4096,8192",
+                    help="mqa_logits: M,N (default the reference benchmark's largest, 4096 x 8192)")
+    ap.add_argument("--paged-shape", default="256,1,8192",
+                    help="paged_mqa_logits: batch,next_n,context (reference benchmark shapes)")
     ap.add_argument("--cpu-sample-tokens", type=int, default=8192)
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="repeat the CPU sample until this much CPU time is spent (min 3 runs)")
@@ -546,6 +551,56 @@ def main():
                                                                       cu_cpu[:nb + 1]),
                     nb * L, "tokens/s", f"first {nb} of {B} requests ({nb * L} tokens; the reference "
                                         f"test's per-token loop)")
+    elif args.op == "mqa_logits":
+        # the sparse indexer's prefill logits at the reference benchmark's
+        # largest shape (benchmark/test_fp8_fp4_mqa_logits.py:61-72), H = 64, D = 128
+        M, N = (int(x) for x in args.mqa_shape.split(","))
+        q, kv, w, ks, ke = W.make_mqa_logits_inputs(M, N, fp4=args.fp4)
+        d = ((q[0].to(dev), q[1].to(dev) if q[1] is not None else None), (kv[0].to(dev), kv[1].to(dev)),
+             w.to(dev), ks.to(dev), ke.to(dev))
+        T = M
+        flops_call = W.mqa_logits_flops(M, N)
+        bytes_call = M * 64 * (68 if args.fp4 else 128) + M * 64 * 4 + N * 132 + 4 * M * N
+
+        def step():  # MFMA-bound: q (M x 8 KiB) and K stay cache-resident by design
+            flaggems_vllm.fp8_fp4_mqa_logits(*d[:2], d[2], d[3], d[4], clean_logits=True)
+
+        kernel = "mqa_logits_kernel"
+        workload = f"M{M}_N{N}_H64" + ("_mxfp4" if args.fp4 else "_fp8")
+        config = {"workload": f"fp8_fp4_mqa_logits M={M} queries x N={N} keys, H=64, D=128, "
+                              f"{'MXFP4' if args.fp4 else 'FP8'} q, FP8 k, clean_logits (ks=0, ke=N)",
+                  "num_queries": M, "num_keys": N, "flops_per_call": flops_call}
+        nc = max(1, min(M, 4))
+        qc = (q[0][:nc], q[1][:nc] if q[1] is not None else None)
+        cpu_case = (lambda: torch_ref.mqa_logits(qc, kv, w[:nc], ks[:nc], ke[:nc], True), nc, "queries/s",
+                    f"first {nc} of {M} queries against all {N} keys (the reference test's float32 loop)")
+    elif args.op == "paged_mqa_logits":
+        # the sparse indexer's decode logits over the paged key cache at a
+        # reference benchmark shape (benchmark/test_fp8_fp4_paged_mqa_logits.py:31-40)
+        B, nn, L = (int(x) for x in args.paged_shape.split(","))
+        q, cache, w, ctx, bt = W.make_paged_mqa_inputs(B, nn, L, fp4=args.fp4)
+        T = B * nn
+        mml = W.PAGED_MAX_MODEL_LEN
+        bytes_call = W.paged_mqa_logits_bytes(ctx.reshape(-1), T, 64, mml, args.fp4)
+        flops_call = int(ctx.reshape(-1).sum()) * 2 * 64 * 128
+        dq = (q[0].to(dev), q[1].to(dev) if q[1] is not None else None)
+        d_w, d_ctx, d_bt = w.to(dev), ctx.to(dev), bt.to(dev)
+
+        def make_step(i):
+            c = cache.to(dev)
+            return lambda: flaggems_vllm.fp8_fp4_paged_mqa_logits(dq, c, d_w, d_ctx, d_bt, None, mml)
+
+        kernel = "paged_mqa_logits_kernel"
+        workload = f"B{B}_N{nn}_L{L}" + ("_mxfp4" if args.fp4 else "_fp8")
+        config = {"workload": f"fp8_fp4_paged_mqa_logits batch={B}, next_n={nn}, contexts ~{L} "
+                              f"(uniform 0.7-1.3x), 64-entry blocks, max_model_len {mml}, H=64, D=128, "
+                              f"{'MXFP4' if args.fp4 else 'FP8'} q", "rows": T,
+                  "context_positions": int(ctx.reshape(-1).sum()), "flops_per_call": flops_call}
+        nb = 1
+        qc = (q[0][:nb], q[1][:nb] if q[1] is not None else None)
+        cpu_case = (lambda: torch_ref.paged_mqa_logits(qc, cache, w[:nb * nn], ctx[:nb], bt[:nb], mml, False),
+                    nb * nn, "rows/s", f"first {nb} of {B} sequences (the reference test's per-row gather "
+                                       f"and float32 loop)")
     elif args.op == "copy":
         n = 512 << 20
         src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
@@ -577,7 +632,8 @@ def main():
                   "num_tokens": T, "num_heads": H, "n_groups": 8}
 
     n_sets = 1
-    if args.op in ("main", "gather", "rmsnorm", "indexer", "mla", "inv_rope", "indexer_k", "indexer_k_gather"):
+    if args.op in ("main", "gather", "rmsnorm", "indexer", "mla", "inv_rope", "indexer_k", "indexer_k_gather",
+                   "paged_mqa_logits"):
         step, n_sets = rotating(make_step, bytes_call)
     if n_sets == 1:
         config["input_sets"] = "one input set"
@@ -592,6 +648,9 @@ def main():
     if args.op == "mla":
         config["mfma_tflops"] = flops_call / t_kernel / 1e12
         config["mfma_frac_of_bf16_dense_peak"] = flops_call / t_kernel / 2.5e15
+    if args.op in ("mqa_logits", "paged_mqa_logits"):
+        config["mfma_tflops"] = flops_call / t_kernel / 1e12
+        config["mfma_frac_of_fp8_dense_peak"] = flops_call / t_kernel / 5.0e15
     traffic = measured_traffic(kernel, workload)
     result = {
         "metric": METRIC,
@@ -604,14 +663,18 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": {"mla": "bf16", "slot_mapping": "int64", "copy": "u8",
-                  "indexer_k_gather": "u8"}.get(args.op, "f32"),
+        "dtype": {"mla": "bf16", "slot_mapping": "int64", "copy": "u8", "indexer_k_gather": "u8",
+                  "mqa_logits": "fp4 x fp8 -> f32" if args.fp4 else "fp8 -> f32",
+                  "paged_mqa_logits": "fp4 x fp8 -> f32" if args.fp4 else "fp8 -> f32"}.get(args.op, "f32"),
         "data": ("synthetic: seeded q ~ N(0,1)/10 bf16, cache NoPE ~ N(0,0.1) quantised to e4m3 + "
                  "E8M0 per 64, RoPE ~ N(0,0.1) bf16, uniform indices and top-k lengths, sink ~ N(0,1)"
                  if args.op == "mla" else
                  "synthetic: seeded N(0,1) keys, distinct random slots (last one -1), cache pre-filled with "
                  "e4m3 codes of N(0,1) and scales U[0.01, 1.01) as the reference's tests fill it"
                  if args.op in ("indexer_k", "indexer_k_gather") else
+                 "synthetic: seeded q, k ~ N(0,1) (bf16, then e4m3fn or MXFP4 q and per-token FP8 k), "
+                 "weights N(0,1) (|N(0,1)| dense), as the reference's tests draw them"
+                 if args.op in ("mqa_logits", "paged_mqa_logits") else
                  "synthetic: seeded N(0,1) bf16 q/kv, fp32 cos/sin (theta 1e4), vLLM-style paged slots"),
         "config": config,
         "kernel_us": t_kernel * 1e6,
@@ -624,9 +687,13 @@ def main():
         # calibrated), per token and over the kernel time measured here
         "traffic_bytes_per_token": traffic / T if traffic else None,
         "traffic_gbps": traffic / t_kernel / 1e9 if traffic else None,
-        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic,
-                     "kernel": kernel},
+        "roofline": ({"bound": "mfma", "achieved": flops_call / t_kernel / 1e12, "peak": 5000.0,
+                      "unit": "TFLOP/s", "frac": flops_call / t_kernel / 5.0e15, "traffic": traffic,
+                      "kernel": kernel, "peak_note": "MI355X dense FP8 MFMA"}
+                     if args.op == "mqa_logits" else
+                     {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                      "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic,
+                      "kernel": kernel}),
     }
     if not args.no_cpu_baseline:
         if args.op == "main":

@@ -72,6 +72,29 @@ __device__ __forceinline__ uint32_t row16_max(uint32_t v) {
     return v;
 }
 
+// Max / sum over the four lanes l, l^16, l^32, l^48 (the four lane groups
+// of one column of a 16x16 MFMA tile) with gfx950's row-swapping permutes: with both operands x,
+// v_permlane16_swap returns {x[l], x[l^16]} (in row order) and
+// v_permlane32_swap {x[l], x[l^32]}, so each step is two VALU operations and
+// every lane of the four gets the same result (no LDS round trip).
+__device__ __forceinline__ float group4_max(float v) {
+    const uint32_t u = __float_as_uint(v);
+    const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const uint32_t w = __float_as_uint(v);
+    const auto b = __builtin_amdgcn_permlane32_swap(w, w, false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+__device__ __forceinline__ float group4_sum(float v) {
+    const uint32_t u = __float_as_uint(v);
+    const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const uint32_t w = __float_as_uint(v);
+    const auto b = __builtin_amdgcn_permlane32_swap(w, w, false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 

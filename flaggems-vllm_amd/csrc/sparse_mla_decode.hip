@@ -334,29 +334,6 @@ __device__ __forceinline__ void dequantize(const uint8_t* raw, uint8_t* kbuf, in
     __shared__ __align__(16) uint8_t lds_kbuf[kChunk * kKRowBytes]; \
     __shared__ float lds_mask[2][kChunk]
 
-// Max / sum over the four lanes l, l^16, l^32, l^48 (one head's lane
-// groups g) with gfx950's row-swapping permutes: with both operands x,
-// v_permlane16_swap returns {x[l], x[l^16]} (in row order) and
-// v_permlane32_swap {x[l], x[l^32]}, so each step is two VALU operations and
-// every lane of the four gets the same result (no LDS round trip).
-__device__ __forceinline__ float group4_max(float v) {
-    const uint32_t u = __float_as_uint(v);
-    const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
-    const uint32_t w = __float_as_uint(v);
-    const auto b = __builtin_amdgcn_permlane32_swap(w, w, false, false);
-    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
-}
-
-__device__ __forceinline__ float group4_sum(float v) {
-    const uint32_t u = __float_as_uint(v);
-    const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
-    const uint32_t w = __float_as_uint(v);
-    const auto b = __builtin_amdgcn_permlane32_swap(w, w, false, false);
-    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
-}
-
 __device__ __forceinline__ uint2 read_tr(const uint8_t* kbuf, int byte) {
     const short4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
         (lds_short4_t*)((__attribute__((address_space(3))) uint8_t*)kbuf + byte));

@@ -5,8 +5,8 @@ Public names follow the reference package (src/flaggems_vllm/__init__.py:21-46):
 their compatibility aliases ``ops_deepseek_v4_qnorm_rope_kv_rope_quant_insert`` and
 ``ops_inv_rope_fp8_quant``, ``SUPPORTED_FP8_DTYPE``, ``device`` and ``vendor_name``;
 and the ops either side of that path (src/flaggems_vllm/ops/__init__.py): the
-K-cache gather, q/kv RMSNorm, indexer q and key-cache ops, slot mapping and
-sparse MLA decode.  Every op runs hand-written HIP kernels through the C ABI declared in
+K-cache gather, q/kv RMSNorm, the sparse indexer (q quant, key cache and
+logits), slot mapping and sparse MLA decode.  Every op runs hand-written HIP kernels through the C ABI declared in
 include/flaggems_vllm_amd.h; there is no Triton, no vendor dispatch and no
 CPU fallback.
 """
@@ -18,6 +18,8 @@ from .ops import (  # noqa: F401
     cp_gather_indexer_k_quant_cache,
     dequantize_and_gather_k_cache,
     flash_mla_with_kvcache,
+    fp8_fp4_mqa_logits,
+    fp8_fp4_paged_mqa_logits,
     fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert,
     fused_indexer_q_rope_quant,
     fused_inv_rope_fp8_quant,
@@ -40,6 +42,8 @@ __all__ = [
     "compute_slot_mapping_parallel",
     "cp_gather_indexer_k_quant_cache",
     "flash_mla_with_kvcache",
+    "fp8_fp4_mqa_logits",
+    "fp8_fp4_paged_mqa_logits",
     "get_mla_metadata",
     "dequantize_and_gather_k_cache",
     "fused_q_kv_rmsnorm",

@@ -156,6 +156,23 @@ def lib():
         _P, ctypes.c_int,  # slot_mapping, use_ue8m0
         _P,  # stream
     ]
+    L.fgv_fp8_fp4_mqa_logits.restype = ctypes.c_int
+    L.fgv_fp8_fp4_mqa_logits.argtypes = [
+        _P, _I64, _I64, _P, _I64, _I64,  # q, strides (bytes), q_scale, strides
+        _P, _I64, _P, _P, _I64, _I64,  # k, stride (bytes), k_scale, weights, strides
+        _P, _P, _P, _I64,  # ks, ke, logits, stride
+        _I64, _I64, _I64, _I64, ctypes.c_int,  # M, N, num_heads, head_dim, clean
+        _P,  # stream
+    ]
+    L.fgv_fp8_fp4_paged_mqa_logits.restype = ctypes.c_int
+    L.fgv_fp8_fp4_paged_mqa_logits.argtypes = [
+        _P, _I64, _I64, _P, _I64, _I64,  # q, strides (bytes), q_scale, strides
+        _P, _I64, _I64, _I64, _I64,  # kv_cache, block stride, num_blocks, block_size, head_dim
+        _P, _I64, _I64,  # weights, strides
+        _P, _I64, _P, _I64, _I64, _I64,  # context_lens, rows per length, block_tables, stride, max blocks, rows per table row
+        _P, _I64, _I64, _I64, _I64, ctypes.c_int,  # logits, stride, rows, num_heads, max_model_len, clean
+        _P,  # stream
+    ]
     L.fgv_cp_gather_indexer_k_quant_cache.restype = ctypes.c_int
     L.fgv_cp_gather_indexer_k_quant_cache.argtypes = [
         _P, _I64, _I64, _I64,  # kv_cache, cache_block_stride, num_blocks, block_size
@@ -194,4 +211,6 @@ EXPORTED_SYMBOLS = (
     "fgv_sparse_mla_decode_model1_no_alloc",
     "fgv_indexer_k_quant_and_cache",
     "fgv_cp_gather_indexer_k_quant_cache",
+    "fgv_fp8_fp4_mqa_logits",
+    "fgv_fp8_fp4_paged_mqa_logits",
 )

@@ -1,7 +1,9 @@
-"""DeepSeek-V4 attention pre-processing ops (reference: src/flaggems_vllm/ops/__init__.py:23-24, 34-38, 55, 61-65, 78)."""
+"""DeepSeek-V4 attention pre-processing ops (reference: src/flaggems_vllm/ops/__init__.py:23-24, 34-38, 55, 58-59, 61-65, 78)."""
 from .cp_gather_indexer_k_quant_cache import cp_gather_indexer_k_quant_cache
 from .deepseek_v4_attention_dequantize_and_gather_k_cache import dequantize_and_gather_k_cache
 from .deepseek_v4_attention_fused_q_kv_rmsnorm import fused_q_kv_rmsnorm
+from .fp8_fp4_mqa_logits import fp8_fp4_mqa_logits
+from .fp8_fp4_paged_mqa_logits import fp8_fp4_paged_mqa_logits
 from .flash_mla_with_kvcache import FlashMLASchedMeta, flash_mla_with_kvcache, get_mla_metadata
 from .fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert import (
     fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert,
@@ -16,6 +18,8 @@ __all__ = [
     "compute_slot_mapping_parallel",
     "cp_gather_indexer_k_quant_cache",
     "flash_mla_with_kvcache",
+    "fp8_fp4_mqa_logits",
+    "fp8_fp4_paged_mqa_logits",
     "get_mla_metadata",
     "dequantize_and_gather_k_cache",
     "fused_q_kv_rmsnorm",

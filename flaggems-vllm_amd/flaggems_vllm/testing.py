@@ -547,3 +547,113 @@ def indexer_k_gather_bytes(num_tokens: int, head_dim: int) -> int:
     """Algorithmic HBM bytes of one gather: per token the cached row read and
     written out, and its 4-byte block-table entry."""
     return num_tokens * (2 * indexer_k_row_bytes(head_dim) + 4)
+
+
+# ---------------------------------------------------------------------------
+# Sparse-indexer logits (fp8_fp4_mqa_logits / fp8_fp4_paged_mqa_logits):
+# inputs drawn as the reference's tests draw them
+# (tests/test_fp8_fp4_mqa_logits.py:168-186, tests/test_fp8_fp4_paged_mqa_logits.py:29-114).
+# ---------------------------------------------------------------------------
+
+MQA_HEADS = 64
+MQA_DECODE_SHAPES = [(1, 1024), (1, 2048), (1, 4096), (4, 2048), (4, 4096)]
+MQA_PREFILL_SHAPES = [(64, 4096), (256, 4096), (1024, 4096), (2048, 4096), (1024, 8192)]
+PAGED_MQA_SHAPES = [(4, 1, 512), (4, 1, 1024), (4, 1, 2048), (8, 1, 1024), (8, 2, 1024), (16, 1, 2048),
+                    (32, 1, 4096), (64, 1, 4096), (128, 1, 2048)]
+PAGED_MQA_BENCH_SHAPES = [(256, 1, 1024), (256, 1, 2048), (256, 1, 4096), (256, 1, 8192), (256, 2, 8192),
+                          (128, 1, 16384), (64, 1, 32768), (32, 1, 65536)]
+PAGED_MAX_MODEL_LEN = 111 * 1024
+_E2M1_MAGS = torch.tensor([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0])
+
+
+def quantize_mxfp4(x: torch.Tensor):
+    """(packed uint8 [..., D/2] (even element in the low nibble), int32 [...]
+    of the D/32 UE8M0 bytes) for float x with D = 128: per 32 elements
+    scale 2^ceil(log2(amax / 6)), elements rounded to the nearest E2M1 value,
+    ties to the even code."""
+    D = x.shape[-1]
+    xb = x.float().reshape(*x.shape[:-1], D // 32, 32)
+    amax = xb.abs().amax(-1, keepdim=True).clamp_min(6.0 * 2.0 ** -126)
+    e = torch.ceil(torch.log2(amax / 6.0))
+    y = (xb / torch.exp2(e)).clamp(-6.0, 6.0)
+    dist = (y.abs()[..., None] - _E2M1_MAGS).abs() + (torch.arange(8) % 2) * 1e-6
+    code = dist.argmin(-1) | ((y < 0).long() << 3)
+    code = code.reshape(*x.shape[:-1], D)
+    packed = (code[..., 0::2] | (code[..., 1::2] << 4)).to(torch.uint8)
+    byte = (e.squeeze(-1) + 127).long()
+    scale = torch.zeros(x.shape[:-1], dtype=torch.int64)
+    for b in range(D // 32):
+        scale |= byte[..., b] << (8 * b)
+    return packed, scale.to(torch.int32)
+
+
+def fp8_per_token(x: torch.Tensor):
+    """(e4m3fn codes, float32 scale per row) with scale = max(amax, 1e-4) / 448."""
+    sf = x.float().abs().amax(-1).clamp_min(1e-4) / 448.0
+    return (x.float() / sf[..., None]).to(torch.float8_e4m3fn), sf
+
+
+def make_mqa_logits_inputs(M: int, N: int, H: int = MQA_HEADS, fp4: bool = False, seed: int = 42):
+    """(q, kv, weights, ks, ke) on the CPU: q ~ N(0, 1) cast to e4m3fn (or
+    MXFP4), k ~ N(0, 1) per-token FP8 with float32 scales, weights |N(0, 1)|,
+    ks = 0 and ke = N as the reference test builds them."""
+    g = torch.Generator().manual_seed(seed)
+    qf = torch.randn(M, H, 128, generator=g).to(torch.bfloat16)
+    kf = torch.randn(N, 128, generator=g).to(torch.bfloat16)
+    w = torch.randn(M, H, generator=g).abs()
+    q = quantize_mxfp4(qf) if fp4 else (qf.to(torch.float8_e4m3fn), None)
+    k, ks = fp8_per_token(kf)
+    return q, (k, ks), w, torch.zeros(M, dtype=torch.int32), torch.full((M,), N, dtype=torch.int32)
+
+
+def make_paged_cache(num_blocks: int, block_size: int, gen: torch.Generator) -> torch.Tensor:
+    """uint8 [num_blocks, block_size, 1, 132] as the reference test fills it:
+    N(0, 1) keys, per-token scale max(amax, 1e-4) / 448, codes then scales."""
+    x = torch.randn(num_blocks, block_size, 128, generator=gen).to(torch.bfloat16)
+    codes, sf = fp8_per_token(x)
+    cache = torch.empty(num_blocks, block_size * 132, dtype=torch.uint8)
+    cache[:, :block_size * 128] = codes.view(torch.uint8).reshape(num_blocks, -1)
+    cache[:, block_size * 128:] = sf.reshape(num_blocks, block_size).contiguous().view(torch.uint8)
+    return cache.view(num_blocks, block_size, 1, 132)
+
+
+def make_paged_mqa_inputs(batch: int, next_n: int, avg_ctx: int, fp4: bool = False, block_size: int = 64,
+                          num_blocks: int = None, seed: int = 0):
+    """(q, kv_cache, weights, context_lens [B, next_n], block_tables) as the
+    reference test draws them: lengths uniform in [0.7, 1.3] x avg_ctx,
+    distinct random blocks per sequence."""
+    g = torch.Generator().manual_seed(seed)
+    qf = torch.randn(batch, next_n, MQA_HEADS, 128, generator=g).to(torch.bfloat16)
+    w = torch.randn(batch * next_n, MQA_HEADS, generator=g)
+    base = torch.randint(max(1, int(0.7 * avg_ctx)), int(1.3 * avg_ctx) + 1, (batch,), generator=g,
+                         dtype=torch.int32)
+    per = (base + block_size - 1) // block_size
+    need = int(per.sum())
+    num_blocks = num_blocks or max(need + 16, 64)
+    cache = make_paged_cache(num_blocks, block_size, g)
+    table = torch.zeros(batch, int(per.max()), dtype=torch.int32)
+    pool = torch.randperm(num_blocks, generator=g).to(torch.int32)
+    off = 0
+    for b in range(batch):
+        n = int(per[b])
+        if off + n > num_blocks:
+            pool, off = torch.randperm(num_blocks, generator=g).to(torch.int32), 0
+        table[b, :n] = pool[off:off + n]
+        off += n
+    q = quantize_mxfp4(qf) if fp4 else (qf.to(torch.float8_e4m3fn), None)
+    if fp4:
+        q = (q[0], q[1])
+    ctx = base[:, None].expand(batch, next_n).contiguous()
+    return q, cache, w, ctx, table
+
+
+def mqa_logits_flops(M: int, N: int, H: int = MQA_HEADS) -> int:
+    return 2 * M * N * H * 128
+
+
+def paged_mqa_logits_bytes(ctx: torch.Tensor, rows: int, H: int, max_model_len: int, fp4: bool) -> int:
+    """Algorithmic HBM bytes of one paged call: each row's context keys (132 B
+    with the scale) and a 4-byte block-table entry per 64 positions, q and
+    weights per row, and the whole float32 output row."""
+    q_bytes = H * (64 + 4 if fp4 else 128) + 4 * H
+    return int(ctx.sum()) * 132 + int(ctx.sum()) // 16 + rows * (q_bytes + 4 * max_model_len)

@@ -265,6 +265,60 @@ int fgv_cp_gather_indexer_k_quant_cache(
     const int32_t* cu_seqlen, int64_t batch_size, int64_t num_tokens, void* stream);
 
 /*
+ * Sparse-indexer logits over dense keys.
+ *
+ * Replaces flaggems_vllm.ops.fp8_fp4_mqa_logits
+ * (reference: src/flaggems_vllm/ops/fp8_fp4_mqa_logits.py:523-651, kernels
+ * :88-187 (FP8), :232-358 (MXFP4), :190-222 (clean); float32 oracle
+ * tests/test_fp8_fp4_mqa_logits.py:40-66).  For m < M, n < N:
+ *   logits[m, n] = sum_h ReLU((sum_d q[m,h,d] k[n,d]) * k_scale[n]) * w[m,h]
+ * and, with clean_logits, -inf where n < ks[m] or n >= ke[m].
+ *   q        q_scale == NULL: e4m3fn [M, H, 128]; else packed E2M1 [M, H, 64]
+ *            (even d in the low nibble) with q_scale int32 [M, H] holding the
+ *            UE8M0 byte of d = 32b..32b+31 in byte b.  Byte strides, multiples
+ *            of 16, 16-byte aligned rows.
+ *   k        e4m3fn [N, 128] (byte row stride, multiple of 16); k_scale float [N]
+ *            (positive, as the producers write it).
+ *   weights  float [M, H]; ks, ke int32 [M] (read only with clean_logits).
+ *   logits   float [M, N], row stride in elements.
+ * num_heads 16, 32, 64 or 128; head_dim 128.  The head sum is taken in
+ * binary32 in an order of this library's choosing, with k_scale applied once
+ * after it (equal to the reference's per-head product since k_scale > 0).
+ */
+int fgv_fp8_fp4_mqa_logits(
+    const void* q, int64_t q_stride_m, int64_t q_stride_h, const int32_t* q_scale, int64_t q_scale_stride_m,
+    int64_t q_scale_stride_h, const void* k, int64_t k_stride_n, const float* k_scale, const float* weights,
+    int64_t w_stride_m, int64_t w_stride_h, const int32_t* cu_seqlen_ks, const int32_t* cu_seqlen_ke,
+    float* logits, int64_t logits_stride_m, int64_t M, int64_t N, int64_t num_heads, int64_t head_dim,
+    int clean_logits, void* stream);
+
+/*
+ * Sparse-indexer logits over the paged key cache (decode).
+ *
+ * Replaces flaggems_vllm.ops.fp8_fp4_paged_mqa_logits
+ * (reference: src/flaggems_vllm/ops/fp8_fp4_paged_mqa_logits.py:410-579,
+ * kernel :68-181, cache layout :185-225).  For each of `rows` query rows
+ * (q, q_scale and weights as in fgv_fp8_fp4_mqa_logits, per row):
+ *   ctx = context_lens[row / rows_per_context_len], clamped to [0, max_model_len];
+ *   position n < ctx reads entry n % block_size of cache block
+ *   clamp(block_tables[(row / rows_per_table_row) * block_table_stride +
+ *   min(n / block_size, max_blocks_per_seq - 1)], 0, num_blocks - 1)
+ *   (block_size x 128 e4m3fn bytes, then block_size float32 scales: the
+ *   cache fgv_indexer_k_quant_and_cache writes at head_dim 128) and gets the
+ *   logit above; every position ctx <= n < max_model_len gets 0, or -inf
+ *   with clean_logits.  Every element of the [rows, max_model_len] output is
+ *   written.  At most 65535 rows.
+ */
+int fgv_fp8_fp4_paged_mqa_logits(
+    const void* q, int64_t q_stride_row, int64_t q_stride_h, const int32_t* q_scale, int64_t q_scale_stride_row,
+    int64_t q_scale_stride_h, const void* kv_cache, int64_t cache_block_stride, int64_t num_blocks,
+    int64_t block_size, int64_t head_dim, const float* weights, int64_t w_stride_row, int64_t w_stride_h,
+    const int32_t* context_lens, int64_t rows_per_context_len, const int32_t* block_tables,
+    int64_t block_table_stride, int64_t max_blocks_per_seq, int64_t rows_per_table_row, float* logits,
+    int64_t logits_stride_row, int64_t rows, int64_t num_heads, int64_t max_model_len, int clean_logits,
+    void* stream);
+
+/*
  * Sparse MLA decode over the 584-byte MODEL1 cache.
  *
  * Replaces the sparse MODEL1 branch of flaggems_vllm.flash_mla_with_kvcache

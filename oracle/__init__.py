@@ -130,6 +130,22 @@ def lib():
             _P, _I64, _I64,  # block_table, stride, max_blocks
             _P, _I64, _I64,  # cu, batch, T
         ]
+        L.oracle_mqa_logits.restype = None
+        L.oracle_mqa_logits.argtypes = [
+            _P, _I64, _I64, _P, _I64, _I64,  # q, strides (bytes), q_scale, strides
+            _P, _I64, _P, _P, _I64, _I64,  # k, stride, k_scale, w, strides
+            _P, _P, ctypes.c_int, _I64, _I64, _I64,  # ks, ke, clean, N, H, D
+            _P, _I64, _P, _P,  # rows, nrows, out, bound
+        ]
+        L.oracle_paged_mqa_logits.restype = None
+        L.oracle_paged_mqa_logits.argtypes = [
+            _P, _I64, _I64, _P, _I64, _I64,  # q, strides, q_scale, strides
+            _P, _I64, _I64, _I64,  # kv, block stride, num_blocks, block_size
+            _P, _I64, _I64,  # w, strides
+            _P, _I64, _P, _I64, _I64, _I64,  # ctx, per len, bt, stride, max blocks, per table
+            _I64, _I64, _I64, ctypes.c_float,  # H, D, max_model_len, fill
+            _P, _I64, _P, _P,  # rows, nrows, out, bound
+        ]
         L.oracle_model1_token_row.restype = None
         L.oracle_model1_token_row.argtypes = [_P, _I64, _I64, _I64, _P]
         L.oracle_sparse_mla_decode_model1.restype = None
@@ -419,3 +435,75 @@ def cp_gather_indexer_k_quant_cache(k_cache, k_fp8, k_fp8_scale, block_table, cu
     lib().oracle_cp_gather_indexer_k_quant_cache(
         cache.data_ptr(), bstride, nblk, bs, head_dim, qbs, kb.data_ptr(), kb.stride(0), sb.data_ptr(),
         sb.stride(0), bt.data_ptr(), bt.stride(0), bt.shape[1], cu.data_ptr(), bt.shape[0], kb.shape[0])
+
+
+def _rows_arg(rows, total):
+    rows = torch.arange(total, dtype=torch.int64) if rows is None else torch.as_tensor(rows, dtype=torch.int64)
+    return rows.contiguous()
+
+
+def mqa_logits(q, kv, weights, cu_seqlen_ks, cu_seqlen_ke, clean_logits=True, rows=None):
+    """Binary64 logits and error bound ([len(rows), N] float64 each) of
+    flaggems_vllm.fp8_fp4_mqa_logits for the listed query rows (all by
+    default); CPU tensors, same argument forms as the product."""
+    q_values, q_scale = q
+    k_values, k_scales = kv
+    M, H = q_values.shape[0], q_values.shape[1]
+    D = q_values.shape[2] * (2 if q_scale is not None else 1)
+    N = k_values.shape[0]
+    qv = _cpu(q_values).view(torch.uint8)
+    kb = _cpu(k_values).view(torch.uint8)
+    assert qv.stride(-1) == 1 and kb.stride(-1) == 1
+    ksc = _cpu(k_scales, torch.float32).reshape(N).contiguous()
+    w = _cpu(weights, torch.float32)
+    qs = _cpu(q_scale, torch.int32).reshape(M, H) if q_scale is not None else None
+    ks = _cpu(cu_seqlen_ks).to(torch.int32).contiguous() if clean_logits else None
+    ke = _cpu(cu_seqlen_ke).to(torch.int32).contiguous() if clean_logits else None
+    r = _rows_arg(rows, M)
+    out = torch.empty(r.numel(), N, dtype=torch.float64)
+    bound = torch.empty_like(out)
+    lib().oracle_mqa_logits(
+        qv.data_ptr(), qv.stride(0), qv.stride(1), qs.data_ptr() if qs is not None else None,
+        qs.stride(0) if qs is not None else 0, qs.stride(1) if qs is not None else 0,
+        kb.data_ptr(), kb.stride(0), ksc.data_ptr(), w.data_ptr(), w.stride(0), w.stride(1),
+        ks.data_ptr() if ks is not None else None, ke.data_ptr() if ke is not None else None,
+        int(bool(clean_logits)), N, H, D, r.data_ptr(), r.numel(), out.data_ptr(), bound.data_ptr())
+    return out, bound
+
+
+def paged_mqa_logits(q, kv_cache, weights, context_lens, block_tables, max_model_len, clean_logits=False,
+                     rows=None):
+    """Binary64 logits and error bound ([len(rows), max_model_len] float64) of
+    flaggems_vllm.fp8_fp4_paged_mqa_logits for the listed rows (all by
+    default); CPU tensors, same argument forms as the product."""
+    q_values, q_scale = q
+    if q_values.dim() == 3:
+        q_values = q_values.unsqueeze(1)
+    B, next_n, H, last = q_values.shape
+    nrows_total = B * next_n
+    D = last * (2 if q_scale is not None else 1)
+    qv = _cpu(q_values).view(torch.uint8).reshape(nrows_total, H, last)
+    qs = _cpu(q_scale, torch.int32).reshape(nrows_total, H) if q_scale is not None else None
+    kv = _cpu(kv_cache).view(torch.uint8)
+    w = _cpu(weights, torch.float32)
+    ctx = _cpu(context_lens).to(torch.int32)
+    if ctx.dim() == 2:
+        ctx, per_len = ctx.reshape(-1)[:nrows_total].contiguous(), 1
+    else:
+        ctx, per_len = ctx.contiguous(), next_n
+    bt = _cpu(block_tables).to(torch.int32)
+    if bt.dim() == 2 and bt.shape[0] == B:
+        per_table = next_n
+    else:
+        bt, per_table = bt.reshape(nrows_total, -1), 1
+    bt = bt.contiguous()
+    r = _rows_arg(rows, nrows_total)
+    out = torch.empty(r.numel(), max_model_len, dtype=torch.float64)
+    bound = torch.empty_like(out)
+    lib().oracle_paged_mqa_logits(
+        qv.data_ptr(), qv.stride(0), qv.stride(1), qs.data_ptr() if qs is not None else None,
+        qs.stride(0) if qs is not None else 0, qs.stride(1) if qs is not None else 0,
+        kv.data_ptr(), kv.stride(0), kv.shape[0], kv.shape[1], w.data_ptr(), w.stride(0), w.stride(1),
+        ctx.data_ptr(), per_len, bt.data_ptr(), bt.stride(0), bt.shape[1], per_table, H, D, int(max_model_len),
+        float("-inf") if clean_logits else 0.0, r.data_ptr(), r.numel(), out.data_ptr(), bound.data_ptr())
+    return out, bound

@@ -31,6 +31,12 @@
  *                    src/flaggems_vllm/ops/cp_gather_indexer_k_quant_cache.py:23-176
  *     reference test tests/test_indexer_k_quant_and_cache.py:99-142 (torch_indexer)
  *                    tests/test_cp_gather_indexer_k_quant_cache.py:83-114 (torch_gather)
+ *   oracle_mqa_logits, oracle_paged_mqa_logits (binary64 logits with an error
+ *   bound for a binary32 implementation, see their comment)
+ *     reference ops  src/flaggems_vllm/ops/fp8_fp4_mqa_logits.py:88-358, 523-651
+ *                    src/flaggems_vllm/ops/fp8_fp4_paged_mqa_logits.py:68-225, 410-579
+ *     reference test tests/test_fp8_fp4_mqa_logits.py:40-66 (reference_fp4_mqa_logits)
+ *                    tests/test_fp8_fp4_paged_mqa_logits.py:196-249
  *   oracle_sparse_mla_decode_model1 (binary64 attention, see its comment)
  *     reference op   src/flaggems_vllm/ops/flash_mla_with_kvcache.py:489-688, 852-1073
  *                    src/flaggems_vllm/ops/flash_mla_with_kvcache_model1.py:389-470, 699-720
@@ -780,5 +786,151 @@ void oracle_cp_gather_indexer_k_quant_cache(const uint8_t* cache, int64_t block_
             memcpy(k_out + t * k_out_st, base + row * head_dim, (size_t)head_dim);
             memcpy(scale_out + t * scale_out_st, base + block_size * head_dim + row * nqb * 4, (size_t)(nqb * 4));
         }
+    }
+}
+
+/* ------------------------------------------------------------------------
+ * Sparse-indexer logits (reference fp8_fp4_mqa_logits / paged variant):
+ *   logit[m, n] = sum_h ReLU((sum_d q[m,h,d] k[n,d]) * k_scale[n]) * w[m,h]
+ * q is e4m3fn, or E2M1 nibbles (even d in the low nibble) times
+ * 2^(byte - 127), byte b of q_scale[m, h] covering d = 32b..32b+31 (MXFP4);
+ * k is e4m3fn.  Everything is binary64: the products of two 4-bit
+ * significands and their 128-term sums are exact.  bound[] receives an error
+ * bound for a binary32 implementation that forms each head's dot product
+ * with at most D roundings of 2^-24 (gamma = D 2^-24 of sum |q k|), gates it,
+ * sums the H weighted heads in any order and multiplies by k_scale:
+ *   k_scale * sum_h |w_h| (gamma a_h + (H + 3) 2^-24 (|dot_h| + gamma a_h))
+ * with a_h = sum_d |q_hd k_d|.  Positions a cleaned output leaves at -inf (or
+ * a paged row's fill value) get that value and bound 0.
+ * ------------------------------------------------------------------------ */
+
+static double oracle_e2m1_value(unsigned nib)
+{
+    static const double mag[8] = {0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0};
+    return (nib & 8u) ? -mag[nib & 7u] : mag[nib & 7u];
+}
+
+/* q row of one query: H x D binary64 values into qd. */
+static void oracle_query_values(const uint8_t* q_row, int64_t q_sh, const int32_t* qs_row, int64_t qs_sh, int64_t H,
+                                int64_t D, double* qd)
+{
+    for (int64_t h = 0; h < H; ++h) {
+        const uint8_t* hr = q_row + h * q_sh;
+        for (int64_t d = 0; d < D; ++d) {
+            if (qs_row) {
+                uint32_t sb = (uint32_t)qs_row[h * qs_sh];
+                int byte = (int)((sb >> (8 * (d / 32))) & 0xffu);
+                unsigned nib = (hr[d / 2] >> (4 * (d % 2))) & 0xfu;
+                qd[h * D + d] = ldexp(oracle_e2m1_value(nib), byte - 127);
+            } else {
+                qd[h * D + d] = (double)oracle_e4m3fn_to_f32(hr[d]);
+            }
+        }
+    }
+}
+
+static void oracle_logit_one(const double* qd, const float* w_row, int64_t w_sh, int64_t H, int64_t D,
+                             const uint8_t* krow, float kscale, double* out, double* bound)
+{
+    const double u = ldexp(1.0, -24), gamma = (double)D * u;
+    double kv[1024];
+    for (int64_t d = 0; d < D; ++d)
+        kv[d] = (double)oracle_e4m3fn_to_f32(krow[d]);
+    double sum = 0.0, err = 0.0;
+    for (int64_t h = 0; h < H; ++h) {
+        double dot = 0.0, a = 0.0;
+        for (int64_t d = 0; d < D; ++d) {
+            dot += qd[h * D + d] * kv[d];
+            a += fabs(qd[h * D + d] * kv[d]);
+        }
+        double s = dot * (double)kscale;
+        double wh = (double)w_row[h * w_sh];
+        sum += (s > 0.0 ? s : 0.0) * wh;
+        err += fabs(wh) * (gamma * a + (double)(H + 3) * u * (fabs(dot) + gamma * a));
+    }
+    *out = sum;
+    *bound = fabs((double)kscale) * err;
+}
+
+/* Dense: the listed query rows (row r of out/bound = query rows[r]) x all N keys. */
+void oracle_mqa_logits(const uint8_t* q, int64_t q_sm, int64_t q_sh, const int32_t* q_scale, int64_t qs_sm,
+                       int64_t qs_sh, const uint8_t* k, int64_t k_sn, const float* k_scale, const float* w,
+                       int64_t w_sm, int64_t w_sh, const int32_t* ks, const int32_t* ke, int clean, int64_t N,
+                       int64_t H, int64_t D, const int64_t* rows, int64_t nrows, double* out, double* bound)
+{
+    if (D > 1024)
+        return;
+#pragma omp parallel for schedule(dynamic)
+    for (int64_t r = 0; r < nrows; ++r) {
+        const int64_t m = rows[r];
+        double* qd = (double*)malloc(sizeof(double) * (size_t)(H * D));
+        if (!qd)
+            continue;
+        oracle_query_values(q + m * q_sm, q_sh, q_scale ? q_scale + m * qs_sm : NULL, qs_sh, H, D, qd);
+        for (int64_t n = 0; n < N; ++n) {
+            if (clean && (n < ks[m] || n >= ke[m])) {
+                out[r * N + n] = -INFINITY;
+                bound[r * N + n] = 0.0;
+                continue;
+            }
+            oracle_logit_one(qd, w + m * w_sm, w_sh, H, D, k + n * k_sn, k_scale[n], &out[r * N + n],
+                             &bound[r * N + n]);
+        }
+        free(qd);
+    }
+}
+
+/* Paged: the listed rows x positions 0..max_model_len-1.  Row `row` reads
+ * context_lens[row / rows_per_context_len] positions through block-table row
+ * row / rows_per_table_row;
+ * position n is entry n % block_size of block clamp(table[min(n / block_size,
+ * max_blocks - 1)], 0, num_blocks - 1) (a position past the table reads
+ * the table's last block); codes at block + slot * 128 (D bytes),
+ * the float32 scale at block + block_size * D + 4 slot. */
+void oracle_paged_mqa_logits(const uint8_t* q, int64_t q_sr, int64_t q_sh, const int32_t* q_scale, int64_t qs_sr,
+                             int64_t qs_sh, const uint8_t* kv, int64_t block_stride, int64_t num_blocks,
+                             int64_t block_size, const float* w, int64_t w_sr, int64_t w_sh, const int32_t* ctx,
+                             int64_t rows_per_context_len, const int32_t* bt, int64_t bt_sr, int64_t max_blocks,
+                             int64_t rows_per_table_row,
+                             int64_t H, int64_t D, int64_t max_model_len, float fill, const int64_t* rows,
+                             int64_t nrows, double* out, double* bound)
+{
+    if (D > 1024)
+        return;
+#pragma omp parallel for schedule(dynamic)
+    for (int64_t r = 0; r < nrows; ++r) {
+        const int64_t row = rows[r];
+        double* qd = (double*)malloc(sizeof(double) * (size_t)(H * D));
+        if (!qd)
+            continue;
+        oracle_query_values(q + row * q_sr, q_sh, q_scale ? q_scale + row * qs_sr : NULL, qs_sh, H, D, qd);
+        int64_t c = ctx[row / rows_per_context_len];
+        if (c < 0)
+            c = 0;
+        if (c > max_model_len)
+            c = max_model_len;
+        const int32_t* tab = bt + (row / rows_per_table_row) * bt_sr;
+        for (int64_t n = 0; n < max_model_len; ++n) {
+            if (n >= c) {
+                out[r * max_model_len + n] = (double)fill;
+                bound[r * max_model_len + n] = 0.0;
+                continue;
+            }
+            int64_t lb = n / block_size;
+            const int64_t slot = n - lb * block_size;
+            if (lb > max_blocks - 1)
+                lb = max_blocks - 1;
+            int64_t blk = tab[lb];
+            if (blk < 0)
+                blk = 0;
+            if (blk > num_blocks - 1)
+                blk = num_blocks - 1;
+            const uint8_t* base = kv + blk * block_stride;
+            float ksc;
+            memcpy(&ksc, base + block_size * D + 4 * slot, 4);
+            oracle_logit_one(qd, w + row * w_sr, w_sh, H, D, base + slot * D, ksc, &out[r * max_model_len + n],
+                             &bound[r * max_model_len + n]);
+        }
+        free(qd);
     }
 }

@@ -22,6 +22,10 @@ oracle that the reference's own tests compare its Triton kernels against:
   index arithmetic, with torch's float8 -> float cast and exp2 scale;
 * sparse MLA decode over the MODEL1 cache: the portable kernel's chunked
   online softmax (ops/flash_mla_with_kvcache.py:489-688);
+* sparse-indexer logits: tests/test_fp8_fp4_mqa_logits.py
+  ``reference_fp4_mqa_logits`` :40-66 (its per-row, per-head float32 loop,
+  applied to FP8 q as well as MXFP4 q) and the paged test's per-row gather of
+  the cache (tests/test_fp8_fp4_paged_mqa_logits.py:196-226);
 * indexer key cache: tests/test_indexer_k_quant_and_cache.py ``torch_indexer``
   :99-142 and tests/test_cp_gather_indexer_k_quant_cache.py ``torch_gather``
   :83-114, with float8_e4m3fn codes.
@@ -342,3 +346,71 @@ def cp_gather_indexer_k_quant_cache(k_cache, k_fp8, k_fp8_scale, block_table, cu
             blk, r = int(block_table[b, pos // block_size]), pos % block_size
             kb[t] = values[blk, r * head_dim:(r + 1) * head_dim]
             sf[t] = scales[blk, r * nqb:(r + 1) * nqb]
+
+
+_E2M1_VALUES = torch.tensor([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0, -0.0, -0.5, -1.0, -1.5, -2.0, -3.0, -4.0, -6.0])
+
+
+def mxfp4_values(packed, q_scale, head_dim):
+    """float32 [..., head_dim] of packed E2M1 (even element in the low nibble)
+    times 2^(byte - 127), byte b of the int32 scale covering 32 b..32 b + 31."""
+    p = packed.view(torch.uint8).long()
+    nib = torch.stack([p & 0xF, p >> 4], dim=-1).reshape(*packed.shape[:-1], head_dim)
+    vals = _E2M1_VALUES[nib]
+    sb = q_scale.reshape(*packed.shape[:-1]).long()
+    blk = torch.arange(head_dim) // 32
+    byte = ((sb[..., None] >> (8 * blk)) & 0xFF).float()
+    return vals * torch.exp2(byte - 127.0)
+
+
+def mqa_logits(q, kv, weights, cu_seqlen_ks, cu_seqlen_ke, clean_logits=True):
+    """The reference test's float32 formulation: per row m and head h,
+    ReLU(sum_d q k * k_scale) * w accumulated over heads."""
+    q_values, q_scale = q
+    k_values, k_scales = kv
+    M, H = q_values.shape[:2]
+    if q_scale is not None:
+        qf = mxfp4_values(q_values, q_scale, q_values.shape[-1] * 2)
+    else:
+        qf = q_values.view(torch.float8_e4m3fn).float()
+    kf = k_values.view(torch.float8_e4m3fn).float()
+    ksc = k_scales.reshape(-1).float()
+    logits = torch.zeros(M, kf.shape[0], dtype=torch.float32)
+    for m in range(M):
+        for h in range(H):
+            dot = torch.sum(qf[m, h].unsqueeze(0) * kf, dim=1) * ksc
+            logits[m] += dot.clamp_min(0.0) * weights[m, h]
+    if clean_logits:
+        for m in range(M):
+            logits[m, :int(cu_seqlen_ks[m])] = float("-inf")
+            logits[m, int(cu_seqlen_ke[m]):] = float("-inf")
+    return logits
+
+
+def paged_mqa_logits(q, kv_cache, weights, context_lens, block_tables, max_model_len, clean_logits=False):
+    """Per row: gather the context's keys and scales from the paged cache as
+    the reference test does, then the dense formulation above."""
+    q_values, q_scale = q
+    if q_values.dim() == 3:
+        q_values = q_values.unsqueeze(1)
+    B, next_n, H, last = q_values.shape
+    rows = B * next_n
+    nblk, bs = kv_cache.shape[0], kv_cache.shape[1]
+    D = kv_cache.shape[3] - 4
+    flat = kv_cache.reshape(nblk, -1)
+    kdata = flat[:, :bs * D].reshape(nblk * bs, D)
+    kscale = flat[:, bs * D:].contiguous().view(torch.float32).reshape(-1)
+    ctx = context_lens.reshape(-1)[:rows] if context_lens.dim() == 2 else context_lens.repeat_interleave(next_n)
+    out = torch.full((rows, max_model_len), float("-inf") if clean_logits else 0.0)
+    qr = q_values.reshape(rows, H, last)
+    qsr = q_scale.reshape(rows, H) if q_scale is not None else None
+    for r in range(rows):
+        c = int(ctx[r])
+        if c == 0:
+            continue
+        pos = torch.arange(c)
+        phys = block_tables[r // next_n, pos // bs].long()
+        idx = phys * bs + pos % bs
+        qq = (qr[r:r + 1], qsr[r:r + 1] if qsr is not None else None)
+        out[r, :c] = mqa_logits(qq, (kdata[idx], kscale[idx]), weights[r:r + 1], None, None, False)[0]
+    return out
