@@ -44,8 +44,9 @@ typedef float v4f_t __attribute__((ext_vector_type(4)));
 
 constexpr int kIdxDim = 128;        // index head dim: one MFMA K
 constexpr int kThreadsM = 256;      // 4 waves
-constexpr int kChunk = 64;          // keys per LDS chunk of the dense kernel
+constexpr int kChunk = 64;          // keys per LDS chunk of the dense kernel (128 and 256 measured slower)
 constexpr int kKeyPitch = 144;      // LDS bytes per key row (128 + 16)
+constexpr int kOneQueryHeads = 128;  // from this many heads a wave holds one query, not two
 
 __device__ __forceinline__ v8i_t fp8_operand(const uint8_t* row, int g) {
     const uint4 lo = *reinterpret_cast<const uint4*>(row + 16 * g);
@@ -95,9 +96,10 @@ struct QueryRegs {
         }
     }
 
-    // sum over all heads of max(q_h . k, 0) * w_h for this lane's key column:
-    // every head tile's MFMA is issued before the first is gated
-    __device__ __forceinline__ float gated_sum(v8i_t b) const {
+    // This lane group's share (its 4 rows of every head tile) of
+    // sum_h max(q_h . k, 0) * w_h for the lane's key column; every head tile's
+    // MFMA is issued before the first is gated.
+    __device__ __forceinline__ float gated_part(v8i_t b) const {
         v4f_t acc[HT];
 #pragma unroll
         for (int t = 0; t < HT; ++t)
@@ -108,9 +110,26 @@ struct QueryRegs {
 #pragma unroll
             for (int i = 0; i < 4; ++i)
                 part = fmaf(relu(acc[t][i]), w[t][i], part);
-        return group4_sum(part);
+        return part;
     }
+
+    __device__ __forceinline__ float gated_sum(v8i_t b) const { return group4_sum(gated_part(b)); }
 };
+
+// Four key tiles' lane-group shares p[kt] -> lane (c, g) gets the head sum of
+// key tile g, column c (key 16 g + c of the 64): a reduce-scatter over the four
+// lane groups in two permute steps (v_permlane32_swap pairs tiles 0/2 and 1/3
+// across lane groups g, g ^ 2; v_permlane16_swap then pairs g, g ^ 1), six
+// VALU operations for the four tiles.  Every total is
+// (p[g0] + p[g2]) + (p[g1] + p[g3]).
+__device__ __forceinline__ float reduce_scatter4(const float (&p)[4]) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(p[0]), __float_as_uint(p[2]), false, false);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(p[1]), __float_as_uint(p[3]), false, false);
+    const float s02 = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const float s13 = __uint_as_float(b[0]) + __uint_as_float(b[1]);
+    const auto c = __builtin_amdgcn_permlane16_swap(__float_as_uint(s02), __float_as_uint(s13), false, false);
+    return __uint_as_float(c[0]) + __uint_as_float(c[1]);
+}
 
 struct MqaArgs {
     const uint8_t* q;
@@ -133,8 +152,10 @@ struct MqaArgs {
 
 // Dense logits.  A workgroup covers WQ * QW queries x keys_per_block keys: its
 // four waves are WQ query groups (QW queries each) x (4 / WQ) key-tile slices,
-// and every 64-key chunk of K is staged once in LDS (double-buffered) for all
-// of them.
+// and every 64-key chunk of K is staged once in LDS (double-buffered, the next
+// chunk's loads in flight under the current chunk's MFMAs) for all of them.
+// (Staging the workgroup's whole key range at once, with no barrier between
+// chunks, measured 14 % slower.)
 template <bool FP4, int HT, int QW, int WQ>
 __global__ void __launch_bounds__(kThreadsM, 2)
 mqa_logits_kernel(MqaArgs a) {
@@ -223,22 +244,46 @@ mqa_logits_kernel(MqaArgs a) {
         if (more)
             fetch(n0 + kChunk, r0, r1);
         const uint8_t* kb = kbuf[ci & 1];
-        float ksc[KTW];
+        const int n0g = n0;
+        if constexpr (KTW == 4) {
+            // all four key tiles per query, then one reduce-scatter: lane l
+            // holds key n0 + l, stored as one 256-byte row segment per query
+            const int n = n0g + lane;
+            const float ksc = a.k_scale[min(n, a.N - 1)];
+            float p[QW][4];
 #pragma unroll
-        for (int kt = 0; kt < KTW; ++kt)
-            ksc[kt] = a.k_scale[min(n0 + 16 * (wk * KTW + kt) + c, a.N - 1)];
+            for (int kt = 0; kt < 4; ++kt) {
+                const v8i_t b = fp8_operand(kb + (16 * kt + c) * kKeyPitch, g);
 #pragma unroll
-        for (int kt = 0; kt < KTW; ++kt) {
-            const int tile = wk * KTW + kt;
-            const v8i_t b = fp8_operand(kb + (16 * tile + c) * kKeyPitch, g);
-            const int n = n0 + 16 * tile + c;
+                for (int j = 0; j < QW; ++j)
+                    p[j][kt] = qr[j].gated_part(b);
+            }
 #pragma unroll
             for (int j = 0; j < QW; ++j) {
-                const float v = qr[j].gated_sum(b) * ksc[kt];
+                const float v = reduce_scatter4(p[j]) * ksc;
                 const int m = m_first + wq * QW + j;
                 const bool outside = n < my_ks[j] || n >= my_ke[j];  // [0, N) unless cleaning
-                if (g == j && m < a.M && n < n_end)
+                if (m < a.M && n < n_end)
                     a.out[(int64_t)m * a.o_sm + n] = outside ? -__builtin_inff() : v;
+            }
+        } else {
+            float ksc[KTW];
+#pragma unroll
+            for (int kt = 0; kt < KTW; ++kt)
+                ksc[kt] = a.k_scale[min(n0g + 16 * (wk * KTW + kt) + c, a.N - 1)];
+#pragma unroll
+            for (int kt = 0; kt < KTW; ++kt) {
+                const int tile = wk * KTW + kt;
+                const v8i_t b = fp8_operand(kb + (16 * tile + c) * kKeyPitch, g);
+                const int n = n0g + 16 * tile + c;
+#pragma unroll
+                for (int j = 0; j < QW; ++j) {
+                    const float v = qr[j].gated_sum(b) * ksc[kt];
+                    const int m = m_first + wq * QW + j;
+                    const bool outside = n < my_ks[j] || n >= my_ke[j];
+                    if (g == j && m < a.M && n < n_end)
+                        a.out[(int64_t)m * a.o_sm + n] = outside ? -__builtin_inff() : v;
+                }
             }
         }
         if (more)
@@ -263,7 +308,8 @@ struct PagedArgs {
     int64_t o_sr;          // float elements
     int32_t rows, bt_row_div, ctx_row_div;
     int32_t num_blocks, block_size, max_blocks;
-    int32_t max_model_len, keys_per_block;  // keys_per_block: multiple of 256
+    int32_t max_model_len, keys_per_block;  // keys_per_block: multiple of 1024
+    int32_t vec_fill;                       // output rows 16-byte aligned, max_model_len % 4 == 0
     float fill;
 };
 
@@ -281,8 +327,14 @@ paged_mqa_logits_kernel(PagedArgs a) {
     const int ctx = min(max(a.ctx[row / a.ctx_row_div], 0), a.max_model_len);
     float* out = a.out + (int64_t)row * a.o_sr;
     if (n_begin >= ctx) {
-        for (int n = n_begin + threadIdx.x; n < n_end; n += kThreadsM)
-            out[n] = a.fill;
+        if (a.vec_fill) {  // rows 16-byte aligned: one float4 per thread per 1024 positions
+            const uint32_t fb = __float_as_uint(a.fill);
+            for (int n = n_begin + 4 * threadIdx.x; n < n_end; n += 4 * kThreadsM)
+                store16(out + n, make_uint4(fb, fb, fb, fb));
+        } else {
+            for (int n = n_begin + threadIdx.x; n < n_end; n += kThreadsM)
+                out[n] = a.fill;
+        }
         return;
     }
     QueryRegs<FP4, HT> qr;
@@ -290,6 +342,10 @@ paged_mqa_logits_kernel(PagedArgs a) {
             a.w + (int64_t)row * a.w_sr, a.w_sh, c, g);
     const int32_t* bt_row = a.bt + (int64_t)(row / a.bt_row_div) * a.bt_sr;
     const int64_t scale_off = (int64_t)a.block_size * kIdxDim;
+    // each wave: positions n0 .. n0 + 63 per step, the four key tiles' cache
+    // loads issued before the first MFMA.  (A two-stage pipeline, the next
+    // step's loads issued before the current one is multiplied, measured 1.6x
+    // slower: 184 VGPRs halve the waves per SIMD.)
     for (int n0 = n_begin + 64 * wave; n0 < n_end; n0 += 256) {
         v8i_t b[4];
         float ksc[4];
@@ -310,14 +366,33 @@ paged_mqa_logits_kernel(PagedArgs a) {
                 ksc[kt] = 0.f;
             }
         }
+        float p[4];
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt) {
-            const float v = qr.gated_sum(b[kt]) * ksc[kt];
-            const int n = n0 + 16 * kt + c;
-            if (g == 0 && n < n_end)
-                out[n] = n < ctx ? v : a.fill;
-        }
+        for (int kt = 0; kt < 4; ++kt)
+            p[kt] = qr.gated_part(b[kt]);
+        // lane l: position n0 + l (its key tile g's scale sits in lane (c, g)'s ksc[g])
+        float my_ksc = ksc[0];
+#pragma unroll
+        for (int kt = 1; kt < 4; ++kt)
+            my_ksc = g == kt ? ksc[kt] : my_ksc;
+        const float v = reduce_scatter4(p) * my_ksc;
+        const int n = n0 + lane;
+        if (n < n_end)
+            out[n] = n < ctx ? v : a.fill;
     }
+}
+
+// Few queries: the four waves split each chunk's key tiles (one query per
+// workgroup); otherwise each wave owns two queries (one from 128 heads, for
+// registers) and all four key tiles.
+template <bool FP4, int HT>
+void launch_dense(bool small, dim3 grid, hipStream_t st, const MqaArgs& a) {
+    if (small)
+        hipLaunchKernelGGL((mqa_logits_kernel<FP4, HT, 1, 1>), grid, dim3(kThreadsM), 0, st, a);
+    else if constexpr (16 * HT >= kOneQueryHeads)
+        hipLaunchKernelGGL((mqa_logits_kernel<FP4, HT, 1, 4>), grid, dim3(kThreadsM), 0, st, a);
+    else
+        hipLaunchKernelGGL((mqa_logits_kernel<FP4, HT, 2, 4>), grid, dim3(kThreadsM), 0, st, a);
 }
 
 int check_h(int64_t h) {
@@ -373,10 +448,9 @@ extern "C" int fgv_fp8_fp4_mqa_logits(
     a.clean = clean_logits != 0;
     const bool fp4 = q_scale != nullptr;
     hipStream_t st = static_cast<hipStream_t>(stream);
-    // Few queries: the four waves split each chunk's key tiles (one query per
-    // workgroup); otherwise each wave owns two queries and all four key tiles.
     const bool small = M < 8;
-    const int64_t qpb = small ? 1 : 8;
+    const int64_t qw = num_heads >= kOneQueryHeads ? 1 : 2;
+    const int64_t qpb = small ? 1 : 4 * qw;
     const int64_t wg_m = (M + qpb - 1) / qpb;
     const int64_t chunks = (N + kChunk - 1) / kChunk;
     const int64_t wg_n = std::min<int64_t>(chunks, std::max<int64_t>(1, (2048 + wg_m - 1) / wg_m));
@@ -384,27 +458,12 @@ extern "C" int fgv_fp8_fp4_mqa_logits(
     const dim3 grid((uint32_t)wg_m, (uint32_t)((N + a.keys_per_block - 1) / a.keys_per_block));
     if (grid.x > 0x7fffffffu || grid.y > 65535u)
         return fail(FGV_E_TOO_LARGE, "grid too large");
-#define FGV_MQA_LAUNCH(FP4, HT)                                                                  \
-    do {                                                                                        \
-        if (small)                                                                              \
-            hipLaunchKernelGGL((mqa_logits_kernel<FP4, HT, 1, 1>), grid, dim3(kThreadsM), 0, st, a); \
-        else                                                                                    \
-            hipLaunchKernelGGL((mqa_logits_kernel<FP4, HT, 2, 4>), grid, dim3(kThreadsM), 0, st, a); \
-    } while (0)
-#define FGV_MQA_HEADS(HT)             \
-    do {                              \
-        if (fp4)                      \
-            FGV_MQA_LAUNCH(true, HT); \
-        else                          \
-            FGV_MQA_LAUNCH(false, HT); \
-    } while (0)
     switch (num_heads) {
-        case 16: FGV_MQA_HEADS(1); break;
-        case 32: FGV_MQA_HEADS(2); break;
-        case 64: FGV_MQA_HEADS(4); break;
-        default: FGV_MQA_HEADS(8); break;
+        case 16: fp4 ? launch_dense<true, 1>(small, grid, st, a) : launch_dense<false, 1>(small, grid, st, a); break;
+        case 32: fp4 ? launch_dense<true, 2>(small, grid, st, a) : launch_dense<false, 2>(small, grid, st, a); break;
+        case 64: fp4 ? launch_dense<true, 4>(small, grid, st, a) : launch_dense<false, 4>(small, grid, st, a); break;
+        default: fp4 ? launch_dense<true, 8>(small, grid, st, a) : launch_dense<false, 8>(small, grid, st, a); break;
     }
-#undef FGV_MQA_HEADS
 #undef FGV_MQA_LAUNCH
     return launch_status();
 }
@@ -466,6 +525,7 @@ extern "C" int fgv_fp8_fp4_paged_mqa_logits(
     a.max_blocks = (int32_t)max_blocks_per_seq;
     a.max_model_len = (int32_t)max_model_len;
     a.keys_per_block = 1024;
+    a.vec_fill = aligned(logits, 16) && logits_stride_row % 4 == 0 && max_model_len % 4 == 0;
     a.fill = clean_logits ? -__builtin_inff() : 0.f;
     const bool fp4 = q_scale != nullptr;
     const dim3 grid((uint32_t)((max_model_len + a.keys_per_block - 1) / a.keys_per_block), (uint32_t)rows);
