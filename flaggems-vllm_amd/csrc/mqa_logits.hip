@@ -199,16 +199,14 @@ mqa_logits_kernel(MqaArgs a) {
     const int c_lo = lo < hi ? n_begin + (lo - n_begin) / kChunk * kChunk : n_end;
     const int c_hi = lo < hi ? min(n_end, n_begin + (hi - n_begin + kChunk - 1) / kChunk * kChunk) : n_end;
 
-    // -inf outside [c_lo, c_hi) (cleaning only): each wave its own queries and key slice
-    if (a.clean) {
-        for (int n0 = n_begin + 16 * wk; n0 < n_end; n0 += 16 * (4 / WQ)) {
-            const int n = n0 + c;
-            if ((n0 >= c_lo && n0 < c_hi) || n >= n_end || g >= QW)
-                continue;
-            const int m = m_first + wq * QW + g;
-            if (m < a.M)
-                a.out[(int64_t)m * a.o_sm + n] = -__builtin_inff();
-        }
+    // -inf on [n_begin, c_lo) and [c_hi, n_end) (cleaning only): lane group g
+    // < QW of each wave its query's row, the wave's key slice
+    if (a.clean && g < QW && m_first + wq * QW + g < a.M) {
+        float* orow = a.out + (int64_t)(m_first + wq * QW + g) * a.o_sm;
+        for (int n = n_begin + 16 * wk + c; n < c_lo; n += 16 * (4 / WQ))
+            orow[n] = -__builtin_inff();
+        for (int n = c_hi + 16 * wk + c; n < n_end; n += 16 * (4 / WQ))
+            orow[n] = -__builtin_inff();
     }
     if (c_lo >= c_hi)
         return;  // workgroup-uniform
