@@ -484,10 +484,11 @@ def main():
         query = _native.lib().fgv_sparse_mla_decode_workspace_bytes
         etopk = w.extra_indices.shape[-1] if w.extra_indices is not None else 0
         entries = w.extra_k_cache.shape[0] * w.extra_k_cache.shape[1] if w.extra_k_cache is not None else 0
-        split = query(B, SQ, HQ, w.indices.shape[-1], etopk, 0) > 0
+        grid = _native.lib().fgv_sparse_mla_decode_grid(B, SQ, HQ, w.indices.shape[-1], etopk)
         expanded = query(B, SQ, HQ, w.indices.shape[-1], etopk, entries) > query(B, SQ, HQ, w.indices.shape[-1],
                                                                                   etopk, 0)
-        kernel = "sparse_mla_decode_split_kernel" if split else "sparse_mla_decode_kernel"
+        kernel = {0: "sparse_mla_decode_kernel", 1: "sparse_mla_decode_split_kernel",
+                  2: "sparse_mla_decode_pair_kernel"}[grid]
         workload = f"mla_{args.mla_case}"
         case = W.MLA_CASES[args.mla_case]
         config = {"workload": f"flash_mla_with_kvcache sparse MODEL1 decode '{args.mla_case}': "
@@ -497,8 +498,10 @@ def main():
                                  f"of {case['extra_page']}" if "extra_topk" in case else ""),
                   "batch": B, "seq_q": SQ, "num_heads": HQ, "attended_entries": w_cpu.used_tokens(),
                   "flops_per_call": flops_call,
-                  "schedule": ("balanced split grid + combine kernel" if split
-                               else "one workgroup per (row, 64-head block)")
+                  "schedule": {0: "one workgroup per (row, 64-head block)",
+                               1: "balanced split grid + combine kernel",
+                               2: "paired grid: one 8-wave workgroup per CU, both halves on each item, "
+                                  "a short item after a long one"}[grid]
                               + ("; extra cache expanded to bf16 once per call" if expanded else "")}
     elif args.op == "indexer_k":
         # indexer key quantise + insert at the reference benchmark's shapes

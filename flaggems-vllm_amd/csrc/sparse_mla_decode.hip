@@ -366,6 +366,123 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("" ::: "memory");
 }
 
+// Attends one chunk for the wave's 16 heads: its bf16 K tile is at `kt`, its
+// score mask (0 or -inf per entry) at `mask`; qf is q (B operand), acc the
+// fp32 O^T accumulators, m_run / l_run the reference maximum (base 2) and the
+// running sum.  qk_base / tr_base are the lane's K-tile byte offsets for the
+// QK row reads and the PV transposing reads, g its 16-lane group.
+// (Each call site passes one fixed LDS array, so the compiler can tell the
+// tile read from the tile the LDS DMA is filling.)
+__device__ __forceinline__ void attend_chunk(const uint8_t* kt, const float* mask, const bf16x8_t (&qf)[kQLoads],
+                                             f32x4_t (&acc)[32], float& m_run, float& l_run, int qk_base,
+                                             int tr_base, int g, float scale_log2) {
+    // ---- S^T = K q^T for the chunk's two 16-entry tiles
+    // K operands read two steps ahead of the MFMAs that consume them
+    f32x4_t s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+    bf16x8_t ka[3], kb[3];
+    auto read_k = [&](int s, bf16x8_t& x, bf16x8_t& y) {
+        x = *reinterpret_cast<const bf16x8_t*>(kt + qk_base + 64 * s);
+        y = *reinterpret_cast<const bf16x8_t*>(kt + qk_base + 64 * s + 16 * kKRowBytes);
+    };
+    read_k(0, ka[0], kb[0]);
+    read_k(1, ka[1], kb[1]);
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+        if (s + 2 < 16)
+            read_k(s + 2, ka[(s + 2) % 3], kb[(s + 2) % 3]);
+        s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[s % 3], qf[s], s0, 0, 0, 0);
+        s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb[s % 3], qf[s], s1, 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);  // keep the reads two steps ahead
+    }
+
+    // ---- online softmax (base 2) for head m16 over entries 4g+r, 16+4g+r
+    float sv[8];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        sv[r] = s0[r] * scale_log2 + mask[4 * g + r];
+        sv[4 + r] = s1[r] * scale_log2 + mask[16 + 4 * g + r];
+    }
+    float cmax = sv[0];
+#pragma unroll
+    for (int i = 1; i < 8; ++i)
+        cmax = fmaxf(cmax, sv[i]);
+    cmax = group4_max(cmax);
+    // Raise the reference maximum (and rescale O and the sum) only when a
+    // score of this wave's heads exceeds it by more than kRescaleSlack.
+    if (__any(cmax > m_run + kRescaleSlack)) {
+        const float m_new = fmaxf(m_run, cmax);
+        const float alpha = __builtin_amdgcn_exp2f(m_run - (m_new == -INFINITY ? 0.f : m_new));
+        l_run *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < 32; ++dt)
+            acc[dt] *= alpha;
+        m_run = m_new;
+    }
+    const float m_use = m_run == -INFINITY ? 0.f : m_run;
+    float p[8], psum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        p[i] = __builtin_amdgcn_exp2f(sv[i] - m_use);
+        psum += p[i];
+    }
+    psum = group4_sum(psum);
+    l_run += psum;
+    // k = 8g+i of the PV product is entry 4g+i (i < 4) or 16+4g+i-4
+    const uint4 pw = make_uint4(pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]),
+                                pack_bf16x2(p[4], p[5]), pack_bf16x2(p[6], p[7]));
+    const bf16x8_t pb = __builtin_bit_cast(bf16x8_t, pw);
+
+    // ---- O^T = alpha * O^T + V^T P^T over the 32 16-dim tiles: the
+    // transposing read hands lane j of group g dim 16dt+j of rows
+    // 4g..4g+3 (then 16+4g..16+4g+3), the A operand of k = 8g..8g+7.
+    // (four steps ahead: one MFMA per step covers less LDS latency than
+    // the two per step of the QK loop)
+    uint2 vlo[5], vhi[5];
+    auto read_v = [&](int dt, uint2& x, uint2& y) {
+        x = read_tr(kt, tr_base + 32 * dt);
+        y = read_tr(kt, tr_base + 32 * dt + 16 * kKRowBytes);
+    };
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        read_v(i, vlo[i], vhi[i]);
+#pragma unroll
+    for (int dt = 0; dt < 32; ++dt) {
+        if (dt + 4 < 32)
+            read_v(dt + 4, vlo[(dt + 4) % 5], vhi[(dt + 4) % 5]);
+        const uint2 lo = vlo[dt % 5], hi = vhi[dt % 5];
+        const bf16x8_t av = __builtin_bit_cast(bf16x8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
+        acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pb, acc[dt], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+// The wave's 16 output rows (lane (m16, g) holds dims 16dt+4g..+3 of head
+// m16 in acc[dt]), times `factor`, go out through LDS: the wave stages them at
+// `stage` (its own 16 rows, 1040 B apart so the staging writes of 32 lanes hit
+// distinct banks), then writes whole 1 KiB rows with 16-byte non-temporal
+// stores.  Only this wave touches `stage`, so a wait on its own LDS writes
+// is the only synchronisation.
+constexpr int kStageRow = kHeadDim * 2 + 16;
+static_assert(2 * 16 * kStageRow <= 2 * kRawBytes && 2 * 16 * kStageRow <= kChunk * kKRowBytes,
+              "two waves' staging fits the gather buffers and the K tile");
+
+__device__ __forceinline__ void store_rows(uint8_t* stage, const f32x4_t (&acc)[32], float factor, uint16_t* obase,
+                                           int64_t o_sh, int m16, int g, int lane) {
+#pragma unroll
+    for (int dt = 0; dt < 32; ++dt) {
+        const f32x4_t v = acc[dt] * factor;
+        *reinterpret_cast<uint2*>(stage + m16 * kStageRow + 32 * dt + 8 * g) =
+            make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+    }
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(kWaitLds);
+    __builtin_amdgcn_wave_barrier();
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int h = 0; h < 16; ++h)
+        store16(obase + h * o_sh + 8 * lane, *reinterpret_cast<const uint4*>(stage + h * kStageRow + 16 * lane));
+}
+
 __device__ __forceinline__ void run_segment(const MlaArgs& a, uint8_t (&raw)[2][kRawBytes], uint8_t* kbuf,
                                             float (&mask_lds)[2][kChunk], int b,
                                             int sq, int hb, int c_lo, int c_hi, int slot, int wave, int lane) {
@@ -431,88 +548,8 @@ __device__ __forceinline__ void run_segment(const MlaArgs& a, uint8_t (&raw)[2][
     const int tr_row = 4 * g + (m16 >> 2);
     const int tr_base = kbuf_byte(tr_row, (m16 & 3) >> 1) + 8 * (m16 & 1);
 
-    // Attends one chunk whose bf16 K tile is at `kt` and score mask at `mask`.
-    // (Each call site passes one fixed LDS array, so the compiler can tell the
-    // tile read from the tile the LDS DMA is filling.)
     auto attend = [&](const uint8_t* kt, const float* mask) __attribute__((always_inline)) {
-        // ---- S^T = K q^T for the chunk's two 16-entry tiles
-        // K operands read two steps ahead of the MFMAs that consume them
-        f32x4_t s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
-        bf16x8_t ka[3], kb[3];
-        auto read_k = [&](int s, bf16x8_t& x, bf16x8_t& y) {
-            x = *reinterpret_cast<const bf16x8_t*>(kt + qk_base + 64 * s);
-            y = *reinterpret_cast<const bf16x8_t*>(kt + qk_base + 64 * s + 16 * kKRowBytes);
-        };
-        read_k(0, ka[0], kb[0]);
-        read_k(1, ka[1], kb[1]);
-#pragma unroll
-        for (int s = 0; s < 16; ++s) {
-            if (s + 2 < 16)
-                read_k(s + 2, ka[(s + 2) % 3], kb[(s + 2) % 3]);
-            s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[s % 3], qf[s], s0, 0, 0, 0);
-            s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb[s % 3], qf[s], s1, 0, 0, 0);
-            __builtin_amdgcn_sched_barrier(0);  // keep the reads two steps ahead
-        }
-
-        // ---- online softmax (base 2) for head m16 over entries 4g+r, 16+4g+r
-        float sv[8];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            sv[r] = s0[r] * a.scale_log2 + mask[4 * g + r];
-            sv[4 + r] = s1[r] * a.scale_log2 + mask[16 + 4 * g + r];
-        }
-        float cmax = sv[0];
-#pragma unroll
-        for (int i = 1; i < 8; ++i)
-            cmax = fmaxf(cmax, sv[i]);
-        cmax = group4_max(cmax);
-        // Raise the reference maximum (and rescale O and the sum) only when a
-        // score of this wave's heads exceeds it by more than kRescaleSlack.
-        if (__any(cmax > m_run + kRescaleSlack)) {
-            const float m_new = fmaxf(m_run, cmax);
-            const float alpha = __builtin_amdgcn_exp2f(m_run - (m_new == -INFINITY ? 0.f : m_new));
-            l_run *= alpha;
-#pragma unroll
-            for (int dt = 0; dt < 32; ++dt)
-                acc[dt] *= alpha;
-            m_run = m_new;
-        }
-        const float m_use = m_run == -INFINITY ? 0.f : m_run;
-        float p[8], psum = 0.f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            p[i] = __builtin_amdgcn_exp2f(sv[i] - m_use);
-            psum += p[i];
-        }
-        psum = group4_sum(psum);
-        l_run += psum;
-        // k = 8g+i of the PV product is entry 4g+i (i < 4) or 16+4g+i-4
-        const uint4 pw = make_uint4(pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]),
-                                    pack_bf16x2(p[4], p[5]), pack_bf16x2(p[6], p[7]));
-        const bf16x8_t pb = __builtin_bit_cast(bf16x8_t, pw);
-
-        // ---- O^T = alpha * O^T + V^T P^T over the 32 16-dim tiles: the
-        // transposing read hands lane j of group g dim 16dt+j of rows
-        // 4g..4g+3 (then 16+4g..16+4g+3), the A operand of k = 8g..8g+7.
-        // (four steps ahead: one MFMA per step covers less LDS latency than
-        // the two per step of the QK loop)
-        uint2 vlo[5], vhi[5];
-        auto read_v = [&](int dt, uint2& x, uint2& y) {
-            x = read_tr(kt, tr_base + 32 * dt);
-            y = read_tr(kt, tr_base + 32 * dt + 16 * kKRowBytes);
-        };
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            read_v(i, vlo[i], vhi[i]);
-#pragma unroll
-        for (int dt = 0; dt < 32; ++dt) {
-            if (dt + 4 < 32)
-                read_v(dt + 4, vlo[(dt + 4) % 5], vhi[(dt + 4) % 5]);
-            const uint2 lo = vlo[dt % 5], hi = vhi[dt % 5];
-            const bf16x8_t av = __builtin_bit_cast(bf16x8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
-            acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pb, acc[dt], 0, 0, 0);
-            __builtin_amdgcn_sched_barrier(0);
-        }
+        attend_chunk(kt, mask, qf, acc, m_run, l_run, qk_base, tr_base, g, a.scale_log2);
     };
 
     for (int c = c_lo; c < c_mid; ++c) {
@@ -585,28 +622,12 @@ __device__ __forceinline__ void run_segment(const MlaArgs& a, uint8_t (&raw)[2][
     float factor = 0.f;
     if (any)
         factor = a.sink ? 1.f / (l_run + expf(a.sink[head] - m_run * kLn2)) : 1.f / l_run;
-    // O goes out through LDS: each wave stages its 16 head rows (lane (m16,
-    // g) holds dims 16dt+4g..+3 of head m16), then writes whole 1 KiB rows
-    // with 16-byte non-temporal stores.  Rows are 1040 B apart so the staging
-    // writes of 32 lanes hit distinct banks.  The gather buffers and the K
-    // tile are free once every wave has left the chunk loop.
-    constexpr int kStageRow = kHeadDim * 2 + 16;
-    static_assert(2 * 16 * kStageRow <= 2 * kRawBytes && 2 * 16 * kStageRow <= kChunk * kKRowBytes,
-                  "two waves' staging fits the gather buffers and the K tile");
+    // The gather buffers and the K tile are free once every wave has left
+    // the chunk loop.
     __syncthreads();
     uint8_t* stage = wave < 2 ? &raw[0][0] + wave * 16 * kStageRow : kbuf + (wave - 2) * 16 * kStageRow;
-#pragma unroll
-    for (int dt = 0; dt < 32; ++dt) {
-        const f32x4_t v = acc[dt] * factor;
-        *reinterpret_cast<uint2*>(stage + m16 * kStageRow + 32 * dt + 8 * g) =
-            make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
-    }
-    __syncthreads();
-    uint16_t* obase = a.out + b * a.o_sb + sq * a.o_ss + (hb * kBlockHeads + wave * 16) * a.o_sh;
-#pragma unroll
-    for (int h = 0; h < 16; ++h)
-        store16(obase + h * a.o_sh + 8 * lane,
-                *reinterpret_cast<const uint4*>(stage + h * kStageRow + 16 * lane));
+    store_rows(stage, acc, factor, a.out + b * a.o_sb + sq * a.o_ss + (hb * kBlockHeads + wave * 16) * a.o_sh,
+               a.o_sh, m16, g, lane);
     if (g == 0)
         a.lse[b * a.l_sb + head * a.l_sh + sq] = any ? m_run * kLn2 + logf(l_run) : INFINITY;
     __syncthreads();  // the next segment reuses the staging buffers
@@ -720,6 +741,340 @@ sparse_mla_decode_split_kernel(MlaArgs a) {
                 n = b < B ? row_chunks(a, b) : 1;
             } while (b < B && n == 0);
         }
+    }
+}
+
+// ---- Paired grid: one 8-wave workgroup per CU, both halves on one item.
+//
+// For long lists over more items than CUs but at most two per CU, one 4-wave
+// workgroup per item runs a single round that lasts as long as the longest
+// list, and the split grid balances it at the cost of fp32 partial slots
+// (128 KiB per crossing piece) and a combine kernel.  Here each CU takes one
+// or two items and attends each with both halves of an 8-wave workgroup:
+// half h (waves 4h..4h+3; wave hw of a half owns heads 16hw..16hw+15 of the
+// block, as in sparse_mla_decode_kernel) takes every other chunk of the item,
+// with its own gather buffers, K tile and masks, at its own pace
+// (half_barrier).  At the end half 1's O, reference maximum and sum merge into
+// half 0 through LDS, and half 0 writes the output: no partials leave the CU.
+// A CU with two items gets a short one after a long one: items [0, G) go
+// first, one per workgroup, and the workgroup whose first item has rank r in
+// ascending chunk count (ties by index) then takes the item of rank r in
+// descending chunk count among items [G, I), if there is one.
+// Barrier over the four waves of one half of a paired workgroup, on a
+// counter in LDS that only grows: each wave adds 1 once its LDS accesses are
+// done, then polls until the half's four waves have all added for this
+// barrier (`gen` counts the wave's barriers so far, times 4).  Like
+// lds_barrier it orders LDS accesses only: callers wait for their own
+// LDS-DMA gathers first.  The poll is bounded (2^24 polls of 64 clocks,
+// about 0.4 s), so the wait ends even if the counts were ever wrong.  The
+// add and the polls are written as ds instructions with their own lgkmcnt
+// waits: as builtins the compiler would also wait for every outstanding
+// global load before them (it cannot tell the counter from the LDS-DMA
+// targets), q's included.
+constexpr uint32_t kHalfWaves = 4;
+
+__device__ __forceinline__ void half_barrier(uint32_t* ctr, uint32_t& gen) {
+    const uint32_t addr = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint32_t*)ctr;
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(kWaitLds);
+    gen += kHalfWaves;
+    if ((threadIdx.x & 63) == 0)
+        asm volatile("ds_add_u32 %0, %1" ::"v"(addr), "v"(1u) : "memory");
+    for (int i = 0; i < (1 << 24); ++i) {
+        uint32_t v;
+        asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(addr) : "memory");
+        if ((int32_t)(__builtin_amdgcn_readfirstlane(v) - gen) >= 0)
+            break;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    asm volatile("" ::: "memory");
+}
+
+constexpr int kPairThreads = 512;
+constexpr int kPairMaxItems = kPairThreads;  // one top-k length per thread and list goes to LDS
+constexpr int kPairBuckets = 256;            // chunk counts ordered exactly up to this value
+
+__device__ __forceinline__ int list_chunks(int len, int topk) {
+    len = len < 0 ? 0 : (len > topk ? topk : len);
+    return (len + kChunk - 1) / kChunk;
+}
+
+__global__ void __launch_bounds__(kPairThreads, 1)
+sparse_mla_decode_pair_kernel(MlaArgs a) {
+    __shared__ __align__(16) uint8_t lds_raw[2][2][kRawBytes];
+    __shared__ __align__(16) uint8_t lds_kbuf[2][kChunk * kKRowBytes];
+    __shared__ float lds_mask[2][2][kChunk];
+    __shared__ int32_t lds_len[2][kPairMaxItems];  // each item's raw top-k lengths (main, extra)
+    __shared__ int32_t lds_hist[kPairBuckets];     // items [G, I) per clamped chunk count
+    __shared__ int32_t lds_sched[16];              // rank, bucket, rank in bucket, pick, wave partials
+    __shared__ uint32_t lds_hbar[2];               // half_barrier counters
+
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int half = wave >> 2, hw = wave & 3;
+    const int m16 = lane & 15, g = lane >> 4;
+    const int R = a.seq_q * a.head_blocks, I = a.batch * R, G = gridDim.x;
+    uint8_t (&raw)[2][kRawBytes] = lds_raw[half];
+    uint8_t* const kbuf = lds_kbuf[half];
+    float (&mask_lds)[2][kChunk] = lds_mask[half];
+    uint8_t* const raw_tile = &raw[0][0];
+
+    uint32_t gen = 0;  // this wave's half_barrier count so far, times 4
+    if (tid < 2)
+        lds_hbar[tid] = 0;
+    __syncthreads();
+
+    // With more items than workgroups, every item's top-k lengths go to LDS
+    // (LDS DMA, counted with the first chunk's gathers) for the choice of the
+    // second item, and the counters start at zero (visible after the first
+    // barrier).
+    const bool pairs = I > G;
+    if (pairs) {
+        if (tid < kPairBuckets)
+            lds_hist[tid] = 0;
+        if (tid == 0) {
+            lds_sched[0] = 0;
+            lds_sched[3] = -1;
+        }
+        const int i = tid < I ? tid : I - 1;
+#pragma unroll
+        for (int L = 0; L < 2; ++L)
+            if (L < a.num_lists && a.list[L].lengths)
+                __builtin_amdgcn_global_load_lds((global_u32_t*)(a.list[L].lengths + i / R),
+                                                 (lds_u32_t*)&lds_len[L][64 * wave], 4, 0, 0);
+    }
+    auto item_chunks = [&](int i) {
+        const int t0 = a.list[0].topk, t1 = a.list[1].topk;
+        int n = list_chunks(a.list[0].lengths ? lds_len[0][i] : t0, t0);
+        if (a.num_lists > 1)
+            n += list_chunks(a.list[1].lengths ? lds_len[1][i] : t1, t1);
+        return n;
+    };
+
+    int item = blockIdx.x;
+    for (int it = 0; it < 2 && item >= 0; ++it) {
+        const int b = item / R, jr = item - b * R;
+        const int sq = jr / a.head_blocks, hb = jr - sq * a.head_blocks;
+        const int head = hb * kBlockHeads + hw * 16 + m16;
+        const ListView v0 = make_view(a.list[0], true, b, sq);
+        const ListView v1 = make_view(a.list[1], a.num_lists > 1, b, sq);
+        // Half h takes main chunks h, h+2, ... and extra chunks (h + n0) % 2,
+        // +2, ...: K0 + K1 chunks, numbered k = 0.. in its own order.
+        const int n0 = (v0.len + kChunk - 1) / kChunk, n1 = (v1.len + kChunk - 1) / kChunk;
+        const int p = n0 & 1;
+        const int K0 = (n0 + 1 - half) >> 1, K1 = (n1 + 1 - (half ^ p)) >> 1, K = K0 + K1;
+        const bool expanded = v1.expanded != nullptr;
+        const int Kc = expanded ? K0 : K;  // chunks through the raw gather (the rest are bf16 rows)
+        auto view_of = [&](int k) { return select(v0, v1, k >= K0); };
+        auto first_of = [&](int k) { return (k < K0 ? 2 * k + half : 2 * (k - K0) + (half ^ p)) * kChunk; };
+
+        const uint16_t* qrow = a.q + b * a.q_sb + sq * a.q_ss + head * a.q_sh;
+        bf16x8_t qf[kQLoads];
+        auto load_q = [&]() __attribute__((always_inline)) {
+            asm volatile("" ::: "memory");  // q's loads stay behind the gather
+#pragma unroll
+            for (int s = 0; s < kQLoads; ++s)
+                qf[s] = __builtin_bit_cast(bf16x8_t, load16(qrow + 32 * s + 8 * g));
+            asm volatile("" ::: "memory");
+        };
+        int id_next = -1;
+        if (K > 0) {
+            const int id_cur = load_id(view_of(0), first_of(0), hw, lane);
+            if (K > 1)
+                id_next = load_id(view_of(1), first_of(1), hw, lane);
+            if (Kc > 0) {
+                issue_gather(view_of(0), mla_zero_entry, hw, lane, id_cur, raw[0], mask_lds[0]);
+                load_q();
+            } else {
+                issue_rows(v1, hw, lane, id_cur, raw_tile, mask_lds[0]);
+                load_q();
+            }
+        } else {
+            load_q();
+        }
+
+        f32x4_t acc[32];
+#pragma unroll
+        for (int i = 0; i < 32; ++i)
+            acc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        float m_run = -INFINITY, l_run = 0.f;
+        const int qk_base = kbuf_byte(m16, g);
+        const int tr_base = kbuf_byte(4 * g + (m16 >> 2), (m16 & 3) >> 1) + 8 * (m16 & 1);
+        auto attend = [&](const uint8_t* kt, const float* mask) __attribute__((always_inline)) {
+            attend_chunk(kt, mask, qf, acc, m_run, l_run, qk_base, tr_base, g, a.scale_log2);
+        };
+
+        // The half's chunks k = 0 .. K-1 at its own pace: its barriers are
+        // half_barrier's, over its four waves only.  FP8 chunks first (the
+        // main list, and the extra list unless it is expanded), as in
+        // run_segment's chunk loop.
+        for (int k = 0; k < Kc; ++k) {
+            int ln = lane;
+            asm volatile("" : "+v"(ln));
+            if (k == 0)
+                __builtin_amdgcn_s_waitcnt(kWaitAllButQ);
+            else
+                __builtin_amdgcn_s_waitcnt(0);
+            half_barrier(&lds_hbar[half], gen);  // the half's gathers landed; its K tile no longer read
+            dequantize(raw[k & 1], kbuf, hw, ln);
+            half_barrier(&lds_hbar[half], gen);
+            if (k + 1 < Kc)
+                issue_gather(view_of(k + 1), mla_zero_entry, hw, ln, id_next, raw[(k + 1) & 1],
+                             mask_lds[(k + 1) & 1]);
+            else if (k + 1 < K)  // the half's first expanded chunk goes to the raw buffers
+                issue_rows(v1, hw, ln, id_next, raw_tile, mask_lds[(k + 1) & 1]);
+            if (k + 2 < K)
+                id_next = load_id(view_of(k + 2), first_of(k + 2), hw, ln);
+            attend(kbuf, mask_lds[k & 1]);
+        }
+        // Expanded chunks: chunk k is read from `tile` while the next one
+        // streams into `other`, in (raw, K tile) pairs as in run_segment.
+        auto expanded_step = [&](int k, uint8_t* tile, uint8_t* other) __attribute__((always_inline)) {
+            int ln = lane;
+            asm volatile("" : "+v"(ln));
+            __builtin_amdgcn_s_waitcnt(0);       // this wave's rows of chunk k (and chunk k+1's index)
+            half_barrier(&lds_hbar[half], gen);  // the half's rows landed; `other` no longer read
+            if (k + 1 < K)
+                issue_rows(v1, hw, ln, id_next, other, mask_lds[(k + 1) & 1]);
+            if (k + 2 < K)
+                id_next = load_id(v1, first_of(k + 2), hw, ln);
+            attend(tile, mask_lds[k & 1]);
+        };
+        for (int k = Kc; k < K; k += 2) {
+            expanded_step(k, raw_tile, kbuf);
+            if (k + 1 < K)
+                expanded_step(k + 1, kbuf, raw_tile);
+        }
+        __syncthreads();  // both halves done: every K tile and gather buffer is free
+
+        // ---- the second item (first pass only): this item's rank among
+        // items [0, G), then the item of that rank from the top among [G, I)
+        int next = -1;
+        if (it == 0 && pairs) {
+            const int nf = item_chunks(item);
+            int cnt = 0;
+            for (int x0 = 0; x0 < G; x0 += kPairThreads) {
+                const int x = x0 + tid;
+                bool before = false;
+                if (x < G) {
+                    const int nx = item_chunks(x);
+                    before = nx < nf || (nx == nf && x < item);
+                }
+                cnt += __popcll(__ballot(before));
+            }
+            for (int y = G + tid; y < I; y += kPairThreads)
+                atomicAdd(&lds_hist[min(item_chunks(y), kPairBuckets - 1)], 1);
+            if (lane == 0)
+                atomicAdd(&lds_sched[0], cnt);
+            __syncthreads();
+            const int r = lds_sched[0];
+            if (r < I - G) {
+                // descending prefix over the buckets: thread t holds bucket 255 - t
+                int h = 0, incl = 0;
+                const int v = kPairBuckets - 1 - tid;
+                if (tid < kPairBuckets) {
+                    h = lds_hist[v];
+                    incl = h;
+#pragma unroll
+                    for (int d = 1; d < 64; d <<= 1) {
+                        const int t = __shfl_up(incl, d);
+                        if (lane >= d)
+                            incl += t;
+                    }
+                    if (lane == 63)
+                        lds_sched[8 + wave] = incl;
+                }
+                __syncthreads();
+                if (tid < kPairBuckets) {
+                    int excl = incl - h;
+                    for (int w = 0; w < wave; ++w)
+                        excl += lds_sched[8 + w];
+                    if (h > 0 && excl <= r && r < excl + h) {
+                        lds_sched[1] = v;
+                        lds_sched[2] = r - excl;
+                    }
+                }
+                __syncthreads();
+                const int vstar = lds_sched[1], j = lds_sched[2];
+                // the j-th item of [G, I) (in index order) in bucket vstar
+                int base = 0;
+                for (int y0 = G; y0 < I; y0 += kPairThreads) {
+                    const int y = y0 + tid;
+                    const bool m = y < I && min(item_chunks(y), kPairBuckets - 1) == vstar;
+                    const uint64_t bal = __ballot(m);
+                    if (lane == 0)
+                        lds_sched[8 + wave] = __popcll(bal);
+                    __syncthreads();
+                    int before = base, total = base;
+                    for (int w = 0; w < kPairThreads / 64; ++w) {
+                        const int c = lds_sched[8 + w];
+                        before += w < wave ? c : 0;
+                        total += c;
+                    }
+                    if (m && before + __popcll(bal & ((1ull << lane) - 1)) == j)
+                        lds_sched[3] = y;
+                    __syncthreads();
+                    base = total;
+                    if (base > j)
+                        break;
+                }
+                next = __builtin_amdgcn_readfirstlane(lds_sched[3]);
+            }
+        }
+
+        // ---- half 1's O, reference maximum and sum merge into half 0: wave
+        // hw of half 1 leaves them in one of four LDS arrays (33280 bytes each),
+        // lane-major, and wave hw of half 0 (the same heads) reads them.
+        float* mrg = hw == 0   ? reinterpret_cast<float*>(&lds_raw[0][0][0])
+                     : hw == 1 ? reinterpret_cast<float*>(&lds_raw[1][0][0])
+                     : hw == 2 ? reinterpret_cast<float*>(&lds_kbuf[0][0])
+                               : reinterpret_cast<float*>(&lds_kbuf[1][0]);
+        static_assert((32 * 64 * 4 + 128) * 4 <= kChunk * kKRowBytes && kChunk * kKRowBytes <= 2 * kRawBytes,
+                      "a wave's merge data fits each of the four arrays");
+        if (half == 1) {
+#pragma unroll
+            for (int dt = 0; dt < 32; ++dt)
+                *reinterpret_cast<f32x4_t*>(mrg + (dt * 64 + lane) * 4) = acc[dt];
+            mrg[32 * 64 * 4 + lane] = m_run;
+            mrg[32 * 64 * 4 + 64 + lane] = l_run;
+        }
+        __syncthreads();
+        if (half == 0) {
+            const float m1 = mrg[32 * 64 * 4 + lane], l1 = mrg[32 * 64 * 4 + 64 + lane];
+            const float m_new = fmaxf(m_run, m1);
+            const float m_ref = m_new == -INFINITY ? 0.f : m_new;
+            const float w0 = __builtin_amdgcn_exp2f(m_run - m_ref), w1 = __builtin_amdgcn_exp2f(m1 - m_ref);
+            l_run = l_run * w0 + l1 * w1;
+            // eight reads in flight at a time (q's registers are free here)
+#pragma unroll
+            for (int d0 = 0; d0 < 32; d0 += 8) {
+                f32x4_t o1[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+                    o1[i] = *reinterpret_cast<const f32x4_t*>(mrg + ((d0 + i) * 64 + lane) * 4);
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+                    acc[d0 + i] = acc[d0 + i] * w0 + o1[i] * w1;
+            }
+            m_run = m_new;
+        }
+        __syncthreads();  // the merge arrays are free again
+
+        // ---- epilogue (half 0), as in run_segment
+        if (half == 0) {
+            const bool any = l_run > 0.f;
+            float factor = 0.f;
+            if (any)
+                factor = a.sink ? 1.f / (l_run + expf(a.sink[head] - m_run * kLn2)) : 1.f / l_run;
+            uint8_t* stage = hw < 2 ? raw_tile + hw * 16 * kStageRow : kbuf + (hw - 2) * 16 * kStageRow;
+            store_rows(stage, acc, factor,
+                       a.out + b * a.o_sb + sq * a.o_ss + (hb * kBlockHeads + hw * 16) * a.o_sh, a.o_sh, m16,
+                       g, lane);
+            if (g == 0)
+                a.lse[b * a.l_sb + head * a.l_sh + sq] = any ? m_run * kLn2 + logf(l_run) : INFINITY;
+        }
+        __syncthreads();  // the next item reuses the staging buffers
+        item = next;
     }
 }
 
@@ -904,13 +1259,47 @@ constexpr int64_t kSplitMinChunks = 64;
 
 int64_t chunks_of(int64_t topk) { return (topk + kChunk - 1) / kChunk; }
 
-// Workgroups of the split grid: two per CU of the current device.
-int split_grid() {
+// CUs of the current device (256 on MI355X).
+int cu_count() {
     int dev = 0, cus = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
         cus = 256;
-    return 2 * cus;
+    return cus;
+}
+
+// Workgroups of the split grid: two per CU of the current device.
+int split_grid() { return 2 * cu_count(); }
+
+// The grids (fgv_sparse_mla_decode_grid's values).
+enum MlaGrid { kGridOneItem = 0, kGridSplit = 1, kGridPair = 2 };
+
+int64_t items_of(int64_t batch, int64_t seq_q, int64_t num_heads) { return batch * seq_q * (num_heads / kBlockHeads); }
+
+// Lists this long (main + extra chunks) need the split or the paired grid.
+bool long_lists(int64_t batch, int64_t items, int64_t topk, int64_t extra_topk) {
+    return chunks_of(topk) + chunks_of(extra_topk) >= kSplitMinChunks && batch <= kMaxSplitRows &&
+           4 * items <= 0x7fffffffLL;
+}
+
+// Long lists over more items than CUs but at most two per CU (and at most
+// kPairMaxItems) take the paired grid: the items already fill the machine,
+// so the split grid's partial slots and combine buy nothing that pairing a
+// short item with a long one does not.  Short lists stay one workgroup per
+// item: each item then waits on a few chunks only, and two items per CU in
+// flight hide each other's latency (measured: the paired grid costs a few
+// microseconds per item, which only long lists amortise).
+bool pair_fits(int64_t batch, int64_t items, int64_t topk, int64_t extra_topk) {
+    const int64_t cus = cu_count();
+    return long_lists(batch, items, topk, extra_topk) && items > cus && items <= 2 * cus && items <= kPairMaxItems;
+}
+
+// The grid a call runs when it gets the workspace it asks for.
+int mla_grid(int64_t batch, int64_t seq_q, int64_t num_heads, int64_t topk, int64_t extra_topk) {
+    const int64_t items = items_of(batch, seq_q, num_heads);
+    if (pair_fits(batch, items, topk, extra_topk))
+        return kGridPair;
+    return long_lists(batch, items, topk, extra_topk) ? kGridSplit : kGridOneItem;
 }
 
 // An extra list gathered at least this many times per cache entry (counting
@@ -929,8 +1318,8 @@ int64_t expand_bytes(int64_t batch, int64_t seq_q, int64_t num_heads, int64_t ex
     return gathers >= kExpandMinReuse * extra_entries ? extra_entries * 2 * kHeadDim : 0;
 }
 
-int64_t split_bytes(int64_t batch, int64_t topk, int64_t extra_topk) {
-    if (chunks_of(topk) + chunks_of(extra_topk) < kSplitMinChunks || batch > kMaxSplitRows)
+int64_t split_bytes(int64_t batch, int64_t seq_q, int64_t num_heads, int64_t topk, int64_t extra_topk) {
+    if (mla_grid(batch, seq_q, num_heads, topk, extra_topk) != kGridSplit)
         return 0;
     const int64_t slots = 2 * (int64_t)split_grid() * kSlotFloats * 4;
     return slots + ((batch + 1) * 4 + 255) / 256 * 256;
@@ -946,7 +1335,14 @@ extern "C" int64_t fgv_sparse_mla_decode_workspace_bytes(int64_t batch, int64_t 
         extra_num_entries < 0)
         return 0;
     return fgv::expand_bytes(batch, seq_q, num_heads, extra_topk, extra_num_entries) +
-           fgv::split_bytes(batch, topk, extra_topk);
+           fgv::split_bytes(batch, seq_q, num_heads, topk, extra_topk);
+}
+
+extern "C" int fgv_sparse_mla_decode_grid(int64_t batch, int64_t seq_q, int64_t num_heads, int64_t topk,
+                                          int64_t extra_topk) {
+    if (batch <= 0 || seq_q <= 0 || num_heads <= 0 || num_heads % fgv::kBlockHeads || topk < 0 || extra_topk < 0)
+        return -1;
+    return fgv::mla_grid(batch, seq_q, num_heads, topk, extra_topk);
 }
 
 // The argument list of fgv_sparse_mla_decode_model1 up to (not including) the
@@ -1031,7 +1427,7 @@ int mla_decode(FGV_MLA_PARAMS, void* workspace, int64_t workspace_bytes, void* s
     // Workspace: [expanded extra cache][split slots][row prefix sums].  A
     // workspace too small for both drops the expansion first, then the split.
     // (the combine kernel runs four workgroups per item)
-    const int64_t need_split = 4 * items <= 0x7fffffffLL ? split_bytes(batch, topk, extra_k_cache ? extra_topk : 0) : 0;
+    const int64_t need_split = split_bytes(batch, seq_q, num_heads, topk, extra_k_cache ? extra_topk : 0);
     const int64_t need_expand =
         extra_k_cache ? expand_bytes(batch, seq_q, num_heads, extra_topk, a.list[1].num_entries) : 0;
     const int64_t have = workspace ? workspace_bytes : 0;
@@ -1060,6 +1456,11 @@ int mla_decode(FGV_MLA_PARAMS, void* workspace, int64_t workspace_bytes, void* s
         if (rc)
             return rc;
         hipLaunchKernelGGL(sparse_mla_combine_kernel, dim3((unsigned)(4 * items)), dim3(kThreads), 0, st, a);
+        return launch_status();
+    }
+    if (pair_fits(batch, items, topk, extra_k_cache ? extra_topk : 0)) {
+        hipLaunchKernelGGL(sparse_mla_decode_pair_kernel, dim3((unsigned)min(items, (int64_t)cu_count())),
+                           dim3(kPairThreads), 0, st, a);
         return launch_status();
     }
     hipLaunchKernelGGL(sparse_mla_decode_kernel, dim3((unsigned)items), dim3(kThreads), 0, st, a);

@@ -148,6 +148,8 @@ def lib():
     L.fgv_sparse_mla_decode_model1_no_alloc.argtypes = L.fgv_sparse_mla_decode_model1.argtypes[:-3] + [_P]
     L.fgv_sparse_mla_decode_workspace_bytes.restype = ctypes.c_int64
     L.fgv_sparse_mla_decode_workspace_bytes.argtypes = [_I64, _I64, _I64, _I64, _I64, _I64]
+    L.fgv_sparse_mla_decode_grid.restype = ctypes.c_int
+    L.fgv_sparse_mla_decode_grid.argtypes = [_I64, _I64, _I64, _I64, _I64]
     L.fgv_indexer_k_quant_and_cache.restype = ctypes.c_int
     L.fgv_indexer_k_quant_and_cache.argtypes = [
         _P, _I64, ctypes.c_int,  # k, k_stride_token, k_is_fp16
@@ -208,6 +210,7 @@ EXPORTED_SYMBOLS = (
     "fgv_compute_slot_mapping",
     "fgv_sparse_mla_decode_model1",
     "fgv_sparse_mla_decode_workspace_bytes",
+    "fgv_sparse_mla_decode_grid",
     "fgv_sparse_mla_decode_model1_no_alloc",
     "fgv_indexer_k_quant_and_cache",
     "fgv_cp_gather_indexer_k_quant_cache",

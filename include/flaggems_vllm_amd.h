@@ -370,9 +370,10 @@ int fgv_sparse_mla_decode_model1(
  *     dequantised once per call into bf16 rows (1 KiB per entry) that the
  *     attention reads without converting.  The results are the same bits.
  *   - the split schedule: for long lists (topk + extra_topk at least 2048
- *     entries, batch at most 8000 rows) a grid of two workgroups per CU splits
- *     all (row, head block) items' chunks evenly, and a combine kernel merges
- *     the items that cross a split (the reference's split-KV schedule and
+ *     entries, batch at most 8000 rows) over at most one (row, head block)
+ *     item per CU, or over more than two per CU, a grid of two workgroups per
+ *     CU splits all items' chunks evenly, and a combine kernel merges the
+ *     items that cross a split (the reference's split-KV schedule and
  *     combine, ops/flash_mla_with_kvcache_model1.py:1212-1395).  Its size
  *     depends on the current device's CU count.
  * extra_num_entries is extra_num_blocks * extra_page_size (0 without an extra
@@ -382,6 +383,23 @@ int fgv_sparse_mla_decode_model1(
  */
 int64_t fgv_sparse_mla_decode_workspace_bytes(int64_t batch, int64_t seq_q, int64_t num_heads,
                                               int64_t topk, int64_t extra_topk, int64_t extra_num_entries);
+
+/*
+ * Which grid fgv_sparse_mla_decode_model1 runs for these sizes on the current
+ * device, given the workspace fgv_sparse_mla_decode_workspace_bytes asks for:
+ *   0  one workgroup per (row, query position, 64-head block) item
+ *      (sparse_mla_decode_kernel);
+ *   1  the split grid and its combine (sparse_mla_decode_split_kernel,
+ *      sparse_mla_combine_kernel);
+ *   2  the paired grid (sparse_mla_decode_pair_kernel): lists as long as the
+ *      split grid's over more items than CUs but at most two per CU (and at
+ *      most 512); one 8-wave workgroup per CU attends each of its items with
+ *      both halves, a short item after a long one, and writes no partials.
+ * -1 for sizes the decode rejects.  No counterpart in the reference: it is
+ * for benchmarks, profilers and tests that need the kernel's name.
+ */
+int fgv_sparse_mla_decode_grid(int64_t batch, int64_t seq_q, int64_t num_heads, int64_t topk,
+                               int64_t extra_topk);
 
 /* Size of the fixed device scratch of fgv_sparse_mla_decode_model1_no_alloc. */
 #define FGV_MLA_NO_ALLOC_SCRATCH_BYTES (64LL << 20)

@@ -81,7 +81,7 @@ def _assert_within_bound(out, o64, vm, what=""):
     out = out.cpu().double()
     err = (out - o64).abs()
     tol = 2.0 ** -8 * (o64.abs() + vm)
-    bad = err > tol
+    bad = ~(err <= tol)  # NaN (an element never written) counts as outside
     assert not bool(bad.any()), (
         f"{what}: {int(bad.sum())} elements outside 2^-8 (|ref| + max|V|); "
         f"worst excess {float((err - tol).max()):.3e}")
@@ -354,12 +354,16 @@ def test_workspace_query():
     from flaggems_vllm import _native
 
     f = _native.lib().fgv_sparse_mla_decode_workspace_bytes
+    grid = _native.lib().fgv_sparse_mla_decode_grid
+    # (no GPU here: the CU count is taken as MI355X's 256)
     assert f(512, 1, 64, 128, 0, 0) == 0            # decode: one workgroup per item
-    assert f(512, 1, 64, 128, 512, 0) == 0          # 20 chunks: still unsplit
-    big = f(512, 1, 64, 128, 8192, 0)
+    assert f(512, 1, 64, 128, 512, 0) == 0          # 20 chunks: still one per item
+    assert f(512, 1, 64, 128, 8192, 0) == 0         # long lists, two items per CU: paired, not split
+    big = f(200, 1, 64, 128, 8192, 0)               # long lists, at most one item per CU: split
     slot = (64 * 512 + 128) * 4
-    prefix = (513 * 4 + 255) // 256 * 256
+    prefix = (201 * 4 + 255) // 256 * 256
     assert big > 0 and (big - prefix) % (2 * slot) == 0 and big % 256 == 0
+    assert f(600, 1, 64, 128, 8192, 0) > 0          # more than two per CU: split again
     assert f(9000, 1, 64, 128, 8192, 0) == 0        # prefix sums must fit in LDS
     assert f(0, 1, 64, 128, 8192, 0) == 0
     # the benchmark's extra caches: 512 rows x 512 over 32768 entries is 8 per entry
@@ -367,8 +371,21 @@ def test_workspace_query():
     assert f(511, 1, 64, 128, 512, 32768) == 0      # just below 8 per entry
     assert f(256, 1, 128, 128, 512, 32768) == 32768 * 1024   # two head blocks gather twice
     assert f(256, 2, 64, 128, 512, 32768) == 32768 * 1024    # so do two query positions
-    assert f(512, 1, 64, 128, 8192, 1024) == big + 1024 * 1024
-    assert f(512, 1, 64, 128, 8192, 65537) == big   # a copy above 64 MiB is not made
+    assert f(200, 1, 64, 128, 8192, 1024) == big + 1024 * 1024
+    assert f(200, 1, 64, 128, 8192, 65537) == big   # a copy above 64 MiB is not made
+    # the grid each size runs: 0 one item per workgroup, 1 split, 2 paired
+    assert grid(512, 1, 64, 128, 0) == 0            # the benchmark's decode case
+    assert grid(512, 1, 64, 128, 512) == 0          # and its extra512 case
+    assert grid(512, 1, 64, 128, 8192) == 2         # and its extra8192 case
+    assert grid(257, 1, 64, 2048, 0) == 2           # long lists, 257..512 items
+    assert grid(100, 2, 128, 2048, 0) == 2          # 400 items
+    assert grid(256, 1, 64, 2048, 0) == 1           # at most one item per CU: split
+    assert grid(200, 1, 64, 128, 8192) == 1
+    assert grid(600, 1, 64, 128, 8192) == 1         # more than two per CU: split
+    assert grid(300, 1, 64, 128, 1888) == 0         # 4 + 59 chunks: short lists
+    assert grid(300, 1, 64, 128, 1920) == 2         # 4 + 60: long
+    assert grid(9000, 1, 64, 128, 8192) == 0
+    assert grid(8, 1, 60, 128, 0) == -1             # heads not a multiple of 64
 
 
 # --------------------------------------------------------------- GPU ----
@@ -601,13 +618,15 @@ def test_gpu_deterministic():
 
 def _gpu_raw(w, workspace, ws_bytes=None, keep_ws=False):
     """Calls the C ABI directly, with or without a workspace (of the queried
-    size, or `ws_bytes`); with keep_ws the workspace tensor is returned too."""
+    size, or `ws_bytes`); with keep_ws the workspace tensor is returned too.
+    out and lse start as NaN, so an element the call never writes fails the
+    bound."""
     from flaggems_vllm import _native
 
     d = w.to(DEV)
     B, SQ, HQ, _ = d.q.shape
-    out = torch.empty(B, SQ, HQ, 512, dtype=torch.bfloat16, device=DEV)
-    lse = torch.empty(B, HQ, SQ, dtype=torch.float32, device=DEV)
+    out = torch.full((B, SQ, HQ, 512), float("nan"), dtype=torch.bfloat16, device=DEV)
+    lse = torch.full((B, HQ, SQ), float("nan"), dtype=torch.float32, device=DEV)
     L = _native.lib()
     etopk = d.extra_indices.shape[-1] if d.extra_indices is not None else 0
     ek, ei = d.extra_k_cache, d.extra_indices
@@ -663,7 +682,7 @@ def test_gpu_split_grid_against_oracle(case):
     fin = torch.isfinite(l64)
     assert torch.equal(torch.isfinite(lse), fin)
     assert torch.allclose(lse.double()[fin], l64[fin], rtol=1e-5, atol=1e-5)
-    # the same call without a workspace (one workgroup per item) agrees
+    # the same call without a workspace (the paired grid) agrees
     out1, lse1, _ = _gpu_raw(w, workspace=False)
     _assert_within_bound(out1, o64, _vmax(w), case + " unsplit")
     assert torch.allclose(lse1.double()[fin], lse.double()[fin], rtol=1e-6, atol=1e-6)
@@ -729,3 +748,110 @@ def test_gpu_split_grid_expanded_matches_split_alone():
     out_s, lse_s, _ = _gpu_raw(w, workspace=True, ws_bytes=split_only)
     assert torch.equal(out_x.view(torch.int16), out_s.view(torch.int16))
     assert torch.equal(lse_x, lse_s)
+
+
+# ------------------------------------------------------ GPU: paired grid ----
+
+def _grid(w):
+    from flaggems_vllm import _native
+
+    B, SQ, HQ, _ = w.q.shape
+    etopk = w.extra_indices.shape[-1] if w.extra_indices is not None else 0
+    return _native.lib().fgv_sparse_mla_decode_grid(B, SQ, HQ, w.indices.shape[-1], etopk)
+
+
+def _lengths(n, hi, seed):
+    return torch.randint(0, hi + 1, (n,), generator=torch.Generator().manual_seed(seed), dtype=torch.int32)
+
+
+def _pair_case(name):
+    """Calls the paired grid takes (long lists, 256 CUs < items <= 512): the
+    workgroups whose first item is among the shortest take a second one.  The
+    lists' capacity (top-k) is long; most rows attend a few hundred entries
+    and a few the whole list, so the binary64 oracle stays quick."""
+    if name == "pairs":       # 300 items: 44 workgroups take a second item
+        w = W.make_mla_workload(batch=300, topk=2048, num_pages=64, seed=51, q_scale=0.1)
+        w.topk_length = _lengths(300, 160, 1)
+        w.topk_length[::7] = 0       # rows that attend nothing
+        w.topk_length[1::5] = 128    # many equal chunk counts (ties go by item index)
+        w.topk_length[[3, 50, 299]] = torch.tensor([2048, 2000, 1999], dtype=torch.int32)
+        return w
+    if name == "full":        # 512 items: every workgroup takes two
+        w = W.make_mla_workload(batch=512, topk=2048, num_pages=64, seed=53, q_scale=0.1)
+        w.topk_length = _lengths(512, 256, 2)
+        w.topk_length[[0, 255, 256, 511]] = 2048
+        return w
+    if name == "extra":       # an extra list, odd main chunk counts, empty extra rows
+        w = W.make_mla_workload(batch=300, topk=128, num_pages=16, extra_topk=2048, extra_page=64,
+                                extra_pages=16, seed=55, q_scale=0.1)
+        w.extra_topk_length = _lengths(300, 300, 3)
+        w.extra_topk_length[::9] = 0
+        w.extra_topk_length[[7, 123]] = 2048
+        return w
+    if name == "h128_sq2":    # 100 rows x 2 query positions x 2 head blocks = 400 items
+        w = W.make_mla_workload(batch=100, topk=2048, num_pages=32, heads=128, seq_q=2, seed=57,
+                                q_scale=0.1)
+        w.topk_length = _lengths(100, 200, 4)
+        return w
+    if name == "clamped":     # chunk counts past the 255 ordered exactly, and ties among them
+        w = W.make_mla_workload(batch=260, topk=8192, num_pages=160, seed=59, q_scale=0.1)
+        lens = _lengths(260, 96, 3)
+        lens[[0, 40, 41, 200, 259]] = torch.tensor([8192, 8100, 8192, 8190, 8161], dtype=torch.int32)
+        w.topk_length = lens
+        return w
+    raise KeyError(name)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", ["pairs", "full", "extra", "h128_sq2", "clamped"])
+def test_gpu_pair_grid_against_oracle(case):
+    print(f"\n[case] sparse MLA paired grid {case}", flush=True)
+    w = _pair_case(case)
+    assert _grid(w) == 2, "the case must take the paired grid"
+    out, lse, _ = _gpu_raw(w, workspace=False)  # (the extra list dequantised per chunk)
+    o64, l64 = _oracle(w)
+    _assert_within_bound(out, o64, _vmax(w), case)
+    fin = torch.isfinite(l64)
+    assert torch.equal(torch.isfinite(lse), fin) and bool((lse[~fin] > 0).all())
+    assert torch.allclose(lse.double()[fin], l64[fin], rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.gpu
+def test_gpu_pair_grid_expanded_bit_exact():
+    """Paired grid with the extra cache expanded once into bf16 rows (a
+    workspace) and dequantised per chunk (none): the same bits, within the
+    bound."""
+    from flaggems_vllm import _native
+
+    print("\n[case] sparse MLA paired grid, expanded vs not", flush=True)
+    w = _pair_case("extra")
+    B, SQ, HQ, _ = w.q.shape
+    need = _native.lib().fgv_sparse_mla_decode_workspace_bytes(B, SQ, HQ, w.indices.shape[-1],
+                                                               w.extra_indices.shape[-1], 1024)
+    assert need == 1024 * 1024 and _grid(w) == 2
+    out_x, lse_x, _ = _gpu_raw(w, workspace=True, ws_bytes=need)
+    out_d, lse_d, _ = _gpu_raw(w, workspace=False)
+    assert torch.equal(out_x.view(torch.int16), out_d.view(torch.int16))
+    assert torch.equal(lse_x, lse_d)
+    o64, _ = _oracle(w)
+    _assert_within_bound(out_x, o64, _vmax(w), "paired expanded")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", ["main", "expanded"])
+def test_gpu_one_item_grid_against_oracle(case):
+    """More than 512 items: one workgroup per item."""
+    print(f"\n[case] sparse MLA one-item grid {case}", flush=True)
+    if case == "main":
+        w = W.make_mla_workload(batch=520, topk=64, num_pages=64, seed=61, q_scale=0.1)
+    else:
+        w = W.make_mla_workload(batch=520, topk=64, num_pages=16, extra_topk=128, extra_page=64, extra_pages=8,
+                                seed=63, q_scale=0.1)
+    assert _grid(w) == 0
+    out, lse, nbytes = _gpu_raw(w, workspace=True)
+    assert nbytes == (512 * 1024 if case == "expanded" else 0)
+    o64, l64 = _oracle(w)
+    _assert_within_bound(out, o64, _vmax(w), case)
+    fin = torch.isfinite(l64)
+    assert torch.equal(torch.isfinite(lse), fin)
+    assert torch.allclose(lse.double()[fin], l64[fin], rtol=1e-5, atol=1e-5)
