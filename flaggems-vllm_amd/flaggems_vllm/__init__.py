@@ -6,7 +6,8 @@ their compatibility aliases ``ops_deepseek_v4_qnorm_rope_kv_rope_quant_insert`` 
 ``ops_inv_rope_fp8_quant``, ``SUPPORTED_FP8_DTYPE``, ``device`` and ``vendor_name``;
 and the ops either side of that path (src/flaggems_vllm/ops/__init__.py): the
 K-cache gather, q/kv RMSNorm, the sparse indexer (q quant, key cache and
-logits), slot mapping and sparse MLA decode.  Every op runs hand-written HIP kernels through the C ABI declared in
+logits), the index rows sparse attention reads (global top-k indices, top-k
+plus sliding window), slot mapping and sparse MLA decode.  Every op runs hand-written HIP kernels through the C ABI declared in
 include/flaggems_vllm_amd.h; there is no Triton, no vendor dispatch and no
 CPU fallback.
 """
@@ -14,6 +15,8 @@ from . import ops  # noqa: F401
 from .ops import (  # noqa: F401
     SUPPORTED_FP8_DTYPE,
     FlashMLASchedMeta,
+    combine_topk_swa_indices,
+    compute_global_topk_indices_and_lens,
     compute_slot_mapping_parallel,
     cp_gather_indexer_k_quant_cache,
     dequantize_and_gather_k_cache,
@@ -39,6 +42,8 @@ ops_inv_rope_fp8_quant = fused_inv_rope_fp8_quant
 
 __all__ = [
     "FlashMLASchedMeta",
+    "combine_topk_swa_indices",
+    "compute_global_topk_indices_and_lens",
     "compute_slot_mapping_parallel",
     "cp_gather_indexer_k_quant_cache",
     "flash_mla_with_kvcache",

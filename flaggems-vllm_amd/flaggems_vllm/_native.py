@@ -150,6 +150,23 @@ def lib():
     L.fgv_sparse_mla_decode_workspace_bytes.argtypes = [_I64, _I64, _I64, _I64, _I64, _I64]
     L.fgv_sparse_mla_decode_grid.restype = ctypes.c_int
     L.fgv_sparse_mla_decode_grid.argtypes = [_I64, _I64, _I64, _I64, _I64]
+    L.fgv_compute_global_topk_indices_and_lens.restype = ctypes.c_int
+    L.fgv_compute_global_topk_indices_and_lens.argtypes = [
+        _P, _I64, _I64, _I64, _I64,  # topk_indices, strides, num_tokens, topk
+        _P, _P, _I64, _I64, _I64, _I64, _P,  # req, block_table, stride, num_reqs, blocks/req, block_size, valid
+        _P, _I64, _I64, _P,  # global_indices, strides, lens
+        _P,  # stream
+    ]
+    L.fgv_combine_topk_swa_width.restype = ctypes.c_int64
+    L.fgv_combine_topk_swa_width.argtypes = [_I64, _I64]
+    L.fgv_combine_topk_swa_indices.restype = ctypes.c_int
+    L.fgv_combine_topk_swa_indices.argtypes = [
+        _P, _I64, _I64, _I64, _I64,  # topk_indices, strides, num_tokens, columns
+        _P, _P, _P, _I64,  # query_start_loc, seq_lens, gather_lens, num_reqs
+        _I64, _I64, _I64, _I64, _I64,  # window, compress_ratio, topk, M, N
+        _P, _I64, _I64, _P,  # combined, strides, lens
+        _P,  # stream
+    ]
     L.fgv_indexer_k_quant_and_cache.restype = ctypes.c_int
     L.fgv_indexer_k_quant_and_cache.argtypes = [
         _P, _I64, ctypes.c_int,  # k, k_stride_token, k_is_fp16
@@ -211,6 +228,9 @@ EXPORTED_SYMBOLS = (
     "fgv_sparse_mla_decode_model1",
     "fgv_sparse_mla_decode_workspace_bytes",
     "fgv_sparse_mla_decode_grid",
+    "fgv_compute_global_topk_indices_and_lens",
+    "fgv_combine_topk_swa_width",
+    "fgv_combine_topk_swa_indices",
     "fgv_sparse_mla_decode_model1_no_alloc",
     "fgv_indexer_k_quant_and_cache",
     "fgv_cp_gather_indexer_k_quant_cache",

@@ -6,7 +6,8 @@ These registrations expose the same ops to torch.compile and graph capture as
 opaque custom ops: the schemas declare what each op writes, namely ``q`` and
 ``k_cache`` for the main op (alias-annotated ``Tensor(a0!) q``, ``Tensor(a2!) k_cache``), ``out``
 for the gather, ``slot_mapping`` for the slot mapping, ``kv_cache`` for the
-indexer key insert and ``k_fp8`` / ``k_fp8_scale`` for its gather.  The fake (meta)
+indexer key insert and ``k_fp8`` / ``k_fp8_scale`` for its gather (the index-row ops write only what
+they return).  The fake (meta)
 implementations give the output shapes and strides the real ops return.
 Each registered op calls the same wrapper, so argument checks and errors are
 the wrapper's.
@@ -21,6 +22,8 @@ from typing import List, Optional, Tuple
 import torch
 
 from .ops import (
+    combine_topk_swa_indices,
+    compute_global_topk_indices_and_lens,
     compute_slot_mapping_parallel,
     cp_gather_indexer_k_quant_cache,
     dequantize_and_gather_k_cache,
@@ -166,6 +169,35 @@ def _(k_cache, k_fp8, k_fp8_scale, block_table, cu_seqlen):
     return None
 
 
+@_op("compute_global_topk_indices_and_lens")
+def _global_topk_indices(topk_indices: torch.Tensor, token_to_req_indices: torch.Tensor, block_table: torch.Tensor,
+                         block_size: int,
+                         is_valid_token: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+    return compute_global_topk_indices_and_lens(topk_indices, token_to_req_indices, block_table, block_size,
+                                                is_valid_token)
+
+
+@_global_topk_indices.register_fake
+def _(topk_indices, token_to_req_indices, block_table, block_size, is_valid_token=None):
+    return (torch.empty_like(topk_indices, dtype=torch.int32),
+            topk_indices.new_empty((topk_indices.shape[0],), dtype=torch.int32))
+
+
+@_op("combine_topk_swa_indices")
+def _combine_topk_swa(topk_indices: torch.Tensor, query_start_loc: torch.Tensor, seq_lens: torch.Tensor,
+                      gather_lens: torch.Tensor, window_size: int, compress_ratio: int, topk: int, M: int,
+                      N: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    return combine_topk_swa_indices(topk_indices, query_start_loc, seq_lens, gather_lens, window_size,
+                                    compress_ratio, topk, M, N)
+
+
+@_combine_topk_swa.register_fake
+def _(topk_indices, query_start_loc, seq_lens, gather_lens, window_size, compress_ratio, topk, M, N):
+    width = (topk + window_size + 127) // 128 * 128
+    t = topk_indices.shape[0]
+    return topk_indices.new_empty((t, width), dtype=torch.int32), topk_indices.new_empty((t,), dtype=torch.int32)
+
+
 REGISTERED: List[str] = [
     "fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert",
     "fused_inv_rope_fp8_quant",
@@ -175,4 +207,6 @@ REGISTERED: List[str] = [
     "compute_slot_mapping_parallel",
     "indexer_k_quant_and_cache",
     "cp_gather_indexer_k_quant_cache",
+    "compute_global_topk_indices_and_lens",
+    "combine_topk_swa_indices",
 ]

@@ -1,5 +1,7 @@
-"""DeepSeek-V4 attention pre-processing ops (reference: src/flaggems_vllm/ops/__init__.py:23-24, 34-38, 55, 58-59, 61-65, 78)."""
+"""DeepSeek-V4 attention pre-processing ops (reference: src/flaggems_vllm/ops/__init__.py:23-38, 55, 58-65, 78, 142-143)."""
 from .cp_gather_indexer_k_quant_cache import cp_gather_indexer_k_quant_cache
+from .deepseek_v4_attention_combine_topk_swa_indices import combine_topk_swa_indices
+from .deepseek_v4_attention_compute_global_topk_indices_and_lens import compute_global_topk_indices_and_lens
 from .deepseek_v4_attention_dequantize_and_gather_k_cache import dequantize_and_gather_k_cache
 from .deepseek_v4_attention_fused_q_kv_rmsnorm import fused_q_kv_rmsnorm
 from .fp8_fp4_mqa_logits import fp8_fp4_mqa_logits
@@ -15,6 +17,8 @@ from .slot_mapping import compute_slot_mapping_parallel
 
 __all__ = [
     "FlashMLASchedMeta",
+    "combine_topk_swa_indices",
+    "compute_global_topk_indices_and_lens",
     "compute_slot_mapping_parallel",
     "cp_gather_indexer_k_quant_cache",
     "flash_mla_with_kvcache",

@@ -441,6 +441,58 @@ int fgv_sparse_mla_decode_model1_no_alloc(
     int64_t batch, int64_t seq_q, int64_t num_heads,
     void* stream);
 
+/*
+ * Request-local top-k indices -> global cache slots, and the row lengths.
+ *
+ * Replaces flaggems_vllm.compute_global_topk_indices_and_lens
+ * (reference: src/flaggems_vllm/ops/deepseek_v4_attention_compute_global_topk_indices_and_lens.py:122-160,
+ * kernel :46-119).  For token t with request r = token_to_req_indices[t] and
+ * each column i < topk with l = topk_indices[t, i]:
+ *   global_indices[t, i] = block_table[r, l / block_size] * block_size + l % block_size   (l >= 0)
+ *                        = -1                                                           (l < 0)
+ *   lens[t] = #{i : l >= 0} if is_valid_token[t] != 0 (or is_valid_token is NULL), else 0.
+ * int32 arithmetic with wrap-around, as the reference computes it.  A block
+ * outside the block table ([num_reqs, blocks_per_req] with row stride
+ * block_table_stride, all in elements) gives -1 and still counts; the
+ * reference reads past the row there.  Strides are in elements.
+ */
+int fgv_compute_global_topk_indices_and_lens(
+    const int32_t* topk_indices, int64_t topk_stride0, int64_t topk_stride1, int64_t num_tokens, int64_t topk,
+    const int32_t* token_to_req_indices, const int32_t* block_table, int64_t block_table_stride,
+    int64_t num_reqs, int64_t blocks_per_req, int64_t block_size, const int32_t* is_valid_token,
+    int32_t* global_indices, int64_t out_stride0, int64_t out_stride1, int32_t* lens, void* stream);
+
+/*
+ * Row width of combine_topk_swa_indices' output: topk + window_size rounded
+ * up to a multiple of 128 (the reference's _SPARSE_PREFILL_TOPK_ALIGNMENT),
+ * or -1 for negative arguments.
+ */
+int64_t fgv_combine_topk_swa_width(int64_t topk, int64_t window_size);
+
+/*
+ * Top-k indices and sliding-window rows combined into one index row per token.
+ *
+ * Replaces flaggems_vllm.combine_topk_swa_indices
+ * (reference: src/flaggems_vllm/ops/deepseek_v4_attention_combine_topk_swa_indices.py:105-150,
+ * kernel :30-102).  For request b (query_start_loc[b] - query_start_loc[0] <=
+ * t < query_start_loc[b + 1] - query_start_loc[0]) with q = its query length,
+ * pos = seq_lens[b] - q + (t - start), gather_start = seq_lens[b] - gather_lens[b]:
+ *   topk_len = min((pos + 1) / compress_ratio, topk), swa_len = min(pos + 1, window_size)
+ *   combined[t, j] = topk_indices[t, j] + M * b                               j < topk_len
+ *   combined[t, topk_len + j] = M * b + N + j + pos - swa_len + 1 - gather_start   j < swa_len
+ *   combined[t, j] = -1 for the rest of the fgv_combine_topk_swa_width columns
+ *   lens[t] = topk_len + swa_len
+ * int32 arithmetic with wrap-around and truncating division, as the
+ * reference computes it.  Rows of tokens outside every request are not
+ * written.  topk must not exceed topk_cols (the reference would read past
+ * the row).  Strides are in elements.
+ */
+int fgv_combine_topk_swa_indices(
+    const int32_t* topk_indices, int64_t topk_stride0, int64_t topk_stride1, int64_t num_tokens,
+    int64_t topk_cols, const int32_t* query_start_loc, const int32_t* seq_lens, const int32_t* gather_lens,
+    int64_t num_reqs, int64_t window_size, int64_t compress_ratio, int64_t topk, int64_t M, int64_t N,
+    int32_t* combined, int64_t out_stride0, int64_t out_stride1, int32_t* lens, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -153,6 +153,12 @@ def lib():
             _P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _I64, _P,
             _P, _I64, _I64, _I64, _P, _I64, _P, _P, ctypes.c_double, _P, _P,
         ]
+        L.oracle_compute_global_topk_indices.restype = None
+        L.oracle_compute_global_topk_indices.argtypes = [
+            _P, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _P]
+        L.oracle_combine_topk_swa_indices.restype = None
+        L.oracle_combine_topk_swa_indices.argtypes = [
+            _P, _I64, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P]
         _lib = L
     return _lib
 
@@ -507,3 +513,38 @@ def paged_mqa_logits(q, kv_cache, weights, context_lens, block_tables, max_model
         ctx.data_ptr(), per_len, bt.data_ptr(), bt.stride(0), bt.shape[1], per_table, H, D, int(max_model_len),
         float("-inf") if clean_logits else 0.0, r.data_ptr(), r.numel(), out.data_ptr(), bound.data_ptr())
     return out, bound
+
+
+def compute_global_topk_indices_and_lens(topk_indices, token_to_req_indices, block_table, block_size,
+                                         is_valid_token=None):
+    """CPU restatement: (global_indices, lens) as int32 CPU tensors."""
+    local = _cpu(topk_indices, torch.int32)
+    req = _cpu(token_to_req_indices, torch.int32).contiguous()
+    bt = _cpu(block_table, torch.int32)
+    valid = _cpu(is_valid_token, torch.int32).contiguous() if is_valid_token is not None else None
+    T, K = local.shape
+    out = torch.empty((T, K), dtype=torch.int32)
+    lens = torch.empty((T,), dtype=torch.int32)
+    lib().oracle_compute_global_topk_indices(
+        local.data_ptr(), local.stride(0), local.stride(1), T, K, req.data_ptr(), bt.data_ptr(), bt.stride(0),
+        bt.shape[0], bt.shape[1], int(block_size), valid.data_ptr() if valid is not None else None,
+        out.data_ptr(), out.stride(0), out.stride(1), lens.data_ptr())
+    return out, lens
+
+
+def combine_topk_swa_indices(topk_indices, query_start_loc, seq_lens, gather_lens, window_size, compress_ratio,
+                             topk, M, N, fill=-7):
+    """CPU restatement: (combined, lens); rows the op leaves unwritten keep
+    ``fill`` (lens: ``fill`` too)."""
+    t = _cpu(topk_indices, torch.int32)
+    qsl = _cpu(query_start_loc, torch.int32).contiguous()
+    seq = _cpu(seq_lens, torch.int32).contiguous()
+    gat = _cpu(gather_lens, torch.int32).contiguous()
+    width = (topk + window_size + 127) // 128 * 128
+    out = torch.full((t.shape[0], width), fill, dtype=torch.int32)
+    lens = torch.full((t.shape[0],), fill, dtype=torch.int32)
+    lib().oracle_combine_topk_swa_indices(
+        t.data_ptr(), t.stride(0), t.stride(1), qsl.data_ptr(), seq.data_ptr(), gat.data_ptr(), seq.shape[0],
+        int(window_size), int(compress_ratio), int(topk), int(M), int(N), out.data_ptr(), out.stride(0),
+        out.stride(1), width, lens.data_ptr())
+    return out, lens

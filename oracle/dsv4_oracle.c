@@ -37,6 +37,12 @@
  *                    src/flaggems_vllm/ops/fp8_fp4_paged_mqa_logits.py:68-225, 410-579
  *     reference test tests/test_fp8_fp4_mqa_logits.py:40-66 (reference_fp4_mqa_logits)
  *                    tests/test_fp8_fp4_paged_mqa_logits.py:196-249
+ *   oracle_compute_global_topk_indices
+ *     reference op   src/flaggems_vllm/ops/deepseek_v4_attention_compute_global_topk_indices_and_lens.py:46-160
+ *     reference test tests/test_deepseek_v4_attention_compute_global_topk_indices_and_lens.py:78-98
+ *   oracle_combine_topk_swa_indices
+ *     reference op   src/flaggems_vllm/ops/deepseek_v4_attention_combine_topk_swa_indices.py:30-150
+ *     reference test tests/test_deepseek_v4_attention_combine_topk_swa_indices.py:119-141
  *   oracle_sparse_mla_decode_model1 (binary64 attention, see its comment)
  *     reference op   src/flaggems_vllm/ops/flash_mla_with_kvcache.py:489-688, 852-1073
  *                    src/flaggems_vllm/ops/flash_mla_with_kvcache_model1.py:389-470, 699-720
@@ -932,5 +938,75 @@ void oracle_paged_mqa_logits(const uint8_t* q, int64_t q_sr, int64_t q_sh, const
                              &bound[r * max_model_len + n]);
         }
         free(qd);
+    }
+}
+
+/*
+ * Request-local top-k indices -> global cache slots, token by token and column
+ * by column as the reference test's loop walks them (test :78-98): local
+ * l >= 0 maps to block_table[req][l / bs] * bs + l % bs (int32 with
+ * wrap-around, like the reference's Triton arithmetic), l < 0 to -1; the
+ * length counts l >= 0, or is 0 for a token marked invalid (valid NULL: all
+ * valid).  A block outside the table ([num_reqs][bpr], row stride bt_stride)
+ * gives -1 and still counts.
+ */
+void oracle_compute_global_topk_indices(const int32_t* local, int64_t ls0, int64_t ls1, int64_t T, int64_t K,
+                                        const int32_t* req, const int32_t* bt, int64_t bt_stride, int64_t num_reqs,
+                                        int64_t bpr, int64_t bs, const int32_t* valid, int32_t* out, int64_t os0,
+                                        int64_t os1, int32_t* lens)
+{
+    const int64_t span = (num_reqs > 0 && bpr > 0) ? (num_reqs - 1) * bt_stride + bpr : 0;
+    for (int64_t t = 0; t < T; ++t) {
+        int32_t count = 0;
+        for (int64_t i = 0; i < K; ++i) {
+            const int32_t l = local[t * ls0 + i * ls1];
+            int32_t slot = -1;
+            if (l >= 0) {
+                ++count;
+                const int64_t blk = l / bs, off = l % bs;
+                const int64_t f = (int64_t)req[t] * bt_stride + blk;
+                if (f >= 0 && f < span)
+                    slot = (int32_t)((uint32_t)bt[f] * (uint32_t)bs + (uint32_t)off);
+            }
+            out[t * os0 + i * os1] = slot;
+        }
+        lens[t] = (!valid || valid[t] != 0) ? count : 0;
+    }
+}
+
+/*
+ * Top-k plus sliding-window index rows, request by request and token by
+ * token as the reference test's loop builds them (test :119-141): the row is
+ * [topk_indices[t, :topk_len] + M*b, the swa_len window rows, -1 ...] over
+ * `width` columns, lens[t] = topk_len + swa_len, with
+ * topk_len = min((pos + 1) / ratio, topk) (truncating division, as Triton
+ * divides int32) and swa_len = min(pos + 1, window).  Rows of tokens outside
+ * every request are not written.
+ */
+void oracle_combine_topk_swa_indices(const int32_t* topk_idx, int64_t ts0, int64_t ts1, const int32_t* qsl,
+                                     const int32_t* seq_lens, const int32_t* gather_lens, int64_t num_reqs,
+                                     int64_t window, int64_t ratio, int64_t topk, int64_t M, int64_t N,
+                                     int32_t* out, int64_t os0, int64_t os1, int64_t width, int32_t* lens)
+{
+    for (int64_t b = 0; b < num_reqs; ++b) {
+        const int64_t start = (int64_t)qsl[b] - qsl[0], end = (int64_t)qsl[b + 1] - qsl[0];
+        const int64_t seq = seq_lens[b];
+        const int64_t start_pos = seq - (end - start), gather_start = seq - gather_lens[b];
+        const uint32_t row_off = (uint32_t)((int32_t)M * (int32_t)b);
+        for (int64_t t = start; t < end; ++t) {
+            const int32_t pos = (int32_t)(start_pos + (t - start));
+            int32_t topk_len = (pos + 1) / (int32_t)ratio;
+            if (topk_len > topk)
+                topk_len = (int32_t)topk;
+            const int32_t swa_len = pos + 1 < window ? pos + 1 : (int32_t)window;
+            for (int64_t c = 0; c < width; ++c)
+                out[t * os0 + c * os1] = -1;
+            for (int32_t j = 0; j < topk_len; ++j)
+                out[t * os0 + j * os1] = (int32_t)((uint32_t)topk_idx[t * ts0 + j * ts1] + row_off);
+            for (int32_t j = 0; j < swa_len; ++j)
+                out[t * os0 + (topk_len + j) * os1] =
+                    (int32_t)(row_off + (uint32_t)(int32_t)N + (uint32_t)(j + pos - swa_len + 1 - (int32_t)gather_start));
+            lens[t] = topk_len + swa_len;
+        }
     }
 }

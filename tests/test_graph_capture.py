@@ -120,14 +120,24 @@ def test_graph_rmsnorm_indexer_gather_slots():
                          outputs=lambda _: (slots,))
 
 
-@pytest.mark.parametrize("extra", [False, True])
+@pytest.mark.parametrize("extra", [False, True, "paired"])
 def test_graph_sparse_mla(extra):
     """Decode over the main list; with `extra`, a long extra list that takes
     the expanded cache and the split grid + combine kernel (workspace
-    allocated by the wrapper inside the capture)."""
+    allocated by the wrapper inside the capture); "paired": long lists over
+    300 items, the paired grid."""
     _say(f"graph: sparse MLA extra={extra}")
-    kw = dict(extra_topk=2048, extra_page=2, extra_pages=256) if extra else {}
-    w = W.make_mla_workload(batch=8, topk=128, num_pages=16, seed=9, q_scale=0.1, **kw).to(DEV)
+    if extra == "paired":
+        w = W.make_mla_workload(batch=300, topk=2048, num_pages=16, seed=9, q_scale=0.1)
+        w.topk_length = torch.randint(0, 200, (300,), generator=torch.Generator().manual_seed(1), dtype=torch.int32)
+        w = w.to(DEV)
+        from flaggems_vllm import _native
+
+        assert _native.lib().fgv_sparse_mla_decode_grid(300, 1, 64, 2048, 0) == 2
+        extra = False
+    else:
+        kw = dict(extra_topk=2048, extra_page=2, extra_pages=256) if extra else {}
+        w = W.make_mla_workload(batch=8, topk=128, num_pages=16, seed=9, q_scale=0.1, **kw).to(DEV)
     meta, _ = flaggems_vllm.get_mla_metadata()
     B, SQ, HQ = w.q.shape[:3]
     if extra:
@@ -142,3 +152,20 @@ def test_graph_sparse_mla(extra):
     replay_matches_eager(lambda: out.fill_(3.0), lambda: flaggems_vllm.flash_mla_with_kvcache(
         w.q, w.k_cache, None, None, 512, meta, is_fp8_kvcache=True, indices=w.indices, out=out,
         **w.kwargs()))
+
+
+def test_graph_topk_index_ops():
+    """compute_global_topk_indices_and_lens and combine_topk_swa_indices (their
+    outputs allocated by the wrappers inside the capture)."""
+    _say("graph: global top-k indices, combine top-k + window")
+    g = torch.Generator().manual_seed(4)
+    local = torch.randint(-1, 64 * 20, (300, 128), generator=g, dtype=torch.int32).to(DEV)
+    req = torch.randint(0, 4, (300,), generator=g, dtype=torch.int32).to(DEV)
+    bt = torch.randint(0, 5000, (4, 20), generator=g, dtype=torch.int32).to(DEV)
+    replay_matches_eager(lambda: None, lambda: flaggems_vllm.compute_global_topk_indices_and_lens(
+        local, req, bt, 64))
+    qsl = torch.tensor([0, 100, 300], dtype=torch.int32, device=DEV)
+    seq = torch.tensor([4000, 900], dtype=torch.int32, device=DEV)
+    gat = torch.tensor([1000, 500], dtype=torch.int32, device=DEV)
+    replay_matches_eager(lambda: None, lambda: flaggems_vllm.combine_topk_swa_indices(
+        local, qsl, seq, gat, 128, 4, 128, 45056, 40960))

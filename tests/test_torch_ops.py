@@ -29,6 +29,8 @@ WRITES = {
     "compute_slot_mapping_parallel": {"slot_mapping"},
     "indexer_k_quant_and_cache": {"kv_cache"},
     "cp_gather_indexer_k_quant_cache": {"k_fp8", "k_fp8_scale"},
+    "compute_global_topk_indices_and_lens": set(),
+    "combine_topk_swa_indices": set(),
 }
 
 
@@ -186,3 +188,30 @@ def test_gpu_indexer_opcheck(fp4, D):
         assert oq.shape == qbig.shape and oq.stride() == qbig.stride()
     torch.library.opcheck(_op("fused_indexer_q_rope_quant"), args,
                           test_utils=("test_schema", "test_faketensor"))
+
+
+@pytest.mark.gpu
+def test_gpu_topk_index_ops_opcheck():
+    """The index-row ops through torch.ops: same outputs as the functions, and
+    the fakes' shapes, dtypes and strides equal the real outputs'."""
+    _say("torch.ops global top-k indices / combine top-k + window opcheck")
+    g = torch.Generator().manual_seed(2)
+    local = torch.randint(-1, 64 * 4, (37, 24), generator=g, dtype=torch.int32).to(DEV)
+    req = torch.randint(0, 3, (37,), generator=g, dtype=torch.int32).to(DEV)
+    bt = torch.randint(0, 999, (3, 4), generator=g, dtype=torch.int32).to(DEV)
+    valid = torch.randint(0, 2, (37,), generator=g, dtype=torch.int32).to(DEV)
+    a = (local, req, bt, 64, valid)
+    f = flaggems_vllm.compute_global_topk_indices_and_lens(*a)
+    o = _op("compute_global_topk_indices_and_lens")(*a)
+    torch.cuda.synchronize()
+    assert torch.equal(f[0], o[0]) and torch.equal(f[1], o[1])
+    torch.library.opcheck(_op("compute_global_topk_indices_and_lens"), a, test_utils=("test_schema", "test_faketensor"))
+    qsl = torch.tensor([0, 20, 37], dtype=torch.int32, device=DEV)
+    seq = torch.tensor([100, 40], dtype=torch.int32, device=DEV)
+    gat = torch.tensor([50, 40], dtype=torch.int32, device=DEV)
+    c = (local, qsl, seq, gat, 16, 4, 24, 1000, 500)
+    f = flaggems_vllm.combine_topk_swa_indices(*c)
+    o = _op("combine_topk_swa_indices")(*c)
+    torch.cuda.synchronize()
+    assert torch.equal(f[0], o[0]) and torch.equal(f[1], o[1])
+    torch.library.opcheck(_op("combine_topk_swa_indices"), c, test_utils=("test_schema", "test_faketensor"))
