@@ -36,7 +36,7 @@ def parse_args():
     ap.add_argument("--config", type=int, default=2, help="main-op workload c0..c4 (default c2)")
     ap.add_argument("--op", choices=["main", "inv_rope", "gather", "rmsnorm", "indexer",
                                      "slot_mapping", "mla", "indexer_k", "indexer_k_gather", "mqa_logits",
-                                     "paged_mqa_logits", "copy"],
+                                     "paged_mqa_logits", "topk", "copy"],
                     default="main",
                     help="copy: torch device copy of 512 MiB, the HBM calibration kernel")
     ap.add_argument("--tma", action="store_true", help="inv_rope: packed UE8M0 scales")
@@ -51,6 +51,10 @@ def parse_args():
                     help="mqa_logits: M,N (default the reference benchmark's largest, 4096 x 8192)")
     ap.add_argument("--paged-shape", default="256,1,8192",
                     help="paged_mqa_logits: batch,next_n,context (reference benchmark shapes)")
+    ap.add_argument("--topk-case", choices=["decode", "prefill", "prefill_short"], default="decode",
+                    help="topk: top_k_per_row at the reference benchmark's largest decode shape (496 x 262144, "
+                         "k 512), its full-vocabulary prefill (64 x 129280, k 1024) or its many short rows "
+                         "(16383 x 4095, row stride 4352, k 512)")
     ap.add_argument("--cpu-sample-tokens", type=int, default=8192)
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="repeat the CPU sample until this much CPU time is spent (min 3 runs)")
@@ -604,6 +608,36 @@ def main():
         cpu_case = (lambda: torch_ref.paged_mqa_logits(qc, cache, w[:nb * nn], ctx[:nb], bt[:nb], mml, False),
                     nb * nn, "rows/s", f"first {nb} of {B} sequences (the reference test's per-row gather "
                                        f"and float32 loop)")
+    elif args.op == "topk":
+        # the sparse indexer's top-k per row at the reference benchmark's shapes
+        # (benchmark/test_top_k_per_row_decode.py:70-83, benchmark/test_top_k_per_row_prefill.py:122-132)
+        R, V, k, s0 = {"decode": (496, 262144, 512, 262144), "prefill": (64, 129280, 1024, 129280),
+                       "prefill_short": (16383, 4095, 512, 4352)}[args.topk_case]
+        g = torch.Generator().manual_seed(42)
+        buf_cpu = torch.randn((R - 1) * s0 + V, generator=g)
+        T = R
+        bytes_call = R * V * 4 + R * k * 4 + R * 8
+
+        def make_step(i):
+            buf = buf_cpu.to(dev)
+            lg = torch.as_strided(buf, (R, V), (s0, 1))
+            idx = torch.empty((R, k), dtype=torch.int32, device=dev)
+            if args.topk_case == "decode":
+                seq = torch.full((R,), V, dtype=torch.int32, device=dev)
+                return lambda: flaggems_vllm.top_k_per_row_decode(lg, 1, seq, idx, R, s0, 1, k)
+            st = torch.zeros(R, dtype=torch.int32, device=dev)
+            en = torch.full((R,), V, dtype=torch.int32, device=dev)
+            return lambda: flaggems_vllm.top_k_per_row_prefill(lg, st, en, idx, R, s0, 1, k)
+
+        kernel = "top_k_per_row_kernel"
+        workload = f"{args.topk_case}_R{R}_V{V}_k{k}"
+        config = {"workload": f"top_k_per_row_{'decode' if args.topk_case == 'decode' else 'prefill'} "
+                              f"{R} rows x {V} float32 logits (row stride {s0}), top_k {k}, full rows",
+                  "rows": R, "vocab": V, "top_k": k}
+        nr = max(1, min(R, 8 if V > 100000 else 256))
+        lg_cpu = torch.as_strided(buf_cpu, (R, V), (s0, 1))[:nr].contiguous()
+        cpu_case = (lambda: torch.topk(lg_cpu, k, dim=1, largest=True, sorted=False), nr, "rows/s",
+                    f"first {nr} of {R} rows: torch.topk on the CPU (the reference test's reference)")
     elif args.op == "copy":
         n = 512 << 20
         src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
@@ -636,7 +670,7 @@ def main():
 
     n_sets = 1
     if args.op in ("main", "gather", "rmsnorm", "indexer", "mla", "inv_rope", "indexer_k", "indexer_k_gather",
-                   "paged_mqa_logits"):
+                   "paged_mqa_logits", "topk"):
         step, n_sets = rotating(make_step, bytes_call)
     if n_sets == 1:
         config["input_sets"] = "one input set"
@@ -678,6 +712,8 @@ def main():
                  "synthetic: seeded q, k ~ N(0,1) (bf16, then e4m3fn or MXFP4 q and per-token FP8 k), "
                  "weights N(0,1) (|N(0,1)| dense), as the reference's tests draw them"
                  if args.op in ("mqa_logits", "paged_mqa_logits") else
+                 "synthetic: seeded N(0,1) float32 logits, as the reference's benchmark draws them"
+                 if args.op == "topk" else
                  "synthetic: seeded N(0,1) bf16 q/kv, fp32 cos/sin (theta 1e4), vLLM-style paged slots"),
         "config": config,
         "kernel_us": t_kernel * 1e6,

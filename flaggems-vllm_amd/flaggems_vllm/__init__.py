@@ -6,8 +6,8 @@ their compatibility aliases ``ops_deepseek_v4_qnorm_rope_kv_rope_quant_insert`` 
 ``ops_inv_rope_fp8_quant``, ``SUPPORTED_FP8_DTYPE``, ``device`` and ``vendor_name``;
 and the ops either side of that path (src/flaggems_vllm/ops/__init__.py): the
 K-cache gather, q/kv RMSNorm, the sparse indexer (q quant, key cache and
-logits), the index rows sparse attention reads (global top-k indices, top-k
-plus sliding window), slot mapping and sparse MLA decode.  Every op runs hand-written HIP kernels through the C ABI declared in
+logits and their top-k per row), the index rows sparse attention reads (global
+top-k indices, top-k plus sliding window), slot mapping and sparse MLA decode.  Every op runs hand-written HIP kernels through the C ABI declared in
 include/flaggems_vllm_amd.h; there is no Triton, no vendor dispatch and no
 CPU fallback.
 """
@@ -29,6 +29,8 @@ from .ops import (  # noqa: F401
     fused_q_kv_rmsnorm,
     get_mla_metadata,
     indexer_k_quant_and_cache,
+    top_k_per_row_decode,
+    top_k_per_row_prefill,
 )
 
 from . import library  # noqa: F401,E402  (torch.ops.flaggems_vllm.* registrations)
@@ -59,4 +61,6 @@ __all__ = [
     "ops_deepseek_v4_qnorm_rope_kv_rope_quant_insert",
     "ops_inv_rope_fp8_quant",
     "SUPPORTED_FP8_DTYPE",
+    "top_k_per_row_decode",
+    "top_k_per_row_prefill",
 ]

@@ -157,6 +157,20 @@ def lib():
         _P, _I64, _I64, _P,  # global_indices, strides, lens
         _P,  # stream
     ]
+    L.fgv_top_k_per_row_decode.restype = ctypes.c_int
+    L.fgv_top_k_per_row_decode.argtypes = [
+        _P, _I64, _I64, _I64, _I64,  # logits, strides, num_rows, width
+        _I64, _P,  # next_n, seq_lens
+        _P, _I64, _I64, _I64,  # indices, strides, top_k
+        _P,  # stream
+    ]
+    L.fgv_top_k_per_row_prefill.restype = ctypes.c_int
+    L.fgv_top_k_per_row_prefill.argtypes = [
+        _P, _I64, _I64, _I64, _I64,  # logits, strides, num_rows, width
+        _P, _P,  # row_starts, row_ends
+        _P, _I64, _I64, _I64,  # indices, strides, top_k
+        _P,  # stream
+    ]
     L.fgv_combine_topk_swa_width.restype = ctypes.c_int64
     L.fgv_combine_topk_swa_width.argtypes = [_I64, _I64]
     L.fgv_combine_topk_swa_indices.restype = ctypes.c_int
@@ -231,6 +245,8 @@ EXPORTED_SYMBOLS = (
     "fgv_compute_global_topk_indices_and_lens",
     "fgv_combine_topk_swa_width",
     "fgv_combine_topk_swa_indices",
+    "fgv_top_k_per_row_decode",
+    "fgv_top_k_per_row_prefill",
     "fgv_sparse_mla_decode_model1_no_alloc",
     "fgv_indexer_k_quant_and_cache",
     "fgv_cp_gather_indexer_k_quant_cache",

@@ -6,8 +6,8 @@ These registrations expose the same ops to torch.compile and graph capture as
 opaque custom ops: the schemas declare what each op writes, namely ``q`` and
 ``k_cache`` for the main op (alias-annotated ``Tensor(a0!) q``, ``Tensor(a2!) k_cache``), ``out``
 for the gather, ``slot_mapping`` for the slot mapping, ``kv_cache`` for the
-indexer key insert and ``k_fp8`` / ``k_fp8_scale`` for its gather (the index-row ops write only what
-they return).  The fake (meta)
+indexer key insert and ``k_fp8`` / ``k_fp8_scale`` for its gather, ``indices`` for the top-k per row
+(the index-row ops write only what they return).  The fake (meta)
 implementations give the output shapes and strides the real ops return.
 Each registered op calls the same wrapper, so argument checks and errors are
 the wrapper's.
@@ -32,6 +32,8 @@ from .ops import (
     fused_inv_rope_fp8_quant,
     fused_q_kv_rmsnorm,
     indexer_k_quant_and_cache,
+    top_k_per_row_decode,
+    top_k_per_row_prefill,
 )
 
 NAMESPACE = "flaggems_vllm"
@@ -198,6 +200,28 @@ def _(topk_indices, query_start_loc, seq_lens, gather_lens, window_size, compres
     return topk_indices.new_empty((t, width), dtype=torch.int32), topk_indices.new_empty((t,), dtype=torch.int32)
 
 
+@_op("top_k_per_row_decode", ("indices",))
+def _top_k_decode(logits: torch.Tensor, next_n: int, seq_lens: torch.Tensor, indices: torch.Tensor, num_rows: int,
+                  stride0: int, stride1: int, top_k: int) -> None:
+    top_k_per_row_decode(logits, next_n, seq_lens, indices, num_rows, stride0, stride1, top_k)
+
+
+@_top_k_decode.register_fake
+def _(logits, next_n, seq_lens, indices, num_rows, stride0, stride1, top_k):
+    return None
+
+
+@_op("top_k_per_row_prefill", ("indices",))
+def _top_k_prefill(logits: torch.Tensor, row_starts: torch.Tensor, row_ends: torch.Tensor, indices: torch.Tensor,
+                   num_rows: int, stride0: int, stride1: int, top_k: int) -> None:
+    top_k_per_row_prefill(logits, row_starts, row_ends, indices, num_rows, stride0, stride1, top_k)
+
+
+@_top_k_prefill.register_fake
+def _(logits, row_starts, row_ends, indices, num_rows, stride0, stride1, top_k):
+    return None
+
+
 REGISTERED: List[str] = [
     "fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert",
     "fused_inv_rope_fp8_quant",
@@ -209,4 +233,6 @@ REGISTERED: List[str] = [
     "cp_gather_indexer_k_quant_cache",
     "compute_global_topk_indices_and_lens",
     "combine_topk_swa_indices",
+    "top_k_per_row_decode",
+    "top_k_per_row_prefill",
 ]

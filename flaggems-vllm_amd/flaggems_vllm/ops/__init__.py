@@ -14,6 +14,7 @@ from .fused_indexer_q_rope_quant import fused_indexer_q_rope_quant
 from .fused_inv_rope_fp8_quant import SUPPORTED_FP8_DTYPE, fused_inv_rope_fp8_quant
 from .indexer_k_quant_and_cache import indexer_k_quant_and_cache
 from .slot_mapping import compute_slot_mapping_parallel
+from .top_k_per_row import top_k_per_row_decode, top_k_per_row_prefill
 
 __all__ = [
     "FlashMLASchedMeta",
@@ -32,4 +33,6 @@ __all__ = [
     "fused_inv_rope_fp8_quant",
     "indexer_k_quant_and_cache",
     "SUPPORTED_FP8_DTYPE",
+    "top_k_per_row_decode",
+    "top_k_per_row_prefill",
 ]

@@ -493,6 +493,28 @@ int fgv_combine_topk_swa_indices(
     int64_t num_reqs, int64_t window_size, int64_t compress_ratio, int64_t topk, int64_t M, int64_t N,
     int32_t* combined, int64_t out_stride0, int64_t out_stride1, int32_t* lens, void* stream);
 
+/*
+ * Top-k per row of float32 logits (the sparse indexer's selection).
+ *
+ * Replace flaggems_vllm.top_k_per_row_decode and top_k_per_row_prefill
+ * (reference: src/flaggems_vllm/ops/top_k_per_row_decode.py:1263-1399, job
+ * :877-1043; src/flaggems_vllm/ops/top_k_per_row_prefill.py:1232-1331).  Row r
+ * of logits [num_rows, width] (strides in elements) holds candidates
+ *   decode:  [0, seq_lens[r / next_n] - next_n + r % next_n + 1)
+ *   prefill: [row_starts[r], row_ends[r])
+ * (clamped to [0, width)).  indices[r, :] receives the column indices,
+ * relative to the row's start, of its top_k largest values in no particular
+ * order; a row of at most top_k values gives 0, 1, ..., len - 1 then -1.
+ * Values equal to the k-th largest are taken lowest index first, so the set
+ * is a function of the values; NaN orders above +inf (as torch.topk).
+ */
+int fgv_top_k_per_row_decode(const float* logits, int64_t stride0, int64_t stride1, int64_t num_rows,
+                             int64_t width, int64_t next_n, const int32_t* seq_lens, int32_t* indices,
+                             int64_t out_stride0, int64_t out_stride1, int64_t top_k, void* stream);
+int fgv_top_k_per_row_prefill(const float* logits, int64_t stride0, int64_t stride1, int64_t num_rows,
+                              int64_t width, const int32_t* row_starts, const int32_t* row_ends, int32_t* indices,
+                              int64_t out_stride0, int64_t out_stride1, int64_t top_k, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

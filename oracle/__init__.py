@@ -159,6 +159,8 @@ def lib():
         L.oracle_combine_topk_swa_indices.restype = None
         L.oracle_combine_topk_swa_indices.argtypes = [
             _P, _I64, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P]
+        L.oracle_top_k_per_row.restype = None
+        L.oracle_top_k_per_row.argtypes = [_P, _I64, _I64, _I64, _I64, _P, _P, _P, _I64, _I64, _P]
         _lib = L
     return _lib
 
@@ -548,3 +550,30 @@ def combine_topk_swa_indices(topk_indices, query_start_loc, seq_lens, gather_len
         int(window_size), int(compress_ratio), int(topk), int(M), int(N), out.data_ptr(), out.stride(0),
         out.stride(1), width, lens.data_ptr())
     return out, lens
+
+
+def top_k_per_row(logits, k, row_starts=None, row_ends=None, seq_lens=None, next_n=1, rows=None):
+    """CPU restatement: int32 [num_rows, k] (or [len(rows), k] for the given
+    rows), each row's selected indices in ascending order (see
+    oracle_top_k_per_row for the rows' ranges and the order of equal values)."""
+    x = _cpu(logits, torch.float32)
+    n = x.shape[0]
+    st = _cpu(row_starts, torch.int32).contiguous() if row_starts is not None else None
+    en = _cpu(row_ends, torch.int32).contiguous() if row_ends is not None else None
+    sl = _cpu(seq_lens, torch.int32).contiguous() if seq_lens is not None else None
+    if rows is not None:
+        rows = torch.as_tensor(rows, dtype=torch.long)
+        x = x[rows]
+        if st is not None:
+            st, en = st[rows].contiguous(), en[rows].contiguous()
+        else:
+            # each picked row keeps its decode range: give it its own seq_len entry
+            r = rows
+            sl = (sl[r // next_n] - next_n + r % next_n + 1).to(torch.int32).contiguous()
+            next_n = 1
+    out = torch.empty((x.shape[0], k), dtype=torch.int32)
+    lib().oracle_top_k_per_row(x.data_ptr(), x.stride(0), x.stride(1), x.shape[0], x.shape[1],
+                               st.data_ptr() if st is not None else None,
+                               en.data_ptr() if en is not None else None,
+                               sl.data_ptr() if sl is not None else None, int(next_n), int(k), out.data_ptr())
+    return out

@@ -43,6 +43,11 @@
  *   oracle_combine_topk_swa_indices
  *     reference op   src/flaggems_vllm/ops/deepseek_v4_attention_combine_topk_swa_indices.py:30-150
  *     reference test tests/test_deepseek_v4_attention_combine_topk_swa_indices.py:119-141
+ *   oracle_top_k_per_row
+ *     reference ops  src/flaggems_vllm/ops/top_k_per_row_decode.py:877-1043, 1263-1399
+ *                    src/flaggems_vllm/ops/top_k_per_row_prefill.py:1232-1331
+ *     reference test tests/test_top_k_per_row_decode.py:98-119 (_torch_topk_ref)
+ *                    tests/test_top_k_per_row_prefill.py:79-100 (reference_top_k_per_row)
  *   oracle_sparse_mla_decode_model1 (binary64 attention, see its comment)
  *     reference op   src/flaggems_vllm/ops/flash_mla_with_kvcache.py:489-688, 852-1073
  *                    src/flaggems_vllm/ops/flash_mla_with_kvcache_model1.py:389-470, 699-720
@@ -1008,5 +1013,81 @@ void oracle_combine_topk_swa_indices(const int32_t* topk_idx, int64_t ts0, int64
                     (int32_t)(row_off + (uint32_t)(int32_t)N + (uint32_t)(j + pos - swa_len + 1 - (int32_t)gather_start));
             lens[t] = topk_len + swa_len;
         }
+    }
+}
+
+/*
+ * Top-k per row by sorting: each candidate (value, index) of the row is sorted
+ * by value, largest first, equal values lowest index first (NaN above +inf,
+ * as torch.topk orders it); the first k indices, relative to the row's start,
+ * are written in ascending order.  A row of at most k values gives
+ * 0..len-1 then -1.  Row r holds [starts[r], ends[r]) (prefill, starts
+ * non-NULL) or [0, seq_lens[r / next_n] - next_n + r % next_n + 1) (decode),
+ * clamped to [0, width).  out is [num_rows][k] contiguous.
+ */
+struct topk_item {
+    float v;
+    int32_t i;
+};
+
+static int topk_before(const struct topk_item* a, const struct topk_item* b)
+{
+    const int an = a->v != a->v, bn = b->v != b->v;
+    if (an != bn)
+        return an;  /* NaN first */
+    if (!an && a->v != b->v)
+        return a->v > b->v;
+    return a->i < b->i;
+}
+
+static int topk_cmp(const void* pa, const void* pb)
+{
+    const struct topk_item* a = (const struct topk_item*)pa;
+    const struct topk_item* b = (const struct topk_item*)pb;
+    return topk_before(a, b) ? -1 : (topk_before(b, a) ? 1 : 0);
+}
+
+static int int_cmp(const void* pa, const void* pb)
+{
+    const int32_t a = *(const int32_t*)pa, b = *(const int32_t*)pb;
+    return (a > b) - (a < b);
+}
+
+void oracle_top_k_per_row(const float* logits, int64_t s0, int64_t s1, int64_t num_rows, int64_t width,
+                          const int32_t* starts, const int32_t* ends, const int32_t* seq_lens, int64_t next_n,
+                          int64_t k, int32_t* out)
+{
+#pragma omp parallel for schedule(dynamic)
+    for (int64_t r = 0; r < num_rows; ++r) {
+        int64_t start = 0, end;
+        if (starts) {
+            start = starts[r];
+            end = ends[r];
+        } else {
+            end = (int64_t)seq_lens[r / next_n] - next_n + r % next_n + 1;
+        }
+        if (start < 0)
+            start = 0;
+        if (end > width)
+            end = width;
+        const int64_t len = end > start ? end - start : 0;
+        int32_t* o = out + r * k;
+        if (len <= k) {
+            for (int64_t i = 0; i < k; ++i)
+                o[i] = i < len ? (int32_t)i : -1;
+            continue;
+        }
+        struct topk_item* it = (struct topk_item*)malloc(sizeof(struct topk_item) * (size_t)len);
+        if (!it)
+            continue;
+        for (int64_t i = 0; i < len; ++i) {
+            it[i].v = logits[r * s0 + (start + i) * s1];
+            it[i].i = (int32_t)i;
+        }
+        qsort(it, (size_t)len, sizeof(*it), topk_cmp);
+        for (int64_t i = 0; i < k; ++i)
+            o[i] = it[i].i;
+        qsort(o, (size_t)k, sizeof(int32_t), int_cmp);
+        free(it);
     }
 }

@@ -169,3 +169,18 @@ def test_graph_topk_index_ops():
     gat = torch.tensor([1000, 500], dtype=torch.int32, device=DEV)
     replay_matches_eager(lambda: None, lambda: flaggems_vllm.combine_topk_swa_indices(
         local, qsl, seq, gat, 128, 4, 128, 45056, 40960))
+
+
+def test_graph_top_k_per_row():
+    """top_k_per_row_decode over rows held in LDS and over long rows; the
+    captured replays select the same index sets as the eager call (their
+    order within a row may differ from call to call)."""
+    _say("graph: top_k_per_row decode")
+    g = torch.Generator().manual_seed(8)
+    for V in (5000, 70000):
+        lg = torch.randn(9, V, generator=g).to(DEV)
+        seq = torch.full((9,), V, dtype=torch.int32, device=DEV)
+        idx = torch.empty(9, 512, dtype=torch.int32, device=DEV)
+        run = lambda: (flaggems_vllm.top_k_per_row_decode(lg, 1, seq, idx, 9, lg.stride(0), 1, 512),
+                       idx.sort(1).values)[1]
+        replay_matches_eager(lambda: idx.fill_(-5), run)

@@ -1,0 +1,256 @@
+"""top_k_per_row_decode / top_k_per_row_prefill: the sparse indexer's top-k.
+
+Reference: src/flaggems_vllm/ops/top_k_per_row_decode.py:877-1043, 1263-1399;
+src/flaggems_vllm/ops/top_k_per_row_prefill.py:1232-1331; tests
+tests/test_top_k_per_row_decode.py:98-260 and tests/test_top_k_per_row_prefill.py:79-260
+(their torch.topk references and shapes), benchmark shapes
+benchmark/test_top_k_per_row_decode.py:70-83, benchmark/test_top_k_per_row_prefill.py:122-132.
+
+The reference's own check is value-based (the selected values, sorted, equal
+torch.topk's).  Here the bar is stronger: equal values are taken lowest index
+first, so each row's selected index set is exact; it is compared, sorted,
+with the oracle's (a sort of the whole row), and the values with torch.topk's.
+"""
+import pytest
+import torch
+
+import oracle
+
+DEV = torch.device("cuda:0")
+I32 = torch.int32
+
+
+# ------------------------------------------------------------- oracle ----
+
+def test_oracle_small_known_answers():
+    x = torch.tensor([[3., 1., 4., 1., 5., 9., 2., 6.]])
+    n = torch.tensor([8], dtype=I32)
+    assert oracle.top_k_per_row(x, 3, seq_lens=n).tolist() == [[4, 5, 7]]          # 5, 9, 6
+    assert oracle.top_k_per_row(x, 2, seq_lens=torch.tensor([4], dtype=I32)).tolist() == [[0, 2]]  # of 3 1 4 1
+    # ties at the k-th value: lowest index first
+    assert oracle.top_k_per_row(torch.ones(1, 6), 2, seq_lens=torch.tensor([6], dtype=I32)).tolist() == [[0, 1]]
+    y = torch.tensor([[1., 7., 7., 2., 7., 7.]])
+    assert oracle.top_k_per_row(y, 3, seq_lens=torch.tensor([6], dtype=I32)).tolist() == [[1, 2, 4]]
+    # NaN above +inf, -inf below everything, -0 == +0 (index order)
+    z = torch.tensor([[float("-inf"), float("inf"), float("nan"), -0.0, 0.0, -1.0]])
+    assert oracle.top_k_per_row(z, 2, seq_lens=torch.tensor([6], dtype=I32)).tolist() == [[1, 2]]
+    assert oracle.top_k_per_row(z, 4, seq_lens=torch.tensor([6], dtype=I32)).tolist() == [[1, 2, 3, 4]]
+    # short rows: 0..len-1 then -1; prefill indices relative to the row start
+    assert oracle.top_k_per_row(x, 5, seq_lens=torch.tensor([3], dtype=I32)).tolist() == [[0, 1, 2, -1, -1]]
+    s, e = torch.tensor([2], dtype=I32), torch.tensor([7], dtype=I32)
+    assert oracle.top_k_per_row(x, 2, row_starts=s, row_ends=e).tolist() == [[2, 3]]   # 5, 9 of 4 1 5 9 2
+
+
+def test_oracle_against_torch_topk_values():
+    """The oracle's selected values equal torch.topk's (the reference test's
+    check), over decode rows with next_n = 2 and prefill rows with ragged
+    ranges, ties and infinities included."""
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(12, 3000, generator=g)
+    x[3] = torch.randint(0, 3, (3000,), generator=g).float()  # heavy ties
+    x[5, ::3] = float("-inf")
+    seq = torch.tensor([3000, 700, 64, 1500, 2999, 100], dtype=I32)
+    k = 100
+    o = oracle.top_k_per_row(x, k, seq_lens=seq, next_n=2)
+    for r in range(12):
+        n = int(seq[r // 2]) - 2 + r % 2 + 1
+        row = x[r, :n]
+        if n <= k:
+            assert o[r].tolist() == list(range(n)) + [-1] * (k - n)
+            continue
+        assert torch.equal(row[o[r].long()].sort().values, row.topk(k).values.sort().values)
+    st = torch.randint(0, 1500, (12,), generator=g, dtype=I32)
+    en = st + torch.randint(0, 1500, (12,), generator=g, dtype=I32)
+    o = oracle.top_k_per_row(x, k, row_starts=st, row_ends=en)
+    for r in range(12):
+        row = x[r, int(st[r]):int(en[r])]
+        if row.numel() <= k:
+            continue
+        assert torch.equal(row[o[r].long()].sort().values, row.topk(k).values.sort().values)
+
+
+def test_c_abi_rejects_bad_arguments():
+    from flaggems_vllm import _native
+
+    L = _native.lib()
+    p = 1 << 12  # never dereferenced
+    d = L.fgv_top_k_per_row_decode
+    assert d(p, 64, 1, 4, 64, 0, p, p, 8, 1, 8, None) == -2        # next_n 0
+    assert d(p, 64, 1, -1, 64, 1, p, p, 8, 1, 8, None) == -2       # negative rows
+    assert d(None, 64, 1, 4, 64, 1, p, p, 8, 1, 8, None) == -1
+    assert d(p + 2, 64, 1, 4, 64, 1, p, p, 8, 1, 8, None) == -3
+    assert d(p, 64, 1, 4, 64, 1, None, p, 8, 1, 8, None) == -1     # no seq_lens
+    assert d(p, 64, 1, 4, 64, 1, p, p, 8, 1, 0, None) == 0         # top_k 0: nothing to do
+    f = L.fgv_top_k_per_row_prefill
+    assert f(p, 64, 1, 4, 64, None, p, p, 8, 1, 8, None) == -1
+    assert f(p, 64, 1, 0, 64, p, p, p, 8, 1, 8, None) == 0
+
+
+def test_wrapper_asserts_like_the_reference():
+    import flaggems_vllm
+
+    x = torch.zeros(4, 16)
+    with pytest.raises(AssertionError):  # num_rows must equal logits.shape[0]
+        flaggems_vllm.top_k_per_row_decode(x, 1, torch.full((4,), 16, dtype=I32), torch.zeros(4, 8, dtype=I32),
+                                           3, 16, 1, 8)
+
+
+# ---------------------------------------------------------------- GPU ----
+
+def _check_rows(got, logits_cpu, k, rows, exp):
+    """got: GPU indices [R, k]; exp: the oracle's sorted sets for `rows`."""
+    g = got.cpu()[rows]
+    short = (exp < 0).any(1)
+    # rows of at most top_k values are positional (0..len-1 then -1); others are sets
+    assert torch.equal(g[short], exp[short]), "short rows differ from 0..len-1, -1..."
+    assert torch.equal(g[~short].sort(1).values, exp[~short]), "selected index sets differ from the oracle's"
+
+
+def _decode_case(B, V, k, next_n=1, seq=None, seed=42, fill=None, stride0=None, stride1=1):
+    g = torch.Generator().manual_seed(seed)
+    rows = B * next_n
+    s0 = stride0 or V
+    buf = torch.randn((rows - 1) * s0 + (V - 1) * stride1 + 1, generator=g)
+    if fill is not None:
+        buf = fill(buf, g)
+    logits = torch.as_strided(buf, (rows, V), (s0, stride1))
+    seq_lens = torch.full((B,), V, dtype=I32) if seq is None else torch.as_tensor(seq, dtype=I32)
+    return buf, logits, seq_lens
+
+
+def _run_decode(buf, logits, seq_lens, k, next_n, rows_checked):
+    import flaggems_vllm
+
+    R = logits.shape[0]
+    dbuf = buf.to(DEV)
+    dl = torch.as_strided(dbuf, logits.shape, logits.stride())
+    idx = torch.full((R, k), -7, dtype=I32, device=DEV)
+    flaggems_vllm.top_k_per_row_decode(dl, next_n, seq_lens.to(DEV), idx, R, dl.stride(0), dl.stride(1), k)
+    torch.cuda.synchronize()
+    exp = oracle.top_k_per_row(logits, k, seq_lens=seq_lens, next_n=next_n, rows=rows_checked)
+    _check_rows(idx, logits, k, rows_checked, exp)
+    return idx
+
+
+DECODE_SHAPES = [(1, 4096, 64), (1, 8192, 128), (1, 16384, 256), (1, 32768, 512), (1, 129280, 1024),
+                 (1, 262144, 512), (496, 262144, 512), (56, 262144, 512)]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("B,V,k", DECODE_SHAPES)
+def test_gpu_decode_reference_shapes(B, V, k):
+    """The reference test's and benchmark's shapes (full rows); the oracle
+    checks up to 64 rows of each, torch.topk's values every row."""
+    print(f"\n[case] top-k decode B={B} V={V} k={k}", flush=True)
+    buf, logits, seq = _decode_case(B, V, k)
+    rows = list(range(min(B, 48))) + ([B - 1] if B > 48 else [])
+    idx = _run_decode(buf, logits, seq, k, 1, rows)
+    vals = torch.gather(logits.to(DEV), 1, idx.long()).sort(1).values
+    assert torch.equal(vals, logits.to(DEV).topk(k, dim=1).values.sort(1).values)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("V,k,s", [(129280, 1024, 100000), (32768, 256, 16384), (8192, 64, 4096),
+                                   (262144, 512, 496), (262144, 512, 512), (262144, 512, 513)])
+def test_gpu_decode_partial_rows(V, k, s):
+    """seq_len below the vocabulary (reference :144-170), and a row of at most
+    top_k values (:174-194): 0..len-1 then -1."""
+    print(f"\n[case] top-k decode partial V={V} k={k} seq={s}", flush=True)
+    buf, logits, seq = _decode_case(1, V, k, seq=[s], seed=123)
+    _run_decode(buf, logits, seq, k, 1, [0])
+
+
+@pytest.mark.gpu
+def test_gpu_decode_next_n_and_ragged():
+    """next_n = 3: each batch's rows end one position apart; ragged seq_lens."""
+    print("\n[case] top-k decode next_n=3 ragged", flush=True)
+    seq = [50000, 700, 3, 262144, 1025, 999]
+    buf, logits, seq_t = _decode_case(6, 262144, 512, next_n=3, seq=seq, seed=9)
+    _run_decode(buf, logits, seq_t, 512, 3, list(range(18)))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kind", ["lsb8", "few_values", "all_equal", "neg_inf_tail", "nan"])
+def test_gpu_decode_ties_and_specials(kind):
+    """Rows whose values share their upper bits (the reference's 8-LSB test,
+    :198-222: every value in one first-level bin, more than LDS holds), few
+    distinct values and all equal (ties at the k-th value, lowest index
+    first), -inf tails, NaN."""
+    print(f"\n[case] top-k decode {kind}", flush=True)
+
+    def fill(buf, g):
+        n = buf.numel()
+        if kind == "lsb8":
+            bits = 0x3F900000 | torch.randint(0, 256, (n,), generator=g, dtype=torch.int32)
+            return bits.view(torch.float32)
+        if kind == "few_values":
+            return torch.randint(0, 5, (n,), generator=g).float()
+        if kind == "all_equal":
+            return torch.full((n,), 0.5)
+        if kind == "neg_inf_tail":
+            buf = buf.clone()
+            buf.view(4, -1)[:, 3000:] = float("-inf")
+            return buf
+        buf = buf.clone()
+        buf[torch.randperm(n, generator=g)[:300]] = float("nan")
+        return buf
+
+    buf, logits, seq = _decode_case(4, 65536, 512, seed=5, fill=fill)
+    _run_decode(buf, logits, seq, 512, 1, [0, 1, 2, 3])
+    buf, logits, seq = _decode_case(2, 5000, 256, seed=6, fill=fill)  # rows held in LDS
+    _run_decode(buf, logits, seq, 256, 1, [0, 1])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("s1", [1, 3])
+def test_gpu_decode_strided(s1):
+    """stride0 above the row (the benchmark passes explicit strides) and a
+    column stride."""
+    print(f"\n[case] top-k decode strided s1={s1}", flush=True)
+    buf, logits, seq = _decode_case(5, 20000, 512, stride0=20000 * s1 + 37, stride1=s1, seed=11)
+    _run_decode(buf, logits, seq, 512, 1, list(range(5)))
+
+
+def _run_prefill(logits, starts, ends, k, rows_checked):
+    import flaggems_vllm
+
+    R = logits.shape[0]
+    dl = logits.to(DEV)
+    idx = torch.full((R, k), -7, dtype=I32, device=DEV)
+    flaggems_vllm.top_k_per_row_prefill(dl, starts.to(DEV), ends.to(DEV), idx, R, dl.stride(0), dl.stride(1), k)
+    torch.cuda.synchronize()
+    exp = oracle.top_k_per_row(logits, k, row_starts=starts, row_ends=ends, rows=rows_checked)
+    _check_rows(idx, logits, k, rows_checked, exp)
+
+
+PREFILL_SHAPES = [(64, 129280, 1024), (4, 8193, 512), (2000, 4095, 512), (4, 16385, 512), (1300, 4100, 512),
+                  (1600, 5115, 512), (4100, 1025, 512)]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("R,V,k", PREFILL_SHAPES)
+def test_gpu_prefill_reference_shapes(R, V, k):
+    """The benchmark's shapes (full rows; its 16383- and 12961-row cases with
+    fewer rows), oracle on up to 64 rows."""
+    print(f"\n[case] top-k prefill R={R} V={V} k={k}", flush=True)
+    g = torch.Generator().manual_seed(42)
+    logits = torch.randn(R, V, generator=g)
+    starts = torch.zeros(R, dtype=I32)
+    ends = torch.full((R,), V, dtype=I32)
+    _run_prefill(logits, starts, ends, k, list(range(min(R, 63))) + [R - 1])
+
+
+@pytest.mark.gpu
+def test_gpu_prefill_ragged_ranges():
+    """Nonzero row starts (reference :210-240), ragged and empty rows, rows
+    past the width, rows of at most top_k values."""
+    print("\n[case] top-k prefill ragged", flush=True)
+    g = torch.Generator().manual_seed(321)
+    R, V, k = 40, 65536, 1024
+    logits = torch.randn(R, V, generator=g)
+    starts = torch.randint(0, 30000, (R,), generator=g, dtype=I32)
+    ends = starts + torch.randint(0, 36000, (R,), generator=g, dtype=I32)
+    starts[:2] = torch.tensor([128, 4096], dtype=I32)
+    ends[:2] = torch.tensor([4096, 8192], dtype=I32)
+    ends[5], ends[6], starts[7] = starts[5], starts[6] + 100, 70000
+    _run_prefill(logits, starts, ends, k, list(range(R)))

@@ -31,6 +31,8 @@ WRITES = {
     "cp_gather_indexer_k_quant_cache": {"k_fp8", "k_fp8_scale"},
     "compute_global_topk_indices_and_lens": set(),
     "combine_topk_swa_indices": set(),
+    "top_k_per_row_decode": {"indices"},
+    "top_k_per_row_prefill": {"indices"},
 }
 
 
@@ -215,3 +217,23 @@ def test_gpu_topk_index_ops_opcheck():
     torch.cuda.synchronize()
     assert torch.equal(f[0], o[0]) and torch.equal(f[1], o[1])
     torch.library.opcheck(_op("combine_topk_swa_indices"), c, test_utils=("test_schema", "test_faketensor"))
+
+
+@pytest.mark.gpu
+def test_gpu_top_k_per_row_ops():
+    """The top-k ops through torch.ops write the same index sets as the functions."""
+    _say("torch.ops top_k_per_row decode / prefill")
+    g = torch.Generator().manual_seed(3)
+    lg = torch.randn(6, 20000, generator=g).to(DEV)
+    seq = torch.tensor([20000, 9000, 300, 20000, 15000, 12345], dtype=torch.int32, device=DEV)
+    a = torch.empty(6, 512, dtype=torch.int32, device=DEV)
+    b = torch.empty_like(a)
+    flaggems_vllm.top_k_per_row_decode(lg, 1, seq, a, 6, lg.stride(0), lg.stride(1), 512)
+    _op("top_k_per_row_decode")(lg, 1, seq, b, 6, lg.stride(0), lg.stride(1), 512)
+    torch.cuda.synchronize()
+    assert torch.equal(a.sort(1).values, b.sort(1).values)
+    st = torch.tensor([0, 100, 5000, 0, 7, 19000], dtype=torch.int32, device=DEV)
+    flaggems_vllm.top_k_per_row_prefill(lg, st, seq, a, 6, lg.stride(0), lg.stride(1), 512)
+    _op("top_k_per_row_prefill")(lg, st, seq, b, 6, lg.stride(0), lg.stride(1), 512)
+    torch.cuda.synchronize()
+    assert torch.equal(a.sort(1).values, b.sort(1).values)
