@@ -629,11 +629,16 @@ def main():
             en = torch.full((R,), V, dtype=torch.int32, device=dev)
             return lambda: flaggems_vllm.top_k_per_row_prefill(lg, st, en, idx, R, s0, 1, k)
 
-        kernel = "top_k_per_row_kernel"
+        from flaggems_vllm import _native
+
+        split = _native.lib().fgv_top_k_per_row_workspace_bytes(R, V, k) > 0
+        kernel = "top_k_part_kernel" if split else "top_k_per_row_kernel"
         workload = f"{args.topk_case}_R{R}_V{V}_k{k}"
         config = {"workload": f"top_k_per_row_{'decode' if args.topk_case == 'decode' else 'prefill'} "
                               f"{R} rows x {V} float32 logits (row stride {s0}), top_k {k}, full rows",
-                  "rows": R, "vocab": V, "top_k": k}
+                  "rows": R, "vocab": V, "top_k": k,
+                  "schedule": "rows split into parts of 16384 + merge kernel (kernel_us covers both)" if split
+                  else "one workgroup per row"}
         nr = max(1, min(R, 8 if V > 100000 else 256))
         lg_cpu = torch.as_strided(buf_cpu, (R, V), (s0, 1))[:nr].contiguous()
         cpu_case = (lambda: torch.topk(lg_cpu, k, dim=1, largest=True, sorted=False), nr, "rows/s",

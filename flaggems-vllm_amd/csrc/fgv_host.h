@@ -21,4 +21,13 @@ inline int launch_status() {
     return e == hipSuccess ? FGV_OK : static_cast<int>(e);
 }
 
+// CUs of the current device (256 on MI355X).
+inline int cu_count() {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        cus = 256;
+    return cus;
+}
+
 }  // namespace fgv

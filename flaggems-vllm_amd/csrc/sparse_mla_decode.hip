@@ -1259,15 +1259,6 @@ constexpr int64_t kSplitMinChunks = 64;
 
 int64_t chunks_of(int64_t topk) { return (topk + kChunk - 1) / kChunk; }
 
-// CUs of the current device (256 on MI355X).
-int cu_count() {
-    int dev = 0, cus = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-        cus = 256;
-    return cus;
-}
-
 // Workgroups of the split grid: two per CU of the current device.
 int split_grid() { return 2 * cu_count(); }
 

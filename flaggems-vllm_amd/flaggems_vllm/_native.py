@@ -162,6 +162,7 @@ def lib():
         _P, _I64, _I64, _I64, _I64,  # logits, strides, num_rows, width
         _I64, _P,  # next_n, seq_lens
         _P, _I64, _I64, _I64,  # indices, strides, top_k
+        _P, _I64,  # workspace, bytes
         _P,  # stream
     ]
     L.fgv_top_k_per_row_prefill.restype = ctypes.c_int
@@ -169,8 +170,11 @@ def lib():
         _P, _I64, _I64, _I64, _I64,  # logits, strides, num_rows, width
         _P, _P,  # row_starts, row_ends
         _P, _I64, _I64, _I64,  # indices, strides, top_k
+        _P, _I64,  # workspace, bytes
         _P,  # stream
     ]
+    L.fgv_top_k_per_row_workspace_bytes.restype = ctypes.c_int64
+    L.fgv_top_k_per_row_workspace_bytes.argtypes = [_I64, _I64, _I64]
     L.fgv_combine_topk_swa_width.restype = ctypes.c_int64
     L.fgv_combine_topk_swa_width.argtypes = [_I64, _I64]
     L.fgv_combine_topk_swa_indices.restype = ctypes.c_int
@@ -247,6 +251,7 @@ EXPORTED_SYMBOLS = (
     "fgv_combine_topk_swa_indices",
     "fgv_top_k_per_row_decode",
     "fgv_top_k_per_row_prefill",
+    "fgv_top_k_per_row_workspace_bytes",
     "fgv_sparse_mla_decode_model1_no_alloc",
     "fgv_indexer_k_quant_and_cache",
     "fgv_cp_gather_indexer_k_quant_cache",

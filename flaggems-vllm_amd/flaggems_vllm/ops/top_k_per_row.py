@@ -24,15 +24,25 @@ def _check(logits, indices, num_rows, top_k):
     assert indices.device == logits.device
 
 
+def _workspace(logits, num_rows, top_k):
+    """The split's candidate buffer for rows wider than 16384 values (None if
+    the sizes need none), allocated per call as the reference allocates its
+    split buffers (ops/top_k_per_row_decode.py:1303-1312)."""
+    n = _native.lib().fgv_top_k_per_row_workspace_bytes(int(num_rows), logits.shape[1], int(top_k))
+    return torch.empty(n, dtype=torch.uint8, device=logits.device) if n > 0 else None
+
+
 def top_k_per_row_decode(logits, next_n, seq_lens, indices, num_rows, stride0, stride1, top_k):
     """Row r holds candidates [0, seq_lens[r // next_n] - next_n + r % next_n + 1)."""
     _check(logits, indices, num_rows, top_k)
     assert seq_lens.dtype == torch.int32 and seq_lens.numel() >= (num_rows + next_n - 1) // next_n
     seq = seq_lens.contiguous()
+    ws = _workspace(logits, num_rows, top_k)
     with on_device_of(logits):
         rc = _native.lib().fgv_top_k_per_row_decode(
             logits.data_ptr(), int(stride0), int(stride1), int(num_rows), logits.shape[1], int(next_n),
             seq.data_ptr(), indices.data_ptr(), indices.stride(0), indices.stride(1), int(top_k),
+            ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0,
             current_stream_ptr(logits.device))
     _native.check(rc, "top_k_per_row_decode")
 
@@ -43,10 +53,12 @@ def top_k_per_row_prefill(logits, row_starts, row_ends, indices, num_rows, strid
     assert row_starts.dtype == torch.int32 and row_ends.dtype == torch.int32
     assert row_starts.numel() >= num_rows and row_ends.numel() >= num_rows
     starts, ends = row_starts.contiguous(), row_ends.contiguous()
+    ws = _workspace(logits, num_rows, top_k)
     with on_device_of(logits):
         rc = _native.lib().fgv_top_k_per_row_prefill(
             logits.data_ptr(), int(stride0), int(stride1), int(num_rows), logits.shape[1], starts.data_ptr(),
             ends.data_ptr(), indices.data_ptr(), indices.stride(0), indices.stride(1), int(top_k),
+            ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0,
             current_stream_ptr(logits.device))
     _native.check(rc, "top_k_per_row_prefill")
 

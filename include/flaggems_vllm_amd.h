@@ -507,13 +507,24 @@ int fgv_combine_topk_swa_indices(
  * order; a row of at most top_k values gives 0, 1, ..., len - 1 then -1.
  * Values equal to the k-th largest are taken lowest index first, so the set
  * is a function of the values; NaN orders above +inf (as torch.topk).
+ * workspace (16-byte aligned, fgv_top_k_per_row_workspace_bytes of it) lets
+ * rows wider than 16384 values be split into parts and merged when there are
+ * fewer rows than the GPU has CUs; without it (NULL or too small), or with
+ * more rows, each row is streamed by one workgroup.  The reference allocates
+ * its split's buffers per call likewise (ops/top_k_per_row_decode.py:1303-1312).
  */
 int fgv_top_k_per_row_decode(const float* logits, int64_t stride0, int64_t stride1, int64_t num_rows,
                              int64_t width, int64_t next_n, const int32_t* seq_lens, int32_t* indices,
-                             int64_t out_stride0, int64_t out_stride1, int64_t top_k, void* stream);
+                             int64_t out_stride0, int64_t out_stride1, int64_t top_k, void* workspace,
+                             int64_t workspace_bytes, void* stream);
 int fgv_top_k_per_row_prefill(const float* logits, int64_t stride0, int64_t stride1, int64_t num_rows,
                               int64_t width, const int32_t* row_starts, const int32_t* row_ends, int32_t* indices,
-                              int64_t out_stride0, int64_t out_stride1, int64_t top_k, void* stream);
+                              int64_t out_stride0, int64_t out_stride1, int64_t top_k, void* workspace,
+                              int64_t workspace_bytes, void* stream);
+
+/* Workspace bytes the top-k entry points can use for these sizes on the
+ * current device (0: they use none). */
+int64_t fgv_top_k_per_row_workspace_bytes(int64_t num_rows, int64_t width, int64_t top_k);
 
 #ifdef __cplusplus
 }

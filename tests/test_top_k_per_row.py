@@ -75,15 +75,21 @@ def test_c_abi_rejects_bad_arguments():
     L = _native.lib()
     p = 1 << 12  # never dereferenced
     d = L.fgv_top_k_per_row_decode
-    assert d(p, 64, 1, 4, 64, 0, p, p, 8, 1, 8, None) == -2        # next_n 0
-    assert d(p, 64, 1, -1, 64, 1, p, p, 8, 1, 8, None) == -2       # negative rows
-    assert d(None, 64, 1, 4, 64, 1, p, p, 8, 1, 8, None) == -1
-    assert d(p + 2, 64, 1, 4, 64, 1, p, p, 8, 1, 8, None) == -3
-    assert d(p, 64, 1, 4, 64, 1, None, p, 8, 1, 8, None) == -1     # no seq_lens
-    assert d(p, 64, 1, 4, 64, 1, p, p, 8, 1, 0, None) == 0         # top_k 0: nothing to do
+    assert d(p, 64, 1, 4, 64, 0, p, p, 8, 1, 8, None, 0, None) == -2        # next_n 0
+    assert d(p, 64, 1, -1, 64, 1, p, p, 8, 1, 8, None, 0, None) == -2       # negative rows
+    assert d(None, 64, 1, 4, 64, 1, p, p, 8, 1, 8, None, 0, None) == -1
+    assert d(p + 2, 64, 1, 4, 64, 1, p, p, 8, 1, 8, None, 0, None) == -3
+    assert d(p, 64, 1, 4, 64, 1, None, p, 8, 1, 8, None, 0, None) == -1     # no seq_lens
+    assert d(p, 64, 1, 4, 64, 1, p, p, 8, 1, 0, None, 0, None) == 0         # top_k 0: nothing to do
+    w = L.fgv_top_k_per_row_workspace_bytes
+    assert w(32, 262144, 512) == 32 * 16 * 512 * 8      # 16 parts of 16384, 512 part workgroups
+    assert w(1, 200000, 512) == 13 * 512 * 8
+    assert w(33, 262144, 512) == 0 and w(496, 262144, 512) == 0   # more than two part workgroups per CU (256)
+    assert w(1, 180224, 512) == 0 and w(64, 129280, 1024) == 0    # under 12 parts: streamed
+    assert w(1, 16384, 1024) == 0 and w(4, 262144, 1024) == 0     # one part; 16 x 1024 over the merge's 8192
     f = L.fgv_top_k_per_row_prefill
-    assert f(p, 64, 1, 4, 64, None, p, p, 8, 1, 8, None) == -1
-    assert f(p, 64, 1, 0, 64, p, p, p, 8, 1, 8, None) == 0
+    assert f(p, 64, 1, 4, 64, None, p, p, 8, 1, 8, None, 0, None) == -1
+    assert f(p, 64, 1, 0, 64, p, p, p, 8, 1, 8, None, 0, None) == 0
 
 
 def test_wrapper_asserts_like_the_reference():
@@ -254,3 +260,76 @@ def test_gpu_prefill_ragged_ranges():
     ends[:2] = torch.tensor([4096, 8192], dtype=I32)
     ends[5], ends[6], starts[7] = starts[5], starts[6] + 100, 70000
     _run_prefill(logits, starts, ends, k, list(range(R)))
+
+
+def _sampled_positions(n):
+    """Positions of the sample a workgroup takes from a row longer than its
+    LDS cache before streaming it: chunks of 256 contiguous values, one every
+    n // chunks values, chunks = max((n // 32) rounded down to 256, 2048) /
+    256 (the cache's size caps it, 8192 or 12288 values: not reached below
+    262144-value rows)."""
+    ns = max((n // 32) & ~255, 2048)
+    nch = ns // 256
+    stride = n // nch
+    return (torch.arange(nch)[:, None] * stride + torch.arange(256)[None, :]).reshape(-1)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("reps", [1, 50])
+@pytest.mark.parametrize("kind", ["random", "lsb8", "few_values", "sample_high", "sample_low", "sorted"])
+def test_gpu_long_rows_without_workspace(kind, reps):
+    """Rows wider than 16384 values with no workspace: one workgroup per row
+    streams it instead of the split into parts and merge (1024 threads for 6
+    rows, 512 for 300); same index sets.  A sample of the row sets the
+    threshold of a single read; rows whose sampled values lie above the rest
+    (fewer than top_k values reach the threshold) or below it (more than LDS
+    holds reach it) are read again, twice (or four times for a threshold bin
+    larger than LDS)."""
+    from flaggems_vllm import _native
+
+    print(f"\n[case] top-k long rows without workspace {kind} x{reps}", flush=True)
+    g = torch.Generator().manual_seed(17)
+    R, V, k = 6, 200000, 512
+    seq = torch.tensor([V, 190000, 40000, 513, V, 16385], dtype=I32)
+    if kind == "lsb8":
+        x = (0x3F900000 | torch.randint(0, 256, (R, V), generator=g, dtype=torch.int32)).view(torch.float32)
+    elif kind == "few_values":
+        x = torch.randint(0, 7, (R, V), generator=g).float()
+    elif kind == "sorted":
+        x = torch.arange(V, dtype=torch.float32).repeat(R, 1) * (1 - 2 * (torch.arange(R) % 2))[:, None]
+    else:
+        x = torch.randn(R, V, generator=g)
+        if kind.startswith("sample"):
+            for r in range(R):
+                n = int(seq[r])
+                if n > 16384:
+                    pos = _sampled_positions(n)
+                    x[r, pos] += 50.0 if kind == "sample_high" else -50.0
+    assert _native.lib().fgv_top_k_per_row_workspace_bytes(R, V, k) > 0, "the split applies to these rows"
+    x, seq = x.repeat(reps, 1), seq.repeat(reps)
+    R *= reps
+    d = x.to(DEV)
+    idx = torch.full((R, k), -7, dtype=I32, device=DEV)
+    rc = _native.lib().fgv_top_k_per_row_decode(d.data_ptr(), V, 1, R, V, 1, seq.to(DEV).data_ptr(),
+                                                idx.data_ptr(), k, 1, k, None, 0,
+                                                torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    torch.cuda.synchronize()
+    rows = list(range(6)) + ([R - 6 + i for i in range(6)] if reps > 1 else [])
+    _check_rows(idx, x, k, rows, oracle.top_k_per_row(x, k, seq_lens=seq, rows=rows))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("R", [32, 33])
+def test_gpu_split_threshold(R):
+    """Either side of the row count where the split stops (its parts over
+    two per CU): the wrapper allocates the workspace only up to it; both
+    give the oracle's sets."""
+    from flaggems_vllm import _native
+
+    print(f"\n[case] top-k split threshold R={R}", flush=True)
+    V, k = 262144, 512
+    split = _native.lib().fgv_top_k_per_row_workspace_bytes(R, V, k) > 0
+    assert split == (16 * R <= 2 * torch.cuda.get_device_properties(0).multi_processor_count)
+    buf, logits, seq = _decode_case(R, V, k, seed=77)
+    _run_decode(buf, logits, seq, k, 1, list(range(0, R, 9)) + [R - 1])
