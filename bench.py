@@ -36,7 +36,7 @@ def parse_args():
     ap.add_argument("--config", type=int, default=2, help="main-op workload c0..c4 (default c2)")
     ap.add_argument("--op", choices=["main", "inv_rope", "gather", "rmsnorm", "indexer",
                                      "slot_mapping", "mla", "indexer_k", "indexer_k_gather", "mqa_logits",
-                                     "paged_mqa_logits", "topk", "copy"],
+                                     "paged_mqa_logits", "topk", "einsum", "copy"],
                     default="main",
                     help="copy: torch device copy of 512 MiB, the HBM calibration kernel")
     ap.add_argument("--tma", action="store_true", help="inv_rope: packed UE8M0 scales")
@@ -55,6 +55,9 @@ def parse_args():
                     help="topk: top_k_per_row at the reference benchmark's largest decode shape (496 x 262144, "
                          "k 512), its full-vocabulary prefill (64 x 129280, k 1024) or its many short rows "
                          "(16383 x 4095, row stride 4352, k 512)")
+    ap.add_argument("--einsum-case", default="flash,8192",
+                    help="einsum: group,b with group flash (h 8, r 4096, d 1024) or pro (h 16, r 7168, d 1024) "
+                         "and b the batch (the reference benchmark's groups and batches 1..32768)")
     ap.add_argument("--cpu-sample-tokens", type=int, default=8192)
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="repeat the CPU sample until this much CPU time is spent (min 3 runs)")
@@ -643,6 +646,42 @@ def main():
         lg_cpu = torch.as_strided(buf_cpu, (R, V), (s0, 1))[:nr].contiguous()
         cpu_case = (lambda: torch.topk(lg_cpu, k, dim=1, largest=True, sorted=False), nr, "rows/s",
                     f"first {nr} of {R} rows: torch.topk on the CPU (the reference test's reference)")
+    elif args.op == "einsum":
+        # the block-FP8 grouped projection at the reference benchmark's shapes
+        # (benchmark/test_fp8_einsum.py: (h, r, d) groups flash / pro, batches 1..32768)
+        grp, eb = args.einsum_case.split(",")
+        H, R, D = {"flash": (8, 4096, 1024), "pro": (16, 7168, 1024)}[grp]
+        Bt = int(eb)
+        g = torch.Generator().manual_seed(0)
+
+        def codes(*shape):
+            c = torch.randint(0, 256, shape, generator=g, dtype=torch.uint8)
+            c[(c & 0x7F) == 0x7F] = 0x38
+            return c.view(torch.float8_e4m3fn)
+
+        x_cpu, y_cpu = codes(Bt, H, R), codes(H, D, R)
+        xs_cpu = torch.ldexp(torch.ones(Bt, H, R // 128), torch.randint(-12, -5, (Bt, H, R // 128), generator=g))
+        ys_cpu = torch.rand(H, D // 128, R // 128, generator=g) * 2 ** -6 + 2 ** -9
+        T = Bt
+        bytes_call = Bt * H * R + Bt * H * (R // 128) * 4 + H * D * R + H * (D // 128) * (R // 128) * 4 + Bt * H * D * 2
+        flops_call = 2 * Bt * H * R * D
+
+        def make_step(i):
+            x, xs, y, ys = x_cpu.to(dev), xs_cpu.to(dev), y_cpu.to(dev), ys_cpu.to(dev)
+            out = torch.empty((Bt, H, D), dtype=torch.bfloat16, device=dev)
+            return lambda: flaggems_vllm.fp8_einsum("bhr,hdr->bhd", x, xs, y, ys, out=out)
+
+        kernel = "fp8_einsum_skinny_kernel" if Bt <= 64 else "fp8_einsum_tile_kernel"
+        workload = f"{grp}_b{Bt}"
+        config = {"workload": f"fp8_einsum 'bhr,hdr->bhd' {grp}: b {Bt}, h {H}, r {R}, d {D}, e4m3fn x and y, "
+                              f"float32 128 / 128x128 block scales, bf16 out",
+                  "b": Bt, "h": H, "r": R, "d": D, "flops_per_call": flops_call}
+        nb = max(1, min(Bt, 16))
+        xd = x_cpu[:nb].float() * xs_cpu[:nb].repeat_interleave(128, dim=2)
+        yd = (y_cpu.float() * ys_cpu.repeat_interleave(128, dim=1).repeat_interleave(128, dim=2))
+        cpu_case = (lambda: torch.einsum("bhr,hdr->bhd", xd, yd), nb, "rows/s",
+                    f"first {nb} of {Bt} rows: the reference test's dequantise-then-einsum in float32 on the CPU "
+                    f"(dequantisation outside the timing)")
     elif args.op == "copy":
         n = 512 << 20
         src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
@@ -675,7 +714,7 @@ def main():
 
     n_sets = 1
     if args.op in ("main", "gather", "rmsnorm", "indexer", "mla", "inv_rope", "indexer_k", "indexer_k_gather",
-                   "paged_mqa_logits", "topk"):
+                   "paged_mqa_logits", "topk", "einsum"):
         step, n_sets = rotating(make_step, bytes_call)
     if n_sets == 1:
         config["input_sets"] = "one input set"
@@ -690,7 +729,7 @@ def main():
     if args.op == "mla":
         config["mfma_tflops"] = flops_call / t_kernel / 1e12
         config["mfma_frac_of_bf16_dense_peak"] = flops_call / t_kernel / 2.5e15
-    if args.op in ("mqa_logits", "paged_mqa_logits"):
+    if args.op in ("mqa_logits", "paged_mqa_logits", "einsum"):
         config["mfma_tflops"] = flops_call / t_kernel / 1e12
         config["mfma_frac_of_fp8_dense_peak"] = flops_call / t_kernel / 5.0e15
     traffic = measured_traffic(kernel, workload)
@@ -707,7 +746,8 @@ def main():
         "vs_baseline": None,
         "dtype": {"mla": "bf16", "slot_mapping": "int64", "copy": "u8", "indexer_k_gather": "u8",
                   "mqa_logits": "fp4 x fp8 -> f32" if args.fp4 else "fp8 -> f32",
-                  "paged_mqa_logits": "fp4 x fp8 -> f32" if args.fp4 else "fp8 -> f32"}.get(args.op, "f32"),
+                  "paged_mqa_logits": "fp4 x fp8 -> f32" if args.fp4 else "fp8 -> f32",
+                  "einsum": "fp8 -> f32 -> bf16"}.get(args.op, "f32"),
         "data": ("synthetic: seeded q ~ N(0,1)/10 bf16, cache NoPE ~ N(0,0.1) quantised to e4m3 + "
                  "E8M0 per 64, RoPE ~ N(0,0.1) bf16, uniform indices and top-k lengths, sink ~ N(0,1)"
                  if args.op == "mla" else
@@ -719,6 +759,9 @@ def main():
                  if args.op in ("mqa_logits", "paged_mqa_logits") else
                  "synthetic: seeded N(0,1) float32 logits, as the reference's benchmark draws them"
                  if args.op == "topk" else
+                 "synthetic: seeded uniform finite e4m3fn codes, power-of-two x scales 2^-12..2^-6, "
+                 "y block scales U[2^-9, 2^-9 + 2^-6)"
+                 if args.op == "einsum" else
                  "synthetic: seeded N(0,1) bf16 q/kv, fp32 cos/sin (theta 1e4), vLLM-style paged slots"),
         "config": config,
         "kernel_us": t_kernel * 1e6,
@@ -734,7 +777,7 @@ def main():
         "roofline": ({"bound": "mfma", "achieved": flops_call / t_kernel / 1e12, "peak": 5000.0,
                       "unit": "TFLOP/s", "frac": flops_call / t_kernel / 5.0e15, "traffic": traffic,
                       "kernel": kernel, "peak_note": "MI355X dense FP8 MFMA"}
-                     if args.op == "mqa_logits" else
+                     if args.op == "mqa_logits" or (args.op == "einsum" and flops_call / bytes_call > 625) else
                      {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                       "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic,
                       "kernel": kernel}),

@@ -1,0 +1,393 @@
+// gfx950 block-scaled FP8 einsum 'bhr,hdr->bhd': the grouped output
+// projection that consumes fused_inv_rope_fp8_quant's e4m3fn activations and
+// per-128 scales.
+//
+// Reference: src/flaggems_vllm/ops/fp8_einsum.py:20-115 (checks :41-97; the
+// work goes to a Hopper block-FP8 batched GEMM), test
+// tests/test_fp8_einsum.py:124-156 (the dequantise-then-einsum oracle):
+//   out[b,h,d] = sum_r (x[b,h,r] xs[b,h,r/128]) (y[h,d,r] ys[h,d/128,r/128])
+// with x, y e4m3fn, xs, ys float32, r and d multiples of 128, output bf16,
+// fp16 or fp32.
+//
+// Each 128-wide K block is one v_mfma_f32_16x16x128_f8f6f4 per 16 x 16
+// output tile: the MFMA forms the block's exact-input partial sum P (e4m3fn
+// products are exact in binary32; the 128-term sum is binary32), and the
+// accumulator takes P * (xs[row] * ys) with one FMA per element.  Register
+// images (the same instruction as the sparse indexer's logits): lane
+// (c, g) = (l % 16, l / 16) holds operand row c, bytes 16g..16g+15 and
+// 64+16g..64+16g+15 of the K block; the accumulator holds output rows
+// 4g..4g+3 of column c.
+//
+// Two kernels:
+//   - skinny (b <= 64, or rows not 16-byte aligned, or r = 0): fragments
+//     straight from memory, the K blocks dealt round-robin to KS waves of a
+//     workgroup and their partials summed in LDS; y (the weights) streams
+//     from HBM once, x is re-read from L2;
+//   - tiled (larger b): 128 x 128 output tiles over four waves (64 x 64
+//     each), the K block's x and y tiles double-buffered in LDS.
+// The result depends only on the inputs: a fixed K-block order per wave and
+// a fixed order over waves.
+#include "fgv_device.h"
+#include "fgv_host.h"
+
+namespace fgv {
+namespace {
+
+typedef int v8i_t __attribute__((ext_vector_type(8)));
+typedef float v4f_t __attribute__((ext_vector_type(4)));
+
+constexpr int kBlockK = 128;   // K block (one scale block, one MFMA)
+constexpr int kTile = 128;     // tiled kernel: output tile rows and columns
+constexpr int kPitch = 144;    // LDS bytes per staged row (128 + 16)
+constexpr int kSkinnyRows = 64;
+
+struct EinsumArgs {
+    const uint8_t* x;      // x[b, h, r] bytes, r contiguous
+    int64_t x_sb, x_sh;
+    const float* xs;       // xs[b, h, r / 128]
+    int64_t xs_sb, xs_sh, xs_sk;
+    const uint8_t* y;      // y[h, d, r] bytes, r contiguous
+    int64_t y_sh, y_sd;
+    const float* ys;       // ys[h, d / 128, r / 128]
+    int64_t ys_sh, ys_sn, ys_sk;
+    void* out;             // out[b, h, d] elements
+    int64_t o_sb, o_sh, o_sd;
+    int32_t b, h, d, nkb;  // nkb = r / 128
+};
+
+enum OutType { kOutBf16 = 0, kOutF16 = 1, kOutF32 = 2 };
+
+__device__ __forceinline__ v4f_t mfma_fp8(v8i_t a, v8i_t b) {
+    const v4f_t z = {0.f, 0.f, 0.f, 0.f};
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, z, 0, 0, 0, 0, 0, 0);  // zero scales: plain FP8 MFMA
+}
+
+// Lane (c, g)'s operand image of one K block of a row (row points at the block).
+template <bool ALIGNED>
+__device__ __forceinline__ v8i_t load_frag(const uint8_t* row, int g) {
+    uint4 lo, hi;
+    if constexpr (ALIGNED) {
+        lo = *reinterpret_cast<const uint4*>(row + 16 * g);
+        hi = *reinterpret_cast<const uint4*>(row + 64 + 16 * g);
+    } else {
+        __builtin_memcpy(&lo, row + 16 * g, 16);
+        __builtin_memcpy(&hi, row + 64 + 16 * g, 16);
+    }
+    const v8i_t v = {(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+    return v;
+}
+
+__device__ __forceinline__ v8i_t lds_frag(const uint8_t* row, int g) {
+    const uint4 lo = *reinterpret_cast<const uint4*>(row + 16 * g);
+    const uint4 hi = *reinterpret_cast<const uint4*>(row + 64 + 16 * g);
+    const v8i_t v = {(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+    return v;
+}
+
+template <int OUT>
+__device__ __forceinline__ void store_out(void* out, int64_t i, float v) {
+    if constexpr (OUT == kOutBf16)
+        reinterpret_cast<uint16_t*>(out)[i] = (uint16_t)(pack_bf16x2(v, 0.f) & 0xffffu);
+    else if constexpr (OUT == kOutF16)
+        reinterpret_cast<_Float16*>(out)[i] = (_Float16)v;
+    else
+        reinterpret_cast<float*>(out)[i] = v;
+}
+
+// ---- skinny: rows m0 .. m0 + 16 MT of x (one workgroup row of the grid),
+// columns n0 .. n0 + 16 NW of y, head blockIdx.z; wave w takes the K blocks
+// w, w + KS, ...
+template <int MT, int NW, int KS, bool ALIGNED, int OUT>
+__global__ void __launch_bounds__(64 * KS) fp8_einsum_skinny_kernel(EinsumArgs a) {
+    __shared__ v4f_t part[KS > 1 ? KS - 1 : 1][MT * NW][64];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int c = lane & 15, g = lane >> 4;
+    const int n0 = blockIdx.x * 16 * NW;
+    const int m0 = blockIdx.y * 16 * MT;
+    const int hh = blockIdx.z;
+    const uint8_t* arow[MT];
+    bool aok[MT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+        const int m = m0 + 16 * i + c;
+        aok[i] = m < a.b;
+        arow[i] = a.x + (int64_t)hh * a.x_sh + (int64_t)(aok[i] ? m : 0) * a.x_sb;
+    }
+    const uint8_t* brow[NW];
+#pragma unroll
+    for (int j = 0; j < NW; ++j)
+        brow[j] = a.y + (int64_t)hh * a.y_sh + (int64_t)(n0 + 16 * j + c) * a.y_sd;
+    const float* ysp = a.ys + (int64_t)hh * a.ys_sh + (int64_t)(n0 / kBlockK) * a.ys_sn;
+    const float* xsp[MT][4];
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int m = m0 + 16 * i + 4 * g + q;
+            xsp[i][q] = m < a.b ? a.xs + (int64_t)hh * a.xs_sh + (int64_t)m * a.xs_sb : nullptr;
+        }
+
+    v4f_t acc[MT][NW];
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < NW; ++j)
+            acc[i][j] = v4f_t{0.f, 0.f, 0.f, 0.f};
+
+    const v8i_t zero = {0, 0, 0, 0, 0, 0, 0, 0};
+    v8i_t A[MT], B[NW];
+    auto fetch = [&](int kb) {
+        const int64_t k0 = (int64_t)kb * kBlockK;
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+            A[i] = aok[i] ? load_frag<ALIGNED>(arow[i] + k0, g) : zero;
+#pragma unroll
+        for (int j = 0; j < NW; ++j)
+            B[j] = load_frag<ALIGNED>(brow[j] + k0, g);
+    };
+    if (w < a.nkb)
+        fetch(w);
+    for (int kb = w; kb < a.nkb; kb += KS) {
+        v8i_t Ac[MT], Bc[NW];
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+            Ac[i] = A[i];
+#pragma unroll
+        for (int j = 0; j < NW; ++j)
+            Bc[j] = B[j];
+        if (kb + KS < a.nkb)
+            fetch(kb + KS);  // the next block's loads fly over this block's MFMAs
+        const float sy = ysp[(int64_t)kb * a.ys_sk];
+        float sx[MT][4];
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                sx[i][q] = xsp[i][q] ? xsp[i][q][(int64_t)kb * a.xs_sk] * sy : 0.f;
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+            for (int j = 0; j < NW; ++j) {
+                const v4f_t p = mfma_fp8(Ac[i], Bc[j]);
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    acc[i][j][q] = fmaf(p[q], sx[i][q], acc[i][j][q]);
+            }
+    }
+
+    if constexpr (KS > 1) {
+        if (w > 0) {
+#pragma unroll
+            for (int i = 0; i < MT; ++i)
+#pragma unroll
+                for (int j = 0; j < NW; ++j)
+                    part[w - 1][i * NW + j][lane] = acc[i][j];
+        }
+        __syncthreads();
+        if (w != 0)
+            return;
+#pragma unroll
+        for (int v = 0; v < KS - 1; ++v)
+#pragma unroll
+            for (int i = 0; i < MT; ++i)
+#pragma unroll
+                for (int j = 0; j < NW; ++j)
+                    acc[i][j] += part[v][i * NW + j][lane];
+    }
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int m = m0 + 16 * i + 4 * g + q;
+            if (m >= a.b)
+                continue;
+#pragma unroll
+            for (int j = 0; j < NW; ++j)
+                store_out<OUT>(a.out, (int64_t)m * a.o_sb + (int64_t)hh * a.o_sh + (int64_t)(n0 + 16 * j + c) * a.o_sd,
+                               acc[i][j][q]);
+        }
+}
+
+// ---- tiled: output tile (mt, nt) of head blockIdx.y, 128 x 128, waves in a
+// 2 x 2 grid of 64 x 64 quadrants; x and y rows 16-byte aligned, r > 0.
+// Consecutive workgroups share a column tile (the same y rows).
+template <int OUT>
+__global__ void __launch_bounds__(256) fp8_einsum_tile_kernel(EinsumArgs a, int32_t mtiles) {
+    __shared__ __attribute__((aligned(16))) uint8_t As[2][kTile * kPitch];
+    __shared__ __attribute__((aligned(16))) uint8_t Bs[2][kTile * kPitch];
+    __shared__ __attribute__((aligned(16))) float xss[2][kTile];
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const int c = lane & 15, g = lane >> 4;
+    const int wm = w >> 1, wn = w & 1;
+    const int hh = blockIdx.y;
+    const int mt = blockIdx.x % mtiles, nt = blockIdx.x / mtiles;
+    const int m0 = mt * kTile, n0 = nt * kTile;
+
+    // staging: thread t moves 16-byte part (t & 7) of rows (t >> 3) + 32 i, i < 4
+    const int srow = t >> 3, spart = t & 7;
+    const uint8_t* ag[4];
+    bool aok[4];
+    const uint8_t* bg[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int m = m0 + srow + 32 * i;
+        aok[i] = m < a.b;
+        ag[i] = a.x + (int64_t)hh * a.x_sh + (int64_t)(aok[i] ? m : 0) * a.x_sb + 16 * spart;
+        bg[i] = a.y + (int64_t)hh * a.y_sh + (int64_t)(n0 + srow + 32 * i) * a.y_sd + 16 * spart;
+    }
+    const float* xsg =
+        (t < kTile && m0 + t < a.b) ? a.xs + (int64_t)hh * a.xs_sh + (int64_t)(m0 + t) * a.xs_sb : nullptr;
+    const float* ysg = a.ys + (int64_t)hh * a.ys_sh + (int64_t)nt * a.ys_sn;
+
+    uint4 ra[4], rb[4];
+    float rx = 0.f;
+    auto fetch = [&](int kb) {
+        const int64_t k0 = (int64_t)kb * kBlockK;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            ra[i] = aok[i] ? *reinterpret_cast<const uint4*>(ag[i] + k0) : make_uint4(0, 0, 0, 0);
+            rb[i] = *reinterpret_cast<const uint4*>(bg[i] + k0);
+        }
+        rx = xsg ? xsg[(int64_t)kb * a.xs_sk] : 0.f;
+    };
+    auto stash = [&](int s) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            *reinterpret_cast<uint4*>(&As[s][(srow + 32 * i) * kPitch + 16 * spart]) = ra[i];
+            *reinterpret_cast<uint4*>(&Bs[s][(srow + 32 * i) * kPitch + 16 * spart]) = rb[i];
+        }
+        if (t < kTile)
+            xss[s][t] = rx;
+    };
+
+    v4f_t acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            acc[i][j] = v4f_t{0.f, 0.f, 0.f, 0.f};
+
+    fetch(0);
+    stash(0);
+    __syncthreads();
+    for (int kb = 0; kb < a.nkb; ++kb) {
+        const int s = kb & 1;
+        if (kb + 1 < a.nkb)
+            fetch(kb + 1);
+        const float sy = ysg[(int64_t)kb * a.ys_sk];
+        v8i_t A[4], B[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            A[i] = lds_frag(&As[s][(wm * 64 + 16 * i + c) * kPitch], g);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            B[j] = lds_frag(&Bs[s][(wn * 64 + 16 * j + c) * kPitch], g);
+        float sx[4][4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float4 v = *reinterpret_cast<const float4*>(&xss[s][wm * 64 + 16 * i + 4 * g]);
+            sx[i][0] = v.x * sy;
+            sx[i][1] = v.y * sy;
+            sx[i][2] = v.z * sy;
+            sx[i][3] = v.w * sy;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const v4f_t p = mfma_fp8(A[i], B[j]);
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    acc[i][j][q] = fmaf(p[q], sx[i][q], acc[i][j][q]);
+            }
+        if (kb + 1 < a.nkb)
+            stash(s ^ 1);
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int m = m0 + wm * 64 + 16 * i + 4 * g + q;
+            if (m >= a.b)
+                continue;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                store_out<OUT>(a.out,
+                               (int64_t)m * a.o_sb + (int64_t)hh * a.o_sh + (int64_t)(n0 + wn * 64 + 16 * j + c) * a.o_sd,
+                               acc[i][j][q]);
+        }
+}
+
+template <int MT, bool ALIGNED, int OUT>
+void launch_skinny(const EinsumArgs& a, hipStream_t st) {
+    constexpr int NW = 2, KS = 4;
+    const dim3 grid((unsigned)(a.d / (16 * NW)), (unsigned)((a.b + 16 * MT - 1) / (16 * MT)), (unsigned)a.h);
+    hipLaunchKernelGGL((fp8_einsum_skinny_kernel<MT, NW, KS, ALIGNED, OUT>), grid, dim3(64 * KS), 0, st, a);
+}
+
+template <bool ALIGNED, int OUT>
+void launch_skinny_rows(const EinsumArgs& a, hipStream_t st) {
+    if (a.b <= 16)
+        launch_skinny<1, ALIGNED, OUT>(a, st);
+    else if (a.b <= 32)
+        launch_skinny<2, ALIGNED, OUT>(a, st);
+    else if (a.b <= 48)
+        launch_skinny<3, ALIGNED, OUT>(a, st);
+    else
+        launch_skinny<4, ALIGNED, OUT>(a, st);
+}
+
+template <int OUT>
+int launch_einsum(const EinsumArgs& a, bool aligned, hipStream_t st) {
+    if (!aligned)
+        launch_skinny_rows<false, OUT>(a, st);
+    else if (a.b <= kSkinnyRows || a.nkb == 0)
+        launch_skinny_rows<true, OUT>(a, st);
+    else {
+        const int32_t mtiles = (a.b + kTile - 1) / kTile;
+        const dim3 grid((unsigned)(mtiles * (a.d / kTile)), (unsigned)a.h);
+        hipLaunchKernelGGL(fp8_einsum_tile_kernel<OUT>, grid, dim3(256), 0, st, a, mtiles);
+    }
+    return launch_status();
+}
+
+}  // namespace
+}  // namespace fgv
+
+extern "C" int fgv_fp8_einsum_bhr_hdr(const uint8_t* x, int64_t x_sb, int64_t x_sh, const float* xs, int64_t xs_sb,
+                                      int64_t xs_sh, int64_t xs_sk, const uint8_t* y, int64_t y_sh, int64_t y_sd,
+                                      const float* ys, int64_t ys_sh, int64_t ys_sn, int64_t ys_sk, int64_t b,
+                                      int64_t h, int64_t r, int64_t d, void* out, int64_t o_sb, int64_t o_sh,
+                                      int64_t o_sd, int32_t out_dtype, void* stream) {
+    using namespace fgv;
+    if (b < 0 || h < 0 || r < 0 || d < 0)
+        return fail(FGV_E_BAD_SHAPE, "negative size");
+    if (r % kBlockK || d % kBlockK)
+        return fail(FGV_E_BAD_SHAPE, "r and d must be multiples of 128");
+    if (out_dtype < kOutBf16 || out_dtype > kOutF32)
+        return fail(FGV_E_BAD_SHAPE, "out_dtype must be 0 (bf16), 1 (fp16) or 2 (fp32)");
+    if (b > 0x7fffffffLL || h > 65535 || r / kBlockK > 0x7fffffffLL || d > 0x7fffffffLL)
+        return fail(FGV_E_TOO_LARGE, "b, r and d must fit in int32 and h in 65535");
+    if (b == 0 || h == 0 || d == 0)
+        return FGV_OK;
+    if (!out || (r > 0 && (!x || !xs || !y || !ys)))
+        return fail(FGV_E_NULL_POINTER, "null tensor");
+    const size_t osz = out_dtype == kOutF32 ? 4 : 2;
+    if (!aligned(out, osz) || (r > 0 && (!aligned(xs, 4) || !aligned(ys, 4))))
+        return fail(FGV_E_MISALIGNED, "out and scales must be aligned to their element size");
+    EinsumArgs a{x,  x_sb,  x_sh,  xs,  xs_sb, xs_sh, xs_sk, y,          y_sh,       y_sd,      ys,
+                 ys_sh, ys_sn, ys_sk, out, o_sb,  o_sh,  o_sd,  (int32_t)b, (int32_t)h, (int32_t)d, (int32_t)(r / kBlockK)};
+    const bool al = aligned(x, 16) && aligned(y, 16) && x_sb % 16 == 0 && x_sh % 16 == 0 && y_sh % 16 == 0 &&
+                    y_sd % 16 == 0;
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    switch (out_dtype) {
+    case kOutBf16:
+        return launch_einsum<kOutBf16>(a, al, st);
+    case kOutF16:
+        return launch_einsum<kOutF16>(a, al, st);
+    default:
+        return launch_einsum<kOutF32>(a, al, st);
+    }
+}

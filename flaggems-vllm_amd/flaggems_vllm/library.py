@@ -6,8 +6,8 @@ These registrations expose the same ops to torch.compile and graph capture as
 opaque custom ops: the schemas declare what each op writes, namely ``q`` and
 ``k_cache`` for the main op (alias-annotated ``Tensor(a0!) q``, ``Tensor(a2!) k_cache``), ``out``
 for the gather, ``slot_mapping`` for the slot mapping, ``kv_cache`` for the
-indexer key insert and ``k_fp8`` / ``k_fp8_scale`` for its gather, ``indices`` for the top-k per row
-(the index-row ops write only what they return).  The fake (meta)
+indexer key insert and ``k_fp8`` / ``k_fp8_scale`` for its gather, ``indices`` for the top-k per row,
+``out`` for ``fp8_einsum_out`` (the index-row ops and ``fp8_einsum`` write only what they return).  The fake (meta)
 implementations give the output shapes and strides the real ops return.
 Each registered op calls the same wrapper, so argument checks and errors are
 the wrapper's.
@@ -27,6 +27,7 @@ from .ops import (
     compute_slot_mapping_parallel,
     cp_gather_indexer_k_quant_cache,
     dequantize_and_gather_k_cache,
+    fp8_einsum,
     fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert,
     fused_indexer_q_rope_quant,
     fused_inv_rope_fp8_quant,
@@ -222,6 +223,28 @@ def _(logits, row_starts, row_ends, indices, num_rows, stride0, stride1, top_k):
     return None
 
 
+@_op("fp8_einsum")
+def _fp8_einsum(equation: str, x: torch.Tensor, xs: torch.Tensor, y: torch.Tensor, ys: torch.Tensor,
+                block_size: List[int], output_dtype: torch.dtype) -> torch.Tensor:
+    return fp8_einsum(equation, x, xs, y, ys, block_size, output_dtype)
+
+
+@_fp8_einsum.register_fake
+def _(equation, x, xs, y, ys, block_size, output_dtype):
+    return x.new_empty((x.shape[0], x.shape[1], y.shape[1]), dtype=output_dtype)
+
+
+@_op("fp8_einsum_out", ("out",))
+def _fp8_einsum_out(equation: str, x: torch.Tensor, xs: torch.Tensor, y: torch.Tensor, ys: torch.Tensor,
+                    block_size: List[int], output_dtype: torch.dtype, out: torch.Tensor) -> None:
+    fp8_einsum(equation, x, xs, y, ys, block_size, output_dtype, out=out)
+
+
+@_fp8_einsum_out.register_fake
+def _(equation, x, xs, y, ys, block_size, output_dtype, out):
+    return None
+
+
 REGISTERED: List[str] = [
     "fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert",
     "fused_inv_rope_fp8_quant",
@@ -235,4 +258,6 @@ REGISTERED: List[str] = [
     "combine_topk_swa_indices",
     "top_k_per_row_decode",
     "top_k_per_row_prefill",
+    "fp8_einsum",
+    "fp8_einsum_out",
 ]

@@ -1,9 +1,10 @@
-"""DeepSeek-V4 attention pre-processing ops (reference: src/flaggems_vllm/ops/__init__.py:23-38, 55, 58-65, 78, 142-143)."""
+"""DeepSeek-V4 attention pre-processing ops (reference: src/flaggems_vllm/ops/__init__.py:23-38, 55, 57, 58-65, 78, 142-143, 187)."""
 from .cp_gather_indexer_k_quant_cache import cp_gather_indexer_k_quant_cache
 from .deepseek_v4_attention_combine_topk_swa_indices import combine_topk_swa_indices
 from .deepseek_v4_attention_compute_global_topk_indices_and_lens import compute_global_topk_indices_and_lens
 from .deepseek_v4_attention_dequantize_and_gather_k_cache import dequantize_and_gather_k_cache
 from .deepseek_v4_attention_fused_q_kv_rmsnorm import fused_q_kv_rmsnorm
+from .fp8_einsum import fp8_einsum
 from .fp8_fp4_mqa_logits import fp8_fp4_mqa_logits
 from .fp8_fp4_paged_mqa_logits import fp8_fp4_paged_mqa_logits
 from .flash_mla_with_kvcache import FlashMLASchedMeta, flash_mla_with_kvcache, get_mla_metadata
@@ -23,6 +24,7 @@ __all__ = [
     "compute_slot_mapping_parallel",
     "cp_gather_indexer_k_quant_cache",
     "flash_mla_with_kvcache",
+    "fp8_einsum",
     "fp8_fp4_mqa_logits",
     "fp8_fp4_paged_mqa_logits",
     "get_mla_metadata",

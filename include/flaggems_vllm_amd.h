@@ -508,10 +508,11 @@ int fgv_combine_topk_swa_indices(
  * Values equal to the k-th largest are taken lowest index first, so the set
  * is a function of the values; NaN orders above +inf (as torch.topk).
  * workspace (16-byte aligned, fgv_top_k_per_row_workspace_bytes of it) lets
- * rows wider than 16384 values be split into parts and merged when there are
- * fewer rows than the GPU has CUs; without it (NULL or too small), or with
- * more rows, each row is streamed by one workgroup.  The reference allocates
- * its split's buffers per call likewise (ops/top_k_per_row_decode.py:1303-1312).
+ * few rows of 12 or more 16384-value parts (192K+ values; at most two parts
+ * per CU in all) be split into parts and merged; without it (NULL or too
+ * small), or otherwise, each row is streamed by one workgroup.  The index
+ * sets are the same either way.  The reference allocates its split's
+ * buffers per call likewise (ops/top_k_per_row_decode.py:1303-1312).
  */
 int fgv_top_k_per_row_decode(const float* logits, int64_t stride0, int64_t stride1, int64_t num_rows,
                              int64_t width, int64_t next_n, const int32_t* seq_lens, int32_t* indices,
@@ -525,6 +526,29 @@ int fgv_top_k_per_row_prefill(const float* logits, int64_t stride0, int64_t stri
 /* Workspace bytes the top-k entry points can use for these sizes on the
  * current device (0: they use none). */
 int64_t fgv_top_k_per_row_workspace_bytes(int64_t num_rows, int64_t width, int64_t top_k);
+
+/*
+ * Block-scaled FP8 einsum 'bhr,hdr->bhd' (the grouped output projection that
+ * consumes fgv_inv_rope_fp8_quant's codes and per-128 scales).
+ *
+ * Replaces flaggems_vllm.fp8_einsum (reference: src/flaggems_vllm/ops/fp8_einsum.py:20-115,
+ * which hands the work to a Hopper block-FP8 batched GEMM):
+ *   out[b,h,d] = sum_r (x[b,h,r] xs[b,h,r/128]) (y[h,d,r] ys[h,d/128,r/128])
+ * x [b,h,r] and y [h,d,r] are e4m3fn codes with r contiguous; xs [b,h,r/128]
+ * and ys [h,d/128,r/128] float32; every stride is in elements of its tensor.
+ * r and d are multiples of 128.  out [b,h,d] is bf16 (out_dtype 0), fp16
+ * (1) or fp32 (2), rounded to nearest even; r = 0 writes zeros, b, h or
+ * d = 0 writes nothing.  Each 128-wide K block's partial sum is formed in
+ * binary32 and accumulated times xs * ys in binary32, in a fixed order, so
+ * the result depends only on the inputs.  Rows of x and y need no
+ * alignment (16-byte aligned ones take the fast paths).
+ */
+int fgv_fp8_einsum_bhr_hdr(const uint8_t* x, int64_t x_stride_b, int64_t x_stride_h, const float* xs,
+                           int64_t xs_stride_b, int64_t xs_stride_h, int64_t xs_stride_k, const uint8_t* y,
+                           int64_t y_stride_h, int64_t y_stride_d, const float* ys, int64_t ys_stride_h,
+                           int64_t ys_stride_n, int64_t ys_stride_k, int64_t b, int64_t h, int64_t r, int64_t d,
+                           void* out, int64_t out_stride_b, int64_t out_stride_h, int64_t out_stride_d,
+                           int32_t out_dtype, void* stream);
 
 #ifdef __cplusplus
 }

@@ -161,6 +161,8 @@ def lib():
             _P, _I64, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P]
         L.oracle_top_k_per_row.restype = None
         L.oracle_top_k_per_row.argtypes = [_P, _I64, _I64, _I64, _I64, _P, _P, _P, _I64, _I64, _P]
+        L.oracle_fp8_einsum.restype = None
+        L.oracle_fp8_einsum.argtypes = [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P]
         _lib = L
     return _lib
 
@@ -577,3 +579,21 @@ def top_k_per_row(logits, k, row_starts=None, row_ends=None, seq_lens=None, next
                                en.data_ptr() if en is not None else None,
                                sl.data_ptr() if sl is not None else None, int(next_n), int(k), out.data_ptr())
     return out
+
+
+def fp8_einsum(x, xs, y, ys):
+    """Binary64 'bhr,hdr->bhd' of flaggems_vllm.fp8_einsum and an error bound
+    for a binary32 implementation before the output rounding ([B, H, D]
+    float64 each); CPU or device tensors of any layout (e4m3fn or uint8
+    codes, float32 scales)."""
+    xb = _cpu(x).view(torch.uint8).contiguous()
+    yb = _cpu(y).view(torch.uint8).contiguous()
+    xsc = _cpu(xs, torch.float32).contiguous()
+    ysc = _cpu(ys, torch.float32).contiguous()
+    B, H, R = xb.shape
+    D = yb.shape[1]
+    out = torch.empty(B, H, D, dtype=torch.float64)
+    bound = torch.empty_like(out)
+    lib().oracle_fp8_einsum(xb.data_ptr(), xsc.data_ptr(), yb.data_ptr(), ysc.data_ptr(), B, H, R, D,
+                            out.data_ptr(), bound.data_ptr())
+    return out, bound

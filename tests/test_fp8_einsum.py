@@ -1,0 +1,464 @@
+"""fp8_einsum 'bhr,hdr->bhd': block-scaled FP8 grouped projection.
+
+Reference: src/flaggems_vllm/ops/fp8_einsum.py:20-115; tests
+tests/test_fp8_einsum.py:44-156 (shapes, the per-token / per-block UE8M0 casts,
+the dequantise-then-einsum reference), :180-330 (layouts, output dtypes,
+repeated calls, empty shapes, invalid inputs); benchmark
+benchmark/test_fp8_einsum.py (the same (h, r, d) groups and batches).
+
+The reference's own bar is loose (rtol 0.2, atol 5 % of the largest output).
+Here each output is checked against the binary64 oracle (exact block sums)
+within the oracle's bound plus the output type's rounding.  The bound models
+the FP8 matrix instruction's block sum (groups of 8 products truncated to 13
+bits below the group's largest exponent, pinned on the GPU by crafted sums)
+and binary32 scaling and accumulation.
+"""
+
+import pytest
+import torch
+
+import oracle
+
+DEV = torch.device("cuda:0")
+E4M3 = torch.float8_e4m3fn
+
+# (h, r, d) groups and batches of the reference test and benchmark
+HRD = {"flash": (8, 4096, 1024), "pro": (16, 7168, 1024)}
+BATCHES = (1, 4, 8, 16, 32, 64, 128)
+
+
+# ------------------------------------------------------------ inputs ----
+
+def _ceil_pow2(s):
+    """Round positive float32 scales up to a power of two (the UE8M0 grid)."""
+    bits = s.view(torch.int32)
+    e = ((bits >> 23) & 0xFF) + ((bits & 0x7FFFFF) != 0).int()
+    return (e.clamp(1, 254) << 23).view(torch.float32)
+
+
+def _cast_rows(x, pow2=True):
+    """Per-row, per-128-column e4m3fn cast (the reference test's per-token cast)."""
+    m, n = x.shape
+    v = x.float().view(m, n // 128, 128)
+    sf = v.abs().amax(2).clamp(min=1e-4) / 448.0
+    sf = _ceil_pow2(sf) if pow2 else sf
+    return (v / sf[..., None]).to(E4M3).view(m, n), sf
+
+
+def _cast_blocks(y, pow2=True):
+    """Per-128x128-block e4m3fn cast (the reference test's per-block cast)."""
+    m, n = y.shape
+    v = y.float().view(m // 128, 128, n // 128, 128)
+    sf = v.abs().amax((1, 3)).clamp(min=1e-4) / 448.0
+    sf = _ceil_pow2(sf) if pow2 else sf
+    return (v / sf[:, None, :, None]).to(E4M3).view(m, n), sf
+
+
+def make_inputs(b, h, r, d, seed=0, pow2=True):
+    """The reference test's construction (bf16 normals, UE8M0 casts), on the CPU."""
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(b, h, r, generator=g).bfloat16()
+    y = torch.randn(h, d, r, generator=g).bfloat16()
+    xq, xs = _cast_rows(x.view(-1, r), pow2)
+    ys, yq = [], []
+    for i in range(h):
+        q, s = _cast_blocks(y[i], pow2)
+        yq.append(q)
+        ys.append(s)
+    return xq.view(b, h, r), xs.view(b, h, r // 128), torch.stack(yq), torch.stack(ys)
+
+
+def random_inputs(b, h, r, d, seed=0):
+    """Every finite e4m3fn code (NaN codes replaced), scales 2^-12 .. 2^-5 and
+    general float32 ones: a wider spread than the casts give."""
+    g = torch.Generator().manual_seed(seed)
+
+    def codes(*shape):
+        c = torch.randint(0, 256, shape, generator=g, dtype=torch.uint8)
+        c[(c & 0x7F) == 0x7F] = 0x38
+        return c.view(E4M3)
+
+    xs = torch.ldexp(torch.ones(b, h, r // 128), torch.randint(-12, -5, (b, h, r // 128), generator=g))
+    ys = torch.rand(h, d // 128, r // 128, generator=g) * 2 ** -6 + 2 ** -9
+    return codes(b, h, r), xs, codes(h, d, r), ys
+
+
+def torch_reference(x, xs, y, ys):
+    """The reference test's dequantise-then-einsum, in float64 on the CPU."""
+    x, xs, y, ys = (t.cpu() for t in (x, xs, y, ys))
+    xd = x.double() * xs.double().repeat_interleave(128, dim=2)
+    yd = y.double() * ys.double().repeat_interleave(128, dim=1).repeat_interleave(128, dim=2)
+    return torch.einsum("bhr,hdr->bhd", xd, yd)
+
+
+def within(got, exact, bound, dtype):
+    """|got - exact| <= bound + the output type's rounding of a value within bound."""
+    got = got.detach().double().cpu()
+    rel = {torch.bfloat16: 2.0 ** -8, torch.float16: 2.0 ** -11, torch.float32: 0.0}[dtype]
+    absr = 2.0 ** -25 if dtype == torch.float16 else 0.0
+    lim = bound + rel * (exact.abs() + bound) + absr
+    err = (got - exact).abs()
+    bad = ~(err <= lim)
+    return int(bad.sum()), float((err / lim.clamp(min=1e-300)).max())
+
+
+# ------------------------------------------------------------ oracle ----
+
+def test_oracle_known_answers():
+    # x codes 0x38 (1.0), y codes 0x40 (2.0): each block sums 256; scales 0.5 and 3
+    b, h, r, d = 2, 3, 256, 128
+    x = torch.full((b, h, r), 0x38, dtype=torch.uint8).view(E4M3)
+    y = torch.full((h, d, r), 0x40, dtype=torch.uint8).view(E4M3)
+    xs = torch.full((b, h, 2), 0.5)
+    ys = torch.full((h, 1, 2), 3.0)
+    out, bound = oracle.fp8_einsum(x, xs, y, ys)
+    assert torch.all(out == 2 * 256 * 1.5)
+    # the second block alone: its scale only
+    xs2 = xs.clone()
+    xs2[..., 0] = 0
+    out2, _ = oracle.fp8_einsum(x, xs2, y, ys)
+    assert torch.all(out2 == 256 * 1.5)
+    # signs and the smallest subnormal (0x01 = 2^-9) times the largest code (0x7e = 448)
+    x3 = torch.zeros((1, 1, 128), dtype=torch.uint8)
+    x3[0, 0, 0], x3[0, 0, 1] = 0x01, 0x80 | 0x7E
+    y3 = torch.zeros((1, 128, 128), dtype=torch.uint8)
+    y3[0, :, 0], y3[0, :, 1] = 0x7E, 0x7E
+    out3, _ = oracle.fp8_einsum(x3.view(E4M3), torch.ones(1, 1, 1), y3.view(E4M3), torch.ones(1, 1, 1))
+    assert torch.all(out3 == 448 * 2.0 ** -9 - 448 * 448)
+    assert torch.all(bound > 0)
+
+
+@pytest.mark.parametrize("pow2", [True, False])
+def test_oracle_against_torch_float64(pow2):
+    """The oracle equals the reference test's dequantise-then-einsum done in
+    float64 by torch (an independent route) up to binary64 rounding."""
+    x, xs, y, ys = make_inputs(3, 2, 512, 256, seed=1, pow2=pow2)
+    out, _ = oracle.fp8_einsum(x, xs, y, ys)
+    ref = torch_reference(x, xs, y, ys)
+    assert torch.allclose(out, ref, rtol=1e-13, atol=1e-9)
+    x, xs, y, ys = random_inputs(2, 3, 384, 128, seed=2)
+    out, _ = oracle.fp8_einsum(x, xs, y, ys)
+    ref = torch_reference(x, xs, y, ys)
+    assert torch.allclose(out, ref, rtol=1e-13, atol=1e-12)
+
+
+def test_oracle_bound_holds_for_a_binary32_model_and_catches_a_dropped_block():
+    """A binary32 implementation (float32 block sums, float32 scale product,
+    float32 accumulation) stays inside the bound; dropping one K block (a
+    plausible indexing slip) does not."""
+    x, xs, y, ys = random_inputs(4, 2, 1024, 256, seed=3)
+    exact, bound = oracle.fp8_einsum(x, xs, y, ys)
+    xf, yf = x.float(), y.float()
+    acc = torch.zeros(4, 2, 256)
+    dropped = torch.zeros(4, 2, 256)
+    for kb in range(8):
+        p = torch.einsum("bhr,hdr->bhd", xf[..., kb * 128:(kb + 1) * 128], yf[..., kb * 128:(kb + 1) * 128])
+        s = xs[..., kb:kb + 1] * ys[:, :, kb].repeat_interleave(128, 1)[None]
+        acc = acc + p * s
+        if kb != 5:
+            dropped = dropped + p * s
+    assert within(acc, exact, bound, torch.float32)[0] == 0
+    assert within(dropped, exact, bound, torch.float32)[0] > 0
+
+
+def test_c_abi_rejects_bad_arguments():
+    from flaggems_vllm import _native
+
+    f = _native.lib().fgv_fp8_einsum_bhr_hdr
+    p = 1 << 12  # never dereferenced
+
+    def call(b=2, h=2, r=256, d=128, out_dtype=0, x=p, out=p):
+        return f(x, 512, 256, p, 4, 2, 1, p, 32768, 256, p, 2, 2, 1, b, h, r, d, out, 256, 128, 1, out_dtype, None)
+
+    assert call(r=200) == -2 and call(d=64) == -2     # multiples of 128
+    assert call(b=-1) == -2 and call(out_dtype=3) == -2
+    assert call(x=None) == -1 and call(out=None) == -1
+    assert call(out=p + 1) == -3                       # bf16 output misaligned
+    assert call(b=0) == 0 and call(d=0) == 0           # nothing to do
+
+
+def test_wrapper_checks_on_the_cpu():
+    """The checks that precede any device work raise what the reference raises."""
+    from flaggems_vllm import fp8_einsum
+
+    x = torch.zeros(2, 2, 256, dtype=E4M3)
+    xs = torch.zeros(2, 2, 2)
+    y = torch.zeros(2, 128, 256, dtype=E4M3)
+    ys = torch.zeros(2, 1, 2)
+    with pytest.raises(NotImplementedError):
+        fp8_einsum("abc,cde->abe", x, xs, y, ys)
+    with pytest.raises(NotImplementedError):
+        fp8_einsum("bhr,hdr->bhd", x, xs, y, ys, block_size=[64, 128])
+    with pytest.raises(NotImplementedError):
+        fp8_einsum("bhr,hdr->bhd", x, xs, y, ys, output_dtype=torch.int8)
+    with pytest.raises(ValueError):
+        fp8_einsum("bhr,hdr->bhd", x[0], xs, y, ys)
+    with pytest.raises(NotImplementedError):  # not a GPU tensor
+        fp8_einsum("bhr,hdr->bhd", x, xs, y, ys)
+
+
+# --------------------------------------------------------------- GPU ----
+
+def _run(x, xs, y, ys, dtype=torch.bfloat16, out=None):
+    from flaggems_vllm import fp8_einsum
+
+    res = fp8_einsum("bhr,hdr->bhd", x, xs, y, ys, output_dtype=dtype, out=out)
+    torch.cuda.synchronize()
+    return res
+
+
+def _check(res, x, xs, y, ys, dtype, rows=None):
+    if rows is not None:
+        x, xs, res = x[rows], xs[rows], res[rows]
+    exact, bound = oracle.fp8_einsum(x, xs, y, ys)
+    nbad, worst = within(res, exact, bound, dtype)
+    assert nbad == 0, f"{nbad} outputs outside the bound (worst {worst:.3g} x the limit)"
+
+
+def _model_block_sum(xv, yv):
+    """The MFMA's 128-term sum as the oracle's bound models it: groups of 8
+    consecutive K, each product truncated toward zero to a multiple of
+    2^(E_g - 13) (E_g the group's largest exponent sum, zero and subnormal
+    codes at -6), the group sums added exactly (the crafted sums below keep
+    them exact in binary32)."""
+    import math as _m
+
+    def ex(v):
+        return -6 if abs(v) < 2.0 ** -6 else _m.frexp(abs(v))[1] - 1
+
+    total = 0.0
+    for g0 in range(0, 128, 8):
+        eg = max(ex(xv[i]) + ex(yv[i]) for i in range(g0, g0 + 8))
+        unit = 2.0 ** (eg - 13)
+        for i in range(g0, g0 + 8):
+            p = xv[i] * yv[i]
+            total += _m.copysign(_m.floor(abs(p) / unit) * unit, p)
+    return total
+
+
+@pytest.mark.gpu
+def test_gpu_mfma_block_sum_model():
+    """Crafted one-block sums through the op (unit scales, float32 out) pin
+    what the oracle's bound assumes of the 16x16x128 FP8 MFMA: which products
+    share a group, the 13-bit window below the group's largest exponent sum,
+    truncation toward zero, and group sums kept to binary32 precision."""
+    from flaggems_vllm import fp8_einsum
+
+    rows = []
+    for p in (0, 5, 8, 31, 64, 100, 127):          # membership: 256 at p, 2^-6 at j
+        for j in (0, 3, 7, 8, 15, 16, 30, 63, 64, 71, 72, 101, 120, 126):
+            if j != p:
+                xv, yv = [0.0] * 128, [0.0] * 128
+                xv[p], yv[p], xv[j], yv[j] = 256.0, 1.0, 2.0 ** -6, 1.0
+                rows.append((xv, yv))
+    for v in (2.0 ** -5, 2.0 ** -6, 1.5 * 2.0 ** -5, -1.5 * 2.0 ** -5, 1.875 * 2.0 ** -5, -2.0 ** -6):
+        xv, yv = [0.0] * 128, [0.0] * 128          # window and truncation
+        xv[0], yv[0], xv[1], yv[1] = 256.0, 1.0, v, 1.0
+        rows.append((xv, yv))
+    for v in (4.0, 8.0, 12.0, 24.0):               # 448 * 448 (exponent sum 16) + v
+        xv, yv = [0.0] * 128, [0.0] * 128
+        xv[0], yv[0], xv[1], yv[1] = 448.0, 448.0, v, 1.0
+        rows.append((xv, yv))
+    xv = [256.0] + [0.125] * 127                   # the small products of other groups survive
+    yv = [256.0] + [0.125] * 127
+    rows.append((xv, yv))
+    xv = [448.0, -448.0, 1.0] + [0.0] * 125        # a cancelled group keeps no trace of its small product
+    yv = [448.0, 448.0, 1.0] + [0.0] * 125
+    rows.append((xv, yv))
+    n = len(rows)
+    D = 128 * ((n + 127) // 128)
+    x = torch.tensor([r[0] for r in rows]).to(E4M3).view(n, 1, 128)
+    y = torch.zeros(D, 128)
+    for j, r in enumerate(rows):
+        y[j] = torch.tensor(r[1])
+    y = y.to(E4M3).view(1, D, 128)
+    out = fp8_einsum("bhr,hdr->bhd", x.to(DEV), torch.ones(n, 1, 1, device=DEV), y.to(DEV),
+                     torch.ones(1, D // 128, 1, device=DEV), output_dtype=torch.float32)
+    torch.cuda.synchronize()
+    got = out[:, 0].cpu()
+    for j, (xr, yr) in enumerate(rows):
+        xq = x[j, 0].float().tolist()
+        yq = y[0, j].float().tolist()
+        assert float(got[j, j]) == _model_block_sum(xq, yq), (j, float(got[j, j]), _model_block_sum(xq, yq))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("group", ["flash", "pro"])
+@pytest.mark.parametrize("b", BATCHES)
+def test_gpu_reference_shapes(group, b):
+    """The reference test's and benchmark's shapes (quick-mode batches), its
+    input construction; every output against the oracle."""
+    h, r, d = HRD[group]
+    print(f"\n[case] fp8_einsum {group} b={b}", flush=True)
+    x, xs, y, ys = make_inputs(b, h, r, d, seed=b)
+    res = _run(x.to(DEV), xs.to(DEV), y.to(DEV), ys.to(DEV))
+    assert res.shape == (b, h, d) and res.dtype == torch.bfloat16
+    _check(res, x, xs, y, ys, torch.bfloat16)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("group", ["flash", "pro"])
+@pytest.mark.parametrize("b", [4096])
+def test_gpu_large_batches(group, b):
+    """The reference's large batches (the smallest of its non-quick set), random codes: 97
+    rows (the first, the last and a spread) against the oracle, every output
+    against torch's float32 einsum of the dequantised tensors on the GPU
+    within the reference test's tolerance."""
+    h, r, d = HRD[group]
+    print(f"\n[case] fp8_einsum {group} b={b}", flush=True)
+    x, xs, y, ys = random_inputs(b, h, r, d, seed=7)
+    dx, dxs, dy, dys = x.to(DEV), xs.to(DEV), y.to(DEV), ys.to(DEV)
+    res = _run(dx, dxs, dy, dys)
+    rows = torch.cat([torch.arange(0, b, b // 95), torch.tensor([b - 1])])
+    _check(res, x, xs, y, ys, torch.bfloat16, rows=rows)
+    for hh in range(h):  # float32 reference head by head (bounded memory)
+        xd = dx[:, hh].float() * dxs[:, hh].repeat_interleave(128, dim=1)
+        yd = dy[hh].float() * dys[hh].repeat_interleave(128, dim=0).repeat_interleave(128, dim=1)
+        ref = xd @ yd.t().contiguous()
+        atol = max(5e-2, ref.abs().max().item() * 5e-2)
+        torch.testing.assert_close(res[:, hh].float(), ref, rtol=2e-1, atol=atol)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("b", [65, 127, 129, 200, 256, 300])
+def test_gpu_tiled_edges(b):
+    """Batches either side of the skinny/tiled switch (64) and ragged tiles
+    (b not a multiple of 128), random codes, h = 3, r = 1280, d = 384."""
+    print(f"\n[case] fp8_einsum tiled edges b={b}", flush=True)
+    x, xs, y, ys = random_inputs(b, 3, 1280, 384, seed=b)
+    res = _run(x.to(DEV), xs.to(DEV), y.to(DEV), ys.to(DEV))
+    _check(res, x, xs, y, ys, torch.bfloat16)
+
+
+def _layout(kind, x, xs, y, ys):
+    b, h, r = x.shape
+    if kind == "vllm":  # head-major x, scales with strides (1, 8, 4)-like
+        x = x.permute(1, 0, 2).contiguous().permute(1, 0, 2)
+        s = torch.empty_strided(xs.shape, (1, xs.shape[0] * xs.shape[2], xs.shape[0]), device=xs.device)
+        s.copy_(xs)
+        xs = s
+    elif kind == "strided":  # every other d row of a wider y, every other scale column
+        d = y.shape[1]
+        buf = torch.empty((h, 2 * d, r), dtype=y.dtype, device=y.device)
+        buf[:, ::2] = y
+        y = buf[:, ::2]
+        sbuf = torch.empty((*ys.shape[:-1], 2 * ys.shape[-1]), device=ys.device)
+        sbuf[..., ::2] = ys
+        ys = sbuf[..., ::2]
+    elif kind == "unaligned":  # x rows one byte off: stride r + 1, base + 1
+        buf = torch.empty((b, h, r + 1), dtype=x.dtype, device=x.device)
+        buf[..., 1:] = x
+        x = buf[..., 1:]
+    return x, xs, y, ys
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("layout", ["contiguous", "vllm", "strided", "unaligned"])
+@pytest.mark.parametrize("b", [3, 200])
+def test_gpu_out_and_layout(dtype, layout, b):
+    """The reference's layout test (:180-220) on both kernels: strided and
+    unaligned inputs, a padded output whose padding stays untouched."""
+    print(f"\n[case] fp8_einsum layout {layout} {dtype} b={b}", flush=True)
+    h, r, d = 2, 256, 128
+    x, xs, y, ys = make_inputs(b, h, r, d, seed=5)
+    dx, dxs, dy, dys = _layout(layout, x.to(DEV), xs.to(DEV), y.to(DEV), ys.to(DEV))
+    out_buf = torch.full((b, h, d + 16), float("nan"), dtype=dtype, device=DEV)
+    out = out_buf[..., :d]
+    res = _run(dx, dxs, dy, dys, dtype, out=out)
+    assert res is out
+    _check(res, x, xs, y, ys, dtype)
+    assert torch.isnan(out_buf[..., d:]).all()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_gpu_repeated_calls_are_identical(dtype):
+    """The reference's repeated-call test (:223-230): the same output every
+    call (nothing accumulates into out), bit for bit."""
+    x, xs, y, ys = (t.to(DEV) for t in make_inputs(3, 1, 4096, 128, seed=9))
+    out = torch.full((3, 1, 128), 123.0, device=DEV, dtype=dtype)
+    first = _run(x, xs, y, ys, dtype, out=out).clone()
+    for _ in range(3):
+        _run(x, xs, y, ys, dtype, out=out)
+        assert torch.equal(out, first)
+    _check(first, *(t.cpu() for t in (x, xs, y, ys)), dtype)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape", [(0, 2, 128, 128), (2, 0, 128, 128), (2, 2, 128, 0), (2, 2, 0, 128)])
+def test_gpu_empty(shape):
+    """Empty shapes (:244-257): r = 0 gives zeros, other empty outputs stay empty."""
+    from flaggems_vllm import fp8_einsum
+
+    b, h, r, d = shape
+    x = torch.empty((b, h, r), device=DEV, dtype=E4M3)
+    xs = torch.empty((b, h, r // 128), device=DEV)
+    y = torch.empty((h, d, r), device=DEV, dtype=E4M3)
+    ys = torch.empty((h, d // 128, r // 128), device=DEV)
+    out = torch.full((b, h, d), float("nan"), device=DEV, dtype=torch.bfloat16)
+    res = fp8_einsum("bhr,hdr->bhd", x, xs, y, ys, out=out)
+    torch.cuda.synchronize()
+    assert res is out
+    torch.testing.assert_close(res, torch.zeros_like(res))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", ["equation", "block_size", "dtype", "scales", "scale_shape", "shape", "stride",
+                                  "out_shape", "out_dtype", "out_overlap", "out_alias", "grad"])
+def test_gpu_invalid_inputs(case):
+    """The reference's invalid-input cases (:260-312), same exception types."""
+    from flaggems_vllm import fp8_einsum
+
+    x, xs, y, ys = (t.to(DEV) for t in make_inputs(2, 2, 256, 128))
+    equation, kwargs, error = "bhr,hdr->bhd", {}, ValueError
+    if case == "equation":
+        equation, error = "abc,cde->abe", NotImplementedError
+    elif case == "block_size":
+        kwargs, error = {"block_size": [64, 128]}, NotImplementedError
+    elif case == "dtype":
+        x, error = x.to(torch.bfloat16), NotImplementedError
+    elif case == "scales":
+        xs, error = xs.to(torch.int32), NotImplementedError
+    elif case == "scale_shape":
+        xs = xs[..., :1]
+    elif case == "shape":
+        y = y[:1]
+    elif case == "stride":
+        x, error = x.transpose(0, 2).contiguous().transpose(0, 2), NotImplementedError
+    elif case == "out_shape":
+        kwargs["out"] = torch.empty((2, 2, 64), device=DEV, dtype=torch.bfloat16)
+    elif case == "out_dtype":
+        kwargs["out"] = torch.empty((2, 2, 128), device=DEV, dtype=torch.float32)
+    elif case == "out_overlap":
+        kwargs["out"] = torch.empty((1, 2, 128), device=DEV, dtype=torch.bfloat16).expand(2, -1, -1)
+    elif case == "out_alias":
+        kwargs["out"] = x.view(torch.bfloat16)
+    elif case == "grad":
+        xs, error = xs.requires_grad_(), NotImplementedError
+    with pytest.raises(error):
+        fp8_einsum(equation, x, xs, y, ys, **kwargs)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("tma", [False])
+def test_gpu_after_inv_rope_fp8_quant(tma):
+    """The data path: fused_inv_rope_fp8_quant's codes and float32 scales
+    ([T, G, hpg * 512] with strides (d, T d, 1), [T, G, hpg * 4]) go straight
+    into fp8_einsum as x and xs with a block-quantised weight."""
+    import flaggems_vllm
+    from flaggems_vllm.testing import make_yarn_cos_sin_cache
+
+    T, H, G, d = 200, 16, 2, 256
+    hpg = H // G
+    g = torch.Generator().manual_seed(11)
+    o = torch.randn(T, H, 512, generator=g).bfloat16().to(DEV)
+    pos = torch.randint(0, 4096, (T,), generator=g).to(DEV)
+    cs = make_yarn_cos_sin_cache(4096).to(DEV)
+    xq, xsc = flaggems_vllm.fused_inv_rope_fp8_quant(o, pos, cs, G, hpg, tma_aligned_scales=tma)
+    assert xq.shape == (T, G, hpg * 512) and xsc.shape == (T, G, hpg * 4)
+    w = torch.randn(G, d, hpg * 512, generator=g).bfloat16()
+    wq, ws = zip(*(_cast_blocks(w[i]) for i in range(G)))
+    wq, ws = torch.stack(wq), torch.stack(ws)
+    res = _run(xq, xsc, wq.to(DEV), ws.to(DEV))
+    _check(res, xq.cpu(), xsc.cpu(), wq, ws, torch.bfloat16)
