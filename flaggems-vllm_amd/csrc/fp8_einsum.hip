@@ -19,12 +19,13 @@
 // 4g..4g+3 of column c.
 //
 // Two kernels:
-//   - skinny (b <= 64, or rows not 16-byte aligned, or r = 0): fragments
+//   - skinny (b <= 128, or rows not 16-byte aligned, or r = 0): fragments
 //     straight from memory, the K blocks dealt round-robin to KS waves of a
 //     workgroup and their partials summed in LDS; y (the weights) streams
 //     from HBM once, x is re-read from L2;
-//   - tiled (larger b): 128 x 128 output tiles over four waves (64 x 64
-//     each), the K block's x and y tiles double-buffered in LDS.
+//   - tiled (larger b): 256 x 128 (or 128 x 128) output tiles over eight
+//     (four) waves of 64 x 64, the K blocks' x and y tiles streamed through a
+//     three-stage LDS ring by LDS DMA, two blocks ahead of the MFMAs.
 // The result depends only on the inputs: a fixed K-block order per wave and
 // a fixed order over waves.
 #include "fgv_device.h"
@@ -38,8 +39,11 @@ typedef float v4f_t __attribute__((ext_vector_type(4)));
 
 constexpr int kBlockK = 128;   // K block (one scale block, one MFMA)
 constexpr int kTile = 128;     // tiled kernel: output tile rows and columns
-constexpr int kPitch = 144;    // LDS bytes per staged row (128 + 16)
-constexpr int kSkinnyRows = 64;
+constexpr int kSkinnyRows = 128;  // b up to this: the skinny kernel
+constexpr int kSkinnyKS = 4;      // skinny: waves per workgroup (K split)
+constexpr int kSkinnyNW1 = 2;     // skinny: 16-column tiles per wave for b <= 16, 32, 128
+constexpr int kSkinnyNW2 = 2;
+constexpr int kSkinnyNW4 = 2;
 
 struct EinsumArgs {
     const uint8_t* x;      // x[b, h, r] bytes, r contiguous
@@ -96,7 +100,8 @@ __device__ __forceinline__ void store_out(void* out, int64_t i, float v) {
 
 // ---- skinny: rows m0 .. m0 + 16 MT of x (one workgroup row of the grid),
 // columns n0 .. n0 + 16 NW of y, head blockIdx.z; wave w takes the K blocks
-// w, w + KS, ...
+// w, w + KS, ...  A block's fragments and scales are loaded while the
+// previous block's MFMAs run.
 template <int MT, int NW, int KS, bool ALIGNED, int OUT>
 __global__ void __launch_bounds__(64 * KS) fp8_einsum_skinny_kernel(EinsumArgs a) {
     __shared__ v4f_t part[KS > 1 ? KS - 1 : 1][MT * NW][64];
@@ -118,13 +123,17 @@ __global__ void __launch_bounds__(64 * KS) fp8_einsum_skinny_kernel(EinsumArgs a
     for (int j = 0; j < NW; ++j)
         brow[j] = a.y + (int64_t)hh * a.y_sh + (int64_t)(n0 + 16 * j + c) * a.y_sd;
     const float* ysp = a.ys + (int64_t)hh * a.ys_sh + (int64_t)(n0 / kBlockK) * a.ys_sn;
-    const float* xsp[MT][4];
+    // the lane's output rows m0 + 16 i + 4 g + q: their xs rows (row 0 stands in past b, scaled by 0)
+    const float* xsh = a.xs + (int64_t)hh * a.xs_sh;
+    int32_t xrow[MT][4];
+    bool xok[MT][4];
 #pragma unroll
     for (int i = 0; i < MT; ++i)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int m = m0 + 16 * i + 4 * g + q;
-            xsp[i][q] = m < a.b ? a.xs + (int64_t)hh * a.xs_sh + (int64_t)m * a.xs_sb : nullptr;
+            xok[i][q] = m < a.b;
+            xrow[i][q] = xok[i][q] ? m : 0;
         }
 
     v4f_t acc[MT][NW];
@@ -136,6 +145,7 @@ __global__ void __launch_bounds__(64 * KS) fp8_einsum_skinny_kernel(EinsumArgs a
 
     const v8i_t zero = {0, 0, 0, 0, 0, 0, 0, 0};
     v8i_t A[MT], B[NW];
+    float X[MT][4], Y = 0.f;
     auto fetch = [&](int kb) {
         const int64_t k0 = (int64_t)kb * kBlockK;
 #pragma unroll
@@ -144,26 +154,31 @@ __global__ void __launch_bounds__(64 * KS) fp8_einsum_skinny_kernel(EinsumArgs a
 #pragma unroll
         for (int j = 0; j < NW; ++j)
             B[j] = load_frag<ALIGNED>(brow[j] + k0, g);
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                X[i][q] = xsh[(int64_t)xrow[i][q] * a.xs_sb + (int64_t)kb * a.xs_sk];
+        Y = ysp[(int64_t)kb * a.ys_sk];
     };
     if (w < a.nkb)
         fetch(w);
     for (int kb = w; kb < a.nkb; kb += KS) {
         v8i_t Ac[MT], Bc[NW];
+        float sx[MT][4];
 #pragma unroll
         for (int i = 0; i < MT; ++i)
             Ac[i] = A[i];
 #pragma unroll
         for (int j = 0; j < NW; ++j)
             Bc[j] = B[j];
-        if (kb + KS < a.nkb)
-            fetch(kb + KS);  // the next block's loads fly over this block's MFMAs
-        const float sy = ysp[(int64_t)kb * a.ys_sk];
-        float sx[MT][4];
 #pragma unroll
         for (int i = 0; i < MT; ++i)
 #pragma unroll
             for (int q = 0; q < 4; ++q)
-                sx[i][q] = xsp[i][q] ? xsp[i][q][(int64_t)kb * a.xs_sk] * sy : 0.f;
+                sx[i][q] = xok[i][q] ? X[i][q] * Y : 0.f;
+        if (kb + KS < a.nkb)
+            fetch(kb + KS);  // the next block's loads fly over this block's MFMAs
 #pragma unroll
         for (int i = 0; i < MT; ++i)
 #pragma unroll
@@ -208,56 +223,113 @@ __global__ void __launch_bounds__(64 * KS) fp8_einsum_skinny_kernel(EinsumArgs a
         }
 }
 
-// ---- tiled: output tile (mt, nt) of head blockIdx.y, 128 x 128, waves in a
-// 2 x 2 grid of 64 x 64 quadrants; x and y rows 16-byte aligned, r > 0.
-// Consecutive workgroups share a column tile (the same y rows).
-template <int OUT>
-__global__ void __launch_bounds__(256) fp8_einsum_tile_kernel(EinsumArgs a, int32_t mtiles) {
-    __shared__ __attribute__((aligned(16))) uint8_t As[2][kTile * kPitch];
-    __shared__ __attribute__((aligned(16))) uint8_t Bs[2][kTile * kPitch];
-    __shared__ __attribute__((aligned(16))) float xss[2][kTile];
-    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+// ---- tiled: output tile (mt, nt) of head blockIdx.y, 64 MW rows x 128
+// columns over 2 MW waves (64 x 64 each, MW along rows, 2 along columns); x
+// and y rows 16-byte aligned, r > 0.  The K blocks stream through a ring of
+// kStages LDS stages by LDS DMA (global_load_lds_dwordx4: each wave
+// instruction lands 64 lanes x 16 bytes = 8 rows contiguously), issued two
+// blocks ahead of the MFMAs.  Rows are stored unpadded with their 16-byte
+// chunks swizzled, chunk c of row r at (c ^ ((r >> 1) & 7)), so that the 16
+// rows of a fragment read hit 16 distinct chunk slots.  Rows of x past b read
+// row b - 1: they only feed outputs that are not stored.
+constexpr int kStages = 3;
+
+// LDS DMA of 16 (4) bytes per lane: lane l's bytes land at LDS address
+// lds + 16 l (4 l).  Issued as inline assembly so that the compiler, which
+// cannot tell the stages apart, does not wait for every DMA in flight before
+// each LDS read; the kernel waits for its own (vmcnt) and has no other vector
+// memory loads in flight while DMAs are.
+__device__ __forceinline__ void dma16(const void* src, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds) : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(const void* src, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(lds) : "memory", "m0");
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+__device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
+
+// s_waitcnt operand: vector memory operations outstanding <= n (expcnt and
+// lgkmcnt not waited for; gfx9 encoding vmcnt bits 3:0 and 15:14).
+constexpr int wait_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+// Workgroup barrier over LDS work only: __syncthreads' fence would wait for
+// every outstanding LDS DMA, the next blocks' included; each wave waits for
+// its own DMAs of the block explicitly before this.  The empty asm statements
+// keep the compiler from moving memory accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));  // lgkmcnt(0): this wave's LDS accesses done
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+template <int MW>
+struct TileShape {
+    static constexpr int kRows = 64 * MW, kWaves = 2 * MW;
+    static constexpr int kABytes = kRows * kBlockK, kBBytes = kTile * kBlockK;
+    static constexpr int kXOff = kABytes + kBBytes, kYOff = kXOff + 4 * kRows;
+    static constexpr int kStageBytes = kYOff + 256;  // + 64 copies of the block's ys
+    static constexpr int kAInstr = kABytes / 1024 / kWaves, kBInstr = kBBytes / 1024 / kWaves;  // DMAs per wave per block
+    static constexpr int kXInstr = kRows / 64;                                                   // xs: waves 0 .. kXInstr-1
+    static constexpr int kYWave = kWaves - 1;                                                    // ys: the last wave
+    static_assert(kAInstr >= 1 && kBInstr >= 1 && kXInstr < kWaves, "tile shape");
+};
+
+template <int MW, int OUT>
+__global__ void __launch_bounds__(128 * MW) fp8_einsum_tile_kernel(EinsumArgs a, int32_t mtiles) {
+    using S = TileShape<MW>;
+    // the three stages are separate objects, named statically by each step of
+    // the 3-unrolled loop, so that the compiler sees that a step's LDS reads
+    // do not touch the stages the DMAs in flight write
+    __shared__ __attribute__((aligned(1024))) uint8_t st0[S::kStageBytes];
+    __shared__ __attribute__((aligned(1024))) uint8_t st1[S::kStageBytes];
+    __shared__ __attribute__((aligned(1024))) uint8_t st2[S::kStageBytes];
+
+    const int t = threadIdx.x, lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const int c = lane & 15, g = lane >> 4;
-    const int wm = w >> 1, wn = w & 1;
+    const int wm = wave >> 1, wn = wave & 1;
     const int hh = blockIdx.y;
     const int mt = blockIdx.x % mtiles, nt = blockIdx.x / mtiles;
-    const int m0 = mt * kTile, n0 = nt * kTile;
+    const int m0 = mt * S::kRows, n0 = nt * kTile;
 
-    // staging: thread t moves 16-byte part (t & 7) of rows (t >> 3) + 32 i, i < 4
-    const int srow = t >> 3, spart = t & 7;
-    const uint8_t* ag[4];
-    bool aok[4];
-    const uint8_t* bg[4];
+    // this lane's DMA sources: A instruction j of the wave covers tile rows
+    // 8 (wave * kAInstr + j) + lane / 8, physical chunk lane % 8
+    const int lrow = lane >> 3, lchunk = lane & 7;
+    const uint8_t* asrc[S::kAInstr];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int m = m0 + srow + 32 * i;
-        aok[i] = m < a.b;
-        ag[i] = a.x + (int64_t)hh * a.x_sh + (int64_t)(aok[i] ? m : 0) * a.x_sb + 16 * spart;
-        bg[i] = a.y + (int64_t)hh * a.y_sh + (int64_t)(n0 + srow + 32 * i) * a.y_sd + 16 * spart;
+    for (int j = 0; j < S::kAInstr; ++j) {
+        const int row = 8 * (wave * S::kAInstr + j) + lrow;
+        const int m = min(m0 + row, a.b - 1);
+        asrc[j] = a.x + (int64_t)hh * a.x_sh + (int64_t)m * a.x_sb + 16 * swz(row, lchunk);
     }
-    const float* xsg =
-        (t < kTile && m0 + t < a.b) ? a.xs + (int64_t)hh * a.xs_sh + (int64_t)(m0 + t) * a.xs_sb : nullptr;
+    const uint8_t* bsrc[S::kBInstr];
+#pragma unroll
+    for (int j = 0; j < S::kBInstr; ++j) {
+        const int row = 8 * (wave * S::kBInstr + j) + lrow;
+        bsrc[j] = a.y + (int64_t)hh * a.y_sh + (int64_t)(n0 + row) * a.y_sd + 16 * swz(row, lchunk);
+    }
+    const float* xsrc = a.xs + (int64_t)hh * a.xs_sh + (int64_t)min(m0 + 64 * wave + lane, a.b - 1) * a.xs_sb;
     const float* ysg = a.ys + (int64_t)hh * a.ys_sh + (int64_t)nt * a.ys_sn;
+    // this wave's DMAs per block (the waitcnt operand while the next block flies)
+    const bool xw = wave < S::kXInstr, yw = wave == S::kYWave;
 
-    uint4 ra[4], rb[4];
-    float rx = 0.f;
-    auto fetch = [&](int kb) {
+    auto issue = [&](int kb, uint8_t* st) {
         const int64_t k0 = (int64_t)kb * kBlockK;
+        const uint32_t base = lds_addr(st);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            ra[i] = aok[i] ? *reinterpret_cast<const uint4*>(ag[i] + k0) : make_uint4(0, 0, 0, 0);
-            rb[i] = *reinterpret_cast<const uint4*>(bg[i] + k0);
-        }
-        rx = xsg ? xsg[(int64_t)kb * a.xs_sk] : 0.f;
-    };
-    auto stash = [&](int s) {
+        for (int j = 0; j < S::kAInstr; ++j)
+            dma16(asrc[j] + k0, base + 1024 * (wave * S::kAInstr + j));
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            *reinterpret_cast<uint4*>(&As[s][(srow + 32 * i) * kPitch + 16 * spart]) = ra[i];
-            *reinterpret_cast<uint4*>(&Bs[s][(srow + 32 * i) * kPitch + 16 * spart]) = rb[i];
-        }
-        if (t < kTile)
-            xss[s][t] = rx;
+        for (int j = 0; j < S::kBInstr; ++j)
+            dma16(bsrc[j] + k0, base + S::kABytes + 1024 * (wave * S::kBInstr + j));
+        if (xw)
+            dma4(xsrc + (int64_t)kb * a.xs_sk, base + S::kXOff + 256 * wave);
+        if (yw)
+            dma4(ysg + (int64_t)kb * a.ys_sk, base + S::kYOff);
     };
 
     v4f_t acc[4][4];
@@ -267,25 +339,44 @@ __global__ void __launch_bounds__(256) fp8_einsum_tile_kernel(EinsumArgs a, int3
         for (int j = 0; j < 4; ++j)
             acc[i][j] = v4f_t{0.f, 0.f, 0.f, 0.f};
 
-    fetch(0);
-    stash(0);
-    __syncthreads();
-    for (int kb = 0; kb < a.nkb; ++kb) {
-        const int s = kb & 1;
-        if (kb + 1 < a.nkb)
-            fetch(kb + 1);
-        const float sy = ysg[(int64_t)kb * a.ys_sk];
+    // one K block: wait for this wave's DMAs of block kb (block kb + 1's may
+    // still fly), barrier (everyone's landed; the stage read in the previous
+    // step is free), send block kb + 2 into it, then the MFMAs on `cur`
+    auto step = [&](int kb, const uint8_t* cur, uint8_t* next2) {
+        if (kb + 1 < a.nkb) {
+            if (xw || yw)
+                __builtin_amdgcn_s_waitcnt(wait_vm(S::kAInstr + S::kBInstr + 1));
+            else
+                __builtin_amdgcn_s_waitcnt(wait_vm(S::kAInstr + S::kBInstr));
+        } else {
+            __builtin_amdgcn_s_waitcnt(wait_vm(0));
+        }
+        lds_barrier();
+        if (kb + 2 < a.nkb)
+            issue(kb + 2, next2);
+        const float sy = reinterpret_cast<const float*>(cur + S::kYOff)[lane];
         v8i_t A[4], B[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            A[i] = lds_frag(&As[s][(wm * 64 + 16 * i + c) * kPitch], g);
+        for (int i = 0; i < 4; ++i) {
+            const int row = wm * 64 + 16 * i + c;
+            const uint8_t* rp = cur + row * kBlockK;
+            const uint4 lo = *reinterpret_cast<const uint4*>(rp + 16 * swz(row, g));
+            const uint4 hi = *reinterpret_cast<const uint4*>(rp + 16 * swz(row, 4 + g));
+            A[i] = v8i_t{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+        }
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            B[j] = lds_frag(&Bs[s][(wn * 64 + 16 * j + c) * kPitch], g);
+        for (int j = 0; j < 4; ++j) {
+            const int row = wn * 64 + 16 * j + c;
+            const uint8_t* rp = cur + S::kABytes + row * kBlockK;
+            const uint4 lo = *reinterpret_cast<const uint4*>(rp + 16 * swz(row, g));
+            const uint4 hi = *reinterpret_cast<const uint4*>(rp + 16 * swz(row, 4 + g));
+            B[j] = v8i_t{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+        }
+        const float* xst = reinterpret_cast<const float*>(cur + S::kXOff);
         float sx[4][4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const float4 v = *reinterpret_cast<const float4*>(&xss[s][wm * 64 + 16 * i + 4 * g]);
+            const float4 v = *reinterpret_cast<const float4*>(xst + wm * 64 + 16 * i + 4 * g);
             sx[i][0] = v.x * sy;
             sx[i][1] = v.y * sy;
             sx[i][2] = v.z * sy;
@@ -300,9 +391,17 @@ __global__ void __launch_bounds__(256) fp8_einsum_tile_kernel(EinsumArgs a, int3
                 for (int q = 0; q < 4; ++q)
                     acc[i][j][q] = fmaf(p[q], sx[i][q], acc[i][j][q]);
             }
+    };
+
+    issue(0, st0);
+    if (a.nkb > 1)
+        issue(1, st1);
+    for (int kb = 0; kb < a.nkb; kb += 3) {
+        step(kb, st0, st2);
         if (kb + 1 < a.nkb)
-            stash(s ^ 1);
-        __syncthreads();
+            step(kb + 1, st1, st0);
+        if (kb + 2 < a.nkb)
+            step(kb + 2, st2, st1);
     }
 
 #pragma unroll
@@ -320,9 +419,8 @@ __global__ void __launch_bounds__(256) fp8_einsum_tile_kernel(EinsumArgs a, int3
         }
 }
 
-template <int MT, bool ALIGNED, int OUT>
+template <int MT, int NW, int KS, bool ALIGNED, int OUT>
 void launch_skinny(const EinsumArgs& a, hipStream_t st) {
-    constexpr int NW = 2, KS = 4;
     const dim3 grid((unsigned)(a.d / (16 * NW)), (unsigned)((a.b + 16 * MT - 1) / (16 * MT)), (unsigned)a.h);
     hipLaunchKernelGGL((fp8_einsum_skinny_kernel<MT, NW, KS, ALIGNED, OUT>), grid, dim3(64 * KS), 0, st, a);
 }
@@ -330,13 +428,11 @@ void launch_skinny(const EinsumArgs& a, hipStream_t st) {
 template <bool ALIGNED, int OUT>
 void launch_skinny_rows(const EinsumArgs& a, hipStream_t st) {
     if (a.b <= 16)
-        launch_skinny<1, ALIGNED, OUT>(a, st);
+        launch_skinny<1, kSkinnyNW1, kSkinnyKS, ALIGNED, OUT>(a, st);
     else if (a.b <= 32)
-        launch_skinny<2, ALIGNED, OUT>(a, st);
-    else if (a.b <= 48)
-        launch_skinny<3, ALIGNED, OUT>(a, st);
+        launch_skinny<2, kSkinnyNW2, kSkinnyKS, ALIGNED, OUT>(a, st);
     else
-        launch_skinny<4, ALIGNED, OUT>(a, st);
+        launch_skinny<4, kSkinnyNW4, kSkinnyKS, ALIGNED, OUT>(a, st);
 }
 
 template <int OUT>
@@ -346,9 +442,17 @@ int launch_einsum(const EinsumArgs& a, bool aligned, hipStream_t st) {
     else if (a.b <= kSkinnyRows || a.nkb == 0)
         launch_skinny_rows<true, OUT>(a, st);
     else {
-        const int32_t mtiles = (a.b + kTile - 1) / kTile;
-        const dim3 grid((unsigned)(mtiles * (a.d / kTile)), (unsigned)a.h);
-        hipLaunchKernelGGL(fp8_einsum_tile_kernel<OUT>, grid, dim3(256), 0, st, a, mtiles);
+        // 256-row tiles while they give every CU a workgroup, else 128 rows
+        const int64_t tiles256 = (int64_t)((a.b + 255) / 256) * (a.d / kTile) * a.h;
+        if (tiles256 >= cu_count()) {
+            const int32_t mtiles = (a.b + 255) / 256;
+            hipLaunchKernelGGL((fp8_einsum_tile_kernel<4, OUT>), dim3((unsigned)(mtiles * (a.d / kTile)), (unsigned)a.h),
+                               dim3(512), 0, st, a, mtiles);
+        } else {
+            const int32_t mtiles = (a.b + 127) / 128;
+            hipLaunchKernelGGL((fp8_einsum_tile_kernel<2, OUT>), dim3((unsigned)(mtiles * (a.d / kTile)), (unsigned)a.h),
+                               dim3(256), 0, st, a, mtiles);
+        }
     }
     return launch_status();
 }

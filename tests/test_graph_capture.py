@@ -184,3 +184,16 @@ def test_graph_top_k_per_row():
         run = lambda: (flaggems_vllm.top_k_per_row_decode(lg, 1, seq, idx, 9, lg.stride(0), 1, 512),
                        idx.sort(1).values)[1]
         replay_matches_eager(lambda: idx.fill_(-5), run)
+
+
+def test_graph_fp8_einsum():
+    """fp8_einsum on both kernels (b 4: skinny; b 200: tiled) into a
+    preallocated output; the replays give the eager bytes."""
+    from .test_fp8_einsum import random_inputs
+
+    _say("graph: fp8_einsum")
+    for b in (4, 200):
+        x, xs, y, ys = (t.to(DEV) for t in random_inputs(b, 2, 1024, 256, seed=b))
+        out = torch.empty((b, 2, 256), dtype=torch.bfloat16, device=DEV)
+        run = lambda: flaggems_vllm.fp8_einsum("bhr,hdr->bhd", x, xs, y, ys, out=out)
+        replay_matches_eager(lambda: out.fill_(7.0), run)

@@ -33,6 +33,8 @@ WRITES = {
     "combine_topk_swa_indices": set(),
     "top_k_per_row_decode": {"indices"},
     "top_k_per_row_prefill": {"indices"},
+    "fp8_einsum": set(),
+    "fp8_einsum_out": {"out"},
 }
 
 
@@ -237,3 +239,25 @@ def test_gpu_top_k_per_row_ops():
     _op("top_k_per_row_prefill")(lg, st, seq, b, 6, lg.stride(0), lg.stride(1), 512)
     torch.cuda.synchronize()
     assert torch.equal(a.sort(1).values, b.sort(1).values)
+
+
+@pytest.mark.gpu
+def test_gpu_fp8_einsum_ops():
+    """torch.ops.flaggems_vllm.fp8_einsum / fp8_einsum_out: the function's
+    bytes, fake layout and opcheck."""
+    from .test_fp8_einsum import make_inputs
+
+    x, xs, y, ys = (t.to(DEV) for t in make_inputs(3, 2, 256, 128, seed=4))
+    ref = flaggems_vllm.fp8_einsum("bhr,hdr->bhd", x, xs, y, ys)
+    got = torch.ops.flaggems_vllm.fp8_einsum("bhr,hdr->bhd", x, xs, y, ys, [128, 128], torch.bfloat16)
+    assert torch.equal(got, ref)
+    out = torch.empty_like(ref)
+    torch.ops.flaggems_vllm.fp8_einsum_out("bhr,hdr->bhd", x, xs, y, ys, [128, 128], torch.bfloat16, out)
+    assert torch.equal(out, ref)
+    # opcheck's schema test multiplies float8 inputs, which torch cannot do on
+    # the GPU; the fake-tensor and autograd-registration tests run
+    utils = ("test_faketensor", "test_autograd_registration")
+    torch.library.opcheck(torch.ops.flaggems_vllm.fp8_einsum.default,
+                          ("bhr,hdr->bhd", x, xs, y, ys, [128, 128], torch.float32), test_utils=utils)
+    torch.library.opcheck(torch.ops.flaggems_vllm.fp8_einsum_out.default,
+                          ("bhr,hdr->bhd", x, xs, y, ys, [128, 128], torch.bfloat16, out), test_utils=utils)
