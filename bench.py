@@ -671,7 +671,10 @@ def main():
             out = torch.empty((Bt, H, D), dtype=torch.bfloat16, device=dev)
             return lambda: flaggems_vllm.fp8_einsum("bhr,hdr->bhd", x, xs, y, ys, out=out)
 
-        kernel = "fp8_einsum_skinny_kernel" if Bt <= 64 else "fp8_einsum_tile_kernel"
+        # the launcher's choice (fp8_einsum.hip launch_einsum): skinny up to 64 rows, and up to 128
+        # while 128-row tiles would fill fewer than half of the 256 CUs
+        skinny = Bt <= 64 or (Bt <= 128 and 2 * ((Bt + 127) // 128) * (D // 128) * H < 256)
+        kernel = "fp8_einsum_skinny_kernel" if skinny else "fp8_einsum_tile_kernel"
         workload = f"{grp}_b{Bt}"
         config = {"workload": f"fp8_einsum 'bhr,hdr->bhd' {grp}: b {Bt}, h {H}, r {R}, d {D}, e4m3fn x and y, "
                               f"float32 128 / 128x128 block scales, bf16 out",

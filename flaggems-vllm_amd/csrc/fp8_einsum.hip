@@ -19,13 +19,15 @@
 // 4g..4g+3 of column c.
 //
 // Two kernels:
-//   - skinny (b <= 128, or rows not 16-byte aligned, or r = 0): fragments
-//     straight from memory, the K blocks dealt round-robin to KS waves of a
-//     workgroup and their partials summed in LDS; y (the weights) streams
-//     from HBM once, x is re-read from L2;
+//   - skinny (b <= 64, b <= 128 with few heads, rows not 16-byte aligned,
+//     or r = 0): fragments straight from memory into a ring of registers
+//     (PD blocks in flight per wave), the K blocks dealt round-robin to KS
+//     waves of a workgroup and their partials summed in LDS; y (the
+//     weights) streams from HBM once, x is re-read from L2;
 //   - tiled (larger b): 256 x 128 (or 128 x 128) output tiles over eight
 //     (four) waves of 64 x 64, the K blocks' x and y tiles streamed through a
-//     three-stage LDS ring by LDS DMA, two blocks ahead of the MFMAs.
+//     three-stage LDS ring by LDS DMA, two blocks ahead of the MFMAs (one
+//     workgroup of eight waves per CU).
 // The result depends only on the inputs: a fixed K-block order per wave and
 // a fixed order over waves.
 #include "fgv_device.h"
@@ -39,11 +41,12 @@ typedef float v4f_t __attribute__((ext_vector_type(4)));
 
 constexpr int kBlockK = 128;   // K block (one scale block, one MFMA)
 constexpr int kTile = 128;     // tiled kernel: output tile rows and columns
-constexpr int kSkinnyRows = 128;  // b up to this: the skinny kernel
-constexpr int kSkinnyKS = 4;      // skinny: waves per workgroup (K split)
-constexpr int kSkinnyNW1 = 2;     // skinny: 16-column tiles per wave for b <= 16, 32, 128
-constexpr int kSkinnyNW2 = 2;
-constexpr int kSkinnyNW4 = 2;
+constexpr int kSkinnyRows = 128;  // b up to this may take the skinny kernel
+// skinny configurations for b <= 16, <= 32 and larger: 16-column tiles per
+// wave (NW), waves per workgroup splitting K (KS), blocks in flight per wave (PD)
+constexpr int kSkinnyNW1 = 2, kSkinnyKS1 = 8, kSkinnyPD1 = 2;
+constexpr int kSkinnyNW2 = 2, kSkinnyKS2 = 4, kSkinnyPD2 = 1;
+constexpr int kSkinnyNW4 = 2, kSkinnyKS4 = 4, kSkinnyPD4 = 1;
 
 struct EinsumArgs {
     const uint8_t* x;      // x[b, h, r] bytes, r contiguous
@@ -100,9 +103,10 @@ __device__ __forceinline__ void store_out(void* out, int64_t i, float v) {
 
 // ---- skinny: rows m0 .. m0 + 16 MT of x (one workgroup row of the grid),
 // columns n0 .. n0 + 16 NW of y, head blockIdx.z; wave w takes the K blocks
-// w, w + KS, ...  A block's fragments and scales are loaded while the
-// previous block's MFMAs run.
-template <int MT, int NW, int KS, bool ALIGNED, int OUT>
+// w, w + KS, ...  A ring of PD register slots keeps PD blocks' fragments and
+// scales in flight: a slot's block is used, then the slot loads the block PD
+// turns later.
+template <int MT, int NW, int KS, int PD, bool ALIGNED, int OUT>
 __global__ void __launch_bounds__(64 * KS) fp8_einsum_skinny_kernel(EinsumArgs a) {
     __shared__ v4f_t part[KS > 1 ? KS - 1 : 1][MT * NW][64];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -144,50 +148,54 @@ __global__ void __launch_bounds__(64 * KS) fp8_einsum_skinny_kernel(EinsumArgs a
             acc[i][j] = v4f_t{0.f, 0.f, 0.f, 0.f};
 
     const v8i_t zero = {0, 0, 0, 0, 0, 0, 0, 0};
-    v8i_t A[MT], B[NW];
-    float X[MT][4], Y = 0.f;
-    auto fetch = [&](int kb) {
+    v8i_t A[PD][MT], B[PD][NW];
+    float X[PD][MT][4], Y[PD];
+    auto fetch = [&](int kb, int s) {
         const int64_t k0 = (int64_t)kb * kBlockK;
 #pragma unroll
         for (int i = 0; i < MT; ++i)
-            A[i] = aok[i] ? load_frag<ALIGNED>(arow[i] + k0, g) : zero;
+            A[s][i] = aok[i] ? load_frag<ALIGNED>(arow[i] + k0, g) : zero;
 #pragma unroll
         for (int j = 0; j < NW; ++j)
-            B[j] = load_frag<ALIGNED>(brow[j] + k0, g);
+            B[s][j] = load_frag<ALIGNED>(brow[j] + k0, g);
 #pragma unroll
         for (int i = 0; i < MT; ++i)
 #pragma unroll
             for (int q = 0; q < 4; ++q)
-                X[i][q] = xsh[(int64_t)xrow[i][q] * a.xs_sb + (int64_t)kb * a.xs_sk];
-        Y = ysp[(int64_t)kb * a.ys_sk];
+                X[s][i][q] = xsh[(int64_t)xrow[i][q] * a.xs_sb + (int64_t)kb * a.xs_sk];
+        Y[s] = ysp[(int64_t)kb * a.ys_sk];
     };
-    if (w < a.nkb)
-        fetch(w);
-    for (int kb = w; kb < a.nkb; kb += KS) {
-        v8i_t Ac[MT], Bc[NW];
+    auto use = [&](int s) {
         float sx[MT][4];
 #pragma unroll
         for (int i = 0; i < MT; ++i)
-            Ac[i] = A[i];
-#pragma unroll
-        for (int j = 0; j < NW; ++j)
-            Bc[j] = B[j];
-#pragma unroll
-        for (int i = 0; i < MT; ++i)
 #pragma unroll
             for (int q = 0; q < 4; ++q)
-                sx[i][q] = xok[i][q] ? X[i][q] * Y : 0.f;
-        if (kb + KS < a.nkb)
-            fetch(kb + KS);  // the next block's loads fly over this block's MFMAs
+                sx[i][q] = xok[i][q] ? X[s][i][q] * Y[s] : 0.f;
 #pragma unroll
         for (int i = 0; i < MT; ++i)
 #pragma unroll
             for (int j = 0; j < NW; ++j) {
-                const v4f_t p = mfma_fp8(Ac[i], Bc[j]);
+                const v4f_t p = mfma_fp8(A[s][i], B[s][j]);
 #pragma unroll
                 for (int q = 0; q < 4; ++q)
                     acc[i][j][q] = fmaf(p[q], sx[i][q], acc[i][j][q]);
             }
+    };
+#pragma unroll
+    for (int s = 0; s < PD; ++s)
+        if (w + s * KS < a.nkb)
+            fetch(w + s * KS, s);
+    for (int kb0 = w; kb0 < a.nkb; kb0 += PD * KS) {
+#pragma unroll
+        for (int s = 0; s < PD; ++s) {
+            const int kb = kb0 + s * KS;
+            if (kb < a.nkb) {
+                use(s);
+                if (kb + PD * KS < a.nkb)
+                    fetch(kb + PD * KS, s);  // PD blocks ahead
+            }
+        }
     }
 
     if constexpr (KS > 1) {
@@ -226,13 +234,14 @@ __global__ void __launch_bounds__(64 * KS) fp8_einsum_skinny_kernel(EinsumArgs a
 // ---- tiled: output tile (mt, nt) of head blockIdx.y, 64 MW rows x 128
 // columns over 2 MW waves (64 x 64 each, MW along rows, 2 along columns); x
 // and y rows 16-byte aligned, r > 0.  The K blocks stream through a ring of
-// kStages LDS stages by LDS DMA (global_load_lds_dwordx4: each wave
-// instruction lands 64 lanes x 16 bytes = 8 rows contiguously), issued two
+// NS LDS stages by LDS DMA (global_load_lds_dwordx4: each wave
+// instruction lands 64 lanes x 16 bytes = 8 rows contiguously), issued NS - 1
 // blocks ahead of the MFMAs.  Rows are stored unpadded with their 16-byte
 // chunks swizzled, chunk c of row r at (c ^ ((r >> 1) & 7)), so that the 16
 // rows of a fragment read hit 16 distinct chunk slots.  Rows of x past b read
 // row b - 1: they only feed outputs that are not stored.
-constexpr int kStages = 3;
+constexpr int kStages4 = 3;  // LDS stages of the 256-row tiles (49 KB each)
+constexpr int kStages2 = 3;  // LDS stages of the 128-row tiles (33 KB each)
 
 // LDS DMA of 16 (4) bytes per lane: lane l's bytes land at LDS address
 // lds + 16 l (4 l).  Issued as inline assembly so that the compiler, which
@@ -278,15 +287,16 @@ struct TileShape {
     static_assert(kAInstr >= 1 && kBInstr >= 1 && kXInstr < kWaves, "tile shape");
 };
 
-template <int MW, int OUT>
+template <int MW, int NS, int OUT>
 __global__ void __launch_bounds__(128 * MW) fp8_einsum_tile_kernel(EinsumArgs a, int32_t mtiles) {
     using S = TileShape<MW>;
-    // the three stages are separate objects, named statically by each step of
-    // the 3-unrolled loop, so that the compiler sees that a step's LDS reads
-    // do not touch the stages the DMAs in flight write
+    static_assert(NS >= 2 && NS <= 4, "two to four stages");
+    // the NS stages, named statically by each step of the NS-unrolled loop
     __shared__ __attribute__((aligned(1024))) uint8_t st0[S::kStageBytes];
     __shared__ __attribute__((aligned(1024))) uint8_t st1[S::kStageBytes];
-    __shared__ __attribute__((aligned(1024))) uint8_t st2[S::kStageBytes];
+    __shared__ __attribute__((aligned(1024))) uint8_t st2[NS > 2 ? S::kStageBytes : 16];
+    __shared__ __attribute__((aligned(1024))) uint8_t st3[NS > 3 ? S::kStageBytes : 16];
+    auto stage = [&](int i) -> uint8_t* { return i == 0 ? st0 : i == 1 ? st1 : i == 2 ? st2 : st3; };
 
     const int t = threadIdx.x, lane = t & 63;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -339,21 +349,29 @@ __global__ void __launch_bounds__(128 * MW) fp8_einsum_tile_kernel(EinsumArgs a,
         for (int j = 0; j < 4; ++j)
             acc[i][j] = v4f_t{0.f, 0.f, 0.f, 0.f};
 
-    // one K block: wait for this wave's DMAs of block kb (block kb + 1's may
-    // still fly), barrier (everyone's landed; the stage read in the previous
-    // step is free), send block kb + 2 into it, then the MFMAs on `cur`
-    auto step = [&](int kb, const uint8_t* cur, uint8_t* next2) {
-        if (kb + 1 < a.nkb) {
+    // one K block: wait for this wave's DMAs of block kb (the next blocks'
+    // may still fly), barrier (everyone's landed; the stage read in the
+    // previous step is free), send block kb + NS - 1 into it, then the MFMAs
+    // on `cur`
+    constexpr int kPer = S::kAInstr + S::kBInstr;  // this wave's DMAs per block (+ 1 with a scale DMA)
+    auto step = [&](int kb, const uint8_t* cur, uint8_t* nxt) {
+        const int after = min(NS - 2, a.nkb - 1 - kb);  // blocks issued after kb
+        if (after >= 2) {
             if (xw || yw)
-                __builtin_amdgcn_s_waitcnt(wait_vm(S::kAInstr + S::kBInstr + 1));
+                __builtin_amdgcn_s_waitcnt(wait_vm(2 * (kPer + 1)));
             else
-                __builtin_amdgcn_s_waitcnt(wait_vm(S::kAInstr + S::kBInstr));
+                __builtin_amdgcn_s_waitcnt(wait_vm(2 * kPer));
+        } else if (after == 1) {
+            if (xw || yw)
+                __builtin_amdgcn_s_waitcnt(wait_vm(kPer + 1));
+            else
+                __builtin_amdgcn_s_waitcnt(wait_vm(kPer));
         } else {
             __builtin_amdgcn_s_waitcnt(wait_vm(0));
         }
         lds_barrier();
-        if (kb + 2 < a.nkb)
-            issue(kb + 2, next2);
+        if (kb + NS - 1 < a.nkb)
+            issue(kb + NS - 1, nxt);
         const float sy = reinterpret_cast<const float*>(cur + S::kYOff)[lane];
         v8i_t A[4], B[4];
 #pragma unroll
@@ -393,15 +411,15 @@ __global__ void __launch_bounds__(128 * MW) fp8_einsum_tile_kernel(EinsumArgs a,
             }
     };
 
-    issue(0, st0);
-    if (a.nkb > 1)
-        issue(1, st1);
-    for (int kb = 0; kb < a.nkb; kb += 3) {
-        step(kb, st0, st2);
-        if (kb + 1 < a.nkb)
-            step(kb + 1, st1, st0);
-        if (kb + 2 < a.nkb)
-            step(kb + 2, st2, st1);
+#pragma unroll
+    for (int j = 0; j < NS - 1; ++j)
+        if (j < a.nkb)
+            issue(j, stage(j));
+    for (int kb0 = 0; kb0 < a.nkb; kb0 += NS) {
+#pragma unroll
+        for (int j = 0; j < NS; ++j)
+            if (kb0 + j < a.nkb)
+                step(kb0 + j, stage(j), stage((j + NS - 1) % NS));
     }
 
 #pragma unroll
@@ -419,39 +437,44 @@ __global__ void __launch_bounds__(128 * MW) fp8_einsum_tile_kernel(EinsumArgs a,
         }
 }
 
-template <int MT, int NW, int KS, bool ALIGNED, int OUT>
+template <int MT, int NW, int KS, int PD, bool ALIGNED, int OUT>
 void launch_skinny(const EinsumArgs& a, hipStream_t st) {
     const dim3 grid((unsigned)(a.d / (16 * NW)), (unsigned)((a.b + 16 * MT - 1) / (16 * MT)), (unsigned)a.h);
-    hipLaunchKernelGGL((fp8_einsum_skinny_kernel<MT, NW, KS, ALIGNED, OUT>), grid, dim3(64 * KS), 0, st, a);
+    hipLaunchKernelGGL((fp8_einsum_skinny_kernel<MT, NW, KS, PD, ALIGNED, OUT>), grid, dim3(64 * KS), 0, st, a);
 }
 
 template <bool ALIGNED, int OUT>
 void launch_skinny_rows(const EinsumArgs& a, hipStream_t st) {
     if (a.b <= 16)
-        launch_skinny<1, kSkinnyNW1, kSkinnyKS, ALIGNED, OUT>(a, st);
+        launch_skinny<1, kSkinnyNW1, kSkinnyKS1, kSkinnyPD1, ALIGNED, OUT>(a, st);
     else if (a.b <= 32)
-        launch_skinny<2, kSkinnyNW2, kSkinnyKS, ALIGNED, OUT>(a, st);
+        launch_skinny<2, kSkinnyNW2, kSkinnyKS2, kSkinnyPD2, ALIGNED, OUT>(a, st);
     else
-        launch_skinny<4, kSkinnyNW4, kSkinnyKS, ALIGNED, OUT>(a, st);
+        launch_skinny<4, kSkinnyNW4, kSkinnyKS4, kSkinnyPD4, ALIGNED, OUT>(a, st);
 }
 
 template <int OUT>
 int launch_einsum(const EinsumArgs& a, bool aligned, hipStream_t st) {
+    // skinny up to 64 rows, and up to 128 while 128-row tiles would fill
+    // fewer than half the CUs (measured: flash b=128 skinny 31 us, tiled 39;
+    // pro b=128 skinny 98 us, tiled 67)
+    const int64_t tiles128 = (int64_t)((a.b + 127) / 128) * (a.d / kTile) * a.h;
+    const bool skinny = a.b <= 64 || (a.b <= kSkinnyRows && 2 * tiles128 < cu_count());
     if (!aligned)
         launch_skinny_rows<false, OUT>(a, st);
-    else if (a.b <= kSkinnyRows || a.nkb == 0)
+    else if (skinny || a.nkb == 0)
         launch_skinny_rows<true, OUT>(a, st);
     else {
         // 256-row tiles while they give every CU a workgroup, else 128 rows
         const int64_t tiles256 = (int64_t)((a.b + 255) / 256) * (a.d / kTile) * a.h;
         if (tiles256 >= cu_count()) {
             const int32_t mtiles = (a.b + 255) / 256;
-            hipLaunchKernelGGL((fp8_einsum_tile_kernel<4, OUT>), dim3((unsigned)(mtiles * (a.d / kTile)), (unsigned)a.h),
-                               dim3(512), 0, st, a, mtiles);
+            hipLaunchKernelGGL((fp8_einsum_tile_kernel<4, kStages4, OUT>),
+                               dim3((unsigned)(mtiles * (a.d / kTile)), (unsigned)a.h), dim3(512), 0, st, a, mtiles);
         } else {
             const int32_t mtiles = (a.b + 127) / 128;
-            hipLaunchKernelGGL((fp8_einsum_tile_kernel<2, OUT>), dim3((unsigned)(mtiles * (a.d / kTile)), (unsigned)a.h),
-                               dim3(256), 0, st, a, mtiles);
+            hipLaunchKernelGGL((fp8_einsum_tile_kernel<2, kStages2, OUT>),
+                               dim3((unsigned)(mtiles * (a.d / kTile)), (unsigned)a.h), dim3(256), 0, st, a, mtiles);
         }
     }
     return launch_status();
