@@ -31,6 +31,7 @@ from .ops import (  # noqa: F401
     fused_q_kv_rmsnorm,
     get_mla_metadata,
     indexer_k_quant_and_cache,
+    persistent_topk,
     top_k_per_row_decode,
     top_k_per_row_prefill,
 )
@@ -64,6 +65,7 @@ __all__ = [
     "ops_deepseek_v4_qnorm_rope_kv_rope_quant_insert",
     "ops_inv_rope_fp8_quant",
     "SUPPORTED_FP8_DTYPE",
+    "persistent_topk",
     "top_k_per_row_decode",
     "top_k_per_row_prefill",
 ]

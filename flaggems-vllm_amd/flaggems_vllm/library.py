@@ -6,7 +6,8 @@ These registrations expose the same ops to torch.compile and graph capture as
 opaque custom ops: the schemas declare what each op writes, namely ``q`` and
 ``k_cache`` for the main op (alias-annotated ``Tensor(a0!) q``, ``Tensor(a2!) k_cache``), ``out``
 for the gather, ``slot_mapping`` for the slot mapping, ``kv_cache`` for the
-indexer key insert and ``k_fp8`` / ``k_fp8_scale`` for its gather, ``indices`` for the top-k per row,
+indexer key insert and ``k_fp8`` / ``k_fp8_scale`` for its gather, ``indices`` for the top-k per row
+(``output`` for ``persistent_topk``),
 ``out`` for ``fp8_einsum_out`` (the index-row ops and ``fp8_einsum`` write only what they return).  The fake (meta)
 implementations give the output shapes and strides the real ops return.
 Each registered op calls the same wrapper, so argument checks and errors are
@@ -33,6 +34,7 @@ from .ops import (
     fused_inv_rope_fp8_quant,
     fused_q_kv_rmsnorm,
     indexer_k_quant_and_cache,
+    persistent_topk,
     top_k_per_row_decode,
     top_k_per_row_prefill,
 )
@@ -223,6 +225,17 @@ def _(logits, row_starts, row_ends, indices, num_rows, stride0, stride1, top_k):
     return None
 
 
+@_op("persistent_topk", ("output",))
+def _persistent_topk(logits: torch.Tensor, lengths: torch.Tensor, output: torch.Tensor, workspace: torch.Tensor,
+                     k: int = 512, max_seq_len: Optional[int] = None) -> None:
+    persistent_topk(logits, lengths, output, workspace, k, max_seq_len)
+
+
+@_persistent_topk.register_fake
+def _(logits, lengths, output, workspace, k=512, max_seq_len=None):
+    return None
+
+
 @_op("fp8_einsum")
 def _fp8_einsum(equation: str, x: torch.Tensor, xs: torch.Tensor, y: torch.Tensor, ys: torch.Tensor,
                 block_size: List[int], output_dtype: torch.dtype) -> torch.Tensor:
@@ -260,4 +273,5 @@ REGISTERED: List[str] = [
     "top_k_per_row_prefill",
     "fp8_einsum",
     "fp8_einsum_out",
+    "persistent_topk",
 ]

@@ -1,4 +1,4 @@
-"""DeepSeek-V4 attention pre-processing ops (reference: src/flaggems_vllm/ops/__init__.py:23-38, 55, 57, 58-65, 78, 142-143, 187)."""
+"""DeepSeek-V4 attention pre-processing ops (reference: src/flaggems_vllm/ops/__init__.py:23-38, 55, 57, 58-65, 78, 122, 142-143, 187, 229)."""
 from .cp_gather_indexer_k_quant_cache import cp_gather_indexer_k_quant_cache
 from .deepseek_v4_attention_combine_topk_swa_indices import combine_topk_swa_indices
 from .deepseek_v4_attention_compute_global_topk_indices_and_lens import compute_global_topk_indices_and_lens
@@ -14,6 +14,7 @@ from .fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert import (
 from .fused_indexer_q_rope_quant import fused_indexer_q_rope_quant
 from .fused_inv_rope_fp8_quant import SUPPORTED_FP8_DTYPE, fused_inv_rope_fp8_quant
 from .indexer_k_quant_and_cache import indexer_k_quant_and_cache
+from .persistent_topk import persistent_topk
 from .slot_mapping import compute_slot_mapping_parallel
 from .top_k_per_row import top_k_per_row_decode, top_k_per_row_prefill
 
@@ -35,6 +36,7 @@ __all__ = [
     "fused_inv_rope_fp8_quant",
     "indexer_k_quant_and_cache",
     "SUPPORTED_FP8_DTYPE",
+    "persistent_topk",
     "top_k_per_row_decode",
     "top_k_per_row_prefill",
 ]
