@@ -106,9 +106,15 @@ __device__ __forceinline__ void store_out(void* out, int64_t i, float v) {
 // w, w + KS, ...  A ring of PD register slots keeps PD blocks' fragments and
 // scales in flight: a slot's block is used, then the slot loads the block PD
 // turns later.
-template <int MT, int NW, int KS, int PD, bool ALIGNED, int OUT>
+// With XT, the workgroup first stages its rows' xs for every K block in LDS
+// (xt[kb][row], rows past b as 0), so that a K block's scales are one
+// 16-byte LDS read per row tile instead of four global loads.
+constexpr int kXsTableBlocks = 64;  // K blocks (r <= 8192) whose xs a workgroup stages in LDS
+
+template <int MT, int NW, int KS, int PD, bool ALIGNED, bool XT, int OUT>
 __global__ void __launch_bounds__(64 * KS) fp8_einsum_skinny_kernel(EinsumArgs a) {
     __shared__ v4f_t part[KS > 1 ? KS - 1 : 1][MT * NW][64];
+    __shared__ __attribute__((aligned(16))) float xt[XT ? 16 * MT * kXsTableBlocks : 4];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int c = lane & 15, g = lane >> 4;
     const int n0 = blockIdx.x * 16 * NW;
@@ -140,6 +146,15 @@ __global__ void __launch_bounds__(64 * KS) fp8_einsum_skinny_kernel(EinsumArgs a
             xrow[i][q] = xok[i][q] ? m : 0;
         }
 
+    if constexpr (XT) {
+        constexpr int kRows = 16 * MT;
+        for (int e = threadIdx.x; e < kRows * a.nkb; e += 64 * KS) {
+            const int row = e % kRows, kb = e / kRows, m = m0 + row;
+            xt[e] = m < a.b ? xsh[(int64_t)m * a.xs_sb + (int64_t)kb * a.xs_sk] : 0.f;
+        }
+        __syncthreads();
+    }
+
     v4f_t acc[MT][NW];
 #pragma unroll
     for (int i = 0; i < MT; ++i)
@@ -158,20 +173,33 @@ __global__ void __launch_bounds__(64 * KS) fp8_einsum_skinny_kernel(EinsumArgs a
 #pragma unroll
         for (int j = 0; j < NW; ++j)
             B[s][j] = load_frag<ALIGNED>(brow[j] + k0, g);
+        if constexpr (!XT) {
 #pragma unroll
-        for (int i = 0; i < MT; ++i)
+            for (int i = 0; i < MT; ++i)
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-                X[s][i][q] = xsh[(int64_t)xrow[i][q] * a.xs_sb + (int64_t)kb * a.xs_sk];
+                for (int q = 0; q < 4; ++q)
+                    X[s][i][q] = xsh[(int64_t)xrow[i][q] * a.xs_sb + (int64_t)kb * a.xs_sk];
+        }
         Y[s] = ysp[(int64_t)kb * a.ys_sk];
     };
-    auto use = [&](int s) {
+    auto use = [&](int s, int kb) {
         float sx[MT][4];
+        if constexpr (XT) {
 #pragma unroll
-        for (int i = 0; i < MT; ++i)
+            for (int i = 0; i < MT; ++i) {
+                const float4 v = *reinterpret_cast<const float4*>(&xt[kb * 16 * MT + 16 * i + 4 * g]);
+                sx[i][0] = v.x * Y[s];
+                sx[i][1] = v.y * Y[s];
+                sx[i][2] = v.z * Y[s];
+                sx[i][3] = v.w * Y[s];
+            }
+        } else {
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-                sx[i][q] = xok[i][q] ? X[s][i][q] * Y[s] : 0.f;
+            for (int i = 0; i < MT; ++i)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    sx[i][q] = xok[i][q] ? X[s][i][q] * Y[s] : 0.f;
+        }
 #pragma unroll
         for (int i = 0; i < MT; ++i)
 #pragma unroll
@@ -191,7 +219,7 @@ __global__ void __launch_bounds__(64 * KS) fp8_einsum_skinny_kernel(EinsumArgs a
         for (int s = 0; s < PD; ++s) {
             const int kb = kb0 + s * KS;
             if (kb < a.nkb) {
-                use(s);
+                use(s, kb);
                 if (kb + PD * KS < a.nkb)
                     fetch(kb + PD * KS, s);  // PD blocks ahead
             }
@@ -440,7 +468,12 @@ __global__ void __launch_bounds__(128 * MW) fp8_einsum_tile_kernel(EinsumArgs a,
 template <int MT, int NW, int KS, int PD, bool ALIGNED, int OUT>
 void launch_skinny(const EinsumArgs& a, hipStream_t st) {
     const dim3 grid((unsigned)(a.d / (16 * NW)), (unsigned)((a.b + 16 * MT - 1) / (16 * MT)), (unsigned)a.h);
-    hipLaunchKernelGGL((fp8_einsum_skinny_kernel<MT, NW, KS, PD, ALIGNED, OUT>), grid, dim3(64 * KS), 0, st, a);
+    if (a.nkb <= kXsTableBlocks)
+        hipLaunchKernelGGL((fp8_einsum_skinny_kernel<MT, NW, KS, PD, ALIGNED, true, OUT>), grid, dim3(64 * KS), 0, st,
+                           a);
+    else
+        hipLaunchKernelGGL((fp8_einsum_skinny_kernel<MT, NW, KS, PD, ALIGNED, false, OUT>), grid, dim3(64 * KS), 0,
+                           st, a);
 }
 
 template <bool ALIGNED, int OUT>
