@@ -36,7 +36,7 @@ def parse_args():
     ap.add_argument("--config", type=int, default=2, help="main-op workload c0..c4 (default c2)")
     ap.add_argument("--op", choices=["main", "inv_rope", "gather", "rmsnorm", "indexer",
                                      "slot_mapping", "mla", "indexer_k", "indexer_k_gather", "mqa_logits",
-                                     "paged_mqa_logits", "topk", "einsum", "copy"],
+                                     "paged_mqa_logits", "topk", "einsum", "mla_sparse", "copy"],
                     default="main",
                     help="copy: torch device copy of 512 MiB, the HBM calibration kernel")
     ap.add_argument("--tma", action="store_true", help="inv_rope: packed UE8M0 scales")
@@ -58,6 +58,10 @@ def parse_args():
     ap.add_argument("--einsum-case", default="flash,8192",
                     help="einsum: group,b with group flash (h 8, r 4096, d 1024) or pro (h 16, r 7168, d 1024) "
                          "and b the batch (the reference benchmark's groups and batches 1..32768)")
+    ap.add_argument("--mla-sparse-case", default="v32_8k",
+                    help="mla_sparse: flash_mla_sparse_fwd at a reference benchmark case (s_q 4096, sink): "
+                         "v32_{8,32,64,96,128}k (topk 2048, h_q 128, d_qk 576), h64_{8,32,48,64}k (topk 512, "
+                         "h_q 64, d_qk 512) or h128_{8,32,48,64}k (topk 1024, h_q 128, d_qk 512)")
     ap.add_argument("--cpu-sample-tokens", type=int, default=8192)
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="repeat the CPU sample until this much CPU time is spent (min 3 runs)")
@@ -685,6 +689,31 @@ def main():
         cpu_case = (lambda: torch.einsum("bhr,hdr->bhd", xd, yd), nb, "rows/s",
                     f"first {nb} of {Bt} rows: the reference test's dequantise-then-einsum in float32 on the CPU "
                     f"(dequantisation outside the timing)")
+    elif args.op == "mla_sparse":
+        # sparse MLA prefill at a reference benchmark case
+        # (benchmark/test_flash_mla_sparse_fwd.py:105-121: s_q 4096 with the attention sink)
+        s_kv, topk, h_q, d_qk = W.MLA_SPARSE_CASES[args.mla_sparse_case]
+        T = 4096
+        w_cpu = W.make_mla_sparse_inputs(T, s_kv, topk, h_q=h_q, d_qk=d_qk, have_attn_sink=True, seed=0,
+                                         sm_scale=d_qk ** -0.5)
+        bytes_call = W.mla_sparse_bytes(w_cpu)
+        flops_call = W.mla_sparse_flops(w_cpu)
+
+        def make_step(i):
+            wd = w_cpu.to(dev)
+            return lambda: flaggems_vllm.flash_mla_sparse_fwd(*wd.args())
+
+        kernel = "sparse_mla_prefill_kernel"
+        workload = args.mla_sparse_case
+        config = {"workload": f"flash_mla_sparse_fwd s_q {T}, s_kv {s_kv}, topk {topk}, h_q {h_q}, d_qk {d_qk}, "
+                              f"d_v 512, attention sink", "s_q": T, "s_kv": s_kv, "topk": topk, "h_q": h_q,
+                  "d_qk": d_qk, "flops_per_call": flops_call,
+                  "gather_bytes_note": "bytes_per_call counts each attended kv row once per 64-head block; "
+                                       "the rows are re-read from L2 / MALL, not HBM"}
+        nt = 16
+        sub = [w_cpu.q[:nt], w_cpu.kv, w_cpu.indices[:nt], w_cpu.sm_scale, w_cpu.attn_sink]
+        cpu_case = (lambda: torch_ref.flash_mla_sparse_fwd(*sub), nt, "tokens/s",
+                    f"first {nt} of {T} tokens: the reference test's torch definition in float32 on the CPU")
     elif args.op == "copy":
         n = 512 << 20
         src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
@@ -717,7 +746,7 @@ def main():
 
     n_sets = 1
     if args.op in ("main", "gather", "rmsnorm", "indexer", "mla", "inv_rope", "indexer_k", "indexer_k_gather",
-                   "paged_mqa_logits", "topk", "einsum"):
+                   "paged_mqa_logits", "topk", "einsum", "mla_sparse"):
         step, n_sets = rotating(make_step, bytes_call)
     if n_sets == 1:
         config["input_sets"] = "one input set"
@@ -729,7 +758,7 @@ def main():
     ms_step, t_kernel, timing = time_gpu(step, args.steps, args.warmup)
     median_us = median_call_us(step, max(20, args.steps))
     achieved = bytes_call / t_kernel / 1e9
-    if args.op == "mla":
+    if args.op in ("mla", "mla_sparse"):
         config["mfma_tflops"] = flops_call / t_kernel / 1e12
         config["mfma_frac_of_bf16_dense_peak"] = flops_call / t_kernel / 2.5e15
     if args.op in ("mqa_logits", "paged_mqa_logits", "einsum"):
@@ -747,7 +776,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": {"mla": "bf16", "slot_mapping": "int64", "copy": "u8", "indexer_k_gather": "u8",
+        "dtype": {"mla": "bf16", "mla_sparse": "bf16", "slot_mapping": "int64", "copy": "u8", "indexer_k_gather": "u8",
                   "mqa_logits": "fp4 x fp8 -> f32" if args.fp4 else "fp8 -> f32",
                   "paged_mqa_logits": "fp4 x fp8 -> f32" if args.fp4 else "fp8 -> f32",
                   "einsum": "fp8 -> f32 -> bf16"}.get(args.op, "f32"),
@@ -765,6 +794,10 @@ def main():
                  "synthetic: seeded uniform finite e4m3fn codes, power-of-two x scales 2^-12..2^-6, "
                  "y block scales U[2^-9, 2^-9 + 2^-6)"
                  if args.op == "einsum" else
+                 "synthetic: seeded q, kv ~ N(0,1)/10 + offset (bf16), index rows distinct random ids "
+                 "(arithmetic progressions mod s_kv), sink ~ N(0,1) with +-inf entries, as the reference's "
+                 "benchmark draws them"
+                 if args.op == "mla_sparse" else
                  "synthetic: seeded N(0,1) bf16 q/kv, fp32 cos/sin (theta 1e4), vLLM-style paged slots"),
         "config": config,
         "kernel_us": t_kernel * 1e6,
@@ -781,6 +814,10 @@ def main():
                       "unit": "TFLOP/s", "frac": flops_call / t_kernel / 5.0e15, "traffic": traffic,
                       "kernel": kernel, "peak_note": "MI355X dense FP8 MFMA"}
                      if args.op == "mqa_logits" or (args.op == "einsum" and flops_call / bytes_call > 625) else
+                     {"bound": "mfma", "achieved": flops_call / t_kernel / 1e12, "peak": 2500.0,
+                      "unit": "TFLOP/s", "frac": flops_call / t_kernel / 2.5e15, "traffic": traffic,
+                      "kernel": kernel, "peak_note": "MI355X dense bf16 MFMA"}
+                     if args.op == "mla_sparse" else
                      {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                       "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic,
                       "kernel": kernel}),

@@ -373,25 +373,43 @@ __device__ __forceinline__ void lds_barrier() {
 // QK row reads and the PV transposing reads, g its 16-lane group.
 // (Each call site passes one fixed LDS array, so the compiler can tell the
 // tile read from the tile the LDS DMA is filling.)
-__device__ __forceinline__ void attend_chunk(const uint8_t* kt, const float* mask, const bf16x8_t (&qf)[kQLoads],
-                                             f32x4_t (&acc)[32], float& m_run, float& l_run, int qk_base,
-                                             int tr_base, int g, float scale_log2) {
+//
+// With TAIL, the scores have 64 more dims (the sparse prefill's d_qk = 576):
+// q's in qt (lane group g: dims 512+32t+8g..+7 of step t), the entries' in
+// the tail tile `tt` (32 rows of 128 bytes; tl_base = the lane's QK offset
+// there); they enter S only, not O.  With MAXL, m_max keeps the exact largest
+// score (base 2), which the lazily raised m_run is not.
+constexpr int kTailDim = 64;
+constexpr int kTailRow = kTailDim * 2;
+
+template <bool MAXL, bool TAIL>
+__device__ __forceinline__ void attend_tile(const uint8_t* kt, const uint8_t* tt, const float* mask,
+                                            const bf16x8_t (&qf)[kQLoads], const bf16x8_t* qt, f32x4_t (&acc)[32],
+                                            float& m_run, float& l_run, float& m_max, int qk_base, int tl_base,
+                                            int tr_base, int g, float scale_log2) {
     // ---- S^T = K q^T for the chunk's two 16-entry tiles
     // K operands read two steps ahead of the MFMAs that consume them
+    constexpr int kSteps = TAIL ? kQLoads + kTailDim / 32 : kQLoads;
     f32x4_t s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
     bf16x8_t ka[3], kb[3];
     auto read_k = [&](int s, bf16x8_t& x, bf16x8_t& y) {
-        x = *reinterpret_cast<const bf16x8_t*>(kt + qk_base + 64 * s);
-        y = *reinterpret_cast<const bf16x8_t*>(kt + qk_base + 64 * s + 16 * kKRowBytes);
+        if (s < kQLoads) {
+            x = *reinterpret_cast<const bf16x8_t*>(kt + qk_base + 64 * s);
+            y = *reinterpret_cast<const bf16x8_t*>(kt + qk_base + 64 * s + 16 * kKRowBytes);
+        } else {
+            x = *reinterpret_cast<const bf16x8_t*>(tt + tl_base + 64 * (s - kQLoads));
+            y = *reinterpret_cast<const bf16x8_t*>(tt + tl_base + 64 * (s - kQLoads) + 16 * kTailRow);
+        }
     };
     read_k(0, ka[0], kb[0]);
     read_k(1, ka[1], kb[1]);
 #pragma unroll
-    for (int s = 0; s < 16; ++s) {
-        if (s + 2 < 16)
+    for (int s = 0; s < kSteps; ++s) {
+        if (s + 2 < kSteps)
             read_k(s + 2, ka[(s + 2) % 3], kb[(s + 2) % 3]);
-        s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[s % 3], qf[s], s0, 0, 0, 0);
-        s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb[s % 3], qf[s], s1, 0, 0, 0);
+        const bf16x8_t qs = s < kQLoads ? qf[s] : qt[s - kQLoads];
+        s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[s % 3], qs, s0, 0, 0, 0);
+        s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb[s % 3], qs, s1, 0, 0, 0);
         __builtin_amdgcn_sched_barrier(0);  // keep the reads two steps ahead
     }
 
@@ -407,6 +425,8 @@ __device__ __forceinline__ void attend_chunk(const uint8_t* kt, const float* mas
     for (int i = 1; i < 8; ++i)
         cmax = fmaxf(cmax, sv[i]);
     cmax = group4_max(cmax);
+    if constexpr (MAXL)
+        m_max = fmaxf(m_max, cmax);
     // Raise the reference maximum (and rescale O and the sum) only when a
     // score of this wave's heads exceeds it by more than kRescaleSlack.
     if (__any(cmax > m_run + kRescaleSlack)) {
@@ -454,6 +474,14 @@ __device__ __forceinline__ void attend_chunk(const uint8_t* kt, const float* mas
         acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, pb, acc[dt], 0, 0, 0);
         __builtin_amdgcn_sched_barrier(0);
     }
+}
+
+__device__ __forceinline__ void attend_chunk(const uint8_t* kt, const float* mask, const bf16x8_t (&qf)[kQLoads],
+                                             f32x4_t (&acc)[32], float& m_run, float& l_run, int qk_base,
+                                             int tr_base, int g, float scale_log2) {
+    float unused;
+    attend_tile<false, false>(kt, nullptr, mask, qf, nullptr, acc, m_run, l_run, unused, qk_base, 0, tr_base, g,
+                              scale_log2);
 }
 
 // The wave's 16 output rows (lane (m16, g) holds dims 16dt+4g..+3 of head
@@ -646,6 +674,155 @@ sparse_mla_decode_kernel(MlaArgs a) {
     const ListView v1 = make_view(a.list[1], a.num_lists > 1, b, sq);
     const int nchunks = (v0.len + kChunk - 1) / kChunk + (v1.len + kChunk - 1) / kChunk;
     run_segment(a, lds_raw, lds_kbuf, lds_mask, b, sq, hb, 0, nchunks, -1, wave, lane);
+}
+
+// ---- sparse prefill (flash_mla_sparse_fwd) over bf16 key/value rows
+//
+// Reference: src/flaggems_vllm/ops/flashmla_sparse.py:1045-1206 (wrapper,
+// asserts) and :50-195 (portable kernel).  Token t's query heads attend the
+// kv rows indices[t, 0, i] for i < topk_length[t] (clamped to [0, topk];
+// topk without topk_length) that lie in [0, s_kv): K = the row's d_qk dims,
+// V = its first 512.  Outputs per (t, head): the largest score, the
+// log-sum-exp of the scores (+inf when none is attended) and O (the sink
+// only rescales O, as in the decode).
+struct PrefillArgs {
+    const uint16_t* q;
+    int64_t q_st, q_sh;
+    const uint8_t* kv;
+    int64_t kv_row_bytes;
+    const int32_t* indices;
+    int64_t idx_st;
+    const int32_t* topk_length;  // [s_q] or null
+    const float* sink;           // [h_q] or null
+    uint16_t* out;
+    int64_t o_st, o_sh;
+    float* max_logits;
+    float* lse;
+    int64_t ml_st, l_st;
+    int32_t s_kv, topk, head_blocks;
+    float scale_log2;
+};
+
+// The chunk's 32 rows into a K tile, as issue_rows does (wave w: entries
+// 8w..8w+7, one wave-wide 16-byte LDS DMA per 1 KiB row; `id` in load_id's
+// layout), and with TAIL each row's 64-dim tail (bytes 1024..1151) into the
+// tail tile: one more DMA per wave, lane l moving block l%8 of entry
+// 8w + l/8, 8 rows of 128 bytes landing contiguously.  Rows not attended come
+// from the zero page.
+template <bool TAIL>
+__device__ __forceinline__ void issue_kv_rows(const PrefillArgs& a, int wave, int lane, int id, uint8_t* tile,
+                                              uint8_t* tail, float* mask) {
+    __attribute__((address_space(3))) uint8_t* dst = (__attribute__((address_space(3))) uint8_t*)tile;
+#pragma unroll
+    for (int j = 0; j < kChunk / 4; ++j) {
+        const int idj = __builtin_amdgcn_readlane(id, 8 * j);
+        const uint8_t* row = idj >= 0 && idj < a.s_kv ? a.kv + (int64_t)idj * a.kv_row_bytes : mla_zero_entry;
+        __builtin_amdgcn_global_load_lds((global_u32_t*)(row + 16 * lane),
+                                         (lds_u32_t*)(dst + (8 * wave + j) * kKRowBytes), 16, 0, 0);
+    }
+    const bool valid = id >= 0 && id < a.s_kv;
+    if constexpr (TAIL) {
+        __attribute__((address_space(3))) uint8_t* tdst = (__attribute__((address_space(3))) uint8_t*)tail;
+        const uint8_t* row = valid ? a.kv + (int64_t)id * a.kv_row_bytes + 2 * kHeadDim : mla_zero_entry;
+        __builtin_amdgcn_global_load_lds((global_u32_t*)(row + 16 * (lane & 7)),
+                                         (lds_u32_t*)(tdst + 8 * kTailRow * wave), 16, 0, 0);
+    }
+    if ((lane & 7) == 0)
+        mask[8 * wave + (lane >> 3)] = valid ? 0.f : -INFINITY;
+}
+
+// One workgroup per (token, 64-head block), head blocks of a token adjacent.
+// The rows alternate between two K tiles (and two tail tiles): chunk c+1's
+// DMA runs while chunk c is attended, one barrier per chunk, as the decode's
+// expanded chunks do.
+template <bool TAIL>
+__global__ void __launch_bounds__(kThreads, 2)
+sparse_mla_prefill_kernel(PrefillArgs a) {
+    __shared__ __align__(16) uint8_t lds_t0[kChunk * kKRowBytes];
+    __shared__ __align__(16) uint8_t lds_t1[kChunk * kKRowBytes];
+    __shared__ __align__(16) uint8_t lds_x0[TAIL ? kChunk * kTailRow : 16];
+    __shared__ __align__(16) uint8_t lds_x1[TAIL ? kChunk * kTailRow : 16];
+    __shared__ float lds_mask[2][kChunk];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int m16 = lane & 15, g = lane >> 4;
+    const int hb = blockIdx.x % a.head_blocks;
+    const int t = blockIdx.x / a.head_blocks;
+    const int head = hb * kBlockHeads + wave * 16 + m16;
+
+    const int32_t* irow = a.indices + t * a.idx_st;
+    int len = a.topk;
+    if (a.topk_length) {
+        const int n = a.topk_length[t];
+        len = n < 0 ? 0 : (n > a.topk ? a.topk : n);
+    }
+    const int nch = (len + kChunk - 1) / kChunk;
+    auto load_id = [&](int c, int ln) {
+        const int e = c * kChunk + 8 * wave + (ln >> 3);
+        return e < len ? irow[e] : -1;
+    };
+    int id_next = -1;
+    if (nch > 0) {
+        const int id0 = load_id(0, lane);
+        if (nch > 1)
+            id_next = load_id(1, lane);
+        issue_kv_rows<TAIL>(a, wave, lane, id0, lds_t0, lds_x0, lds_mask[0]);
+    }
+
+    // q as the B operand (lane group g: dims 32s+8g..+7 of head m16)
+    const uint16_t* qrow = a.q + t * a.q_st + head * a.q_sh;
+    bf16x8_t qf[kQLoads], qt[TAIL ? kTailDim / 32 : 1];
+#pragma unroll
+    for (int s = 0; s < kQLoads; ++s)
+        qf[s] = __builtin_bit_cast(bf16x8_t, load16(qrow + 32 * s + 8 * g));
+    if constexpr (TAIL) {
+#pragma unroll
+        for (int s = 0; s < kTailDim / 32; ++s)
+            qt[s] = __builtin_bit_cast(bf16x8_t, load16(qrow + kHeadDim + 32 * s + 8 * g));
+    }
+
+    f32x4_t acc[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i)
+        acc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY, l_run = 0.f, m_max = -INFINITY;
+    const int qk_base = kbuf_byte(m16, g);
+    const int tl_base = m16 * kTailRow + 16 * g;
+    const int tr_base = kbuf_byte(4 * g + (m16 >> 2), (m16 & 3) >> 1) + 8 * (m16 & 1);
+
+    // Chunk c from (tile, tail) while chunk c+1 streams into (other, other_tail).
+    auto step = [&](int c, uint8_t* tile, uint8_t* tail, uint8_t* other, uint8_t* other_tail)
+                    __attribute__((always_inline)) {
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's rows of chunk c (and chunk c+1's index)
+        __syncthreads();                // everyone's rows landed; `other` no longer read
+        if (c + 1 < nch)
+            issue_kv_rows<TAIL>(a, wave, ln, id_next, other, other_tail, lds_mask[(c + 1) & 1]);
+        if (c + 2 < nch)
+            id_next = load_id(c + 2, ln);
+        attend_tile<true, TAIL>(tile, tail, lds_mask[c & 1], qf, qt, acc, m_run, l_run, m_max, qk_base, tl_base,
+                                tr_base, g, a.scale_log2);
+    };
+    for (int c = 0; c < nch; c += 2) {
+        step(c, lds_t0, lds_x0, lds_t1, lds_x1);
+        if (c + 1 < nch)
+            step(c + 1, lds_t1, lds_x1, lds_t0, lds_x0);
+    }
+
+    // ---- epilogue, as the decode's: lse and the largest score exclude the
+    // sink, which only rescales O; m_run is the reference maximum (base 2).
+    const bool any = l_run > 0.f;
+    float factor = 0.f;
+    if (any)
+        factor = a.sink ? 1.f / (l_run + expf(a.sink[head] - m_run * kLn2)) : 1.f / l_run;
+    __syncthreads();  // the K tiles are free once every wave has left the loop
+    uint8_t* stage = wave < 2 ? lds_t0 + wave * 16 * kStageRow : lds_t1 + (wave - 2) * 16 * kStageRow;
+    store_rows(stage, acc, factor, a.out + t * a.o_st + (hb * kBlockHeads + wave * 16) * a.o_sh, a.o_sh, m16, g,
+               lane);
+    if (g == 0) {
+        a.lse[t * a.l_st + head] = any ? m_run * kLn2 + logf(l_run) : INFINITY;
+        a.max_logits[t * a.ml_st + head] = m_max * kLn2;
+    }
 }
 
 // Chunks a batch row's items have (the same for every query position and
@@ -1521,4 +1698,69 @@ extern "C" int fgv_sparse_mla_decode_model1_no_alloc(FGV_MLA_PARAMS, void* strea
             return rc;
     }
     return mla_decode(FGV_MLA_ARGS, ws, need, stream);
+}
+
+// Sparse prefill over bf16 rows (sparse_mla_prefill_kernel).
+extern "C" int fgv_flash_mla_sparse_fwd(const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* kv,
+                                        int64_t kv_stride_row, int64_t s_kv, const int32_t* indices,
+                                        int64_t idx_stride_t, int64_t topk, const int32_t* topk_length,
+                                        const float* attn_sink, float sm_scale, int64_t s_q, int64_t h_q,
+                                        int64_t d_qk, void* out, int64_t out_stride_t, int64_t out_stride_h,
+                                        float* max_logits, int64_t max_logits_stride_t, float* lse,
+                                        int64_t lse_stride_t, void* stream) {
+    using namespace fgv;
+    if (s_q < 0 || h_q < 0 || s_kv < 0 || topk < 0)
+        return fail(FGV_E_BAD_SHAPE, "negative size");
+    if (d_qk != kHeadDim && d_qk != kHeadDim + kTailDim)
+        return fail(FGV_E_BAD_SHAPE, "d_qk must be 512 or 576");
+    if (h_q % kBlockHeads)
+        return fail(FGV_E_BAD_SHAPE, "h_q must be a multiple of 64");
+    if (s_q == 0 || h_q == 0)
+        return FGV_OK;
+    if (kv_stride_row < d_qk)
+        return fail(FGV_E_BAD_STRIDE, "kv rows overlap (kv_stride_row < d_qk)");
+    if (out_stride_h < kHeadDim || out_stride_t < h_q * out_stride_h || max_logits_stride_t < h_q ||
+        lse_stride_t < h_q)
+        return fail(FGV_E_BAD_STRIDE, "out, max_logits or lse rows overlap");
+    if (s_q * (h_q / kBlockHeads) > 0x7fffffffLL || s_kv > 0x7fffffffLL || topk > 0x7fffffffLL)
+        return fail(FGV_E_TOO_LARGE, "s_q * h_q / 64, s_kv and topk must fit in int32");
+    if (!q || !out || !lse || !max_logits || (topk > 0 && (!indices || (s_kv > 0 && !kv))))
+        return fail(FGV_E_NULL_POINTER, "null q, kv, indices, out, max_logits or lse");
+    if (!aligned(q, 16) || q_stride_t % 8 || q_stride_h % 8)
+        return fail(FGV_E_MISALIGNED, "q must be 16-byte aligned with strides a multiple of 8 elements");
+    if (!aligned(out, 16) || out_stride_t % 8 || out_stride_h % 8)
+        return fail(FGV_E_MISALIGNED, "out must be 16-byte aligned with strides a multiple of 8 elements");
+    if (!aligned(kv, 16) || kv_stride_row % 8)
+        return fail(FGV_E_MISALIGNED, "kv must be 16-byte aligned with a row stride a multiple of 8 elements");
+    if (!aligned(indices, 4) || !aligned(lse, 4) || !aligned(max_logits, 4))
+        return fail(FGV_E_MISALIGNED, "indices, lse and max_logits must be 4-byte aligned");
+    PrefillArgs a;
+    a.q = static_cast<const uint16_t*>(q);
+    a.q_st = q_stride_t;
+    a.q_sh = q_stride_h;
+    a.kv = static_cast<const uint8_t*>(kv);
+    a.kv_row_bytes = 2 * kv_stride_row;
+    a.indices = indices;
+    a.idx_st = idx_stride_t;
+    a.topk_length = topk_length;
+    a.sink = attn_sink;
+    a.out = static_cast<uint16_t*>(out);
+    a.o_st = out_stride_t;
+    a.o_sh = out_stride_h;
+    a.max_logits = max_logits;
+    a.lse = lse;
+    a.ml_st = max_logits_stride_t;
+    a.l_st = lse_stride_t;
+    a.s_kv = (int32_t)s_kv;
+    a.topk = (int32_t)topk;
+    a.head_blocks = (int32_t)(h_q / kBlockHeads);
+    a.scale_log2 = (float)((double)sm_scale * 1.4426950408889634);
+    const dim3 grid((unsigned)(s_q * a.head_blocks));
+    if (d_qk == kHeadDim)
+        hipLaunchKernelGGL(sparse_mla_prefill_kernel<false>, grid, dim3(kThreads), 0,
+                           static_cast<hipStream_t>(stream), a);
+    else
+        hipLaunchKernelGGL(sparse_mla_prefill_kernel<true>, grid, dim3(kThreads), 0,
+                           static_cast<hipStream_t>(stream), a);
+    return launch_status();
 }

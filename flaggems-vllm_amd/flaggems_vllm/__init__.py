@@ -7,8 +7,8 @@ their compatibility aliases ``ops_deepseek_v4_qnorm_rope_kv_rope_quant_insert`` 
 and the ops either side of that path (src/flaggems_vllm/ops/__init__.py): the
 K-cache gather, q/kv RMSNorm, the sparse indexer (q quant, key cache and
 logits and their top-k per row), the index rows sparse attention reads (global
-top-k indices, top-k plus sliding window), slot mapping, sparse MLA decode and
-the block-FP8 grouped output projection (``fp8_einsum``) after the sibling op.  Every op runs hand-written HIP kernels through the C ABI declared in
+top-k indices, top-k plus sliding window), slot mapping, sparse MLA decode, sparse MLA prefill
+(``flash_mla_sparse_fwd``) and the block-FP8 grouped output projection (``fp8_einsum``) after the sibling op.  Every op runs hand-written HIP kernels through the C ABI declared in
 include/flaggems_vllm_amd.h; there is no Triton, no vendor dispatch and no
 CPU fallback.
 """
@@ -21,6 +21,7 @@ from .ops import (  # noqa: F401
     compute_slot_mapping_parallel,
     cp_gather_indexer_k_quant_cache,
     dequantize_and_gather_k_cache,
+    flash_mla_sparse_fwd,
     flash_mla_with_kvcache,
     fp8_einsum,
     fp8_fp4_mqa_logits,
@@ -51,6 +52,7 @@ __all__ = [
     "compute_global_topk_indices_and_lens",
     "compute_slot_mapping_parallel",
     "cp_gather_indexer_k_quant_cache",
+    "flash_mla_sparse_fwd",
     "flash_mla_with_kvcache",
     "fp8_einsum",
     "fp8_fp4_mqa_logits",

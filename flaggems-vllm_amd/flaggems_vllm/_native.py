@@ -146,6 +146,18 @@ def lib():
     ]
     L.fgv_sparse_mla_decode_model1_no_alloc.restype = ctypes.c_int
     L.fgv_sparse_mla_decode_model1_no_alloc.argtypes = L.fgv_sparse_mla_decode_model1.argtypes[:-3] + [_P]
+    L.fgv_flash_mla_sparse_fwd.restype = ctypes.c_int
+    L.fgv_flash_mla_sparse_fwd.argtypes = [
+        _P, _I64, _I64,  # q, strides (token, head)
+        _P, _I64, _I64,  # kv, row stride, s_kv
+        _P, _I64, _I64,  # indices, token stride, topk
+        _P, _P, ctypes.c_float,  # topk_length, attn_sink, sm_scale
+        _I64, _I64, _I64,  # s_q, h_q, d_qk
+        _P, _I64, _I64,  # out, strides (token, head)
+        _P, _I64,  # max_logits, token stride
+        _P, _I64,  # lse, token stride
+        _P,  # stream
+    ]
     L.fgv_sparse_mla_decode_workspace_bytes.restype = ctypes.c_int64
     L.fgv_sparse_mla_decode_workspace_bytes.argtypes = [_I64, _I64, _I64, _I64, _I64, _I64]
     L.fgv_sparse_mla_decode_grid.restype = ctypes.c_int
@@ -257,6 +269,7 @@ EXPORTED_SYMBOLS = (
     "fgv_top_k_per_row_workspace_bytes",
     "fgv_fp8_einsum_bhr_hdr",
     "fgv_sparse_mla_decode_model1_no_alloc",
+    "fgv_flash_mla_sparse_fwd",
     "fgv_indexer_k_quant_and_cache",
     "fgv_cp_gather_indexer_k_quant_cache",
     "fgv_fp8_fp4_mqa_logits",

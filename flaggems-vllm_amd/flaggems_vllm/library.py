@@ -8,7 +8,7 @@ opaque custom ops: the schemas declare what each op writes, namely ``q`` and
 for the gather, ``slot_mapping`` for the slot mapping, ``kv_cache`` for the
 indexer key insert and ``k_fp8`` / ``k_fp8_scale`` for its gather, ``indices`` for the top-k per row
 (``output`` for ``persistent_topk``),
-``out`` for ``fp8_einsum_out`` (the index-row ops and ``fp8_einsum`` write only what they return).  The fake (meta)
+``out`` for ``fp8_einsum_out`` (the index-row ops, ``fp8_einsum`` and ``flash_mla_sparse_fwd`` write only what they return).  The fake (meta)
 implementations give the output shapes and strides the real ops return.
 Each registered op calls the same wrapper, so argument checks and errors are
 the wrapper's.
@@ -28,6 +28,7 @@ from .ops import (
     compute_slot_mapping_parallel,
     cp_gather_indexer_k_quant_cache,
     dequantize_and_gather_k_cache,
+    flash_mla_sparse_fwd,
     fp8_einsum,
     fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert,
     fused_indexer_q_rope_quant,
@@ -258,6 +259,20 @@ def _(equation, x, xs, y, ys, block_size, output_dtype, out):
     return None
 
 
+@_op("flash_mla_sparse_fwd")
+def _flash_mla_sparse_fwd(q: torch.Tensor, kv: torch.Tensor, indices: torch.Tensor, sm_scale: float, d_v: int = 512,
+                          attn_sink: Optional[torch.Tensor] = None,
+                          topk_length: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    return flash_mla_sparse_fwd(q, kv, indices, sm_scale, d_v, attn_sink, topk_length)
+
+
+@_flash_mla_sparse_fwd.register_fake
+def _(q, kv, indices, sm_scale, d_v=512, attn_sink=None, topk_length=None):
+    s_q, h_q = q.shape[0], q.shape[1]
+    return (q.new_empty((s_q, h_q, d_v)), q.new_empty((s_q, h_q), dtype=torch.float32),
+            q.new_empty((s_q, h_q), dtype=torch.float32))
+
+
 REGISTERED: List[str] = [
     "fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert",
     "fused_inv_rope_fp8_quant",
@@ -274,4 +289,5 @@ REGISTERED: List[str] = [
     "fp8_einsum",
     "fp8_einsum_out",
     "persistent_topk",
+    "flash_mla_sparse_fwd",
 ]

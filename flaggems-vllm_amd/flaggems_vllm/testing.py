@@ -470,6 +470,122 @@ def mla_flops(w: MlaWorkload) -> int:
 
 
 # ---------------------------------------------------------------------------
+# Sparse MLA prefill over bf16 rows (flash_mla_sparse_fwd).  Inputs drawn as
+# the reference's FlashMLA-style cases draw them
+# (tests/test_flash_mla_sparse_fwd.py:232-370): q, kv ~ randn / 10 plus a
+# per-call offset, clamped to [-10, 10]; index rows a random permutation of
+# [0, s_kv) (as much of it as fits), padded with invalid values; sink ~ randn
+# with about a third set to -inf and a third to +inf; top-k lengths uniform in
+# [0, max(topk + 1, 64)) clamped to topk.
+# ---------------------------------------------------------------------------
+
+MLA_SPARSE_INVALID = (-2147483648, -123456, -1, None, 114514, 1919810, 2147480000, 2147483647)  # None: s_kv
+
+# Reference benchmark cases (benchmark/test_flash_mla_sparse_fwd.py:105-121):
+# s_q 4096 with the attention sink, name -> (s_kv, topk, h_q, d_qk).
+MLA_SPARSE_CASES = {
+    **{f"v32_{s // 1024}k": (s, 2048, 128, 576) for s in (8192, 32768, 65536, 98304, 131072)},
+    **{f"h64_{s // 1024}k": (s, 512, 64, 512) for s in (8192, 32768, 49152, 65536)},
+    **{f"h128_{s // 1024}k": (s, 1024, 128, 512) for s in (8192, 32768, 49152, 65536)},
+}
+
+
+@dataclass
+class MlaSparseInputs:
+    q: torch.Tensor            # [s_q, h_q, d_qk] bf16
+    kv: torch.Tensor           # [s_kv, 1, d_qk] bf16
+    indices: torch.Tensor      # [s_q, 1, topk] int32
+    attn_sink: Optional[torch.Tensor]
+    topk_length: Optional[torch.Tensor]
+    sm_scale: float
+
+    def to(self, device) -> "MlaSparseInputs":
+        mv = lambda t: t.to(device) if t is not None else None
+        return MlaSparseInputs(mv(self.q), mv(self.kv), mv(self.indices), mv(self.attn_sink),
+                               mv(self.topk_length), self.sm_scale)
+
+    def args(self):
+        return (self.q, self.kv, self.indices, self.sm_scale, 512, self.attn_sink, self.topk_length)
+
+
+def _index_rows(s_q: int, s_kv: int, topk: int, g: torch.Generator, affine: bool) -> torch.Tensor:
+    """[s_q, topk] int32: row t is distinct ids of [0, s_kv) (min(s_kv, topk)
+    of them) then invalid padding.  affine: the ids are an arithmetic
+    progression mod s_kv with a step coprime to s_kv (O(topk) per row, for the
+    benchmark's sizes); otherwise a uniformly random permutation prefix."""
+    n = min(s_kv, topk)
+    rows = torch.empty(s_q, topk, dtype=torch.int32)
+    if n:
+        if affine:
+            pos = torch.arange(n, dtype=torch.int64)
+            off = torch.randint(0, s_kv, (s_q,), generator=g)
+            step = torch.randint(1, max(2, s_kv), (s_q,), generator=g).tolist()
+            for t in range(s_q):
+                while s_kv > 1 and math.gcd(step[t], s_kv) != 1:
+                    step[t] = step[t] % (s_kv - 1) + 1
+            rows[:, :n] = ((off[:, None] + torch.tensor(step)[:, None] * pos) % s_kv).to(torch.int32)
+        else:
+            rows[:, :n] = torch.rand(s_q, s_kv, generator=g).argsort(-1)[:, :n].to(torch.int32)
+    if n < topk:
+        cands = torch.tensor([s_kv if c is None else c for c in MLA_SPARSE_INVALID], dtype=torch.int64)
+        pick = torch.randint(0, len(cands), (s_q, topk - n), generator=g)
+        rows[:, n:] = cands[pick].to(torch.int32)
+    return rows
+
+
+def make_mla_sparse_inputs(s_q: int, s_kv: int, topk: int, h_q: int = 128, d_qk: int = 512,
+                           have_attn_sink: bool = False, have_topk_length: bool = False,
+                           all_invalid_rows: bool = False, seed: int = 0, sm_scale: float = 0.5,
+                           affine: Optional[bool] = None) -> MlaSparseInputs:
+    """Seeded CPU inputs for flash_mla_sparse_fwd (see the section comment)."""
+    g = torch.Generator().manual_seed(seed)
+    off_q, off_kv = (torch.rand(2, generator=g) - 0.5) / 10
+    q = (randn_bf16((s_q, h_q, d_qk), g).float() / 10 + off_q).clamp_(-10, 10).to(torch.bfloat16)
+    kv = (randn_bf16((s_kv, 1, d_qk), g).float() / 10 + off_kv).clamp_(-10, 10).to(torch.bfloat16)
+    if affine is None:
+        affine = s_q * s_kv > (1 << 26)
+    idx = _index_rows(s_q, s_kv, topk, g, affine)
+    if all_invalid_rows:
+        dead = torch.randn(s_q, generator=g) < -1
+        idx[dead] = -1
+    sink = None
+    if have_attn_sink:
+        sink = torch.randn(h_q, generator=g)
+        m = torch.randn(h_q, generator=g)
+        sink[m < -0.5] = float("-inf")
+        sink[m > 0.5] = float("inf")
+    lens = None
+    if have_topk_length:
+        lens = torch.randint(0, max(topk + 1, 64), (s_q,), generator=g).clamp_max(topk).to(torch.int32)
+    return MlaSparseInputs(q, kv, idx.view(s_q, 1, topk), sink, lens, sm_scale)
+
+
+def mla_sparse_used(w: MlaSparseInputs) -> int:
+    """(token, entry) pairs attended: entries inside the length with an id in [0, s_kv)."""
+    s_q, _, topk = w.indices.shape
+    idx = w.indices.reshape(s_q, topk).cpu().long()
+    ok = (idx >= 0) & (idx < w.kv.shape[0])
+    if w.topk_length is not None:
+        ok &= torch.arange(topk)[None, :] < w.topk_length.cpu().long().clamp(0, topk)[:, None]
+    return int(ok.sum())
+
+
+def mla_sparse_flops(w: MlaSparseInputs) -> int:
+    """MFMA work: per (head, attended entry) d_qk multiply-adds for QK and 512 for PV."""
+    h_q, d_qk = w.q.shape[1], w.q.shape[2]
+    return 2 * (d_qk + HEAD_DIM) * h_q * mla_sparse_used(w)
+
+
+def mla_sparse_bytes(w: MlaSparseInputs) -> int:
+    """Algorithmic bytes: q read, out written (bf16), max_logits and lse
+    (float32), the index rows, and each attended row (2 d_qk bytes) once per
+    64-head block."""
+    s_q, h_q, d_qk = w.q.shape
+    return (2 * s_q * h_q * (d_qk + HEAD_DIM) + 8 * s_q * h_q + 4 * w.indices.numel()
+            + (h_q // 64) * mla_sparse_used(w) * 2 * d_qk)
+
+
+# ---------------------------------------------------------------------------
 # Sparse-indexer key cache (indexer_k_quant_and_cache / its gather).  Shapes of
 # the reference's tests (tests/test_indexer_k_quant_and_cache.py:177-185,
 # tests/test_cp_gather_indexer_k_quant_cache.py:168-175) and benchmarks

@@ -442,6 +442,38 @@ int fgv_sparse_mla_decode_model1_no_alloc(
     void* stream);
 
 /*
+ * Sparse MLA prefill over bf16 key/value rows.
+ *
+ * Replaces flaggems_vllm.flash_mla_sparse_fwd (reference:
+ * src/flaggems_vllm/ops/flashmla_sparse.py:1045-1206 wrapper and asserts,
+ * kernel :50-195; definitions of the outputs in tests/test_flash_mla_sparse_fwd.py:93-150).
+ *
+ *   q    bf16 [s_q, h_q, d_qk] (strides in elements, last dim contiguous)
+ *   kv   bf16 [s_kv, d_qk] rows kv_stride_row elements apart (h_kv = 1)
+ *   indices  int32 [s_q, topk] (token stride idx_stride_t, last dim contiguous)
+ *   topk_length  int32 [s_q] or NULL (then topk); clamped to [0, topk]
+ *   attn_sink  float [h_q] or NULL
+ *   out  bf16 [s_q, h_q, 512];  max_logits, lse  float [s_q, h_q] (head stride 1)
+ *
+ * Entry i of token t is attended when i < its length and 0 <= id < s_kv.
+ * Per (t, head): s = sm_scale * q . kv[id] over the d_qk dims (512 or 576),
+ * max_logits = max s (-inf if nothing is attended), lse = log sum exp s (+inf
+ * if nothing is attended), out = sum exp(s - m) V / (sum exp(s - m) +
+ * exp(sink - m)) with V = kv[id][0:512] (no sink term without attn_sink; 0
+ * if nothing is attended).  The sink does not enter max_logits or lse.
+ * h_q must be a multiple of 64 (the reference allows 64 and 128).
+ */
+int fgv_flash_mla_sparse_fwd(
+    const void* q, int64_t q_stride_t, int64_t q_stride_h,
+    const void* kv, int64_t kv_stride_row, int64_t s_kv,
+    const int32_t* indices, int64_t idx_stride_t, int64_t topk,
+    const int32_t* topk_length, const float* attn_sink, float sm_scale,
+    int64_t s_q, int64_t h_q, int64_t d_qk,
+    void* out, int64_t out_stride_t, int64_t out_stride_h,
+    float* max_logits, int64_t max_logits_stride_t,
+    float* lse, int64_t lse_stride_t, void* stream);
+
+/*
  * Request-local top-k indices -> global cache slots, and the row lengths.
  *
  * Replaces flaggems_vllm.compute_global_topk_indices_and_lens

@@ -153,6 +153,10 @@ def lib():
             _P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _I64, _P,
             _P, _I64, _I64, _I64, _P, _I64, _P, _P, ctypes.c_double, _P, _P,
         ]
+        L.oracle_sparse_mla_prefill.restype = None
+        L.oracle_sparse_mla_prefill.argtypes = [
+            _P, _P, _I64, _I64, _P, _I64, _P, _P, ctypes.c_double, _I64, _I64, _I64, _P, _P, _P,
+        ]
         L.oracle_compute_global_topk_indices.restype = None
         L.oracle_compute_global_topk_indices.argtypes = [
             _P, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _P]
@@ -405,6 +409,30 @@ def sparse_mla_decode_model1(q, k_cache, indices, topk_length=None, attn_sink=No
         out.data_ptr(), lse.data_ptr())
     del keep0, keep1
     return out, lse
+
+
+def sparse_mla_prefill(q, kv, indices, sm_scale, attn_sink=None, topk_length=None):
+    """Exact (binary64) sparse MLA prefill over bf16 rows.
+
+    Returns ``(out, max_logits, lse)`` as float64 tensors shaped
+    [s_q, h_q, 512], [s_q, h_q], [s_q, h_q]; arguments as in
+    flaggems_vllm.flash_mla_sparse_fwd (kv [s_kv, 1, d_qk] or [s_kv, d_qk],
+    indices [s_q, 1, topk] or [s_q, topk])."""
+    q = _cpu(q, torch.bfloat16).contiguous()
+    s_q, h_q, d_qk = q.shape
+    kv = _cpu(kv, torch.bfloat16).reshape(kv.shape[0], -1).contiguous()
+    assert kv.shape[1] == d_qk
+    idx = _cpu(indices, torch.int32).reshape(s_q, -1).contiguous()
+    sink = _cpu(attn_sink, torch.float32).contiguous() if attn_sink is not None else None
+    tl = _cpu(topk_length, torch.int32).contiguous() if topk_length is not None else None
+    out = torch.empty(s_q, h_q, 512, dtype=torch.float64)
+    ml = torch.empty(s_q, h_q, dtype=torch.float64)
+    lse = torch.empty(s_q, h_q, dtype=torch.float64)
+    lib().oracle_sparse_mla_prefill(
+        q.data_ptr(), kv.data_ptr(), kv.stride(0), kv.shape[0], idx.data_ptr(), idx.shape[1],
+        tl.data_ptr() if tl is not None else None, sink.data_ptr() if sink is not None else None,
+        float(sm_scale), s_q, h_q, d_qk, out.data_ptr(), ml.data_ptr(), lse.data_ptr())
+    return out, ml, lse
 
 
 def _cache_bytes(kv_cache):

@@ -726,6 +726,84 @@ void oracle_sparse_mla_decode_model1(const uint16_t* q, int64_t B, int64_t SQ, i
     }
 }
 
+/*
+ * Sparse MLA prefill over bf16 kv rows (reference wrapper
+ * ops/flashmla_sparse.py:1045-1206, kernel :50-195; the outputs as the
+ * reference test defines them, tests/test_flash_mla_sparse_fwd.py:93-150):
+ *
+ *   Token t attends entry i of indices[t] when i < len (topk, or
+ *   topk_length[t] clamped to [0, topk]) and 0 <= id < s_kv.
+ *   K = kv[id][0:d_qk], V = kv[id][0:512].  For each head:
+ *   s_i = sm_scale * q . K_i, max_logits = max s_i (-inf when nothing is
+ *   used), lse = m + log sum exp(s_i - m) (+inf when nothing is used),
+ *   out = sum exp(s_i - m) V_i / (l + exp(sink - m)) (sink term only with
+ *   attn_sink; 0 when nothing is used).  Binary64 throughout.
+ * q: [s_q][h_q][d_qk] contiguous; kv rows kv_row elements apart;
+ * indices [s_q][topk]; out [s_q][h_q][512]; max_logits, lse [s_q][h_q].
+ */
+void oracle_sparse_mla_prefill(const uint16_t* q, const uint16_t* kv, int64_t kv_row, int64_t s_kv,
+                               const int32_t* idx, int64_t topk, const int32_t* topk_len, const float* sink,
+                               double sm_scale, int64_t s_q, int64_t h_q, int64_t d_qk, double* out,
+                               double* max_logits, double* lse)
+{
+    for (int64_t t = 0; t < s_q; ++t) {
+        int64_t len = topk;
+        if (topk_len) {
+            len = topk_len[t];
+            len = len < 0 ? 0 : len > topk ? topk : len;
+        }
+        int64_t* ids = (int64_t*)malloc(sizeof(int64_t) * (topk ? topk : 1));
+        int64_t n = 0;
+        for (int64_t i = 0; i < len; ++i) {
+            int64_t id = idx[t * topk + i];
+            if (id >= 0 && id < s_kv)
+                ids[n++] = id;
+        }
+        double* k = (double*)malloc(sizeof(double) * d_qk * (n ? n : 1));
+        for (int64_t i = 0; i < n; ++i)
+            for (int64_t d = 0; d < d_qk; ++d)
+                k[i * d_qk + d] = oracle_bf16_to_f32(kv[ids[i] * kv_row + d]);
+        #pragma omp parallel for schedule(static)
+        for (int64_t h = 0; h < h_q; ++h) {
+            const uint16_t* qh = q + (t * h_q + h) * d_qk;
+            double* oh = out + (t * h_q + h) * HEAD_DIM;
+            for (int d = 0; d < HEAD_DIM; ++d)
+                oh[d] = 0.0;
+            if (n == 0) {
+                max_logits[t * h_q + h] = -INFINITY;
+                lse[t * h_q + h] = INFINITY;
+                continue;
+            }
+            double* s = (double*)malloc(sizeof(double) * n);
+            double m = -INFINITY;
+            for (int64_t i = 0; i < n; ++i) {
+                double acc = 0.0;
+                for (int64_t d = 0; d < d_qk; ++d)
+                    acc += (double)oracle_bf16_to_f32(qh[d]) * k[i * d_qk + d];
+                s[i] = acc * sm_scale;
+                if (s[i] > m)
+                    m = s[i];
+            }
+            double l = 0.0;
+            for (int64_t i = 0; i < n; ++i) {
+                s[i] = exp(s[i] - m);
+                l += s[i];
+            }
+            max_logits[t * h_q + h] = m;
+            lse[t * h_q + h] = m + log(l);
+            double denom = l + (sink ? exp((double)sink[h] - m) : 0.0);
+            for (int64_t i = 0; i < n; ++i) {
+                double w = s[i] / denom;
+                for (int d = 0; d < HEAD_DIM; ++d)
+                    oh[d] += w * k[i * d_qk + d];
+            }
+            free(s);
+        }
+        free(k);
+        free(ids);
+    }
+}
+
 /* ------------------------------------------------------------------------
  * Sparse indexer key cache (reference test torch_indexer / torch_gather).
  * Cache block b at cache + b * block_stride: block_size x head_dim e4m3fn

@@ -22,6 +22,9 @@ oracle that the reference's own tests compare its Triton kernels against:
   index arithmetic, with torch's float8 -> float cast and exp2 scale;
 * sparse MLA decode over the MODEL1 cache: the portable kernel's chunked
   online softmax (ops/flash_mla_with_kvcache.py:489-688);
+* sparse MLA prefill over bf16 rows: tests/test_flash_mla_sparse_fwd.py
+  ``torch_flash_mla_sparse_fwd`` :93-150 (float32 gather, masked scores,
+  logsumexp, the sink merged as a second logsumexp term);
 * sparse-indexer logits: tests/test_fp8_fp4_mqa_logits.py
   ``reference_fp4_mqa_logits`` :40-66 (its per-row, per-head float32 loop,
   applied to FP8 q as well as MXFP4 q) and the paged test's per-row gather of
@@ -298,6 +301,29 @@ def sparse_mla_decode_model1(q, k_cache, indices, topk_length=None, attn_sink=No
             o = acc / torch.where(empty, 1.0, denom)[:, None]
             out[b, s] = torch.where(empty[:, None], 0.0, o).to(torch.bfloat16)
     return out, lse
+
+
+def flash_mla_sparse_fwd(q, kv, indices, sm_scale, attn_sink=None, topk_length=None):
+    """(out bf16, max_logits, lse) as the reference test defines them, in
+    float32 on CPU tensors (q [s_q, h_q, d_qk], kv [s_kv, 1, d_qk], indices
+    [s_q, 1, topk])."""
+    s_q, h_q, d_qk = q.shape
+    s_kv, topk = kv.shape[0], indices.shape[-1]
+    idx = indices.reshape(s_q, topk).clone()
+    if topk_length is not None:
+        idx[torch.arange(topk)[None, :] >= topk_length[:, None]] = -1
+    invalid = (idx < 0) | (idx >= s_kv)
+    idx[invalid] = 0
+    rows = kv.reshape(s_kv, d_qk).index_select(0, idx.reshape(-1).long()).reshape(s_q, topk, d_qk).float()
+    p = torch.bmm(q.float(), rows.transpose(1, 2).contiguous()) * sm_scale
+    p[invalid[:, None, :].expand(p.shape)] = float("-inf")
+    lse = torch.logsumexp(p, -1)
+    max_logits = p.amax(-1)
+    lse_o = lse if attn_sink is None else torch.logsumexp(torch.stack([lse, attn_sink.expand_as(lse)]), 0)
+    lse_o = torch.where(lse_o == float("-inf"), float("inf"), lse_o)
+    out = torch.bmm(torch.exp(p - lse_o[..., None]), rows[..., :512].contiguous())
+    lse = torch.where(lse == float("-inf"), float("inf"), lse)
+    return out.to(torch.bfloat16), max_logits, lse
 
 
 def indexer_k_quant_and_cache(k, kv_cache, slot_mapping, quant_block_size, scale_fmt):

@@ -36,6 +36,7 @@ WRITES = {
     "fp8_einsum": set(),
     "fp8_einsum_out": {"out"},
     "persistent_topk": {"output"},
+    "flash_mla_sparse_fwd": set(),
 }
 
 
@@ -262,3 +263,19 @@ def test_gpu_fp8_einsum_ops():
                           ("bhr,hdr->bhd", x, xs, y, ys, [128, 128], torch.float32), test_utils=utils)
     torch.library.opcheck(torch.ops.flaggems_vllm.fp8_einsum_out.default,
                           ("bhr,hdr->bhd", x, xs, y, ys, [128, 128], torch.bfloat16, out), test_utils=utils)
+
+
+@pytest.mark.gpu
+def test_gpu_flash_mla_sparse_op():
+    """torch.ops.flaggems_vllm.flash_mla_sparse_fwd: the function's bytes, fake
+    layout and opcheck."""
+    from flaggems_vllm import testing as W
+
+    w = W.make_mla_sparse_inputs(5, 300, 128, h_q=64, d_qk=576, have_attn_sink=True, have_topk_length=True,
+                                 seed=3).to(DEV)
+    ref = flaggems_vllm.flash_mla_sparse_fwd(*w.args())
+    got = torch.ops.flaggems_vllm.flash_mla_sparse_fwd(*w.args())
+    for a, b in zip(got, ref):
+        assert torch.equal(a, b)
+    torch.library.opcheck(_op("flash_mla_sparse_fwd"), w.args(),
+                          test_utils=("test_schema", "test_faketensor", "test_autograd_registration"))
