@@ -731,7 +731,7 @@ __device__ __forceinline__ void issue_kv_rows(const PrefillArgs& a, int wave, in
         mask[8 * wave + (lane >> 3)] = valid ? 0.f : -INFINITY;
 }
 
-// One workgroup per (token, 64-head block), head blocks of a token adjacent.
+// One workgroup per (token, 64-head block).
 // The rows alternate between two K tiles (and two tail tiles): chunk c+1's
 // DMA runs while chunk c is attended, one barrier per chunk, as the decode's
 // expanded chunks do.
@@ -745,8 +745,22 @@ sparse_mla_prefill_kernel(PrefillArgs a) {
     __shared__ float lds_mask[2][kChunk];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int m16 = lane & 15, g = lane >> 4;
-    const int hb = blockIdx.x % a.head_blocks;
-    const int t = blockIdx.x / a.head_blocks;
+    // Workgroup i runs on XCD i % 8.  With two head blocks, workgroups i and
+    // i + 8 (same XCD, dispatched one round apart) take the two head blocks of
+    // one token, so its rows are fetched into one L2 for both (measured 4-7%
+    // faster at h_q 128 than head blocks on neighbouring XCDs); a last
+    // partial group of 16 keeps the plain order.
+    int hb, t;
+    {
+        const int bid = blockIdx.x, paired = (int)(gridDim.x / 16) * 16;
+        if (a.head_blocks == 2 && bid < paired) {
+            t = (bid >> 4) * 8 + (bid & 7);
+            hb = (bid >> 3) & 1;
+        } else {
+            hb = bid % a.head_blocks;
+            t = bid / a.head_blocks;
+        }
+    }
     const int head = hb * kBlockHeads + wave * 16 + m16;
 
     const int32_t* irow = a.indices + t * a.idx_st;
