@@ -197,3 +197,13 @@ def test_graph_fp8_einsum():
         out = torch.empty((b, 2, 256), dtype=torch.bfloat16, device=DEV)
         run = lambda: flaggems_vllm.fp8_einsum("bhr,hdr->bhd", x, xs, y, ys, out=out)
         replay_matches_eager(lambda: out.fill_(7.0), run)
+
+
+@pytest.mark.parametrize("d_qk", [512, 576])
+def test_graph_flash_mla_sparse(d_qk):
+    """Sparse prefill (outputs allocated inside the capture) with the sink and
+    top-k lengths; the replays give the eager bytes of all three outputs."""
+    _say(f"graph: flash_mla_sparse_fwd d_qk={d_qk}")
+    w = W.make_mla_sparse_inputs(40, 700, 256, h_q=128, d_qk=d_qk, have_attn_sink=True, have_topk_length=True,
+                                 seed=d_qk).to(DEV)
+    replay_matches_eager(lambda: None, lambda: flaggems_vllm.flash_mla_sparse_fwd(*w.args()))
