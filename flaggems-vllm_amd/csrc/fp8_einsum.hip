@@ -315,8 +315,12 @@ struct TileShape {
     static_assert(kAInstr >= 1 && kBInstr >= 1 && kXInstr < kWaves, "tile shape");
 };
 
+// Split K: with gridDim.z = S > 1, workgroup z takes K blocks
+// [nkb z / S, nkb (z + 1) / S) and writes its fp32 tile to partial slot z of
+// `part` ([S][b][h][d]) instead of the output; fp8_einsum_reduce_kernel sums
+// the slots in order.
 template <int MW, int NS, int OUT>
-__global__ void __launch_bounds__(128 * MW) fp8_einsum_tile_kernel(EinsumArgs a, int32_t mtiles) {
+__global__ void __launch_bounds__(128 * MW) fp8_einsum_tile_kernel(EinsumArgs a, int32_t mtiles, float* part) {
     using S = TileShape<MW>;
     static_assert(NS >= 2 && NS <= 4, "two to four stages");
     // the NS stages, named statically by each step of the NS-unrolled loop
@@ -333,6 +337,8 @@ __global__ void __launch_bounds__(128 * MW) fp8_einsum_tile_kernel(EinsumArgs a,
     const int hh = blockIdx.y;
     const int mt = blockIdx.x % mtiles, nt = blockIdx.x / mtiles;
     const int m0 = mt * S::kRows, n0 = nt * kTile;
+    const int kb_lo = (int)((int64_t)a.nkb * blockIdx.z / gridDim.z);
+    const int kb_hi = (int)((int64_t)a.nkb * (blockIdx.z + 1) / gridDim.z);
 
     // this lane's DMA sources: A instruction j of the wave covers tile rows
     // 8 (wave * kAInstr + j) + lane / 8, physical chunk lane % 8
@@ -383,7 +389,7 @@ __global__ void __launch_bounds__(128 * MW) fp8_einsum_tile_kernel(EinsumArgs a,
     // on `cur`
     constexpr int kPer = S::kAInstr + S::kBInstr;  // this wave's DMAs per block (+ 1 with a scale DMA)
     auto step = [&](int kb, const uint8_t* cur, uint8_t* nxt) {
-        const int after = min(NS - 2, a.nkb - 1 - kb);  // blocks issued after kb
+        const int after = min(NS - 2, kb_hi - 1 - kb);  // blocks issued after kb
         if (after >= 2) {
             if (xw || yw)
                 __builtin_amdgcn_s_waitcnt(wait_vm(2 * (kPer + 1)));
@@ -398,7 +404,7 @@ __global__ void __launch_bounds__(128 * MW) fp8_einsum_tile_kernel(EinsumArgs a,
             __builtin_amdgcn_s_waitcnt(wait_vm(0));
         }
         lds_barrier();
-        if (kb + NS - 1 < a.nkb)
+        if (kb + NS - 1 < kb_hi)
             issue(kb + NS - 1, nxt);
         const float sy = reinterpret_cast<const float*>(cur + S::kYOff)[lane];
         v8i_t A[4], B[4];
@@ -441,13 +447,30 @@ __global__ void __launch_bounds__(128 * MW) fp8_einsum_tile_kernel(EinsumArgs a,
 
 #pragma unroll
     for (int j = 0; j < NS - 1; ++j)
-        if (j < a.nkb)
-            issue(j, stage(j));
-    for (int kb0 = 0; kb0 < a.nkb; kb0 += NS) {
+        if (kb_lo + j < kb_hi)
+            issue(kb_lo + j, stage(j));
+    for (int kb0 = kb_lo; kb0 < kb_hi; kb0 += NS) {
 #pragma unroll
         for (int j = 0; j < NS; ++j)
-            if (kb0 + j < a.nkb)
+            if (kb0 + j < kb_hi)
                 step(kb0 + j, stage(j), stage((j + NS - 1) % NS));
+    }
+
+    if (gridDim.z > 1) {
+        float* ps = part + (int64_t)blockIdx.z * a.b * a.h * a.d;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int m = m0 + wm * 64 + 16 * i + 4 * g + q;
+                if (m >= a.b)
+                    continue;
+                float* prow = ps + ((int64_t)m * a.h + hh) * a.d + n0 + wn * 64 + c;
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    prow[16 * j] = acc[i][j][q];
+            }
+        return;
     }
 
 #pragma unroll
@@ -463,6 +486,31 @@ __global__ void __launch_bounds__(128 * MW) fp8_einsum_tile_kernel(EinsumArgs a,
                                (int64_t)m * a.o_sb + (int64_t)hh * a.o_sh + (int64_t)(n0 + wn * 64 + 16 * j + c) * a.o_sd,
                                acc[i][j][q]);
         }
+}
+
+// out[m, h, n] = sum over z = 0 .. splits-1, in that order, of part[z][m][h][n]:
+// four consecutive n per thread.
+template <int OUT>
+__global__ void __launch_bounds__(256) fp8_einsum_reduce_kernel(EinsumArgs a, const float* part, int32_t splits) {
+    const int64_t slot = (int64_t)a.b * a.h * a.d, n4 = slot / 4;
+    for (int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; u < n4; u += (int64_t)gridDim.x * blockDim.x) {
+        float4 v = reinterpret_cast<const float4*>(part)[u];
+        for (int z = 1; z < splits; ++z) {
+            const float4 w = reinterpret_cast<const float4*>(part + z * slot)[u];
+            v.x += w.x;
+            v.y += w.y;
+            v.z += w.z;
+            v.w += w.w;
+        }
+        const int64_t e = 4 * u, row = e / a.d;
+        const int n = (int)(e - row * a.d), hh = (int)(row % a.h);
+        const int64_t m = row / a.h;
+        const int64_t o = m * a.o_sb + (int64_t)hh * a.o_sh + (int64_t)n * a.o_sd;
+        store_out<OUT>(a.out, o, v.x);
+        store_out<OUT>(a.out, o + a.o_sd, v.y);
+        store_out<OUT>(a.out, o + 2 * a.o_sd, v.z);
+        store_out<OUT>(a.out, o + 3 * a.o_sd, v.w);
+    }
 }
 
 template <int MT, int NW, int KS, int PD, bool ALIGNED, int OUT>
@@ -486,14 +534,54 @@ void launch_skinny_rows(const EinsumArgs& a, hipStream_t st) {
         launch_skinny<4, kSkinnyNW4, kSkinnyKS4, kSkinnyPD4, ALIGNED, OUT>(a, st);
 }
 
+// Split-K for the 128-row tiles when they would cover at most half the CUs:
+// enough splits for two workgroups per CU, at least kSplitMinBlocks K blocks
+// each.  The partial tiles need splits * b * h * d fp32 of workspace.
+// Measured (graph replay, bf16 out, unsplit -> split): pro (h 16, r 7168,
+// d 1024) b 65 / 96 / 128 66 -> 48 / 53 / 57 us; flash (h 8, r 4096,
+// d 1024) b 192 / 256 41 -> 37 / 40 us; with three splits (flash b 384) the
+// partials' traffic made it slower (44 -> 60 us), hence the half-the-CUs
+// condition.
+constexpr int kSplitMinBlocks = 8;
+
+int einsum_splits(int64_t b, int64_t h, int64_t nkb, int64_t d) {
+    if (b <= 64 || nkb < 2 * kSplitMinBlocks)
+        return 1;
+    const int64_t tiles128 = ((b + 127) / 128) * (d / kTile) * h;
+    const int64_t cus = cu_count();
+    if (2 * tiles128 > cus)
+        return 1;
+    const int64_t want = (2 * cus + tiles128 - 1) / tiles128;
+    return (int)std::min<int64_t>(want, nkb / kSplitMinBlocks);
+}
+
+int64_t einsum_workspace_bytes(int64_t b, int64_t h, int64_t nkb, int64_t d) {
+    const int splits = einsum_splits(b, h, nkb, d);
+    return splits > 1 ? ((int64_t)splits * b * h * d * 4 + 255) / 256 * 256 : 0;
+}
+
 template <int OUT>
-int launch_einsum(const EinsumArgs& a, bool aligned, hipStream_t st) {
+int launch_einsum(const EinsumArgs& a, bool rows_aligned, void* workspace, int64_t workspace_bytes, hipStream_t st) {
     // skinny up to 64 rows, and up to 128 while 128-row tiles would fill
     // fewer than half the CUs (measured: flash b=128 skinny 31 us, tiled 39;
-    // pro b=128 skinny 98 us, tiled 67)
+    // pro b=128 skinny 98 us, tiled 67); with a workspace, split-K tiles
+    // take b > 64 whenever 128-row tiles would not fill the CUs
     const int64_t tiles128 = (int64_t)((a.b + 127) / 128) * (a.d / kTile) * a.h;
+    const int splits = einsum_splits(a.b, a.h, a.nkb, a.d);
+    const bool split = rows_aligned && splits > 1 && workspace && aligned(workspace, 16) &&
+                       workspace_bytes >= einsum_workspace_bytes(a.b, a.h, a.nkb, a.d);
     const bool skinny = a.b <= 64 || (a.b <= kSkinnyRows && 2 * tiles128 < cu_count());
-    if (!aligned)
+    if (split) {
+        const int32_t mtiles = (a.b + 127) / 128;
+        float* part = static_cast<float*>(workspace);
+        hipLaunchKernelGGL((fp8_einsum_tile_kernel<2, kStages2, OUT>),
+                           dim3((unsigned)(mtiles * (a.d / kTile)), (unsigned)a.h, (unsigned)splits), dim3(256), 0, st,
+                           a, mtiles, part);
+        const int64_t n4 = (int64_t)a.b * a.h * a.d / 4;
+        const int64_t blocks = std::min<int64_t>((n4 + 255) / 256, 8 * (int64_t)cu_count());
+        hipLaunchKernelGGL(fp8_einsum_reduce_kernel<OUT>, dim3((unsigned)blocks), dim3(256), 0, st, a,
+                           (const float*)part, (int32_t)splits);
+    } else if (!rows_aligned)
         launch_skinny_rows<false, OUT>(a, st);
     else if (skinny || a.nkb == 0)
         launch_skinny_rows<true, OUT>(a, st);
@@ -503,11 +591,13 @@ int launch_einsum(const EinsumArgs& a, bool aligned, hipStream_t st) {
         if (tiles256 >= cu_count()) {
             const int32_t mtiles = (a.b + 255) / 256;
             hipLaunchKernelGGL((fp8_einsum_tile_kernel<4, kStages4, OUT>),
-                               dim3((unsigned)(mtiles * (a.d / kTile)), (unsigned)a.h), dim3(512), 0, st, a, mtiles);
+                               dim3((unsigned)(mtiles * (a.d / kTile)), (unsigned)a.h), dim3(512), 0, st, a, mtiles,
+                               nullptr);
         } else {
             const int32_t mtiles = (a.b + 127) / 128;
             hipLaunchKernelGGL((fp8_einsum_tile_kernel<2, kStages2, OUT>),
-                               dim3((unsigned)(mtiles * (a.d / kTile)), (unsigned)a.h), dim3(256), 0, st, a, mtiles);
+                               dim3((unsigned)(mtiles * (a.d / kTile)), (unsigned)a.h), dim3(256), 0, st, a, mtiles,
+                               nullptr);
         }
     }
     return launch_status();
@@ -516,11 +606,18 @@ int launch_einsum(const EinsumArgs& a, bool aligned, hipStream_t st) {
 }  // namespace
 }  // namespace fgv
 
-extern "C" int fgv_fp8_einsum_bhr_hdr(const uint8_t* x, int64_t x_sb, int64_t x_sh, const float* xs, int64_t xs_sb,
-                                      int64_t xs_sh, int64_t xs_sk, const uint8_t* y, int64_t y_sh, int64_t y_sd,
-                                      const float* ys, int64_t ys_sh, int64_t ys_sn, int64_t ys_sk, int64_t b,
-                                      int64_t h, int64_t r, int64_t d, void* out, int64_t o_sb, int64_t o_sh,
-                                      int64_t o_sd, int32_t out_dtype, void* stream) {
+extern "C" int64_t fgv_fp8_einsum_workspace_bytes(int64_t b, int64_t h, int64_t r, int64_t d) {
+    if (b <= 0 || h <= 0 || r <= 0 || d <= 0 || r % fgv::kBlockK || d % fgv::kBlockK)
+        return 0;
+    return fgv::einsum_workspace_bytes(b, h, r / fgv::kBlockK, d);
+}
+
+extern "C" int fgv_fp8_einsum_bhr_hdr_ws(const uint8_t* x, int64_t x_sb, int64_t x_sh, const float* xs, int64_t xs_sb,
+                                         int64_t xs_sh, int64_t xs_sk, const uint8_t* y, int64_t y_sh, int64_t y_sd,
+                                         const float* ys, int64_t ys_sh, int64_t ys_sn, int64_t ys_sk, int64_t b,
+                                         int64_t h, int64_t r, int64_t d, void* out, int64_t o_sb, int64_t o_sh,
+                                         int64_t o_sd, int32_t out_dtype, void* workspace, int64_t workspace_bytes,
+                                         void* stream) {
     using namespace fgv;
     if (b < 0 || h < 0 || r < 0 || d < 0)
         return fail(FGV_E_BAD_SHAPE, "negative size");
@@ -544,10 +641,19 @@ extern "C" int fgv_fp8_einsum_bhr_hdr(const uint8_t* x, int64_t x_sb, int64_t x_
     const hipStream_t st = static_cast<hipStream_t>(stream);
     switch (out_dtype) {
     case kOutBf16:
-        return launch_einsum<kOutBf16>(a, al, st);
+        return launch_einsum<kOutBf16>(a, al, workspace, workspace_bytes, st);
     case kOutF16:
-        return launch_einsum<kOutF16>(a, al, st);
+        return launch_einsum<kOutF16>(a, al, workspace, workspace_bytes, st);
     default:
-        return launch_einsum<kOutF32>(a, al, st);
+        return launch_einsum<kOutF32>(a, al, workspace, workspace_bytes, st);
     }
+}
+
+extern "C" int fgv_fp8_einsum_bhr_hdr(const uint8_t* x, int64_t x_sb, int64_t x_sh, const float* xs, int64_t xs_sb,
+                                      int64_t xs_sh, int64_t xs_sk, const uint8_t* y, int64_t y_sh, int64_t y_sd,
+                                      const float* ys, int64_t ys_sh, int64_t ys_sn, int64_t ys_sk, int64_t b,
+                                      int64_t h, int64_t r, int64_t d, void* out, int64_t o_sb, int64_t o_sh,
+                                      int64_t o_sd, int32_t out_dtype, void* stream) {
+    return fgv_fp8_einsum_bhr_hdr_ws(x, x_sb, x_sh, xs, xs_sb, xs_sh, xs_sk, y, y_sh, y_sd, ys, ys_sh, ys_sn, ys_sk, b,
+                                     h, r, d, out, o_sb, o_sh, o_sd, out_dtype, nullptr, 0, stream);
 }

@@ -190,6 +190,10 @@ def lib():
     L.fgv_fp8_einsum_bhr_hdr.restype = ctypes.c_int
     L.fgv_fp8_einsum_bhr_hdr.argtypes = [_P, _I64, _I64, _P, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64,
                                          _I64, _I64, _I64, _I64, _I64, _P, _I64, _I64, _I64, ctypes.c_int32, _P]
+    L.fgv_fp8_einsum_bhr_hdr_ws.restype = ctypes.c_int
+    L.fgv_fp8_einsum_bhr_hdr_ws.argtypes = L.fgv_fp8_einsum_bhr_hdr.argtypes[:-1] + [_P, _I64, _P]
+    L.fgv_fp8_einsum_workspace_bytes.restype = ctypes.c_int64
+    L.fgv_fp8_einsum_workspace_bytes.argtypes = [_I64, _I64, _I64, _I64]
     L.fgv_combine_topk_swa_width.restype = ctypes.c_int64
     L.fgv_combine_topk_swa_width.argtypes = [_I64, _I64]
     L.fgv_combine_topk_swa_indices.restype = ctypes.c_int
@@ -268,6 +272,8 @@ EXPORTED_SYMBOLS = (
     "fgv_top_k_per_row_prefill",
     "fgv_top_k_per_row_workspace_bytes",
     "fgv_fp8_einsum_bhr_hdr",
+    "fgv_fp8_einsum_bhr_hdr_ws",
+    "fgv_fp8_einsum_workspace_bytes",
     "fgv_sparse_mla_decode_model1_no_alloc",
     "fgv_flash_mla_sparse_fwd",
     "fgv_indexer_k_quant_and_cache",

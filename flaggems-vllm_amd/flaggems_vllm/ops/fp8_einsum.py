@@ -6,9 +6,11 @@ same signature, the same checks in the same order with the same exception
 types (NotImplementedError for what the op does not support, ValueError for
 inconsistent arguments), a new tensor or ``out`` returned.  The reference's
 Hopper requirement becomes a HIP device requirement.  The work is the gfx950
-kernels of ``fp8_einsum.hip`` (C ABI ``fgv_fp8_einsum_bhr_hdr``): 16x16x128
+kernels of ``fp8_einsum.hip`` (C ABI ``fgv_fp8_einsum_bhr_hdr_ws``): 16x16x128
 FP8 MFMAs, one per 128-wide K block, each block's partial sum scaled by
-``xs * ys`` into a float32 accumulator.
+``xs * ys`` into a float32 accumulator; mid-size b splits the K blocks over
+several workgroups per output tile, with the partial tiles in a workspace
+this wrapper allocates.
 """
 from typing import Optional, Sequence
 
@@ -85,11 +87,15 @@ def fp8_einsum(
     if out.numel() == 0:
         return out
     with on_device_of(x):
-        rc = _native.lib().fgv_fp8_einsum_bhr_hdr(
+        # fp32 partial tiles of the split-K schedule (mid-size b), from torch's
+        # caching allocator; 0 bytes when the sizes take an unsplit kernel
+        ws_bytes = _native.lib().fgv_fp8_einsum_workspace_bytes(b, h, r, d)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes > 0 else None
+        rc = _native.lib().fgv_fp8_einsum_bhr_hdr_ws(
             x.data_ptr(), x.stride(0), x.stride(1), xs.data_ptr(), xs.stride(0), xs.stride(1), xs.stride(2),
             y.data_ptr(), y.stride(0), y.stride(1), ys.data_ptr(), ys.stride(0), ys.stride(1), ys.stride(2),
             b, h, r, d, out.data_ptr(), out.stride(0), out.stride(1), out.stride(2), _OUT_CODES[output_dtype],
-            current_stream_ptr(x.device))
+            ws.data_ptr() if ws is not None else None, ws_bytes, current_stream_ptr(x.device))
     _native.check(rc, "fp8_einsum")
     return out
 

@@ -582,6 +582,33 @@ int fgv_fp8_einsum_bhr_hdr(const uint8_t* x, int64_t x_stride_b, int64_t x_strid
                            void* out, int64_t out_stride_b, int64_t out_stride_h, int64_t out_stride_d,
                            int32_t out_dtype, void* stream);
 
+/*
+ * Bytes of device workspace fgv_fp8_einsum_bhr_hdr_ws can use for these
+ * sizes on the current device, or 0 when it would not use any.  With b > 64
+ * and at most CUs / 2 128-row output tiles, the K blocks are split over up to
+ * 2 x CUs / tiles workgroups per tile (at least 8 blocks each); each writes
+ * its fp32 partial tile, and a second kernel sums the partials in a fixed
+ * order (splits * b * h * d * 4 bytes, rounded up to 256).  Same call as
+ * fgv_fp8_einsum_bhr_hdr (reference: src/flaggems_vllm/ops/fp8_einsum.py:20-115).
+ */
+int64_t fgv_fp8_einsum_workspace_bytes(int64_t b, int64_t h, int64_t r, int64_t d);
+
+/*
+ * fgv_fp8_einsum_bhr_hdr with a caller workspace (16-byte aligned) for the
+ * split-K schedule above.  A NULL or too small workspace runs the unsplit
+ * schedule of fgv_fp8_einsum_bhr_hdr.  The results depend only on the inputs
+ * and on whether the workspace was used: the split sums each K range's
+ * scaled blocks in fp32, then the ranges in order, a different fp32
+ * summation order from the unsplit kernel's.  Calls that share a workspace
+ * must be ordered on one stream.
+ */
+int fgv_fp8_einsum_bhr_hdr_ws(const uint8_t* x, int64_t x_stride_b, int64_t x_stride_h, const float* xs,
+                              int64_t xs_stride_b, int64_t xs_stride_h, int64_t xs_stride_k, const uint8_t* y,
+                              int64_t y_stride_h, int64_t y_stride_d, const float* ys, int64_t ys_stride_h,
+                              int64_t ys_stride_n, int64_t ys_stride_k, int64_t b, int64_t h, int64_t r, int64_t d,
+                              void* out, int64_t out_stride_b, int64_t out_stride_h, int64_t out_stride_d,
+                              int32_t out_dtype, void* workspace, int64_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

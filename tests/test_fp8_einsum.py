@@ -462,3 +462,62 @@ def test_gpu_after_inv_rope_fp8_quant(tma):
     wq, ws = torch.stack(wq), torch.stack(ws)
     res = _run(xq, xsc, wq.to(DEV), ws.to(DEV))
     _check(res, xq.cpu(), xsc.cpu(), wq, ws, torch.bfloat16)
+
+
+def test_workspace_query():
+    """Split-K workspace: none up to b = 64, with fewer than 16 K blocks, or
+    when 128-row tiles cover more than half the CUs; otherwise
+    splits * b * h * d fp32 (splits = min(ceil(2 CUs / tiles), nkb / 8);
+    256 CUs where no GPU is visible, as on MI355X)."""
+    from flaggems_vllm import _native
+
+    q = _native.lib().fgv_fp8_einsum_workspace_bytes
+    assert q(64, 8, 4096, 1024) == 0 and q(128, 8, 1920, 1024) == 0 and q(0, 8, 4096, 1024) == 0
+    assert q(128, 8, 4000, 1024) == 0  # r not a multiple of 128
+    assert q(384, 8, 4096, 1024) == 0 and q(256, 16, 7168, 1024) == 0  # tiles over half the CUs
+    if q(128, 8, 4096, 1024) != 4 * 128 * 8 * 1024 * 4:
+        pytest.skip("this device does not have 256 CUs")
+    assert q(256, 8, 4096, 1024) == 4 * 256 * 8 * 1024 * 4
+    assert q(128, 16, 7168, 1024) == 4 * 128 * 16 * 1024 * 4
+    assert q(200, 3, 2560, 384) == 2 * 200 * 3 * 384 * 4
+
+
+def _abi(x, xs, y, ys, out, ws=None, ws_bytes=0):
+    from flaggems_vllm import _native
+
+    b, h, r = x.shape
+    d = y.shape[1]
+    rc = _native.lib().fgv_fp8_einsum_bhr_hdr_ws(
+        x.data_ptr(), x.stride(0), x.stride(1), xs.data_ptr(), *xs.stride(), y.data_ptr(), y.stride(0), y.stride(1),
+        ys.data_ptr(), *ys.stride(), b, h, r, d, out.data_ptr(), *out.stride(), 2,
+        ws.data_ptr() if ws is not None else None, ws_bytes, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert rc == 0
+    return out
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("group,b", [("flash", 96), ("flash", 256), ("pro", 128), ("small", 300)])
+def test_gpu_split_k(group, b):
+    """The split-K schedule and the unsplit one (no workspace) both within the
+    oracle's bound (float32 out, so the accumulation is what is compared);
+    a workspace one byte short runs the unsplit schedule, bit for bit; two
+    split calls give the same bits."""
+    from flaggems_vllm import _native
+
+    h, r, d = HRD[group] if group in HRD else (3, 2560, 384)
+    print(f"\n[case] fp8_einsum split-K {group} b={b}", flush=True)
+    x, xs, y, ys = random_inputs(b, h, r, d, seed=b + 1)
+    dx, dxs, dy, dys = x.to(DEV), xs.to(DEV), y.to(DEV), ys.to(DEV)
+    need = _native.lib().fgv_fp8_einsum_workspace_bytes(b, h, r, d)
+    assert need > 0
+    ws = torch.empty(need, dtype=torch.uint8, device=DEV)
+    new = lambda: torch.full((b, h, d), float("nan"), device=DEV)
+    split = _abi(dx, dxs, dy, dys, new(), ws, need)
+    again = _abi(dx, dxs, dy, dys, new(), ws, need)
+    plain = _abi(dx, dxs, dy, dys, new())
+    short = _abi(dx, dxs, dy, dys, new(), ws, need - 1)
+    assert torch.equal(split, again) and torch.equal(short, plain)
+    rows = torch.cat([torch.arange(0, b, max(1, b // 24)), torch.tensor([b - 1])])
+    for res in (split, plain):
+        _check(res, x, xs, y, ys, torch.float32, rows=rows)
