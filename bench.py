@@ -675,14 +675,20 @@ def main():
             out = torch.empty((Bt, H, D), dtype=torch.bfloat16, device=dev)
             return lambda: flaggems_vllm.fp8_einsum("bhr,hdr->bhd", x, xs, y, ys, out=out)
 
-        # the launcher's choice (fp8_einsum.hip launch_einsum): skinny up to 64 rows, and up to 128
-        # while 128-row tiles would fill fewer than half of the 256 CUs
-        skinny = Bt <= 64 or (Bt <= 128 and 2 * ((Bt + 127) // 128) * (D // 128) * H < 256)
+        # the launcher's choice (fp8_einsum.hip launch_einsum): split-K tiles when the wrapper's
+        # workspace query asks for one; else skinny up to 64 rows, and up to 128 while 128-row tiles
+        # would fill fewer than half of the 256 CUs
+        from flaggems_vllm import _native
+
+        split = _native.lib().fgv_fp8_einsum_workspace_bytes(Bt, H, R, D) > 0
+        skinny = not split and (Bt <= 64 or (Bt <= 128 and 2 * ((Bt + 127) // 128) * (D // 128) * H < 256))
         kernel = "fp8_einsum_skinny_kernel" if skinny else "fp8_einsum_tile_kernel"
         workload = f"{grp}_b{Bt}"
         config = {"workload": f"fp8_einsum 'bhr,hdr->bhd' {grp}: b {Bt}, h {H}, r {R}, d {D}, e4m3fn x and y, "
                               f"float32 128 / 128x128 block scales, bf16 out",
-                  "b": Bt, "h": H, "r": R, "d": D, "flops_per_call": flops_call}
+                  "b": Bt, "h": H, "r": R, "d": D, "flops_per_call": flops_call,
+                  "schedule": "split-K tiles + fp8_einsum_reduce_kernel (kernel_us covers both)" if split
+                  else "one workgroup per output tile"}
         nb = max(1, min(Bt, 16))
         xd = x_cpu[:nb].float() * xs_cpu[:nb].repeat_interleave(128, dim=2)
         yd = (y_cpu.float() * ys_cpu.repeat_interleave(128, dim=1).repeat_interleave(128, dim=2))

@@ -187,13 +187,16 @@ def test_graph_top_k_per_row():
 
 
 def test_graph_fp8_einsum():
-    """fp8_einsum on both kernels (b 4: skinny; b 200: tiled) into a
-    preallocated output; the replays give the eager bytes."""
+    """fp8_einsum on its three schedules (b 4: skinny; b 200: tiled; b 100
+    with 16 K blocks: split-K, its workspace allocated inside the capture)
+    into a preallocated output; the replays give the eager bytes."""
+    from flaggems_vllm import _native
     from .test_fp8_einsum import random_inputs
 
     _say("graph: fp8_einsum")
-    for b in (4, 200):
-        x, xs, y, ys = (t.to(DEV) for t in random_inputs(b, 2, 1024, 256, seed=b))
+    assert _native.lib().fgv_fp8_einsum_workspace_bytes(100, 2, 2048, 256) > 0
+    for b, r in ((4, 1024), (200, 1024), (100, 2048)):
+        x, xs, y, ys = (t.to(DEV) for t in random_inputs(b, 2, r, 256, seed=b))
         out = torch.empty((b, 2, 256), dtype=torch.bfloat16, device=DEV)
         run = lambda: flaggems_vllm.fp8_einsum("bhr,hdr->bhd", x, xs, y, ys, out=out)
         replay_matches_eager(lambda: out.fill_(7.0), run)
