@@ -333,3 +333,28 @@ def test_gpu_split_threshold(R):
     assert split == (16 * R <= 2 * torch.cuda.get_device_properties(0).multi_processor_count)
     buf, logits, seq = _decode_case(R, V, k, seed=77)
     _run_decode(buf, logits, seq, k, 1, list(range(0, R, 9)) + [R - 1])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("k", [1, 100, 512, 2048])
+def test_gpu_many_short_rows(k):
+    """Many short rows (1100 x 4096, the LDS-cached kernel): ragged ranges
+    (empty rows, rows of at most k values, rows past the width), and rows of
+    ties (8 distinct low bits, 5 distinct values, all equal), NaN, -inf;
+    160 rows against the oracle's sets."""
+    print(f"\n[case] top-k many short rows k={k}", flush=True)
+    g = torch.Generator().manual_seed(900 + k)
+    R, V = 1100, 4096
+    logits = torch.randn(R, V, generator=g)
+    logits[1::7] = (logits[1::7] * 256).round() / 256          # 8-bit ties
+    logits[2::7] = torch.randint(0, 5, (len(range(2, R, 7)), V), generator=g).float()
+    logits[3::7] = 1.5                                           # all equal
+    logits[4::7, ::9] = float("nan")
+    logits[5::7, V // 2:] = float("-inf")
+    starts = torch.randint(0, 600, (R,), generator=g, dtype=I32)
+    ends = starts + torch.randint(0, V - 400, (R,), generator=g, dtype=I32)
+    ends[::11] = starts[::11] + torch.randint(0, k + 1, (len(range(0, R, 11)),), generator=g, dtype=I32)
+    ends[6::50] = starts[6::50]                                  # empty
+    ends[8::50] = V + 5                                          # past the width
+    rows = sorted(set(range(0, R, 7)) | set(range(1, 80)) | {R - 1})
+    _run_prefill(logits, starts, ends, k, rows)
