@@ -713,17 +713,23 @@ template <bool TAIL>
 __device__ __forceinline__ void issue_kv_rows(const PrefillArgs& a, int wave, int lane, int id, uint8_t* tile,
                                               uint8_t* tail, float* mask) {
     __attribute__((address_space(3))) uint8_t* dst = (__attribute__((address_space(3))) uint8_t*)tile;
+    // every lane forms its entry's row address once (vector ALU); row j's
+    // address is then read from lane 8j, with no scalar arithmetic or branch
+    // per row
+    const bool valid = id >= 0 && id < a.s_kv;
+    const uint8_t* mine = valid ? a.kv + (int64_t)id * a.kv_row_bytes : mla_zero_entry;
+    const uint64_t maddr = reinterpret_cast<uint64_t>(mine);
 #pragma unroll
     for (int j = 0; j < kChunk / 4; ++j) {
-        const int idj = __builtin_amdgcn_readlane(id, 8 * j);
-        const uint8_t* row = idj >= 0 && idj < a.s_kv ? a.kv + (int64_t)idj * a.kv_row_bytes : mla_zero_entry;
+        const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)maddr, 8 * j);
+        const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(maddr >> 32), 8 * j);
+        const uint8_t* row = reinterpret_cast<const uint8_t*>(((uint64_t)hi << 32) | lo);
         __builtin_amdgcn_global_load_lds((global_u32_t*)(row + 16 * lane),
                                          (lds_u32_t*)(dst + (8 * wave + j) * kKRowBytes), 16, 0, 0);
     }
-    const bool valid = id >= 0 && id < a.s_kv;
     if constexpr (TAIL) {
         __attribute__((address_space(3))) uint8_t* tdst = (__attribute__((address_space(3))) uint8_t*)tail;
-        const uint8_t* row = valid ? a.kv + (int64_t)id * a.kv_row_bytes + 2 * kHeadDim : mla_zero_entry;
+        const uint8_t* row = valid ? mine + 2 * kHeadDim : mla_zero_entry;
         __builtin_amdgcn_global_load_lds((global_u32_t*)(row + 16 * (lane & 7)),
                                          (lds_u32_t*)(tdst + 8 * kTailRow * wave), 16, 0, 0);
     }
