@@ -38,6 +38,12 @@
 // plus constant offsets.  Entries that are
 // not attended (past the top-k length, negative, or past the cache) are
 // gathered from a zero page, and their scores masked to -inf.
+//
+// The sparse prefill over bf16 rows (flash_mla_sparse_fwd,
+// sparse_mla_prefill_kernel near the end of the kernels) reuses the attend
+// routine and the row DMAs: its rows need no dequantisation, d_qk may be 576
+// (a 64-dim tail that enters the scores only) and it also reports the largest
+// score per head.
 #include <math.h>
 
 #include <mutex>
