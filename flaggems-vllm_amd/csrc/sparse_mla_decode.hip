@@ -272,11 +272,14 @@ __device__ __forceinline__ void issue_rows(const ListView& v, int wave, int lane
                                            float* mask) {
     __attribute__((address_space(3))) uint8_t* dst = (__attribute__((address_space(3))) uint8_t*)tile;
     const int src_off = 16 * lane;
+    // each lane forms its entry's row address once; row j's is read from lane 8j
+    const uint8_t* mine = id >= 0 && id < v.num_entries ? v.expanded + (int64_t)id * (2 * kHeadDim) : mla_zero_entry;
+    const uint64_t maddr = reinterpret_cast<uint64_t>(mine);
 #pragma unroll
     for (int j = 0; j < kChunk / 4; ++j) {
-        const int idj = __builtin_amdgcn_readlane(id, 8 * j);
-        const uint8_t* row = idj >= 0 && idj < v.num_entries ? v.expanded + (int64_t)idj * (2 * kHeadDim)
-                                                             : mla_zero_entry;
+        const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)maddr, 8 * j);
+        const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(maddr >> 32), 8 * j);
+        const uint8_t* row = reinterpret_cast<const uint8_t*>(((uint64_t)hi << 32) | lo);
         __builtin_amdgcn_global_load_lds((global_u32_t*)(row + src_off),
                                          (lds_u32_t*)(dst + (8 * wave + j) * kKRowBytes), 16, 0, 0);
     }
