@@ -85,12 +85,15 @@ struct CombineArgs {
     int32_t* out;
     int64_t out_s0, out_s1;
     int32_t* lens;
+    int32_t num_tokens;  // rows of topk, combined and lens
     int32_t window, ratio, topk_n, m, n, width;
 };
 
 // Grid (requests, workers): wave w of worker k takes the request's tokens
 // k * 4 + w, stepping by 4 * workers, as the reference's programs stride
-// over a request's tokens.  Tokens outside every request are not written.
+// over a request's tokens.  Tokens outside every request are not written, and
+// neither are tokens that query_start_loc places outside [0, num_tokens) (the
+// tensors' rows), which the reference would read and write out of bounds.
 __global__ void __launch_bounds__(kThreads)
 combine_topk_swa_kernel(CombineArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -101,7 +104,10 @@ combine_topk_swa_kernel(CombineArgs a) {
     const int32_t start_pos = seq - (qe - qs), gather_start = seq - a.gather_lens[b];
     const int32_t row_off = wrap_mul(a.m, b);
     const int32_t step = (int32_t)gridDim.y * kRowsPerBlock;
-    for (int32_t t = qs + (int32_t)blockIdx.y * kRowsPerBlock + wave; t < qe; t += step) {
+    const int32_t end = min(qe, a.num_tokens);
+    for (int32_t t = qs + (int32_t)blockIdx.y * kRowsPerBlock + wave; t < end; t += step) {
+        if (t < 0)
+            continue;
         const int32_t pos = start_pos + (t - qs);
         // C (truncating) division, as Triton divides int32
         const int32_t topk_len = min((pos + 1) / a.ratio, a.topk_n);
@@ -208,6 +214,7 @@ extern "C" int fgv_combine_topk_swa_indices(
     a.out_s0 = out_stride0;
     a.out_s1 = out_stride1;
     a.lens = lens;
+    a.num_tokens = (int32_t)num_tokens;
     a.window = (int32_t)window_size;
     a.ratio = (int32_t)compress_ratio;
     a.topk_n = (int32_t)topk;

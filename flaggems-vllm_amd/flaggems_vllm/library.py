@@ -7,7 +7,7 @@ opaque custom ops: the schemas declare what each op writes, namely ``q`` and
 ``k_cache`` for the main op (alias-annotated ``Tensor(a0!) q``, ``Tensor(a2!) k_cache``), ``out``
 for the gather, ``slot_mapping`` for the slot mapping, ``kv_cache`` for the
 indexer key insert and ``k_fp8`` / ``k_fp8_scale`` for its gather, ``indices`` for the top-k per row
-(``output`` for ``persistent_topk``),
+(``output`` and, for rows long enough to split, ``workspace`` for ``persistent_topk``),
 ``out`` for ``fp8_einsum_out`` (the index-row ops, ``fp8_einsum`` and ``flash_mla_sparse_fwd`` write only what they return).  The fake (meta)
 implementations give the output shapes and strides the real ops return.
 Each registered op calls the same wrapper, so argument checks and errors are
@@ -226,7 +226,7 @@ def _(logits, row_starts, row_ends, indices, num_rows, stride0, stride1, top_k):
     return None
 
 
-@_op("persistent_topk", ("output",))
+@_op("persistent_topk", ("output", "workspace"))
 def _persistent_topk(logits: torch.Tensor, lengths: torch.Tensor, output: torch.Tensor, workspace: torch.Tensor,
                      k: int = 512, max_seq_len: Optional[int] = None) -> None:
     persistent_topk(logits, lengths, output, workspace, k, max_seq_len)

@@ -283,7 +283,12 @@ int fgv_cp_gather_indexer_k_quant_cache(
  *   logits   float [M, N], row stride in elements.
  * num_heads 16, 32, 64 or 128; head_dim 128.  The head sum is taken in
  * binary32 in an order of this library's choosing, with k_scale applied once
- * after it (equal to the reference's per-head product since k_scale > 0).
+ * after it.  Precondition: k_scale[n] >= 0 (the producers write amax / 448 >
+ * 0).  For k_scale > 0 this equals the reference's per-head product; for
+ * k_scale = 0 both give 0.  A negative k_scale[n] is not rejected (that would
+ * need a device read) and gives k_scale[n] * sum_h ReLU(dot_h) * w[m,h], not
+ * the reference's sum_h ReLU(dot_h * k_scale[n]) * w[m,h].  The paged
+ * variant below has the same precondition on the cache's scales.
  */
 int fgv_fp8_fp4_mqa_logits(
     const void* q, int64_t q_stride_m, int64_t q_stride_h, const int32_t* q_scale, int64_t q_scale_stride_m,
@@ -401,7 +406,18 @@ int64_t fgv_sparse_mla_decode_workspace_bytes(int64_t batch, int64_t seq_q, int6
 int fgv_sparse_mla_decode_grid(int64_t batch, int64_t seq_q, int64_t num_heads, int64_t topk,
                                int64_t extra_topk);
 
-/* Size of the fixed device scratch of fgv_sparse_mla_decode_model1_no_alloc. */
+/*
+ * Size of the fixed device scratch of fgv_sparse_mla_decode_model1_no_alloc.
+ * Two costs every caller of this library carries:
+ *   - Memory: the array is part of the library's GPU code object, so every
+ *     process that runs any op of this library on a device holds these
+ *     64 MiB of that device's memory until it exits, whether or not it ever
+ *     calls the no-allocation entry point.
+ *   - Concurrency: all no-allocation calls on one device share the array.
+ *     Calls that overlap in time (two streams, two host threads) race on it
+ *     and give wrong results; nothing in the library detects or prevents
+ *     this, so the caller must order them (one stream, or events).
+ */
 #define FGV_MLA_NO_ALLOC_SCRATCH_BYTES (64LL << 20)
 
 /*

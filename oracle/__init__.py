@@ -162,7 +162,7 @@ def lib():
             _P, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _P]
         L.oracle_combine_topk_swa_indices.restype = None
         L.oracle_combine_topk_swa_indices.argtypes = [
-            _P, _I64, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P]
+            _P, _I64, _I64, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P]
         L.oracle_top_k_per_row.restype = None
         L.oracle_top_k_per_row.argtypes = [_P, _I64, _I64, _I64, _I64, _P, _P, _P, _I64, _I64, _P]
         L.oracle_fp8_einsum.restype = None
@@ -576,7 +576,8 @@ def combine_topk_swa_indices(topk_indices, query_start_loc, seq_lens, gather_len
     out = torch.full((t.shape[0], width), fill, dtype=torch.int32)
     lens = torch.full((t.shape[0],), fill, dtype=torch.int32)
     lib().oracle_combine_topk_swa_indices(
-        t.data_ptr(), t.stride(0), t.stride(1), qsl.data_ptr(), seq.data_ptr(), gat.data_ptr(), seq.shape[0],
+        t.data_ptr(), t.stride(0), t.stride(1), t.shape[0], qsl.data_ptr(), seq.data_ptr(), gat.data_ptr(),
+        seq.shape[0],
         int(window_size), int(compress_ratio), int(topk), int(M), int(N), out.data_ptr(), out.stride(0),
         out.stride(1), width, lens.data_ptr())
     return out, lens

@@ -1111,10 +1111,10 @@ void oracle_compute_global_topk_indices(const int32_t* local, int64_t ls0, int64
  * divides int32) and swa_len = min(pos + 1, window).  Rows of tokens outside
  * every request are not written.
  */
-void oracle_combine_topk_swa_indices(const int32_t* topk_idx, int64_t ts0, int64_t ts1, const int32_t* qsl,
-                                     const int32_t* seq_lens, const int32_t* gather_lens, int64_t num_reqs,
-                                     int64_t window, int64_t ratio, int64_t topk, int64_t M, int64_t N,
-                                     int32_t* out, int64_t os0, int64_t os1, int64_t width, int32_t* lens)
+void oracle_combine_topk_swa_indices(const int32_t* topk_idx, int64_t ts0, int64_t ts1, int64_t num_tokens,
+                                     const int32_t* qsl, const int32_t* seq_lens, const int32_t* gather_lens,
+                                     int64_t num_reqs, int64_t window, int64_t ratio, int64_t topk, int64_t M,
+                                     int64_t N, int32_t* out, int64_t os0, int64_t os1, int64_t width, int32_t* lens)
 {
     for (int64_t b = 0; b < num_reqs; ++b) {
         const int64_t start = (int64_t)qsl[b] - qsl[0], end = (int64_t)qsl[b + 1] - qsl[0];
@@ -1122,6 +1122,8 @@ void oracle_combine_topk_swa_indices(const int32_t* topk_idx, int64_t ts0, int64
         const int64_t start_pos = seq - (end - start), gather_start = seq - gather_lens[b];
         const uint32_t row_off = (uint32_t)((int32_t)M * (int32_t)b);
         for (int64_t t = start; t < end; ++t) {
+            if (t < 0 || t >= num_tokens)  /* rows outside the tensors are not touched */
+                continue;
             const int32_t pos = (int32_t)(start_pos + (t - start));
             int32_t topk_len = (pos + 1) / (int32_t)ratio;
             if (topk_len > topk)

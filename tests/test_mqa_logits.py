@@ -298,6 +298,35 @@ def test_gpu_head_counts(H, fp4):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("fp4", [False, True])
+def test_gpu_zero_and_negative_k_scale(fp4):
+    """The kernels apply k_scale once to the ReLU'd head sum, the reference
+    inside each head's ReLU.  For k_scale = 0 both give 0 (pinned against the
+    oracle, which follows the reference's order); for k_scale > 0 they agree;
+    for k_scale < 0 (outside the op's stated precondition) the kernels return
+    k_scale * sum_h w_h ReLU(dot_h), which is -(the oracle's logit at |k_scale|)."""
+    _say(f"mqa logits k_scale zero and negative fp4={fp4}")
+    M, N = 24, 200
+    q, kv, w, ks, ke = W.make_mqa_logits_inputs(M, N, fp4=fp4, seed=9)
+    k_scale = kv[1].reshape(N).clone()
+    k_scale[::5] = 0.0
+    k_scale[1::5] = -k_scale[1::5].abs()
+    neg = k_scale < 0
+    gq, gkv, gw, gks, gke = _dev(q, (kv[0], k_scale), w, ks, ke)
+    got = flaggems_vllm.fp8_fp4_mqa_logits(gq, gkv, gw, gks, gke, clean_logits=True)
+    torch.cuda.synchronize()
+    got = got.cpu()
+    rows = torch.arange(M)
+    want, bound = oracle.mqa_logits(q, (kv[0], k_scale), w, ks, ke, True, rows=rows)
+    _within(got[:, ~neg], want[:, ~neg], bound[:, ~neg], "k_scale >= 0 vs oracle")
+    inside = torch.isfinite(want)
+    assert bool((got[:, ::5][inside[:, ::5]] == 0).all()), "k_scale = 0 gives 0"
+    want_abs, bound_abs = oracle.mqa_logits(q, (kv[0], k_scale.abs()), w, ks, ke, True, rows=rows)
+    fin = torch.isfinite(want_abs[:, neg])
+    _within(-got[:, neg][fin], want_abs[:, neg][fin], bound_abs[:, neg][fin], "k_scale < 0 (documented)")
+
+
+@pytest.mark.gpu
 def test_gpu_strided_inputs():
     """q and k as slices of wider buffers, weights transposed, k_scale [N, 1]."""
     _say("mqa logits strided inputs")

@@ -140,3 +140,27 @@ def test_gpu_torch_op():
     exp = oracle.top_k_per_row(x.cpu(), K, seq_lens=lens.cpu())
     assert torch.equal(out.cpu()[0].sort().values, exp[0])
     assert torch.equal(out.cpu()[1], exp[1])
+
+
+@pytest.mark.gpu
+def test_gpu_torch_op_split_rows_opcheck():
+    """Rows long enough to split write their candidates into the workspace:
+    the schema declares it written, and opcheck's schema test (which flags an
+    undeclared mutation) passes on that path."""
+    from flaggems_vllm import _native
+
+    print("\n[case] persistent_topk torch.ops split path opcheck", flush=True)
+    lengths = [262144, 250000, 262144, 200000]
+    need = _native.lib().fgv_top_k_per_row_workspace_bytes(len(lengths), STRIDE, K)
+    assert need > 0, "the rows must take the split path"
+    x = _hetero(lengths, seed=13).to(DEV)
+    lens = torch.tensor(lengths, dtype=I32, device=DEV)
+    out = torch.empty(len(lengths), K, dtype=I32, device=DEV)
+    ws = torch.zeros(need, dtype=torch.uint8, device=DEV)
+    torch.ops.flaggems_vllm.persistent_topk(x, lens, out, ws, K, None)
+    torch.cuda.synchronize()
+    assert bool(ws.any()), "the split path leaves candidates in the workspace"
+    exp = oracle.top_k_per_row(x.cpu(), K, seq_lens=lens.cpu())
+    assert torch.equal(out.cpu().sort(1).values, exp)
+    torch.library.opcheck(torch.ops.flaggems_vllm.persistent_topk.default, (x, lens, out, ws, K, None),
+                          test_utils=("test_schema", "test_faketensor"))

@@ -605,6 +605,57 @@ def test_gpu_bench_case_against_oracle():
     assert torch.allclose(lse.cpu().double(), l64, rtol=1e-5, atol=1e-5)
 
 
+def _rows_of(w, rows):
+    """The workload restricted to batch rows `rows` (same caches)."""
+    pick = lambda t: None if t is None else t[rows]
+    return W.MlaWorkload(w.name, w.q[rows], w.k_cache, w.indices[rows], pick(w.topk_length), w.attn_sink,
+                         w.extra_k_cache, pick(w.extra_indices), pick(w.extra_topk_length))
+
+
+def _sampled_rows(w, n, seed):
+    """n batch rows: the first and last 8, the 16 with the longest lists (main
+    plus extra), the rest drawn at random."""
+    B = w.q.shape[0]
+    total = torch.zeros(B, dtype=torch.long)
+    for idx, length in ((w.indices, w.topk_length), (w.extra_indices, w.extra_topk_length)):
+        if idx is not None:
+            total += (torch.full((B,), idx.shape[-1]) if length is None
+                      else length.long().clamp(0, idx.shape[-1]))
+    chosen = list(range(8)) + list(range(B - 8, B)) + total.argsort(descending=True)[:16].tolist()
+    rest = [r for r in torch.randperm(B, generator=torch.Generator().manual_seed(seed)).tolist()
+            if r not in chosen]
+    chosen = sorted(set(chosen)) + rest
+    return torch.tensor(sorted(chosen[:n]))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case,grid,rows", [("extra512", 0, None), ("extra8192", 2, 160)])
+def test_gpu_bench_extra_cases_against_oracle(case, grid, rows):
+    """The benchmark's two extra-cache cases at full size, through the wrapper
+    exactly as bench.py times them (its workspace holds the expanded bf16 copy
+    of the extra cache): extra512 on the one-item grid, extra8192 on the paired
+    grid.  extra512 is compared with the binary64 oracle on every batch row,
+    extra8192 on `rows` sampled rows; every output element is finite."""
+    from flaggems_vllm import _native
+
+    print(f"\n[case] sparse MLA bench {case} case", flush=True)
+    w = W.make_mla_case(case)
+    B, SQ, HQ, _ = w.q.shape
+    entries = w.extra_k_cache.shape[0] * w.extra_k_cache.shape[1]
+    assert _grid(w) == grid, f"{case} must take grid {grid}"
+    need = _native.lib().fgv_sparse_mla_decode_workspace_bytes(B, SQ, HQ, w.indices.shape[-1],
+                                                               w.extra_indices.shape[-1], entries)
+    assert need == entries * 1024, "the extra cache must be expanded, with no split partials"
+    out, lse = _gpu(w)
+    out, lse = out.cpu(), lse.cpu()
+    assert bool(torch.isfinite(out.float()).all())
+    sel = torch.arange(B) if rows is None else _sampled_rows(w, rows, seed=17)
+    sub = _rows_of(w, sel)
+    o64, l64 = _oracle(sub)
+    _assert_within_bound(out[sel], o64, _vmax(sub), case)
+    assert torch.allclose(lse[sel].double(), l64, rtol=1e-5, atol=1e-5)
+
+
 @pytest.mark.gpu
 def test_gpu_deterministic():
     print("\n[case] sparse MLA determinism", flush=True)

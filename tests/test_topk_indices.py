@@ -278,3 +278,49 @@ def test_gpu_combine_against_oracle(shape):
     n = sum(qlens)
     assert out.shape == exp.shape
     assert torch.equal(out.cpu()[:n], exp[:n]) and torch.equal(lens.cpu()[:n], exp_lens[:n])
+
+
+def test_combine_oracle_skips_rows_past_the_tensor():
+    """query_start_loc running past topk_indices' rows: the rows inside are the
+    in-bounds result, nothing past them is read or written."""
+    g = torch.Generator().manual_seed(5)
+    T = 20
+    topk_idx = torch.randint(0, 1000, (T, 8), generator=g, dtype=I32)
+    qsl, seq, gat = _t([0, 12, 31]), _t([40, 50]), _t([30, 25])
+    out, lens = oracle.combine_topk_swa_indices(topk_idx, qsl, seq, gat, 16, 4, 8, 64, 32)
+    # the first request lies inside; rows 12..19 of the second are the same
+    # rows as a call whose tensors hold all 31 tokens
+    big = torch.cat([topk_idx, torch.zeros(11, 8, dtype=I32)])
+    eo, el = oracle.combine_topk_swa_indices(big, qsl, seq, gat, 16, 4, 8, 64, 32)
+    assert torch.equal(out, eo[:T]) and torch.equal(lens, el[:T])
+
+
+@pytest.mark.gpu
+def test_gpu_combine_rows_past_the_tensor_untouched():
+    """query_start_loc whose last request runs 11 tokens past topk_indices'
+    rows (and a first entry of 0): the kernel writes the rows inside, as the
+    oracle does, and leaves guard rows after combined and lens untouched."""
+    from flaggems_vllm import _native
+
+    print("\n[case] combine top-k + window, query_start_loc past the rows", flush=True)
+    g = torch.Generator().manual_seed(5)
+    T, guard = 20, 16
+    topk_idx = torch.randint(0, 1000, (T, 8), generator=g, dtype=I32)
+    qsl, seq, gat = _t([0, 12, 31]), _t([40, 50]), _t([30, 25])
+    k, window, ratio, M, N = 8, 16, 4, 64, 32
+    width = _native.lib().fgv_combine_topk_swa_width(k, window)
+    exp, exp_lens = oracle.combine_topk_swa_indices(topk_idx, qsl, seq, gat, window, ratio, k, M, N)
+    comb = torch.full((T + guard, width), -7, dtype=I32, device=DEV)
+    lens = torch.full((T + guard,), -7, dtype=I32, device=DEV)
+    # topk_indices also sits in front of guard rows, so every access the
+    # kernel could make stays inside allocated memory
+    d = torch.cat([topk_idx, torch.zeros(guard, 8, dtype=I32)]).to(DEV)[:T]
+    q, s, ga = qsl.to(DEV), seq.to(DEV), gat.to(DEV)
+    rc = _native.lib().fgv_combine_topk_swa_indices(
+        d.data_ptr(), d.stride(0), d.stride(1), T, k, q.data_ptr(), s.data_ptr(), ga.data_ptr(), 2,
+        window, ratio, k, M, N, comb.data_ptr(), comb.stride(0), comb.stride(1), lens.data_ptr(),
+        torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert torch.equal(comb.cpu()[:T], exp) and torch.equal(lens.cpu()[:T], exp_lens)
+    assert bool((comb.cpu()[T:] == -7).all()) and bool((lens.cpu()[T:] == -7).all())

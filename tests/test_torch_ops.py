@@ -35,7 +35,7 @@ WRITES = {
     "top_k_per_row_prefill": {"indices"},
     "fp8_einsum": set(),
     "fp8_einsum_out": {"out"},
-    "persistent_topk": {"output"},
+    "persistent_topk": {"output", "workspace"},
     "flash_mla_sparse_fwd": set(),
 }
 
