@@ -70,6 +70,9 @@ def parse_args():
                     help="main op over the reference benchmark's grid (T x H); one JSON line per point "
                          "and a markdown table, instead of the single headline line")
     ap.add_argument("--grid-max-tokens", type=int, default=131072)
+    ap.add_argument("--eager", action="store_true",
+                    help="host cost of eager calls of the main op and the sibling at decode sizes "
+                         "(T 1..64, H 64 and 128); a markdown table instead of the headline line")
     return ap.parse_args()
 
 
@@ -333,6 +336,68 @@ def run_grid(args):
               f"| {100 * r['frac_of_8tbps']:.1f} | {r['tokens_per_s']:.3g} |", flush=True)
 
 
+def host_us_per_call(fn, calls):
+    """Host wall time per call of `calls` back-to-back eager calls (no
+    synchronisation inside the loop), microseconds."""
+    import torch
+
+    fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(calls):
+        fn()
+    t1 = time.perf_counter()
+    torch.cuda.synchronize()
+    return (t1 - t0) / calls * 1e6
+
+
+def run_eager(args):
+    """Eager host cost of the two ops at decode sizes: per-call intervals
+    between HIP events (median) and host wall time per call, beside the
+    graph-replay kernel time; the main op through the Python drop-in and
+    through torch.ops."""
+    import torch
+
+    import flaggems_vllm
+    from flaggems_vllm import testing as W
+
+    dev = torch.device("cuda:0")
+    main_op = flaggems_vllm.fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert
+    torch_op = torch.ops.flaggems_vllm.fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert
+    calls = 2000
+    rows = []
+    for T in (1, 4, 17, 64):
+        for H in (64, 128):
+            g = torch.Generator(device=dev).manual_seed(T * 1000 + H)
+            q = torch.randn(T, H, 512, generator=g, device=dev, dtype=torch.bfloat16)
+            kv = torch.randn(T, 512, generator=g, device=dev, dtype=torch.bfloat16)
+            cs = W.make_cos_sin_cache(4096).to(dev)
+            pos = torch.arange(T, dtype=torch.int64, device=dev)
+            cache = torch.zeros(T // 64 + 2, 64 * W.HEAD_BYTES, dtype=torch.uint8, device=dev)
+            a = (q, kv, cache, pos, pos, cs, 1e-6, 64)
+            o = torch.randn(T, H, 512, generator=g, device=dev, dtype=torch.bfloat16)
+            sib = (o, pos, cs, 8, H // 8)
+            r = {"num_tokens": T, "num_heads": H}
+            _, t_kernel, _ = time_gpu(lambda: main_op(*a), 200, args.warmup)
+            r["main_kernel_us"] = t_kernel * 1e6
+            r["main_event_median_us"] = median_call_us(lambda: main_op(*a), calls)
+            r["main_host_us"] = host_us_per_call(lambda: main_op(*a), calls)
+            r["main_torch_ops_host_us"] = host_us_per_call(lambda: torch_op(*a), calls)
+            r["sibling_event_median_us"] = median_call_us(lambda: flaggems_vllm.fused_inv_rope_fp8_quant(*sib),
+                                                          calls)
+            r["sibling_host_us"] = host_us_per_call(lambda: flaggems_vllm.fused_inv_rope_fp8_quant(*sib), calls)
+            print(json.dumps(r), flush=True)
+            rows.append(r)
+    print("\n| T | H | main: kernel µs (graph) | main: µs median per eager call (events) | main: host µs per call "
+          "| main via torch.ops: host µs per call | sibling: µs median per eager call (events) "
+          "| sibling: host µs per call |")
+    print("|---|---|---|---|---|---|---|---|")
+    for r in rows:
+        print(f"| {r['num_tokens']} | {r['num_heads']} | {r['main_kernel_us']:.2f} | {r['main_event_median_us']:.2f} "
+              f"| {r['main_host_us']:.2f} | {r['main_torch_ops_host_us']:.2f} | {r['sibling_event_median_us']:.2f} "
+              f"| {r['sibling_host_us']:.2f} |", flush=True)
+
+
 def main():
     args = parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -350,6 +415,9 @@ def main():
     torch.cuda.set_device(dev)
     if args.grid:
         run_grid(args)
+        return
+    if args.eager:
+        run_eager(args)
         return
     from oracle import torch_ref
 

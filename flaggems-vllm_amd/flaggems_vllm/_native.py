@@ -1,19 +1,28 @@
-"""Build and load the gfx950 HIP library ``libflaggems_vllm_amd.so``.
+"""Build and load the gfx950 HIP library ``libflaggems_vllm_amd.so`` and the
+torch extension ``_fgv_torch.so`` over it.
 
-The library is built in-tree (next to this file) by ``build()`` and loaded
-with ctypes by ``lib()``.  There is no fallback: if the library is missing or
-cannot be loaded, every op raises.
+Both are built in-tree (next to this file) by ``build()``.  ``lib()`` loads
+the C-ABI library with ctypes; ``torch_ext()`` imports the extension, whose
+C++ functions check arguments and launch the main op and the sibling op
+through the same C ABI (and register them as torch.ops.flaggems_vllm ops).
+There is no fallback: if either is missing or cannot be loaded, the ops raise.
 """
 import ctypes
 import glob
+import importlib.machinery
+import importlib.util
 import os
 import subprocess
+import sysconfig
 
 _PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 _ROOT = os.path.dirname(_PKG_DIR)  # flaggems-vllm_amd/
 _CSRC = os.path.join(_ROOT, "csrc")
 _INCLUDE = os.path.join(os.path.dirname(_ROOT), "include")
 LIB_PATH = os.path.join(_PKG_DIR, "libflaggems_vllm_amd.so")
+EXT_NAME = "_fgv_torch"
+EXT_PATH = os.path.join(_PKG_DIR, EXT_NAME + ".so")
+EXT_SOURCE = os.path.join(_CSRC, "torch_ops.cpp")
 
 ARCH = "gfx950"
 HIPCC_FLAGS = [
@@ -34,18 +43,78 @@ def sources():
     return sorted(glob.glob(os.path.join(_CSRC, "*.hip")))
 
 
-def build(verbose=False):
-    """Compile every HIP source into LIB_PATH (always recompiles)."""
-    hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
-    tmp = LIB_PATH + ".tmp"
-    cmd = [hipcc, *HIPCC_FLAGS, f"-I{_INCLUDE}", f"-I{_CSRC}", *sources(), "-o", tmp]
+def _run(cmd, what, verbose):
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stdout}\n{res.stderr}")
+        raise RuntimeError(f"{what} failed ({res.returncode}):\n{res.stdout}\n{res.stderr}")
+
+
+def ext_command(out):
+    """g++ line of the torch extension: host C++ against torch's headers and
+    libraries and the C-ABI library next to it (found at run time through
+    an $ORIGIN rpath)."""
+    import torch
+
+    tdir = os.path.dirname(os.path.abspath(torch.__file__))
+    tinc, tlib = os.path.join(tdir, "include"), os.path.join(tdir, "lib")
+    abi = int(bool(torch._C._GLIBCXX_USE_CXX11_ABI))
+    return [
+        os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall",
+        f"-D_GLIBCXX_USE_CXX11_ABI={abi}", f"-DTORCH_EXTENSION_NAME={EXT_NAME}", "-DTORCH_API_INCLUDE_EXTENSION_H",
+        "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
+        f"-I{tinc}", f"-I{os.path.join(tinc, 'torch', 'csrc', 'api', 'include')}",
+        f"-I{sysconfig.get_paths()['include']}", "-I/opt/rocm/include", f"-I{_INCLUDE}",
+        EXT_SOURCE, "-o", out,
+        f"-L{tlib}", "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_hip", "-ltorch_python",
+        f"-Wl,-rpath,{tlib}",
+        f"-L{_PKG_DIR}", "-lflaggems_vllm_amd", "-Wl,-rpath,$ORIGIN",
+    ]
+
+
+def build(verbose=False):
+    """Compile every HIP source into LIB_PATH, then the torch extension into
+    EXT_PATH (always recompiles both)."""
+    hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+    tmp = LIB_PATH + ".tmp"
+    _run([hipcc, *HIPCC_FLAGS, f"-I{_INCLUDE}", f"-I{_CSRC}", *sources(), "-o", tmp], "hipcc", verbose)
     os.replace(tmp, LIB_PATH)
+    tmp = EXT_PATH + ".tmp"
+    _run(ext_command(tmp), "g++ (torch extension)", verbose)
+    os.replace(tmp, EXT_PATH)
     return LIB_PATH
+
+
+_ext = None
+
+
+def torch_ext():
+    """The imported torch extension (registers torch.ops.flaggems_vllm's C++
+    ops on first import); raises RuntimeError if it is not built."""
+    global _ext
+    if _ext is not None:
+        return _ext
+    if not os.path.exists(EXT_PATH):
+        raise RuntimeError(
+            f"{EXT_PATH} is missing: build it with `python -c 'import __graft_entry__ as g; "
+            "g.build()'`. flaggems_vllm has no non-HIP fallback."
+        )
+    lib()  # the C ABI it links, loaded first from this directory
+    loader = importlib.machinery.ExtensionFileLoader(f"flaggems_vllm.{EXT_NAME}", EXT_PATH)
+    spec = importlib.util.spec_from_file_location(f"flaggems_vllm.{EXT_NAME}", EXT_PATH, loader=loader)
+    mod = importlib.util.module_from_spec(spec)
+    loader.exec_module(mod)
+    _ext = mod
+    return _ext
+
+
+def raise_status(rc: int, what: str):
+    """Raise for a non-zero status of a torch-extension function:
+    AssertionError for a failed reference assertion, otherwise as check()."""
+    if rc == _ext.ASSERT_FAILED:
+        raise AssertionError(f"{what}: {_ext.assert_message()}")
+    check(rc, what)
 
 
 _lib = None

@@ -10,8 +10,11 @@ indexer key insert and ``k_fp8`` / ``k_fp8_scale`` for its gather, ``indices`` f
 (``output`` and, for rows long enough to split, ``workspace`` for ``persistent_topk``),
 ``out`` for ``fp8_einsum_out`` (the index-row ops, ``fp8_einsum`` and ``flash_mla_sparse_fwd`` write only what they return).  The fake (meta)
 implementations give the output shapes and strides the real ops return.
-Each registered op calls the same wrapper, so argument checks and errors are
-the wrapper's.
+The main op and the sibling are C++ ops (the torch extension's
+``torch_ops.cpp``, loaded here): the same checks and launch the Python
+functions call, raising RuntimeError on a failure as vLLM's compiled op does.
+Every other registered op calls its Python wrapper, so argument checks and
+errors are the wrapper's.
 
 ``fused_indexer_q_rope_quant`` returns ``(q, q_scale, weights)`` here, with an
 empty ``q_scale`` for FP8, because an op schema cannot return the nested tuple
@@ -22,6 +25,7 @@ from typing import List, Optional, Tuple
 
 import torch
 
+from . import _native
 from .ops import (
     combine_topk_swa_indices,
     compute_global_topk_indices_and_lens,
@@ -30,9 +34,7 @@ from .ops import (
     dequantize_and_gather_k_cache,
     flash_mla_sparse_fwd,
     fp8_einsum,
-    fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert,
     fused_indexer_q_rope_quant,
-    fused_inv_rope_fp8_quant,
     fused_q_kv_rmsnorm,
     indexer_k_quant_and_cache,
     persistent_topk,
@@ -47,29 +49,17 @@ def _op(name: str, mutates: Tuple[str, ...] = ()):
     return torch.library.custom_op(f"{NAMESPACE}::{name}", mutates_args=mutates, device_types="cuda")
 
 
-@_op("fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert", ("q", "k_cache"))
-def _qnorm_rope_kv_insert(q: torch.Tensor, kv: torch.Tensor, k_cache: torch.Tensor, slot_mapping: torch.Tensor,
-                          position_ids: torch.Tensor, cos_sin_cache: torch.Tensor, eps: float,
-                          cache_block_size: int) -> None:
-    fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert(q, kv, k_cache, slot_mapping, position_ids, cos_sin_cache,
-                                                      eps, cache_block_size)
+# The main op and the sibling are C++ ops (torch_ops.cpp), registered in this
+# namespace when the torch extension loads; their fakes are registered here.
+_native.torch_ext()
 
 
-@_qnorm_rope_kv_insert.register_fake
+@torch.library.register_fake(f"{NAMESPACE}::fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert")
 def _(q, kv, k_cache, slot_mapping, position_ids, cos_sin_cache, eps, cache_block_size):
     return None
 
 
-@_op("fused_inv_rope_fp8_quant")
-def _inv_rope_fp8_quant(o: torch.Tensor, positions: torch.Tensor, cos_sin_cache: torch.Tensor, n_groups: int,
-                        heads_per_group: int, nope_dim: int = 448, rope_dim: int = 64,
-                        quant_group_size: int = 128, eps: float = 1e-10,
-                        tma_aligned_scales: bool = False) -> Tuple[torch.Tensor, torch.Tensor]:
-    return fused_inv_rope_fp8_quant(o, positions, cos_sin_cache, n_groups, heads_per_group, nope_dim, rope_dim,
-                                    quant_group_size, eps, None, tma_aligned_scales)
-
-
-@_inv_rope_fp8_quant.register_fake
+@torch.library.register_fake(f"{NAMESPACE}::fused_inv_rope_fp8_quant")
 def _(o, positions, cos_sin_cache, n_groups, heads_per_group, nope_dim=448, rope_dim=64, quant_group_size=128,
       eps=1e-10, tma_aligned_scales=False):
     # the real op's layout: fp8 (G, T, d) and scales (G, K, Tpad), both

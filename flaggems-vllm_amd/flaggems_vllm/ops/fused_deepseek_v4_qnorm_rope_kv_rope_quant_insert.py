@@ -4,9 +4,12 @@ Drop-in for the reference op of the same name
 (src/flaggems_vllm/ops/fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert.py:289-351):
 same positional signature, same in-place contract (q and k_cache mutated, kv
 and the index tensors untouched), same AssertionError for the same bad inputs.
-The work is one launch of the gfx950 HIP kernel ``qnorm_rope_kv_insert_kernel``
-through the C ABI ``fgv_qnorm_rope_kv_rope_quant_insert``, on the current
-stream, with no host synchronisation and no allocation.
+The argument checks and the launch run in C++ (``torch_ops.cpp``,
+``qnorm_rope_kv_insert``): one launch of the gfx950 HIP kernel
+``qnorm_rope_kv_insert_kernel`` through the C ABI
+``fgv_qnorm_rope_kv_rope_quant_insert``, on the current stream, with no host
+synchronisation and no allocation.  An eager call costs a few microseconds of
+host time.
 
 Beyond the reference: q and kv may be strided views (unit last stride, row
 strides multiple of 8 elements), as when they are slices of one fused
@@ -17,14 +20,14 @@ cache's rows instead of being read out of bounds.
 import torch
 
 from .. import _native
-from ._common import current_stream_ptr, on_device_of
 
 HEAD_DIM = 512
 ROPE_DIM = 64
 
 
 def cache_geometry(k_cache: torch.Tensor):
-    """(num_blocks, block stride in bytes) the kernel addresses k_cache with.
+    """(num_blocks, block stride in bytes) the kernel addresses k_cache with
+    (the rule the C++ op applies before its launch).
 
     A [num_blocks, block_bytes] cache (or any cache with more dimensions)
     has k_cache.shape[0] blocks, stride(0) bytes apart.  A 1-D cache is one
@@ -62,44 +65,7 @@ def fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert(
         eps: RMSNorm epsilon.
         cache_block_size: tokens per cache block.
     """
-    assert q.dim() == 3 and kv.dim() == 2, "q must be 3-D and kv 2-D"
-    assert q.stride(-1) == 1 and kv.stride(-1) == 1, "q and kv need a unit last stride"
-    num_tokens, num_heads, head_dims = q.shape
-    assert head_dims == HEAD_DIM
-    assert kv.shape == (num_tokens, HEAD_DIM)
-    assert q.dtype == torch.bfloat16 and kv.dtype == torch.bfloat16
-    assert k_cache.dtype == torch.uint8
-    assert slot_mapping.dim() == 1
-    num_tokens_insert = slot_mapping.shape[0]
-    assert num_tokens_insert <= num_tokens
-    assert slot_mapping.dtype == torch.int64
-    assert position_ids.shape == (num_tokens,)
-    assert position_ids.dtype == torch.int64
-    assert cos_sin_cache.dim() == 2 and cos_sin_cache.shape[1] == ROPE_DIM
-    assert cos_sin_cache.dtype == torch.float32
-    assert cos_sin_cache.stride(1) == 1, "cos_sin_cache rows must be contiguous"
-    assert slot_mapping.stride(0) == 1 or num_tokens_insert <= 1
-    assert position_ids.stride(0) == 1 or num_tokens <= 1
-    assert k_cache.dim() >= 1 and (k_cache.dim() == 1 or k_cache[0].is_contiguous()), (
-        "each k_cache block must be contiguous bytes"
-    )
-    for t in (kv, k_cache, slot_mapping, position_ids, cos_sin_cache):
-        assert t.device == q.device, "all tensors must be on q's device"
-    assert q.device.type == "cuda", "flaggems_vllm runs on the GPU (HIP) only"
-
-    if num_tokens == 0:
-        return
-    num_blocks, block_stride = cache_geometry(k_cache)
-    with on_device_of(q):
-        rc = _native.lib().fgv_qnorm_rope_kv_rope_quant_insert(
-            q.data_ptr(), q.stride(0), q.stride(1),
-            kv.data_ptr(), kv.stride(0),
-            k_cache.data_ptr(), block_stride, num_blocks,
-            slot_mapping.data_ptr(), num_tokens_insert,
-            position_ids.data_ptr(),
-            cos_sin_cache.data_ptr(), cos_sin_cache.stride(0), cos_sin_cache.shape[0],
-            num_tokens, num_heads,
-            float(eps), int(cache_block_size),
-            current_stream_ptr(q.device),
-        )
-    _native.check(rc, "fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert")
+    rc = _native.torch_ext().qnorm_rope_kv_insert(q, kv, k_cache, slot_mapping, position_ids, cos_sin_cache,
+                                                  eps, cache_block_size)
+    if rc:
+        _native.raise_status(rc, "fused_deepseek_v4_qnorm_rope_kv_rope_quant_insert")
