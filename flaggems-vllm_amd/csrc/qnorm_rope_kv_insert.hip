@@ -13,6 +13,9 @@
 // the per-row math uses DPP reductions only, and q blocks hold one pass of 16
 // rows (16 KiB in, 16 KiB out); large grids run four workgroups per CU
 // (kOccupancyLds below), 4 waves per SIMD with 4 KiB of loads in flight each.
+// The cos/sin row of a token is read from L2 by each row's rope lanes, except
+// on one-round grids with whole tokens per block, where it is staged in LDS
+// once per block (q_block's kCsLds: measured faster there, slower elsewhere).
 //
 // Which 16 rows a q block takes (QMap):
 //   kMapRows / kMapRowsOneToken: rows 16b .. 16b+15 in (token, head) order.
@@ -117,6 +120,29 @@ __device__ __forceinline__ void unpack8(uint4 v, float (&x)[8]) {
     x[6] = bf16_lo(v.w); x[7] = bf16_hi(v.w);
 }
 
+// RMSNorm of one q row held in v (this lane's four pieces), GPT-J rotation of
+// its rope lanes with this lane's cos/sin, bf16 stores in place.
+__device__ __forceinline__ void q_row_math(const QnormArgs& a, uint16_t* rowp, const uint4 (&v)[4], int lane16,
+                                           bool rope_lane, float4 cs_c, float4 cs_s) {
+    const float r = rms_factor(v, a.eps);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        float x[8];
+        unpack8(v[k], x);
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            x[i] = x[i] * r;
+        uint4 out;
+        if (k == 3 && rope_lane) {
+            out = rope_piece(x, cs_c, cs_s);
+        } else {
+            out = make_uint4(pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3]),
+                             pack_bf16x2(x[4], x[5]), pack_bf16x2(x[6], x[7]));
+        }
+        store16(rowp + (lane16 + 16 * k) * 8, out);
+    }
+}
+
 enum QMap { kMapRows = 0, kMapRowsOneToken = 1, kMapAligned = 2 };
 
 // v / p for v, p < 2^32 (p >= 1).  The binary64 estimate v * (1/p) is within
@@ -135,7 +161,14 @@ __device__ __forceinline__ uint32_t div_pitch(uint32_t v, uint32_t p, double inv
 // in-order vmcnt counter would otherwise make that dependent load wait for
 // the q loads issued before it.  kMapRowsOneToken (num_heads a multiple of
 // 16): all rows of the block share one token, whose position is a scalar load.
-template <int kMap>
+// kCsLds (kMapRowsOneToken, grids of one round): the cos/sin row is staged in
+// LDS once per block instead of loaded by each row's rope lanes.  Measured on
+// MI355X (same-box A/B): c1 (T = 256, H = 64, one round of 1040 workgroups)
+// 7.07-7.20 -> 6.43-6.61 us; on grids of several rounds the block barrier
+// costs more than it saves (c2 +2.7-3.2 %, c3 +2.4 %), so they load per row.
+// A per-wave variant without the barrier (the wave's first row loads, row
+// permutes broadcast) measured no faster than per-row loads on c1.
+template <int kMap, bool kCsLds>
 __device__ void q_block(const QnormArgs& a, uint32_t qb, int lane16, int row_in_pass) {
     const bool rope_lane = lane16 >= 8;
     uint32_t t;
@@ -169,6 +202,28 @@ __device__ void q_block(const QnormArgs& a, uint32_t qb, int lane16, int row_in_
         const uint32_t h = row - t * a.num_heads;
         rowp = a.q + (int64_t)t * a.q_st + (int64_t)h * a.q_sh;
     }
+    if (kCsLds) {
+        // One-round grids: the token's 256-byte cos/sin row is loaded once
+        // per block (by threads 0..15) into LDS.  Every row of the block has
+        // that token (kMapRowsOneToken).
+        __shared__ float4 cs_row[16];
+        uint4 v[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            v[k] = load16(rowp + (lane16 + 16 * k) * 8);
+        if (threadIdx.x < 16) {
+            const int64_t pos = clamp_position(pos_raw, a.max_pos);
+            cs_row[threadIdx.x] = *reinterpret_cast<const float4*>(a.cos_sin + pos * a.cs_stride + threadIdx.x * 4);
+        }
+        __syncthreads();
+        float4 cs_c = make_float4(0.f, 0.f, 0.f, 0.f), cs_s = cs_c;
+        if (rope_lane) {
+            cs_c = cs_row[lane16 - 8];  // cos of pairs 4(lane16-8) ..
+            cs_s = cs_row[lane16];      // sin of the same pairs
+        }
+        q_row_math(a, rowp, v, lane16, rope_lane, cs_c, cs_s);
+        return;
+    }
     if (!valid)
         return;
     uint4 v[4];
@@ -182,25 +237,9 @@ __device__ void q_block(const QnormArgs& a, uint32_t qb, int lane16, int row_in_
         cs_c = *reinterpret_cast<const float4*>(cs);
         cs_s = *reinterpret_cast<const float4*>(cs + kHalfRope);
     }
-
-    const float r = rms_factor(v, a.eps);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        float x[8];
-        unpack8(v[k], x);
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-            x[i] = x[i] * r;
-        uint4 out;
-        if (k == 3 && rope_lane) {
-            out = rope_piece(x, cs_c, cs_s);
-        } else {
-            out = make_uint4(pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3]),
-                             pack_bf16x2(x[4], x[5]), pack_bf16x2(x[6], x[7]));
-        }
-        store16(rowp + (lane16 + 16 * k) * 8, out);
-    }
+    q_row_math(a, rowp, v, lane16, rope_lane, cs_c, cs_s);
 }
+
 
 // UE8M0 exponent of a 64-element group: ceil(log2(max(amax, 1e-4) / 448)).
 // With a = m * 2^E (1 <= m < 2) and 448 = 1.75 * 2^8 this is
@@ -245,6 +284,15 @@ __device__ void kv_block(const QnormArgs& a, uint32_t kvb, int lane16, int row_i
     uint8_t* tok = base + pib * kTokenDataBytes;
     uint8_t* scl = base + a.block_size * kTokenDataBytes + pib * kScaleBytesPerToken;
 
+    // Cache stores are 8 bytes per lane (the codes of the lane's 8 dims; two
+    // per RoPE lane).  16-byte stores (odd lanes' codes moved to even lanes by
+    // DPP, the RoPE bytes in one store, when the cache allows 16-byte
+    // alignment) measured slower in a same-box A/B: c0 2.25 -> 2.61 us, c1
+    // unchanged, c2 +1.1 %.  The kv rows are 1.4 % of c2's bytes, and the
+    // measured HBM traffic is already 1.008 x the algorithmic bytes.
+    // Folding each token's kv row into a fifth wave of that token's first q
+    // block (one-round grids, no kv blocks) measured slower too: c1 7.20 ->
+    // 8.0 us.
     uint32_t my_bytes = 0;  // byte k = scale byte of the group in piece k
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -284,7 +332,7 @@ __device__ void kv_block(const QnormArgs& a, uint32_t kvb, int lane16, int row_i
     }
 }
 
-template <int kMap>
+template <int kMap, bool kCsLds>
 __global__ void __launch_bounds__(kThreads)
 qnorm_rope_kv_insert_kernel(QnormArgs a) {
     const int lane16 = threadIdx.x & 15;
@@ -292,7 +340,7 @@ qnorm_rope_kv_insert_kernel(QnormArgs a) {
     if (blockIdx.x < a.kv_blocks)
         kv_block(a, blockIdx.x, lane16, row_in_pass);
     else
-        q_block<kMap>(a, blockIdx.x - a.kv_blocks, lane16, row_in_pass);
+        q_block<kMap, kCsLds>(a, blockIdx.x - a.kv_blocks, lane16, row_in_pass);
 }
 
 }  // namespace
@@ -389,13 +437,16 @@ extern "C" int fgv_qnorm_rope_kv_rope_quant_insert(
     const hipStream_t st = static_cast<hipStream_t>(stream);
     const size_t lds = grid > kUncappedRound ? kOccupancyLds : 0;
     if (map == kMapAligned)
-        hipLaunchKernelGGL(qnorm_rope_kv_insert_kernel<kMapAligned>, dim3((uint32_t)grid), dim3(kThreads),
+        hipLaunchKernelGGL((qnorm_rope_kv_insert_kernel<kMapAligned, false>), dim3((uint32_t)grid), dim3(kThreads),
                            lds, st, a);
+    else if (map == kMapRowsOneToken && grid <= kUncappedRound)
+        hipLaunchKernelGGL((qnorm_rope_kv_insert_kernel<kMapRowsOneToken, true>), dim3((uint32_t)grid),
+                           dim3(kThreads), lds, st, a);
     else if (map == kMapRowsOneToken)
-        hipLaunchKernelGGL(qnorm_rope_kv_insert_kernel<kMapRowsOneToken>, dim3((uint32_t)grid),
+        hipLaunchKernelGGL((qnorm_rope_kv_insert_kernel<kMapRowsOneToken, false>), dim3((uint32_t)grid),
                            dim3(kThreads), lds, st, a);
     else
-        hipLaunchKernelGGL(qnorm_rope_kv_insert_kernel<kMapRows>, dim3((uint32_t)grid), dim3(kThreads),
+        hipLaunchKernelGGL((qnorm_rope_kv_insert_kernel<kMapRows, false>), dim3((uint32_t)grid), dim3(kThreads),
                            lds, st, a);
     return launch_status();
 }
