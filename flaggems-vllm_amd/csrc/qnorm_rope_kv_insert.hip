@@ -14,8 +14,9 @@
 // rows (16 KiB in, 16 KiB out); large grids run four workgroups per CU
 // (kOccupancyLds below), 4 waves per SIMD with 4 KiB of loads in flight each.
 // The cos/sin row of a token is read from L2 by each row's rope lanes, except
-// on one-round grids with whole tokens per block, where it is staged in LDS
-// once per block (q_block's kCsLds: measured faster there, slower elsewhere).
+// on one-round grids of 4-8 workgroups per CU with whole tokens per block,
+// where it is staged in LDS once per block (q_block's kCsLds: measured faster
+// there, slower elsewhere).
 //
 // Which 16 rows a q block takes (QMap):
 //   kMapRows / kMapRowsOneToken: rows 16b .. 16b+15 in (token, head) order.
@@ -51,6 +52,11 @@ constexpr size_t kOccupancyLds = 40 * 1024;
 // while the cap would split it: c1 (T = 256, H = 64) is 1040 workgroups, one
 // round uncapped, but 1024 + 16 with four per CU.
 constexpr int64_t kUncappedRound = 8 * 256;
+// One-round grids of at least four workgroups per CU stage the cos/sin row in
+// LDS (q_block's kCsLds); smaller ones load it per row.  Same-box A/B, µs per
+// call: c1 (1040 workgroups) 7.12 -> 6.62; T = 64 x H = 128 (516) 4.23 ->
+// 4.40, T = 17 x H = 64 (72) 2.20 -> 2.29, T = 1 and 4 unchanged.
+constexpr int64_t kCsLdsMinGrid = 4 * 256;
 
 struct QnormArgs {
     uint16_t* q;
@@ -161,13 +167,15 @@ __device__ __forceinline__ uint32_t div_pitch(uint32_t v, uint32_t p, double inv
 // in-order vmcnt counter would otherwise make that dependent load wait for
 // the q loads issued before it.  kMapRowsOneToken (num_heads a multiple of
 // 16): all rows of the block share one token, whose position is a scalar load.
-// kCsLds (kMapRowsOneToken, grids of one round): the cos/sin row is staged in
-// LDS once per block instead of loaded by each row's rope lanes.  Measured on
-// MI355X (same-box A/B): c1 (T = 256, H = 64, one round of 1040 workgroups)
-// 7.07-7.20 -> 6.43-6.61 us; on grids of several rounds the block barrier
-// costs more than it saves (c2 +2.7-3.2 %, c3 +2.4 %), so they load per row.
-// A per-wave variant without the barrier (the wave's first row loads, row
-// permutes broadcast) measured no faster than per-row loads on c1.
+// kCsLds (kMapRowsOneToken, one-round grids of 1024..2048 workgroups): the
+// cos/sin row is staged in LDS once per block instead of loaded by each row's
+// rope lanes.  Measured on MI355X (same-box A/Bs): c1 (T = 256, H = 64, one
+// round of 1040 workgroups) 7.07-7.20 -> 6.43-6.62 us; on grids of several
+// rounds the block barrier costs more than it saves (c2 +2.7-3.2 %, c3
+// +2.4 %), and on one-round grids below four workgroups per CU it is up to
+// 4 % slower (kCsLdsMinGrid), so those load per row.  A per-wave variant
+// without the barrier (the wave's first row loads, row permutes broadcast)
+// measured no faster than per-row loads on c1.
 template <int kMap, bool kCsLds>
 __device__ void q_block(const QnormArgs& a, uint32_t qb, int lane16, int row_in_pass) {
     const bool rope_lane = lane16 >= 8;
@@ -439,7 +447,7 @@ extern "C" int fgv_qnorm_rope_kv_rope_quant_insert(
     if (map == kMapAligned)
         hipLaunchKernelGGL((qnorm_rope_kv_insert_kernel<kMapAligned, false>), dim3((uint32_t)grid), dim3(kThreads),
                            lds, st, a);
-    else if (map == kMapRowsOneToken && grid <= kUncappedRound)
+    else if (map == kMapRowsOneToken && grid >= kCsLdsMinGrid && grid <= kUncappedRound)
         hipLaunchKernelGGL((qnorm_rope_kv_insert_kernel<kMapRowsOneToken, true>), dim3((uint32_t)grid),
                            dim3(kThreads), lds, st, a);
     else if (map == kMapRowsOneToken)

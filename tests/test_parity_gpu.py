@@ -355,8 +355,11 @@ def test_combined_largest(T, H, bs):
 # Grids around one round of workgroups (T * H from 8192 to 32769 rows, 512 to
 # 2049 blocks): head counts that are and are not multiples of the 16-row block
 # (one token per block or not), ragged last blocks, H = 1.
+# (256, 64), (129, 128), (160, 112), (200, 128) and (496, 64) are one-round
+# grids of 1024-2048 workgroups with whole tokens per block: the cos/sin row is
+# staged in LDS there (1028, 1041, 1130, 1613 and 2015 workgroups).
 @pytest.mark.parametrize("T,H", [(8193, 1), (600, 16), (257, 37), (300, 48), (256, 64), (129, 128),
-                                 (512, 64), (8192, 1), (32769, 1)])
+                                 (160, 112), (200, 128), (496, 64), (512, 64), (8192, 1), (32769, 1)])
 def test_mid_size_grids(T, H):
     _say(f"mid-size grid T={T} H={H}")
     g = torch.Generator().manual_seed(T + H)
@@ -367,6 +370,28 @@ def test_mid_size_grids(T, H):
                    torch.zeros(nblk, 64 * W.HEAD_BYTES, dtype=torch.uint8), slots,
                    torch.randint(0, 4096, (T,), generator=g, dtype=torch.int64),
                    W.make_cos_sin_cache(4096), 1e-6, 64)
+    gw = run_gpu(w)
+    ref = oracle_main(w)
+    assert_q_exact(gw.q.cpu(), ref.q, w.name)
+    assert torch.equal(gw.k_cache.cpu(), ref.k_cache), f"{w.name}: cache differs"
+
+
+def test_lds_cos_sin_path_clamps_positions():
+    """The one-round grid that stages cos/sin in LDS (T = 256, H = 64: 1028
+    workgroups) with positions below 0 and past the cache's rows: clamped into
+    the table as on every other path, bit-exact against the oracle."""
+    _say("main op, LDS cos/sin path with out-of-range positions")
+    T, H = 256, 64
+    g = torch.Generator().manual_seed(77)
+    nblk = (T + 63) // 64 + 2
+    slots = torch.randperm(nblk * 64, generator=g)[:T].to(torch.int64)
+    pos = torch.randint(0, 2048, (T,), generator=g, dtype=torch.int64)
+    pos[::7] = -3
+    pos[3::7] = 2048 + 17
+    pos[5::7] = 2047
+    w = W.Workload("lds cos/sin clamp", W.randn_bf16((T, H, 512), g), W.randn_bf16((T, 512), g),
+                   torch.zeros(nblk, 64 * W.HEAD_BYTES, dtype=torch.uint8), slots, pos,
+                   W.make_cos_sin_cache(2048), 1e-6, 64)
     gw = run_gpu(w)
     ref = oracle_main(w)
     assert_q_exact(gw.q.cpu(), ref.q, w.name)
