@@ -36,6 +36,11 @@ struct InvRopeArgs {
     uint32_t row_blocks;
     float eps;
     int tma;
+    // geometry (inv_rope_fp8_quant_any_kernel; the DeepSeek-V4 kernel has
+    // head_dim 512, rope 64 from 448, four chunks of 128)
+    uint32_t head_dim, rope_dim, rope_start, chunks;
+    uint32_t pieces;           // 16-byte pieces per head row: head_dim / 8, a power of two <= 64
+    uint32_t seg;              // pieces per chunk: quant_group_size / 8
 };
 
 __device__ __forceinline__ void unpack8(uint4 v, float (&x)[8]) {
@@ -169,7 +174,7 @@ __device__ void row_block(const InvRopeArgs& a, uint32_t rb, int lane16, int row
 
 // Zero the scales of padding tokens T..Tpad-1 (ops/fused_inv_rope_fp8_quant.py:69-88).
 __device__ void pad_block(const InvRopeArgs& a) {
-    const uint32_t per_group = a.tma ? a.heads_per_group : a.heads_per_group * 4;
+    const uint32_t per_group = a.tma ? a.heads_per_group : a.heads_per_group * a.chunks;
     const uint32_t npad = a.padded_tokens - a.num_tokens;
     const uint32_t total = a.n_groups * per_group * npad;
     for (uint32_t i = threadIdx.x; i < total; i += kThreads) {
@@ -188,6 +193,104 @@ inv_rope_fp8_quant_kernel(InvRopeArgs a) {
         pad_block(a);
 }
 
+// ---- every other geometry the reference accepts (nope_dim, rope_dim,
+// quant_group_size with head_dim = nope + rope, the rope dims inside the last
+// chunk), for head_dim a power of two in [8, 512] and chunks of at least 8.
+// One lane per 16-byte piece (8 values): a head row is `pieces` consecutive
+// lanes of a wave, a chunk `seg` of them, and a chunk's amax is a butterfly
+// over its lanes.  A workgroup takes 256 / pieces consecutive tokens of one
+// head.  The same arithmetic as row_block: inverse rotation of each rope pair
+// rounded to bf16, scale max(amax, eps) / 448 (or its power of two at least
+// 2^ceil(log2(max(s, 1e-10))) for packed scales), codes x / scale correctly
+// rounded, clamped to +-448.
+__device__ void row_block_any(const InvRopeArgs& a, uint32_t rb) {
+    const uint32_t P = a.pieces, S = a.seg;
+    const uint32_t rows = kThreads / P;
+    const uint32_t row_in_block = threadIdx.x / P, p = threadIdx.x % P;
+    const uint32_t head = rb % a.num_heads, t0 = (rb / a.num_heads) * rows;
+    const uint32_t t = t0 + row_in_block;
+    const bool valid = t < a.num_tokens;
+    const uint32_t tt = valid ? t : t0;
+    const int64_t praw = a.positions[tt];
+    __builtin_amdgcn_sched_barrier(0);
+    const uint4 v = load16(a.o + (int64_t)tt * a.o_st + (int64_t)head * a.o_sh + 8 * p);
+    float x[8];
+    unpack8(v, x);
+    const uint32_t i0 = 8 * p;
+    if (i0 + 8 > a.rope_start) {
+        const int64_t pos = clamp_position(praw, a.max_pos);
+        const float* cs = a.cos_sin + pos * a.cs_stride;
+        const uint32_t half = a.rope_dim / 2;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t i = i0 + 2 * j;
+            if (i >= a.rope_start) {
+                const uint32_t jj = (i - a.rope_start) / 2;
+                const float c = cs[jj], sn = cs[half + jj];
+                const float e = x[2 * j], o = x[2 * j + 1];
+                const float ec = e * c, os = o * sn, oc = o * c, es = e * sn;
+                const uint32_t w = pack_bf16x2(ec + os, oc - es);
+                x[2 * j] = bf16_lo(w);
+                x[2 * j + 1] = bf16_hi(w);
+            }
+        }
+    }
+    uint32_t m = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        m = max(m, __float_as_uint(x[i]) & 0x7fffffffu);
+    for (uint32_t off = 1; off < S; off <<= 1)  // the chunk's lanes: aligned runs of S
+        m = max(m, (uint32_t)__shfl_xor((int)m, (int)off));
+    const uint32_t eps_bits = __float_as_uint(a.eps);
+    m = m > eps_bits ? m : eps_bits;
+    float sc = __uint_as_float(m) * (float)(1.0 / 448.0);
+    uint32_t lo, hi, byte = 0;
+    if (a.tma) {
+        uint32_t b = __float_as_uint(sc);
+        b = b > 0x2EDBE6FFu ? b : 0x2EDBE6FFu;  // 1e-10f
+        const int e = (int)(b >> 23) - 127 + ((b & 0x7fffffu) ? 1 : 0);
+        byte = (uint32_t)(e + 127);
+        const float inv = exp2_neg_int(e);
+        lo = pack_fp8x4(clamp_fp8(x[0] * inv), clamp_fp8(x[1] * inv), clamp_fp8(x[2] * inv), clamp_fp8(x[3] * inv));
+        hi = pack_fp8x4(clamp_fp8(x[4] * inv), clamp_fp8(x[5] * inv), clamp_fp8(x[6] * inv), clamp_fp8(x[7] * inv));
+    } else {
+        const float y = 1.0f / sc;
+        float qv[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            qv[i] = clamp_fp8(div_by_scale(x[i], sc, y));
+        lo = pack_fp8x4(qv[0], qv[1], qv[2], qv[3]);
+        hi = pack_fp8x4(qv[4], qv[5], qv[6], qv[7]);
+    }
+    const uint32_t g = head / a.heads_per_group, hig = head - g * a.heads_per_group;
+    if (valid)
+        store8(a.fp8 + (int64_t)g * a.fp8_sg + (int64_t)t * a.fp8_st + hig * a.head_dim + 8 * p, lo, hi);
+    if (a.tma) {
+        // the row's first lane packs the chunks' bytes (at most four chunks)
+        const int base = (int)((threadIdx.x & 63) - p);
+        uint32_t packed = 0;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const uint32_t bc = (uint32_t)__shfl((int)byte, base + (int)(min((uint32_t)c, a.chunks - 1) * S));
+            if ((uint32_t)c < a.chunks)
+                packed |= bc << (8 * c);
+        }
+        if (valid && p == 0)
+            static_cast<uint32_t*>(a.scale)[(int64_t)g * a.sc_sg + (int64_t)hig * a.sc_sk + t] = packed;
+    } else if (valid && p % S == 0) {
+        const uint32_t c = p / S;
+        static_cast<float*>(a.scale)[(int64_t)g * a.sc_sg + (int64_t)(hig * a.chunks + c) * a.sc_sk + t] = sc;
+    }
+}
+
+__global__ void __launch_bounds__(kThreads)
+inv_rope_fp8_quant_any_kernel(InvRopeArgs a) {
+    if (blockIdx.x < a.row_blocks)
+        row_block_any(a, blockIdx.x);
+    else
+        pad_block(a);
+}
+
 }  // namespace
 }  // namespace fgv
 
@@ -196,6 +299,7 @@ extern "C" int fgv_inv_rope_fp8_quant(
     const int64_t* positions,
     const float* cos_sin_cache, int64_t cos_sin_stride, int64_t max_pos,
     int64_t num_tokens, int64_t n_groups, int64_t heads_per_group,
+    int64_t nope_dim, int64_t rope_dim, int64_t quant_group_size,
     void* fp8_out, int64_t fp8_stride_group, int64_t fp8_stride_token,
     void* scale_out, int64_t scale_stride_group, int64_t scale_stride_k,
     int64_t padded_tokens, float eps, int tma_aligned_scales,
@@ -203,12 +307,30 @@ extern "C" int fgv_inv_rope_fp8_quant(
     using namespace fgv;
     if (num_tokens < 0 || n_groups <= 0 || heads_per_group <= 0)
         return fail(FGV_E_BAD_SHAPE, "bad num_tokens, n_groups or heads_per_group");
+    // the reference's geometry assertions (ops/fused_inv_rope_fp8_quant.py:192-205)
+    const int64_t head_dim = nope_dim + rope_dim;
+    if (nope_dim < 0 || rope_dim <= 0 || rope_dim % 2 || quant_group_size <= 0 || head_dim % quant_group_size ||
+        nope_dim % quant_group_size != quant_group_size - rope_dim)
+        return fail(FGV_E_BAD_SHAPE, "geometry: rope_dim even, quant_group_size | head_dim, "
+                                     "nope_dim % quant_group_size == quant_group_size - rope_dim");
+    const int64_t chunks = head_dim / quant_group_size;
+    if (tma_aligned_scales && chunks > 4)
+        return fail(FGV_E_BAD_SHAPE, "packed UE8M0 scales take at most 4 chunks per head");
+    // this build's limits: head_dim a power of two in [8, 512], chunks of at
+    // least 8 values; packed scales need a word per head in the reference's
+    // packed scale tensor (four chunks per head, or one head per group)
+    const bool pow2 = (head_dim & (head_dim - 1)) == 0 && (quant_group_size & (quant_group_size - 1)) == 0;
+    if (!pow2 || head_dim < 8 || head_dim > 512 || quant_group_size < 8)
+        return fail(FGV_E_BAD_SHAPE, "head_dim must be a power of two in [8, 512], quant_group_size one >= 8");
+    if (tma_aligned_scales && chunks != 4 && heads_per_group != 1)
+        return fail(FGV_E_BAD_SHAPE, "packed scales with fewer than 4 chunks per head need heads_per_group 1");
     if (padded_tokens < num_tokens || padded_tokens > num_tokens + 3)
         return fail(FGV_E_BAD_SHAPE, "padded_tokens must be num_tokens rounded up to 4");
     const int64_t num_heads = n_groups * heads_per_group;
     const int64_t rows = num_tokens * num_heads;
-    if (rows > 0x7fffffffLL || padded_tokens * num_heads * 4 > 0x7fffffffLL)
-        return fail(FGV_E_TOO_LARGE, "num_tokens * num_heads must be below 2^29");
+    if (rows > 0x7fffffffLL || padded_tokens * num_heads * chunks > 0x7fffffffLL ||
+        num_tokens * num_heads * head_dim > (1LL << 46))
+        return fail(FGV_E_TOO_LARGE, "num_tokens * num_heads * chunks must be below 2^31");
     if (padded_tokens == 0)
         return FGV_OK;
     if (!scale_out || (rows > 0 && (!o || !positions || !cos_sin_cache || !fp8_out)))
@@ -217,12 +339,15 @@ extern "C" int fgv_inv_rope_fp8_quant(
         return fail(FGV_E_BAD_SHAPE, "cos_sin_cache has no rows");
     if (!(eps > 0.0f))
         return fail(FGV_E_BAD_SHAPE, "eps must be positive");
-    if (!aligned(o, 16) || !aligned(cos_sin_cache, 16) || !aligned(fp8_out, 8) ||
+    // DeepSeek-V4's kernel reads cos/sin rows as 16-byte pieces; the general
+    // one reads single floats
+    const bool dsv4 = nope_dim == kNopeDim && rope_dim == kRopeDim && quant_group_size == 128;
+    if (!aligned(o, 16) || !aligned(cos_sin_cache, dsv4 ? 16 : 4) || !aligned(fp8_out, 8) ||
         !aligned(scale_out, 4))
-        return fail(FGV_E_MISALIGNED, "o and cos_sin_cache must be 16-byte aligned, fp8_out 8");
-    if (o_stride_token % 8 || o_stride_head % 8 || cos_sin_stride % 4 ||
+        return fail(FGV_E_MISALIGNED, "o (and cos_sin_cache for 64 rope dims) must be 16-byte aligned, fp8_out 8");
+    if (o_stride_token % 8 || o_stride_head % 8 || (dsv4 && cos_sin_stride % 4) ||
         fp8_stride_group % 8 || fp8_stride_token % 8)
-        return fail(FGV_E_BAD_STRIDE, "o/fp8 strides must be multiples of 8, cos_sin of 4");
+        return fail(FGV_E_BAD_STRIDE, "o/fp8 strides must be multiples of 8 (cos_sin of 4 for 64 rope dims)");
 
     InvRopeArgs a;
     a.o = static_cast<const uint16_t*>(o);
@@ -243,10 +368,25 @@ extern "C" int fgv_inv_rope_fp8_quant(
     a.num_tokens = (uint32_t)num_tokens;
     a.padded_tokens = (uint32_t)padded_tokens;
     a.n_groups = (uint32_t)n_groups;
-    a.row_blocks = (uint32_t)((num_tokens + kTokensPerBlock - 1) / kTokensPerBlock * num_heads);
     a.eps = eps;
     a.tma = tma_aligned_scales ? 1 : 0;
+    a.head_dim = (uint32_t)head_dim;
+    a.rope_dim = (uint32_t)rope_dim;
+    a.rope_start = (uint32_t)nope_dim;
+    a.chunks = (uint32_t)chunks;
+    a.pieces = (uint32_t)(head_dim / 8);
+    a.seg = (uint32_t)(quant_group_size / 8);
+    const int64_t tokens_per_block = dsv4 ? kTokensPerBlock : kThreads / a.pieces;
+    const int64_t row_blocks = (num_tokens + tokens_per_block - 1) / tokens_per_block * num_heads;
+    if (row_blocks >= 0x7fffffffLL)
+        return fail(FGV_E_TOO_LARGE, "grid exceeds 2^31 - 1 workgroups");
+    a.row_blocks = (uint32_t)row_blocks;
     const uint32_t grid = a.row_blocks + (padded_tokens > num_tokens ? 1u : 0u);
-    hipLaunchKernelGGL(inv_rope_fp8_quant_kernel, dim3(grid), dim3(kThreads), 0, static_cast<hipStream_t>(stream), a);
+    if (dsv4)
+        hipLaunchKernelGGL(inv_rope_fp8_quant_kernel, dim3(grid), dim3(kThreads), 0, static_cast<hipStream_t>(stream),
+                           a);
+    else
+        hipLaunchKernelGGL(inv_rope_fp8_quant_any_kernel, dim3(grid), dim3(kThreads), 0,
+                           static_cast<hipStream_t>(stream), a);
     return launch_status();
 }

@@ -117,10 +117,10 @@ int qnorm_rope_kv_insert(const at::Tensor& q, const at::Tensor& kv, const at::Te
 
 using SiblingOut = std::tuple<at::Tensor, at::Tensor>;
 
-// The reference's assertions in its order (:184-205; this build implements the
-// DeepSeek-V4 geometry only), its output allocation (:207-227): codes
-// [G, T, hpg * 512] e4m3fn and scales stored (G, K, Tpad4) token-fastest,
-// returned transposed to [T, G, d] and [T, G, K]; then one C-ABI launch.
+// The reference's assertions in its order (:184-205, plus this build's
+// geometry limits), its output allocation (:207-227): codes [G, T, hpg * D]
+// e4m3fn and scales stored (G, K, Tpad4) token-fastest, returned transposed to
+// [T, G, d] and [T, G, K]; then one C-ABI launch.
 int inv_rope_fp8_quant(const at::Tensor& o, const at::Tensor& positions_in, const at::Tensor& cos_sin_cache,
                        int64_t n_groups, int64_t heads_per_group, int64_t nope_dim, int64_t rope_dim,
                        int64_t quant_group_size, double eps, bool fp8_e4m3fn, bool tma_aligned_scales,
@@ -141,17 +141,23 @@ int inv_rope_fp8_quant(const at::Tensor& o, const at::Tensor& positions_in, cons
     FGV_ASSERT(rope_dim % 2 == 0, "rope_dim must be even");
     FGV_ASSERT(cos_sin_cache.size(1) == rope_dim, "cos_sin_cache's last dim must be rope_dim");
     FGV_ASSERT(cos_sin_cache.scalar_type() == at::kFloat, "cos_sin_cache must be float32");
-    FGV_ASSERT(nope_dim == 448 && rope_dim == 64 && quant_group_size == 128,
-               "this build implements the DeepSeek-V4 geometry: nope_dim=448, rope_dim=64, "
-               "quant_group_size=128");
+    FGV_ASSERT((head_dim & (head_dim - 1)) == 0 && head_dim >= 8 && head_dim <= 512 &&
+                   (quant_group_size & (quant_group_size - 1)) == 0 && quant_group_size >= 8,
+               "this build takes head_dim a power of two in [8, 512] and quant_group_size a power of two >= 8");
     FGV_ASSERT(o.scalar_type() == at::kBFloat16, "`o` must be bfloat16");
     FGV_ASSERT(cos_sin_cache.stride(1) == 1, "cos_sin_cache rows must be contiguous");
     const c10::Device dev = o.device();
     FGV_ASSERT(dev.is_cuda(), "flaggems_vllm runs on the GPU (HIP) only");
     FGV_ASSERT(positions_in.device() == dev && cos_sin_cache.device() == dev, "all tensors must be on o's device");
     const int64_t chunks_per_head = head_dim / quant_group_size;
-    if (tma_aligned_scales)
+    if (tma_aligned_scales) {
         FGV_ASSERT(chunks_per_head <= 4, "packed UE8M0 path currently expects at most 4 scale blocks per head");
+        // the reference's packed tensor holds (hpg * chunks + 3) / 4 words per
+        // (group, token) and its kernel writes one per head: below four chunks
+        // that is past the tensor unless there is one head per group
+        FGV_ASSERT(chunks_per_head == 4 || heads_per_group == 1,
+                   "packed scales with fewer than 4 scale blocks per head need heads_per_group 1");
+    }
 
     const at::Tensor positions = (positions_in.scalar_type() != at::kLong || positions_in.stride(0) != 1)
                                      ? positions_in.to(at::kLong).contiguous()
@@ -169,7 +175,8 @@ int inv_rope_fp8_quant(const at::Tensor& o, const at::Tensor& positions_in, cons
         const c10::DeviceGuard guard(dev);
         rc = fgv_inv_rope_fp8_quant(o.data_ptr(), o.stride(0), o.stride(1), positions.data_ptr<int64_t>(),
                                     cos_sin_cache.data_ptr<float>(), cos_sin_cache.stride(0), cos_sin_cache.size(0),
-                                    num_tokens, n_groups, heads_per_group, fp8.data_ptr(), fp8.stride(0),
+                                    num_tokens, n_groups, heads_per_group, nope_dim, rope_dim, quant_group_size,
+                                    fp8.data_ptr(), fp8.stride(0),
                                     fp8.stride(1), scale.data_ptr(), scale.stride(0), scale.stride(2), tpad,
                                     static_cast<float>(eps), tma_aligned_scales ? 1 : 0, current_stream(o));
     }

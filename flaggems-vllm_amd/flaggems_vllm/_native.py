@@ -155,6 +155,7 @@ def lib():
         _P,  # positions
         _P, _I64, _I64,  # cos_sin_cache, cos_sin_stride, max_pos
         _I64, _I64, _I64,  # num_tokens, n_groups, heads_per_group
+        _I64, _I64, _I64,  # nope_dim, rope_dim, quant_group_size
         _P, _I64, _I64,  # fp8_out, fp8_stride_group, fp8_stride_token
         _P, _I64, _I64,  # scale_out, scale_stride_group, scale_stride_k
         _I64, ctypes.c_float, ctypes.c_int,  # padded_tokens, eps, tma_aligned_scales

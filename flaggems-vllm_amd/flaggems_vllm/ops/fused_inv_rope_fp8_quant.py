@@ -17,8 +17,13 @@ Differences from the reference, all deliberate:
   as the reference's torch oracle does
   (tests/test_fused_inv_rope_fp8_quant.py:167-170), so codes and scales match
   that oracle bit for bit.
-* Only the DeepSeek-V4 geometry is implemented: head_dim 512 = 448 nope + 64
-  rope, quant_group_size 128.
+* Every geometry the reference asserts accept (head_dim = nope_dim +
+  rope_dim, quant_group_size | head_dim, the rope dims inside the last
+  chunk), for head_dim a power of two in [8, 512] and quant_group_size a power
+  of two >= 8 (the reference's Triton kernel needs powers of two too).
+  DeepSeek-V4's (448, 64, 128) runs its own kernel, the rest a general one.
+  Packed scales with fewer than four chunks per head need heads_per_group 1:
+  the reference's packed scale tensor only then has a word for every head.
 """
 import logging
 from typing import Optional, Tuple

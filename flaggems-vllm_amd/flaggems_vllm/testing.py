@@ -322,14 +322,16 @@ class InvRopeWorkload:
 
 
 def make_inv_rope_workload(num_tokens: int = 8192, num_heads: int = 64, n_groups: int = 8,
-                           seed: int = 0, scale: float = 1.0, max_pos: int = 65536) -> InvRopeWorkload:
-    """Seeded CPU inputs for the sibling op (default: T=8192, H=64, G=8)."""
+                           seed: int = 0, scale: float = 1.0, max_pos: int = 65536, head_dim: int = HEAD_DIM,
+                           rope_dim: int = ROPE_DIM) -> InvRopeWorkload:
+    """Seeded CPU inputs for the sibling op (default: T=8192, H=64, G=8,
+    DeepSeek-V4's head_dim 512 with 64 rope dims)."""
     g = torch.Generator().manual_seed(seed)
-    o = randn_bf16((num_tokens, num_heads, HEAD_DIM), g)
+    o = randn_bf16((num_tokens, num_heads, head_dim), g)
     if scale != 1.0:
         o = (o.float() * scale).to(torch.bfloat16)
     positions = torch.randint(0, max_pos, (num_tokens,), generator=g, dtype=torch.int64)
-    return InvRopeWorkload(o, positions, make_cos_sin_cache(max_pos), n_groups,
+    return InvRopeWorkload(o, positions, make_cos_sin_cache(max_pos, rope_dim=rope_dim), n_groups,
                            num_heads // n_groups)
 
 

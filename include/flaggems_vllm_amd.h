@@ -74,29 +74,37 @@ int fgv_qnorm_rope_kv_rope_quant_insert(
     void* stream);
 
 /*
- * Fused DeepSeek-V4 inverse GPT-J RoPE + per-128 FP8 e4m3fn group quant.
+ * Fused DeepSeek-V4 inverse GPT-J RoPE + per-group FP8 e4m3fn quant.
  *
  * Replaces flaggems_vllm.fused_inv_rope_fp8_quant
  * (reference: src/flaggems_vllm/ops/fused_inv_rope_fp8_quant.py:157-256,
- * kernel :37-154) for nope_dim=448, rope_dim=64, quant_group_size=128.
+ * kernel :37-154), with its geometry arguments: head_dim D = nope_dim +
+ * rope_dim, quant_group_size Q dividing D, nope_dim % Q == Q - rope_dim (the
+ * rope dims inside the last chunk), rope_dim even (the reference's
+ * assertions, :192-205).  This build takes D a power of two in [8, 512] and
+ * Q a power of two >= 8; DeepSeek-V4's (448, 64, 128) runs a kernel of its
+ * own, every other geometry a general one.  Packed scales need at most four
+ * chunks per head, and four unless heads_per_group is 1: the reference's
+ * packed scale tensor has a word per head only then.
  *
- *   o          bf16 [num_tokens, n_groups*heads_per_group, 512], element
+ *   o          bf16 [num_tokens, n_groups*heads_per_group, D], element
  *              (t,h,i) at o + t*o_stride_token + h*o_stride_head + i.
  *   positions  int64 [num_tokens], clamped into [0, max_pos).
- *   fp8_out    uint8 e4m3fn codes, element (g,t,i), i < heads_per_group*512,
+ *   fp8_out    uint8 e4m3fn codes, element (g,t,i), i < heads_per_group*D,
  *              at fp8_out + g*fp8_stride_group + t*fp8_stride_token + i.
  *   scale_out  tma_aligned_scales == 0: float scale of chunk k
- *              (k < 4*heads_per_group) at scale_out + g*scale_stride_group
- *              + k*scale_stride_k + t;  != 0: int32 with the four UE8M0
- *              bytes of head j at scale_out + g*scale_stride_group
- *              + j*scale_stride_k + t.  Tokens num_tokens..padded_tokens-1
- *              get zero scales.
+ *              (k < (D/Q)*heads_per_group) at scale_out + g*scale_stride_group
+ *              + k*scale_stride_k + t;  != 0: int32 with the UE8M0 bytes of
+ *              head j's chunks (byte c for chunk c) at scale_out +
+ *              g*scale_stride_group + j*scale_stride_k + t.  Tokens
+ *              num_tokens..padded_tokens-1 get zero scales.
  */
 int fgv_inv_rope_fp8_quant(
     const void* o, int64_t o_stride_token, int64_t o_stride_head,
     const int64_t* positions,
     const float* cos_sin_cache, int64_t cos_sin_stride, int64_t max_pos,
     int64_t num_tokens, int64_t n_groups, int64_t heads_per_group,
+    int64_t nope_dim, int64_t rope_dim, int64_t quant_group_size,
     void* fp8_out, int64_t fp8_stride_group, int64_t fp8_stride_token,
     void* scale_out, int64_t scale_stride_group, int64_t scale_stride_k,
     int64_t padded_tokens, float eps, int tma_aligned_scales,

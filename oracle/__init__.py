@@ -76,6 +76,7 @@ def lib():
             _P, _I64, _I64,  # o, o_st, o_sh
             _P, _P, _I64, _I64,  # positions, cos_sin, cs_stride, max_pos
             _I64, _I64, _I64,  # num_tokens, n_groups, heads_per_group
+            _I64, _I64, _I64,  # nope_dim, rope_dim, quant_group_size
             _P, _I64, _I64,  # fp8, fp8_sg, fp8_st
             _P, _I64, _I64, _I64,  # scale, sc_sg, sc_sk, tpad
             ctypes.c_float, ctypes.c_int, ctypes.c_int,  # eps, tma, nthreads
@@ -235,15 +236,24 @@ def qnorm_rope_kv_insert(q, kv, k_cache, slot_mapping, position_ids, cos_sin_cac
 
 
 def inv_rope_fp8_quant(o, positions, cos_sin_cache, n_groups, heads_per_group,
-                       eps=1e-10, tma_aligned_scales=False, nthreads=None):
+                       eps=1e-10, tma_aligned_scales=False, nthreads=None, nope_dim=448, rope_dim=64,
+                       quant_group_size=128):
     """CPU restatement of the sibling op.  Returns (fp8 codes as uint8 [T, G, d]
     with the reference's strides, scales [T, G, K] with the reference's
-    token-fastest padded storage: float32, or int32 when packed)."""
+    token-fastest padded storage: float32, or int32 when packed).  Any
+    geometry the reference's assertions accept (head_dim = nope_dim +
+    rope_dim, quant_group_size | head_dim, rope in the last chunk); packed
+    scales need four chunks per head or one head per group, as the
+    reference's packed scale tensor only then holds every head's word."""
     _cpu(o, torch.bfloat16), _cpu(positions, torch.int64), _cpu(cos_sin_cache, torch.float32)
     T, H, D = o.shape
-    assert D == 512 and o.stride(2) == 1 and H == n_groups * heads_per_group
-    d = heads_per_group * 512
-    k_blocks = d // 128
+    G = quant_group_size
+    assert D == nope_dim + rope_dim and D % G == 0 and nope_dim % G == G - rope_dim and rope_dim % 2 == 0
+    assert o.stride(2) == 1 and H == n_groups * heads_per_group and cos_sin_cache.shape[1] == rope_dim
+    chunks = D // G
+    assert not tma_aligned_scales or chunks == 4 or (chunks < 4 and heads_per_group == 1)
+    d = heads_per_group * D
+    k_blocks = d // G
     tpad = (T + 3) // 4 * 4
     inner = (k_blocks + 3) // 4 if tma_aligned_scales else k_blocks
     fp8 = torch.empty((n_groups, T, d), dtype=torch.uint8)
@@ -254,7 +264,7 @@ def inv_rope_fp8_quant(o, positions, cos_sin_cache, n_groups, heads_per_group,
     lib().oracle_inv_rope_fp8_quant(
         o.data_ptr(), o.stride(0), o.stride(1),
         positions.data_ptr(), cos_sin_cache.data_ptr(), cos_sin_cache.stride(0),
-        cos_sin_cache.shape[0], T, n_groups, heads_per_group,
+        cos_sin_cache.shape[0], T, n_groups, heads_per_group, nope_dim, rope_dim, G,
         fp8.data_ptr(), fp8.stride(0), fp8.stride(1),
         scale.data_ptr(), scale.stride(0), scale.stride(2), tpad,
         float(eps), int(bool(tma_aligned_scales)), _threads(nthreads),

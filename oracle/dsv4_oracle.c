@@ -303,50 +303,56 @@ void oracle_qnorm_rope_kv_insert(uint16_t* q, int64_t q_st, int64_t q_sh,
 }
 
 /*
- * Sibling op.  Inverse GPT-J RoPE on dims 448..511 of each head, rope part
- * rounded to bf16 (tests/test_fused_inv_rope_fp8_quant.py:163-170), then one
- * scale per 128-element chunk and e4m3fn codes (:177-198).
+ * Sibling op.  Inverse GPT-J RoPE on the last rope_dim dims of each head
+ * (head_dim = nope_dim + rope_dim), rope part rounded to bf16
+ * (tests/test_fused_inv_rope_fp8_quant.py:163-170), then one scale per
+ * quant_group_size-element chunk and e4m3fn codes (:177-198); the geometry
+ * follows ops/fused_inv_rope_fp8_quant.py:192-205 (the kernel's rope start
+ * ROPE_START = nope_dim % quant_group_size inside the last chunk, :229-247).
  *
  * fp8 output element (g, t, i) at fp8 + g*fp8_sg + t*fp8_st + i.
- * Scales: fp32 (tma == 0) at scale + g*sc_sg + k*sc_sk + t with k = hig*4 + c;
- * packed int32 (tma != 0) at scale + g*sc_sg + hig*sc_sk + t.  Tokens
- * T..Tpad-1 get zero scales (ops/fused_inv_rope_fp8_quant.py:69-88).
+ * Scales: fp32 (tma == 0) at scale + g*sc_sg + k*sc_sk + t with
+ * k = hig*chunks + c; packed int32 (tma != 0) at scale + g*sc_sg + hig*sc_sk
+ * + t, byte c for chunk c < chunks (<= 4).  Tokens T..Tpad-1 get zero
+ * scales (ops/fused_inv_rope_fp8_quant.py:69-88).
  */
 void oracle_inv_rope_fp8_quant(const uint16_t* o, int64_t o_st, int64_t o_sh,
                                const int64_t* positions, const float* cos_sin, int64_t cs_stride,
                                int64_t max_pos, int64_t num_tokens, int64_t n_groups,
-                               int64_t heads_per_group, uint8_t* fp8, int64_t fp8_sg, int64_t fp8_st,
+                               int64_t heads_per_group, int64_t nope_dim, int64_t rope_dim, int64_t group,
+                               uint8_t* fp8, int64_t fp8_sg, int64_t fp8_st,
                                void* scale, int64_t sc_sg, int64_t sc_sk, int64_t tpad,
                                float eps, int tma, int nthreads)
 {
     (void)nthreads;
     const float inv_max = (float)(1.0 / 448.0);
-    int64_t num_heads = n_groups * heads_per_group;
+    const int64_t num_heads = n_groups * heads_per_group;
+    const int64_t head_dim = nope_dim + rope_dim, half = rope_dim / 2, chunks = head_dim / group;
 #pragma omp parallel for schedule(static) num_threads(nthreads > 0 ? nthreads : 1)
     for (int64_t row = 0; row < num_tokens * num_heads; ++row) {
         int64_t t = row / num_heads, h = row % num_heads;
         int64_t g = h / heads_per_group, hig = h % heads_per_group;
         const uint16_t* x = o + t * o_st + h * o_sh;
         const float* cs = cos_sin + clamp_pos(positions[t], max_pos) * cs_stride;
-        float v[HEAD_DIM];
-        for (int i = 0; i < NOPE_DIM; ++i)
+        float* v = (float*)malloc(sizeof(float) * (size_t)head_dim);
+        for (int64_t i = 0; i < nope_dim; ++i)
             v[i] = oracle_bf16_to_f32(x[i]);
-        for (int j = 0; j < HALF_ROPE; ++j) {
-            float e = oracle_bf16_to_f32(x[NOPE_DIM + 2 * j]);
-            float od = oracle_bf16_to_f32(x[NOPE_DIM + 2 * j + 1]);
-            float c = cs[j], s = cs[HALF_ROPE + j];
+        for (int64_t j = 0; j < half; ++j) {
+            float e = oracle_bf16_to_f32(x[nope_dim + 2 * j]);
+            float od = oracle_bf16_to_f32(x[nope_dim + 2 * j + 1]);
+            float c = cs[j], s = cs[half + j];
             float ec = e * c, os = od * s, oc = od * c, es = e * s;
             float e2 = ec + os; /* inverse rotation */
             float o2 = oc - es;
-            v[NOPE_DIM + 2 * j] = oracle_bf16_to_f32(oracle_f32_to_bf16(e2));
-            v[NOPE_DIM + 2 * j + 1] = oracle_bf16_to_f32(oracle_f32_to_bf16(o2));
+            v[nope_dim + 2 * j] = oracle_bf16_to_f32(oracle_f32_to_bf16(e2));
+            v[nope_dim + 2 * j + 1] = oracle_bf16_to_f32(oracle_f32_to_bf16(o2));
         }
-        uint8_t* out = fp8 + g * fp8_sg + t * fp8_st + hig * HEAD_DIM;
+        uint8_t* out = fp8 + g * fp8_sg + t * fp8_st + hig * head_dim;
         uint32_t packed = 0;
-        for (int c = 0; c < 4; ++c) {
+        for (int64_t c = 0; c < chunks; ++c) {
             float amax = 0.0f;
-            for (int i = 0; i < 128; ++i) {
-                float a = fabsf(v[c * 128 + i]);
+            for (int64_t i = 0; i < group; ++i) {
+                float a = fabsf(v[c * group + i]);
                 amax = a > amax ? a : amax;
             }
             float absmax = amax > eps ? amax : eps;
@@ -356,16 +362,17 @@ void oracle_inv_rope_fp8_quant(const uint16_t* o, int64_t o_st, int64_t o_sh,
                 sc = ldexpf(1.0f, (int)ceilf(log2f(cl)));
                 packed |= ((f2u(sc) >> 23) & 0xffu) << (8 * c);
             } else {
-                ((float*)scale)[g * sc_sg + (hig * 4 + c) * sc_sk + t] = sc;
+                ((float*)scale)[g * sc_sg + (hig * chunks + c) * sc_sk + t] = sc;
             }
-            for (int i = 0; i < 128; ++i) {
-                float qv = v[c * 128 + i] / sc;
+            for (int64_t i = 0; i < group; ++i) {
+                float qv = v[c * group + i] / sc;
                 qv = qv < -FP8_MAX ? -FP8_MAX : (qv > FP8_MAX ? FP8_MAX : qv);
-                out[c * 128 + i] = oracle_e4m3fn(qv);
+                out[c * group + i] = oracle_e4m3fn(qv);
             }
         }
         if (tma)
             ((int32_t*)scale)[g * sc_sg + hig * sc_sk + t] = (int32_t)packed;
+        free(v);
     }
     for (int64_t t = num_tokens; t < tpad; ++t)
         for (int64_t g = 0; g < n_groups; ++g) {
@@ -373,7 +380,7 @@ void oracle_inv_rope_fp8_quant(const uint16_t* o, int64_t o_st, int64_t o_sh,
                 for (int64_t hig = 0; hig < heads_per_group; ++hig)
                     ((int32_t*)scale)[g * sc_sg + hig * sc_sk + t] = 0;
             } else {
-                for (int64_t k = 0; k < heads_per_group * 4; ++k)
+                for (int64_t k = 0; k < heads_per_group * chunks; ++k)
                     ((float*)scale)[g * sc_sg + k * sc_sk + t] = 0.0f;
             }
         }

@@ -108,18 +108,23 @@ def qnorm_rope_kv_insert(q, kv, k_cache, slot_mapping, position_ids, cos_sin_cac
 
 
 def inv_rope_fp8_quant(o, positions, cos_sin_cache, n_groups, heads_per_group,
-                       eps=1e-10, tma_aligned_scales=False):
+                       eps=1e-10, tma_aligned_scales=False, nope_dim=NOPE_DIM, rope_dim=ROPE_DIM,
+                       quant_group_size=128):
     """Returns (fp8 codes as uint8 [T, G, d], scales [T, G, K] float32 or
-    packed int32 [T, G, hpg]) as plain contiguous tensors."""
+    packed int32 [T, G, hpg]) as plain contiguous tensors; any geometry the
+    reference accepts (the test's oracle is written for nope_dim 448, rope_dim
+    64, groups of 128: the same steps with those three as parameters)."""
     T, H, D = o.shape
+    half = rope_dim // 2
     cs = cos_sin_cache[positions].float()
-    cos, sin = cs[:, None, :HALF_ROPE], cs[:, None, HALF_ROPE:]
-    rf = o[..., NOPE_DIM:].float()
+    cos, sin = cs[:, None, :half], cs[:, None, half:rope_dim]
+    rf = o[..., nope_dim:].float()
     even, odd = rf[..., 0::2], rf[..., 1::2]
     inv = torch.stack((even * cos + odd * sin, odd * cos - even * sin), dim=-1).flatten(-2)
-    x = torch.cat((o[..., :NOPE_DIM], inv.to(o.dtype)), dim=-1).float()
+    x = torch.cat((o[..., :nope_dim], inv.to(o.dtype)), dim=-1).float()
     d = heads_per_group * D
-    blocks = x.reshape(T, n_groups, d // 128, 128)
+    G = quant_group_size
+    blocks = x.reshape(T, n_groups, d // G, G)
     scales = blocks.abs().amax(dim=-1).clamp(min=eps) * (1.0 / FP8_MAX)
     if tma_aligned_scales:
         scales = _pow2_exact(torch.ceil(torch.log2(scales.clamp(min=1e-10))))
@@ -127,10 +132,11 @@ def inv_rope_fp8_quant(o, positions, cos_sin_cache, n_groups, heads_per_group,
     codes = codes.to(torch.float8_e4m3fn).view(torch.uint8).reshape(T, n_groups, d)
     if not tma_aligned_scales:
         return codes, scales
+    chunks = D // G
     byte = (scales.view(torch.int32) >> 23) & 0xFF
-    byte = byte.reshape(T, n_groups, heads_per_group, 4)
+    byte = byte.reshape(T, n_groups, heads_per_group, chunks)
     packed = torch.zeros(T, n_groups, heads_per_group, dtype=torch.int32)
-    for c in range(4):
+    for c in range(chunks):
         packed |= byte[..., c] << (8 * c)
     return codes, packed
 

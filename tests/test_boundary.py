@@ -73,20 +73,29 @@ def test_c_abi_empty_call_is_a_no_op():
 
 def test_inv_rope_c_abi_rejects_bad_arguments():
     f = _native.lib().fgv_inv_rope_fp8_quant
-    ok = dict(o=16, ost=64 * 512, osh=512, pos=16, cs=16, css=64, mp=16, T=4, G=8, hpg=8,
-              f8=16, f8g=4 * 4096, f8t=4096, sc=16, scg=32 * 4, sck=4, tpad=4, eps=1e-10, tma=0)
+    ok = dict(o=16, ost=64 * 512, osh=512, pos=16, cs=16, css=64, mp=16, T=4, G=8, hpg=8, nope=448, rope=64,
+              grp=128, f8=16, f8g=4 * 4096, f8t=4096, sc=16, scg=32 * 4, sck=4, tpad=4, eps=1e-10, tma=0)
 
     def call(**kw):
         a = dict(ok, **kw)
         return f(a["o"], a["ost"], a["osh"], a["pos"], a["cs"], a["css"], a["mp"], a["T"], a["G"],
-                 a["hpg"], a["f8"], a["f8g"], a["f8t"], a["sc"], a["scg"], a["sck"], a["tpad"],
-                 a["eps"], a["tma"], None)
+                 a["hpg"], a["nope"], a["rope"], a["grp"], a["f8"], a["f8g"], a["f8t"], a["sc"], a["scg"],
+                 a["sck"], a["tpad"], a["eps"], a["tma"], None)
 
     assert call(tpad=9) == -2
     assert call(G=0) == -2
     assert call(o=24) == -3
     assert call(eps=0.0) == -2
     assert call(T=0, tpad=0) == 0
+    # geometry: the reference's conditions, then this build's limits
+    assert call(nope=440) == -2                       # rope not inside the last chunk
+    assert call(rope=63, nope=449) == -2              # odd rope_dim
+    assert call(nope=448, rope=64, grp=96) == -2      # group does not divide head_dim
+    assert call(nope=64, rope=64, grp=128, tma=0, T=0, tpad=0) == 0  # D = 128: accepted
+    assert call(nope=960, rope=64, grp=128) == -2     # D = 1024: beyond this build's 512
+    assert call(nope=448, rope=64, grp=64, tma=1) == -2   # 8 chunks cannot be packed
+    assert call(nope=192, rope=64, grp=128, tma=1) == -2  # 2 chunks packed, 8 heads per group
+    assert call(nope=192, rope=64, grp=128, tma=1, hpg=1, G=64, T=0, tpad=0) == 0
 
 
 def test_signatures_match_reference():
@@ -141,7 +150,10 @@ def test_main_wrapper_refuses_cpu_tensors():
     ({}, dict(n_groups=3)),
     ({"o": torch.zeros(4, 64, 256, dtype=torch.bfloat16)}, {}),
     ({"positions": torch.zeros(5, dtype=torch.int64)}, {}),
-    ({}, dict(nope_dim=192, rope_dim=64)),
+    ({}, dict(nope_dim=192, rope_dim=64)),             # head_dim 512 != 192 + 64
+    ({}, dict(nope_dim=440, rope_dim=72)),             # rope not inside the last chunk
+    ({"o": torch.zeros(4, 64, 1024, dtype=torch.bfloat16)}, dict(nope_dim=960, rope_dim=64)),  # D beyond 512
+    ({}, dict(quant_group_size=64, tma_aligned_scales=True)),  # 8 chunks cannot be packed
     ({"cos_sin_cache": torch.zeros(16, 64, dtype=torch.float64)}, {}),
     ({}, {}),  # valid, but CPU tensors
 ])

@@ -172,3 +172,43 @@ def test_real_deepseek_v4_rope(T, tma):
     x[..., 448::2], x[..., 449::2] = e * c + o * s_, o * c - e * s_
     cos = torch.nn.functional.cosine_similarity(deq.flatten(), x.flatten(), dim=0)
     assert float(1 - cos) < 1e-3
+
+
+# ------------------------------------------------- other geometries ----
+
+from .test_oracle_pins import SIBLING_GEOMETRIES, _packed_ok  # noqa: E402
+
+
+@pytest.mark.parametrize("tma", [False, True])
+@pytest.mark.parametrize("nope,rope,group", SIBLING_GEOMETRIES)
+def test_other_geometries_match_oracle(nope, rope, group, tma):
+    """Every geometry the reference accepts (head_dim 64..512, groups 32..512,
+    rope 2..128 dims, rope starting inside a 16-byte piece), codes and scales
+    bit for bit against the oracle; ragged token counts (pad tokens' scales
+    zero); o a strided view (head and token strides beyond head_dim)."""
+    D = nope + rope
+    for T, H, G in ((5, 8, 2), (37, 4, 4), (64, 16, 16)):
+        hpg = H // G
+        if tma and not _packed_ok(nope, rope, group, hpg):
+            continue
+        _say(f"inv rope geometry nope={nope} rope={rope} group={group} T={T} H={H} G={G} tma={tma}")
+        w = W.make_inv_rope_workload(T, H, G, seed=D + group + T, max_pos=1024, head_dim=D, rope_dim=rope)
+        # o inside a wider buffer: head stride D + 8, token stride H * (D + 8) + 16
+        buf = torch.zeros(T, H * (D + 8) + 16, dtype=torch.bfloat16)
+        view = buf[:, :H * (D + 8)].view(T, H, D + 8)[..., :D]
+        view.copy_(w.o)
+        dbuf = buf.to(DEV)
+        do = dbuf[:, :H * (D + 8)].view(T, H, D + 8)[..., :D]
+        kw = dict(nope_dim=nope, rope_dim=rope, quant_group_size=group, tma_aligned_scales=tma)
+        out, scale = flaggems_vllm.fused_inv_rope_fp8_quant(do, w.positions.to(DEV), w.cos_sin_cache.to(DEV),
+                                                            G, hpg, **kw)
+        torch.cuda.synchronize()
+        r8, rs = oracle.inv_rope_fp8_quant(w.o, w.positions, w.cos_sin_cache, G, hpg, **kw)
+        assert out.shape == (T, G, hpg * D) and out.stride() == r8.stride()
+        assert torch.equal(out.cpu().view(torch.uint8), r8)
+        assert scale.shape == rs.shape and scale.stride() == rs.stride()
+        assert torch.equal(scale.cpu(), rs)
+        tpad = (T + 3) // 4 * 4
+        if tpad > T:  # the pad tokens' scales are zero, as the reference writes them
+            store = torch.as_strided(scale, (G, scale.shape[-1], tpad), (scale.stride(1), scale.stride(2), 1))
+            assert int(store[..., T:].cpu().view(torch.int32).abs().sum()) == 0

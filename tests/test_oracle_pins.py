@@ -297,3 +297,66 @@ def test_sibling_c_oracle_vs_torch_ref(T, H, G, scale, tma):
     assert torch.equal(c8, t8)
     assert torch.equal(cs.contiguous(), ts)
     assert c8.stride() == (H // G * 512, T * H // G * 512, 1)
+
+
+# Sibling geometries the reference's assertions accept besides DeepSeek-V4's
+# (head_dim = nope + rope, quant_group_size | head_dim, the rope dims inside
+# the last chunk: nope % group == group - rope), as (nope, rope, group).
+SIBLING_GEOMETRIES = [(448, 64, 128), (192, 64, 128), (64, 64, 128), (448, 64, 64), (480, 32, 128),
+                      (224, 32, 64), (384, 128, 256), (448, 64, 512), (56, 8, 32), (62, 2, 64), (124, 4, 32)]
+
+
+def _packed_ok(nope, rope, group, hpg):
+    chunks = (nope + rope) // group
+    return chunks == 4 or (chunks < 4 and hpg == 1)
+
+
+@pytest.mark.parametrize("tma", [False, True])
+@pytest.mark.parametrize("nope,rope,group", SIBLING_GEOMETRIES)
+def test_sibling_geometries_c_oracle_vs_torch_ref(nope, rope, group, tma):
+    """The C oracle and the torch restatement agree bit for bit (codes and
+    scales) on every geometry, packed scales where the reference's packed
+    tensor holds every head's word."""
+    for H, G in ((8, 2), (4, 4)):
+        hpg = H // G
+        if tma and not _packed_ok(nope, rope, group, hpg):
+            continue
+        w = W.make_inv_rope_workload(9, H, G, seed=nope + rope + group, max_pos=512, head_dim=nope + rope,
+                                     rope_dim=rope)
+        kw = dict(tma_aligned_scales=tma, nope_dim=nope, rope_dim=rope, quant_group_size=group)
+        c8, cs = oracle.inv_rope_fp8_quant(w.o, w.positions, w.cos_sin_cache, G, hpg, **kw)
+        t8, ts = torch_ref.inv_rope_fp8_quant(w.o, w.positions, w.cos_sin_cache, G, hpg, **kw)
+        assert torch.equal(c8, t8)
+        assert torch.equal(cs.contiguous(), ts)
+        d = hpg * (nope + rope)
+        assert c8.stride() == (d, 9 * d, 1)
+
+
+@pytest.mark.parametrize("nope,rope,group", SIBLING_GEOMETRIES)
+def test_sibling_geometries_closed_forms(nope, rope, group):
+    """Position 0 (cos 1, sin 0) leaves every dim as it is, so each chunk's
+    codes are the plain quantisation of o; a chunk holding one non-zero
+    value v gets scale |v| / 448 and code 0x7E (+448) or 0xFE there, zeros
+    elsewhere."""
+    D = nope + rope
+    T, H = 3, 2
+    g = torch.Generator().manual_seed(D + group)
+    o = torch.zeros(T, H, D, dtype=torch.bfloat16)
+    where = torch.randint(0, group, (T, H, D // group), generator=g)
+    vals = (torch.rand(T, H, D // group, generator=g) * 8 + 0.5) * torch.where(
+        torch.rand(T, H, D // group, generator=g) < 0.5, -1.0, 1.0)
+    for t in range(T):
+        for h in range(H):
+            for c in range(D // group):
+                o[t, h, c * group + int(where[t, h, c])] = vals[t, h, c]
+    pos = torch.zeros(T, dtype=torch.int64)
+    cs = W.make_cos_sin_cache(16, rope_dim=rope)
+    codes, scales = oracle.inv_rope_fp8_quant(o, pos, cs, 1, H, nope_dim=nope, rope_dim=rope,
+                                              quant_group_size=group)
+    codes = codes.contiguous().view(T, H, D // group, group)
+    scales = scales.contiguous().view(T, H, D // group)
+    v = o.float().view(T, H, D // group, group).gather(-1, where[..., None])[..., 0]
+    assert torch.equal(scales, v.abs() * torch.tensor(1.0 / 448.0, dtype=torch.float32))
+    hit = codes.gather(-1, where[..., None])[..., 0]
+    assert torch.equal(hit, torch.where(v > 0, 0x7E, 0xFE).to(torch.uint8))
+    assert int(codes.sum()) == int(hit.long().sum())
