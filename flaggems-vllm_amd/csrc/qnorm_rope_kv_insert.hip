@@ -58,6 +58,25 @@ constexpr int64_t kUncappedRound = 8 * 256;
 // 4.40, T = 17 x H = 64 (72) 2.20 -> 2.29, T = 1 and 4 unchanged.
 constexpr int64_t kCsLdsMinGrid = 4 * 256;
 
+// Block order.  Workgroups are dispatched to the 8 XCDs round-robin (block b
+// on XCD b % 8); with xcd_per = grid / 8 the kernel runs logical block
+// (b % 8) * xcd_per + b / 8 instead (a bijection on [0, 8 * xcd_per); the
+// tail maps to itself), so each XCD takes a contiguous eighth of the rows.
+// Same-box A/Bs (bit-identical outputs, HIP-graph replay, median of 5):
+// one-round grids of 256..1030 workgroups gain 1.3-3 % (c1, T = 256, H = 64:
+// 6.54 -> 6.35 us; the rows of one token and their cos/sin row stay on one
+// XCD's L2), 1285 are level, 1536..2048 lose 1-6 %, multi-round grids up to
+// 4 GiB of q lose up to 12 % (c2 162.6 -> 174.5 us), and from 2^19
+// workgroups (8 GiB of q) the order gains again, 0.7-2.1 %
+// (T = 131072, H = 128: 5637 -> 5520 us).
+constexpr int64_t kXcdOrderMinGrid = 256;
+constexpr int64_t kXcdOrderMaxOneRound = 1152;
+constexpr int64_t kXcdOrderMinLarge = int64_t(1) << 19;
+
+bool xcd_order(int64_t grid) {
+    return (grid >= kXcdOrderMinGrid && grid <= kXcdOrderMaxOneRound) || grid >= kXcdOrderMinLarge;
+}
+
 struct QnormArgs {
     uint16_t* q;
     const uint16_t* kv;
@@ -76,6 +95,7 @@ struct QnormArgs {
     double inv_pitch;          // kMapAligned: 1.0 / pitch_units
     uint32_t num_tokens_insert;
     uint32_t kv_blocks;
+    uint32_t xcd_per;          // 0, or grid / 8: blocks run in XCD-contiguous order
     float eps;
 };
 
@@ -345,10 +365,13 @@ __global__ void __launch_bounds__(kThreads)
 qnorm_rope_kv_insert_kernel(QnormArgs a) {
     const int lane16 = threadIdx.x & 15;
     const int row_in_pass = threadIdx.x >> 4;
-    if (blockIdx.x < a.kv_blocks)
-        kv_block(a, blockIdx.x, lane16, row_in_pass);
+    uint32_t b = blockIdx.x;
+    if (a.xcd_per && b < 8 * a.xcd_per)
+        b = (b % 8) * a.xcd_per + b / 8;
+    if (b < a.kv_blocks)
+        kv_block(a, b, lane16, row_in_pass);
     else
-        q_block<kMap, kCsLds>(a, blockIdx.x - a.kv_blocks, lane16, row_in_pass);
+        q_block<kMap, kCsLds>(a, b - a.kv_blocks, lane16, row_in_pass);
 }
 
 }  // namespace
@@ -442,6 +465,7 @@ extern "C" int fgv_qnorm_rope_kv_rope_quant_insert(
     const int64_t grid = (int64_t)a.kv_blocks + q_blocks;
     if (grid > 0x7fffffffLL)
         return fail(FGV_E_TOO_LARGE, "grid exceeds 2^31 - 1 workgroups");
+    a.xcd_per = xcd_order(grid) ? (uint32_t)(grid / 8) : 0u;
     const hipStream_t st = static_cast<hipStream_t>(stream);
     const size_t lds = grid > kUncappedRound ? kOccupancyLds : 0;
     if (map == kMapAligned)
