@@ -16,7 +16,9 @@
 // The cos/sin row of a token is read from L2 by each row's rope lanes, except
 // on one-round grids of 4-8 workgroups per CU with whole tokens per block,
 // where it is staged in LDS once per block (q_block's kCsLds: measured faster
-// there, slower elsewhere).
+// there, slower elsewhere).  One-round grids of 256..1152 workgroups and grids
+// from 2^19 workgroups run their blocks in XCD-contiguous order (xcd_order),
+// so that each XCD takes a contiguous eighth of the rows.
 //
 // Which 16 rows a q block takes (QMap):
 //   kMapRows / kMapRowsOneToken: rows 16b .. 16b+15 in (token, head) order.
