@@ -221,6 +221,7 @@ LAYOUTS = [
     (33, 128, 5, 15),
     (200, 1, 2, 7),
     (64, 64, 0, 0),    # aligned and contiguous: the row-order mapping
+    (100, 64, 1, 3),   # a grid of 414 workgroups: chunk mapping in XCD-contiguous order
 ]
 
 
@@ -392,6 +393,30 @@ def test_lds_cos_sin_path_clamps_positions():
     w = W.Workload("lds cos/sin clamp", W.randn_bf16((T, H, 512), g), W.randn_bf16((T, 512), g),
                    torch.zeros(nblk, 64 * W.HEAD_BYTES, dtype=torch.uint8), slots, pos,
                    W.make_cos_sin_cache(2048), 1e-6, 64)
+    gw = run_gpu(w)
+    ref = oracle_main(w)
+    assert_q_exact(gw.q.cpu(), ref.q, w.name)
+    assert torch.equal(gw.k_cache.cpu(), ref.k_cache), f"{w.name}: cache differs"
+
+
+# The kernel runs blocks in XCD-contiguous order on one-round grids of 256..1152
+# workgroups (and from 2^19, covered by test_combined_largest): the first
+# 8 * (grid / 8) blocks permuted, the tail in place.  Grids at both edges
+# (kv blocks included: T q blocks of 16 heads plus ceil(Tins / 16)), one with
+# heads not a multiple of 16, all bit-exact against the oracle.
+@pytest.mark.parametrize("T,H,n_ins", [(240, 16, 240), (241, 16, 240), (1084, 16, 1084), (1085, 16, 1085),
+                                       (1100, 3, 1100), (150, 48, 149)])
+def test_block_order_boundaries(T, H, n_ins):
+    grid = -(-T * H // 16) + -(-n_ins // 16)
+    _say(f"block order T={T} H={H} inserted={n_ins} grid={grid}")
+    g = torch.Generator().manual_seed(5 * T + H)
+    nblk = (T + 63) // 64 + 2
+    slots = torch.randperm(nblk * 64, generator=g)[:n_ins].to(torch.int64)
+    slots[::13] = -1
+    w = W.Workload(f"order T{T} H{H}", W.randn_bf16((T, H, 512), g), W.randn_bf16((T, 512), g),
+                   torch.zeros(nblk, 64 * W.HEAD_BYTES, dtype=torch.uint8), slots,
+                   torch.randint(0, 4096, (T,), generator=g, dtype=torch.int64),
+                   W.make_cos_sin_cache(4096), 1e-6, 64)
     gw = run_gpu(w)
     ref = oracle_main(w)
     assert_q_exact(gw.q.cpu(), ref.q, w.name)
