@@ -16,9 +16,9 @@
 // The cos/sin row of a token is read from L2 by each row's rope lanes, except
 // on one-round grids of 4-8 workgroups per CU with whole tokens per block,
 // where it is staged in LDS once per block (q_block's kCsLds: measured faster
-// there, slower elsewhere).  One-round grids of 256..1152 workgroups and grids
-// from 2^19 workgroups run their blocks in XCD-contiguous order (xcd_order),
-// so that each XCD takes a contiguous eighth of the rows.
+// there, slower elsewhere).  One-round grids of 256..1152 workgroups run their
+// blocks in XCD-contiguous order, and grids from 1.25 GiB of q in runs of 16
+// blocks per XCD (see "Block order" below).
 //
 // Which 16 rows a q block takes (QMap):
 //   kMapRows / kMapRowsOneToken: rows 16b .. 16b+15 in (token, head) order.
@@ -61,22 +61,35 @@ constexpr int64_t kUncappedRound = 8 * 256;
 constexpr int64_t kCsLdsMinGrid = 4 * 256;
 
 // Block order.  Workgroups are dispatched to the 8 XCDs round-robin (block b
-// on XCD b % 8); with xcd_per = grid / 8 the kernel runs logical block
-// (b % 8) * xcd_per + b / 8 instead (a bijection on [0, 8 * xcd_per); the
-// tail maps to itself), so each XCD takes a contiguous eighth of the rows.
-// Same-box A/Bs (bit-identical outputs, HIP-graph replay, median of 5):
-// one-round grids of 256..1030 workgroups gain 1.3-3 % (c1, T = 256, H = 64:
-// 6.54 -> 6.35 us; the rows of one token and their cos/sin row stay on one
-// XCD's L2), 1285 are level, 1536..2048 lose 1-6 %, multi-round grids up to
-// 4 GiB of q lose up to 12 % (c2 162.6 -> 174.5 us), and from 2^19
-// workgroups (8 GiB of q) the order gains again, 0.7-2.1 %
-// (T = 131072, H = 128: 5637 -> 5520 us).
+// on XCD b % 8).  Two remaps (bijections on a prefix of the grid; the tail
+// maps to itself), measured in same-box A/Bs (bit-identical outputs,
+// HIP-graph replay, median of 5):
+//   - XCD-contiguous (xcd_per = grid / 8): logical block
+//     (b % 8) * xcd_per + b / 8, each XCD a contiguous eighth of the rows.
+//     One-round grids of 256..1152 workgroups gain 1.3-3 % (c1, T = 256,
+//     H = 64: 6.54 -> 6.35 us; the rows of one token and their cos/sin row
+//     stay on one XCD's L2); from 1285 workgroups on it loses (c2 -7 %).
+//   - Runs of kXcdRun blocks (group_full > 0): 8 consecutive runs of 16
+//     blocks (256 KiB of q each) go one to each XCD, so each XCD streams
+//     256 KiB stretches while all XCDs stay inside one 2 MiB window.  From
+//     1.5 GiB of q it gains 1.9-5.2 % (c3 1385 -> 1321 us, c4 1231 -> 1178,
+//     T = 65536 x H = 128 2772 -> 2627, T = 131072 x H = 128 5523 -> 5268);
+//     at 1 GiB it is level, at 0.5 GiB (c2) 1-1.6 % slower.  Runs of 8
+//     blocks did 1-3 % worse than 16 on most shapes, runs of 2, 4, 32, 64
+//     and 128 worse still.
 constexpr int64_t kXcdOrderMinGrid = 256;
 constexpr int64_t kXcdOrderMaxOneRound = 1152;
-constexpr int64_t kXcdOrderMinLarge = int64_t(1) << 19;
+constexpr uint32_t kXcdRun = 16;
+constexpr int64_t kXcdRunsMinGrid = 81920;  // 1.25 GiB of q rows
 
-bool xcd_order(int64_t grid) {
-    return (grid >= kXcdOrderMinGrid && grid <= kXcdOrderMaxOneRound) || grid >= kXcdOrderMinLarge;
+// The block order is a template parameter, so each launch carries only the
+// remap its grid uses.
+enum BlockOrder { kOrderRoundRobin = 0, kOrderContiguous = 1, kOrderRuns = 2 };
+
+BlockOrder block_order(int64_t grid) {
+    if (grid >= kXcdOrderMinGrid && grid <= kXcdOrderMaxOneRound)
+        return kOrderContiguous;
+    return grid >= kXcdRunsMinGrid ? kOrderRuns : kOrderRoundRobin;
 }
 
 struct QnormArgs {
@@ -97,7 +110,8 @@ struct QnormArgs {
     double inv_pitch;          // kMapAligned: 1.0 / pitch_units
     uint32_t num_tokens_insert;
     uint32_t kv_blocks;
-    uint32_t xcd_per;          // 0, or grid / 8: blocks run in XCD-contiguous order
+    uint32_t xcd_per;          // 0, or grid / 8: blocks [0, 8 xcd_per) run in XCD-contiguous order
+    uint32_t group_full;       // 0, or the blocks [0, group_full) run in runs of kXcdRun per XCD
     float eps;
 };
 
@@ -362,18 +376,51 @@ __device__ void kv_block(const QnormArgs& a, uint32_t kvb, int lane16, int row_i
     }
 }
 
-template <int kMap, bool kCsLds>
+template <int kMap, bool kCsLds, int kOrder>
 __global__ void __launch_bounds__(kThreads)
 qnorm_rope_kv_insert_kernel(QnormArgs a) {
     const int lane16 = threadIdx.x & 15;
     const int row_in_pass = threadIdx.x >> 4;
     uint32_t b = blockIdx.x;
-    if (a.xcd_per && b < 8 * a.xcd_per)
+    if (kOrder == kOrderContiguous && b < 8 * a.xcd_per)
         b = (b % 8) * a.xcd_per + b / 8;
+    else if (kOrder == kOrderRuns && b < a.group_full)
+        b = b / (8 * kXcdRun) * (8 * kXcdRun) + (b % 8) * kXcdRun + (b / 8) % kXcdRun;
     if (b < a.kv_blocks)
         kv_block(a, b, lane16, row_in_pass);
     else
         q_block<kMap, kCsLds>(a, b - a.kv_blocks, lane16, row_in_pass);
+}
+
+template <int kMap, bool kCsLds>
+void launch_ordered(BlockOrder order, dim3 grid, size_t lds, hipStream_t st, const QnormArgs& a) {
+    if (order == kOrderContiguous)
+        hipLaunchKernelGGL((qnorm_rope_kv_insert_kernel<kMap, kCsLds, kOrderContiguous>), grid, dim3(kThreads), lds,
+                           st, a);
+    else if (order == kOrderRuns)
+        hipLaunchKernelGGL((qnorm_rope_kv_insert_kernel<kMap, kCsLds, kOrderRuns>), grid, dim3(kThreads), lds, st,
+                           a);
+    else
+        hipLaunchKernelGGL((qnorm_rope_kv_insert_kernel<kMap, kCsLds, kOrderRoundRobin>), grid, dim3(kThreads), lds,
+                           st, a);
+}
+
+// cs_lds grids are one round (at most kUncappedRound workgroups), so they never
+// take the runs order.
+void launch_q_kernel(int map, bool cs_lds, BlockOrder order, dim3 grid, size_t lds, hipStream_t st,
+                     const QnormArgs& a) {
+    if (map == kMapAligned)
+        launch_ordered<kMapAligned, false>(order, grid, lds, st, a);
+    else if (cs_lds && order == kOrderContiguous)
+        hipLaunchKernelGGL((qnorm_rope_kv_insert_kernel<kMapRowsOneToken, true, kOrderContiguous>), grid,
+                           dim3(kThreads), lds, st, a);
+    else if (cs_lds)
+        hipLaunchKernelGGL((qnorm_rope_kv_insert_kernel<kMapRowsOneToken, true, kOrderRoundRobin>), grid,
+                           dim3(kThreads), lds, st, a);
+    else if (map == kMapRowsOneToken)
+        launch_ordered<kMapRowsOneToken, false>(order, grid, lds, st, a);
+    else
+        launch_ordered<kMapRows, false>(order, grid, lds, st, a);
 }
 
 }  // namespace
@@ -467,20 +514,12 @@ extern "C" int fgv_qnorm_rope_kv_rope_quant_insert(
     const int64_t grid = (int64_t)a.kv_blocks + q_blocks;
     if (grid > 0x7fffffffLL)
         return fail(FGV_E_TOO_LARGE, "grid exceeds 2^31 - 1 workgroups");
-    a.xcd_per = xcd_order(grid) ? (uint32_t)(grid / 8) : 0u;
+    const BlockOrder order = block_order(grid);
+    a.xcd_per = order == kOrderContiguous ? (uint32_t)(grid / 8) : 0u;
+    a.group_full = order == kOrderRuns ? (uint32_t)(grid / (8 * kXcdRun) * (8 * kXcdRun)) : 0u;
     const hipStream_t st = static_cast<hipStream_t>(stream);
     const size_t lds = grid > kUncappedRound ? kOccupancyLds : 0;
-    if (map == kMapAligned)
-        hipLaunchKernelGGL((qnorm_rope_kv_insert_kernel<kMapAligned, false>), dim3((uint32_t)grid), dim3(kThreads),
-                           lds, st, a);
-    else if (map == kMapRowsOneToken && grid >= kCsLdsMinGrid && grid <= kUncappedRound)
-        hipLaunchKernelGGL((qnorm_rope_kv_insert_kernel<kMapRowsOneToken, true>), dim3((uint32_t)grid),
-                           dim3(kThreads), lds, st, a);
-    else if (map == kMapRowsOneToken)
-        hipLaunchKernelGGL((qnorm_rope_kv_insert_kernel<kMapRowsOneToken, false>), dim3((uint32_t)grid),
-                           dim3(kThreads), lds, st, a);
-    else
-        hipLaunchKernelGGL((qnorm_rope_kv_insert_kernel<kMapRows, false>), dim3((uint32_t)grid), dim3(kThreads),
-                           lds, st, a);
+    const bool cs_lds = map == kMapRowsOneToken && grid >= kCsLdsMinGrid && grid <= kUncappedRound;
+    launch_q_kernel(map, cs_lds, order, dim3((uint32_t)grid), lds, st, a);
     return launch_status();
 }
