@@ -400,8 +400,9 @@ def test_lds_cos_sin_path_clamps_positions():
 
 
 # The kernel runs blocks in XCD-contiguous order on one-round grids of 256..1152
-# workgroups (and from 2^19, covered by test_combined_largest): the first
-# 8 * (grid / 8) blocks permuted, the tail in place.  Grids at both edges
+# workgroups, and in runs of 16 blocks per XCD from 81920 workgroups (also
+# taken by c3, c4 and test_combined_largest): a prefix of the grid permuted,
+# the tail in place.  Grids at both edges
 # (kv blocks included: T q blocks of 16 heads plus ceil(Tins / 16)), one with
 # heads not a multiple of 16, all bit-exact against the oracle.
 @pytest.mark.parametrize("T,H,n_ins", [(240, 16, 240), (241, 16, 240), (1084, 16, 1084), (1085, 16, 1085),
@@ -417,6 +418,28 @@ def test_block_order_boundaries(T, H, n_ins):
                    torch.zeros(nblk, 64 * W.HEAD_BYTES, dtype=torch.uint8), slots,
                    torch.randint(0, 4096, (T,), generator=g, dtype=torch.int64),
                    W.make_cos_sin_cache(4096), 1e-6, 64)
+    gw = run_gpu(w)
+    ref = oracle_main(w)
+    assert_q_exact(gw.q.cpu(), ref.q, w.name)
+    assert torch.equal(gw.k_cache.cpu(), ref.k_cache), f"{w.name}: cache differs"
+
+
+# Just below and above the runs order's 81920 workgroups (T * 8 q blocks at
+# H = 128 plus ceil(T / 16) kv blocks): 80625 and 82569, the latter with a
+# tail of 9 blocks past the last whole group of 128.  Whole q bit-exact.
+@pytest.mark.parametrize("T", [10000, 10241])
+def test_block_runs_boundary(T):
+    H = 128
+    grid = T * H // 16 + -(-T // 16)
+    _say(f"block runs T={T} H={H} grid={grid}")
+    g = torch.Generator().manual_seed(T)
+    nblk = (T + 63) // 64 + 2
+    slots = torch.randperm(nblk * 64, generator=g)[:T].to(torch.int64)
+    slots[::17] = -1
+    w = W.Workload(f"runs T{T}", W.randn_bf16((T, H, 512), g), W.randn_bf16((T, 512), g),
+                   torch.zeros(nblk, 64 * W.HEAD_BYTES, dtype=torch.uint8), slots,
+                   torch.randint(0, 65536, (T,), generator=g, dtype=torch.int64),
+                   W.make_cos_sin_cache(65536), 1e-6, 64)
     gw = run_gpu(w)
     ref = oracle_main(w)
     assert_q_exact(gw.q.cpu(), ref.q, w.name)
