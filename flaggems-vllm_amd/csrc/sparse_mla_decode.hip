@@ -671,13 +671,29 @@ __device__ __forceinline__ void run_segment(const MlaArgs& a, uint8_t (&raw)[2][
 }
 
 
+// Items in runs of kItemRun per XCD (kRuns): workgroups are dispatched to the
+// 8 XCDs round-robin (workgroup w on XCD w % 8); workgroup w takes item
+// floor(w / 8R) 8R + (w % 8) R + floor(w / 8) % R instead (R = kItemRun; the
+// tail past the last whole 8R takes its own index), so each XCD streams R
+// consecutive items' q and output rows.  Same-box A/Bs on the decode bench
+// case (512 items, one round; same bits, medians of 11-15 graph replays, four
+// runs): 0.6-1.9 % faster, e.g. 20.22 -> 20.00 us on one input set and 21.63
+// -> 21.45 us over 8 rotating sets; runs of 8 and 32 the same; extra512 level
+// (+-0.5 %).  The item count is taken from the grid: computing it from the
+// arguments in the prologue cost the gain.
+constexpr uint32_t kItemRun = 16;
+
 // One workgroup per (batch row, query position, 64-head block).
+template <bool kRuns>
 __global__ void __launch_bounds__(kThreads, 2)
 sparse_mla_decode_kernel(MlaArgs a) {
     FGV_MLA_LDS;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-    const int hb = blockIdx.x % a.head_blocks;
-    const int bs = blockIdx.x / a.head_blocks;
+    uint32_t item = blockIdx.x;
+    if (kRuns && item < gridDim.x / (8 * kItemRun) * (8 * kItemRun))
+        item = item / (8 * kItemRun) * (8 * kItemRun) + (item % 8) * kItemRun + (item / 8) % kItemRun;
+    const int hb = item % a.head_blocks;
+    const int bs = item / a.head_blocks;
     const int sq = bs % a.seq_q, b = bs / a.seq_q;
     const ListView v0 = make_view(a.list[0], true, b, sq);
     const ListView v1 = make_view(a.list[1], a.num_lists > 1, b, sq);
@@ -1660,7 +1676,11 @@ int mla_decode(FGV_MLA_PARAMS, void* workspace, int64_t workspace_bytes, void* s
                            dim3(kPairThreads), 0, st, a);
         return launch_status();
     }
-    hipLaunchKernelGGL(sparse_mla_decode_kernel, dim3((unsigned)items), dim3(kThreads), 0, st, a);
+    // one round of two workgroups per CU: items in runs per XCD (measured there)
+    if (items <= 2 * (int64_t)cu_count())
+        hipLaunchKernelGGL(sparse_mla_decode_kernel<true>, dim3((unsigned)items), dim3(kThreads), 0, st, a);
+    else
+        hipLaunchKernelGGL(sparse_mla_decode_kernel<false>, dim3((unsigned)items), dim3(kThreads), 0, st, a);
     return launch_status();
 }
 
