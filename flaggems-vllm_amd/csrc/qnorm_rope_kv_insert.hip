@@ -407,7 +407,7 @@ void launch_ordered(BlockOrder order, dim3 grid, size_t lds, hipStream_t st, con
 
 // cs_lds grids are one round (at most kUncappedRound workgroups), so they never
 // take the runs order.
-void launch_q_kernel(int map, bool cs_lds, BlockOrder order, dim3 grid, size_t lds, hipStream_t st,
+void launch_insert_kernel(int map, bool cs_lds, BlockOrder order, dim3 grid, size_t lds, hipStream_t st,
                      const QnormArgs& a) {
     if (map == kMapAligned)
         launch_ordered<kMapAligned, false>(order, grid, lds, st, a);
@@ -520,6 +520,6 @@ extern "C" int fgv_qnorm_rope_kv_rope_quant_insert(
     const hipStream_t st = static_cast<hipStream_t>(stream);
     const size_t lds = grid > kUncappedRound ? kOccupancyLds : 0;
     const bool cs_lds = map == kMapRowsOneToken && grid >= kCsLdsMinGrid && grid <= kUncappedRound;
-    launch_q_kernel(map, cs_lds, order, dim3((uint32_t)grid), lds, st, a);
+    launch_insert_kernel(map, cs_lds, order, dim3((uint32_t)grid), lds, st, a);
     return launch_status();
 }
