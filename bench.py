@@ -12,6 +12,7 @@ workload.
 """
 import argparse
 import json
+import math
 import os
 import re
 import statistics
@@ -118,11 +119,14 @@ def time_gpu(fn, steps, warmup):
     kernel time was taken).
 
     The eager loop of `steps` calls through the public API gives the step time.
-    The kernel time comes from HIP events around one replay of a HIP graph that
+    The kernel time comes from HIP events around replays of a HIP graph that
     holds the same `steps` calls, so that the host-side cost of the Python
     wrappers (tens of microseconds, more than some of these kernels take) leaves
-    no idle gaps between the launches being timed.  Where capture is not
-    possible, the eager loop's events are used instead.
+    no idle gaps between the launches being timed.  The graph is replayed back
+    to back until about 2 ms of GPU work lie between the events (once for
+    calls of 40 us or more at 50 steps), so that the graph's own launch does not
+    weigh on short calls; each replay runs exactly `steps` calls.  Where capture
+    is not possible, the eager loop's events are used instead.
     """
     import torch
 
@@ -150,11 +154,16 @@ def time_gpu(fn, steps, warmup):
             for _ in range(steps):
                 fn()
         torch.cuda.synchronize()
-        start.record()
         graph.replay()
+        torch.cuda.synchronize()
+        replays = max(1, min(32, math.ceil(2e-3 / max(steps * eager, 1e-9))))
+        start.record()
+        for _ in range(replays):
+            graph.replay()
         end.record()
         torch.cuda.synchronize()
-        return wall / steps, start.elapsed_time(end) / 1000.0 / steps, "hip graph replay of the timed steps"
+        return (wall / steps, start.elapsed_time(end) / 1000.0 / (steps * replays),
+                f"hip graph of the timed steps, {replays} back-to-back replay(s)")
     except RuntimeError as e:
         print(f"bench.py: graph capture unavailable ({e}); kernel time from the eager loop", file=sys.stderr)
         return wall / steps, eager, "events around the eager loop"
