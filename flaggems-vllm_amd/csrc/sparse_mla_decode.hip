@@ -110,6 +110,9 @@ struct MlaArgs {
     float* partials;       // 2 slots per workgroup of kSlotFloats
     int32_t* row_prefix;   // batch + 1 prefix sums of per-item chunk counts
     int32_t split_grid;
+    // one-item kernel in the paired order: the CU count C (workgroups j and
+    // C + j share a CU)
+    int32_t pair_cus;
 };
 
 // K tile addressing: 16-byte block b of row r at r * kKRowBytes + 16 b, rows
@@ -170,7 +173,18 @@ struct ListView {
     int page_size, num_blocks, len;
 };
 
-__device__ __forceinline__ ListView make_view(const CacheList& L, bool present, int b, int sq) {
+// The list's clamped length for batch row b.
+__device__ __forceinline__ int list_len(const CacheList& L, bool present, int b) {
+    if (!present)
+        return 0;
+    if (!L.lengths)
+        return L.topk;
+    const int n = L.lengths[b];
+    return n < 0 ? 0 : (n > L.topk ? L.topk : n);
+}
+
+// known_len >= 0: the length list_len gives, already loaded by the caller.
+__device__ __forceinline__ ListView make_view(const CacheList& L, bool present, int b, int sq, int known_len = -1) {
     ListView v;
     v.cache = L.cache;
     v.row = L.indices + b * L.idx_stride_b + sq * L.idx_stride_s;
@@ -180,15 +194,7 @@ __device__ __forceinline__ ListView make_view(const CacheList& L, bool present, 
     v.inv_page = L.inv_page;
     v.page_size = L.page_size;
     v.num_blocks = L.num_blocks;
-    int len = 0;
-    if (present) {
-        len = L.topk;
-        if (L.lengths) {
-            const int n = L.lengths[b];
-            len = n < 0 ? 0 : (n > L.topk ? L.topk : n);
-        }
-    }
-    v.len = len;
+    v.len = known_len >= 0 ? known_len : list_len(L, present, b);
     return v;
 }
 
@@ -522,12 +528,13 @@ __device__ __forceinline__ void store_rows(uint8_t* stage, const f32x4_t (&acc)[
 
 __device__ __forceinline__ void run_segment(const MlaArgs& a, uint8_t (&raw)[2][kRawBytes], uint8_t* kbuf,
                                             float (&mask_lds)[2][kChunk], int b,
-                                            int sq, int hb, int c_lo, int c_hi, int slot, int wave, int lane) {
+                                            int sq, int hb, int c_lo, int c_hi, int slot, int wave, int lane,
+                                            int len0 = -1, int len1 = -1) {
     const int m16 = lane & 15, g = lane >> 4;
     const int head = hb * kBlockHeads + wave * 16 + m16;
 
-    const ListView v0 = make_view(a.list[0], true, b, sq);
-    const ListView v1 = make_view(a.list[1], a.num_lists > 1, b, sq);
+    const ListView v0 = make_view(a.list[0], true, b, sq, len0);
+    const ListView v1 = make_view(a.list[1], a.num_lists > 1, b, sq, len1);
     const int n0 = (v0.len + kChunk - 1) / kChunk;
     const uint8_t* dummy = mla_zero_entry;
 
@@ -671,34 +678,107 @@ __device__ __forceinline__ void run_segment(const MlaArgs& a, uint8_t (&raw)[2][
 }
 
 
-// Items in runs of kItemRun per XCD (kRuns): workgroups are dispatched to the
-// 8 XCDs round-robin (workgroup w on XCD w % 8); workgroup w takes item
-// floor(w / 8R) 8R + (w % 8) R + floor(w / 8) % R instead (R = kItemRun; the
-// tail past the last whole 8R takes its own index), so each XCD streams R
-// consecutive items' q and output rows.  Same-box A/Bs on the decode bench
-// case (512 items, one round; same bits, medians of 11-15 graph replays, four
-// runs): 0.6-1.9 % faster, e.g. 20.22 -> 20.00 us on one input set and 21.63
-// -> 21.45 us over 8 rotating sets; runs of 8 and 32 the same; extra512 level
-// (+-0.5 %).  The item count is taken from the grid: computing it from the
-// arguments in the prologue cost the gain.
+// Items in runs of kItemRun per XCD (kItemsInRuns, grids of at most one
+// workgroup per CU): workgroups are dispatched to the 8 XCDs round-robin
+// (workgroup w on XCD w % 8); workgroup w takes item floor(w / 8R) 8R +
+// (w % 8) R + floor(w / 8) % R instead (R = kItemRun; the tail past the last
+// whole 8R takes its own index), so each XCD streams R consecutive items' q
+// and output rows.  Same-box A/Bs on the decode bench case when it ran in
+// this order (512 items, one round; same bits, medians of 11-15 graph
+// replays, four runs): 0.6-1.9 % faster, e.g. 20.22 -> 20.00 us on one input
+// set and 21.63 -> 21.45 us over 8 rotating sets; runs of 8 and 32 the same;
+// extra512 level (+-0.5 %).  The item count is taken from the grid: computing
+// it from the arguments in the prologue cost the gain.  Grids of two
+// workgroups per CU take the paired order below instead.
 constexpr uint32_t kItemRun = 16;
 
+// Paired order, for grids of C < G <= 2C workgroups (C = CUs).  Workgroups j
+// and C + j share a CU: the dispatcher gives every CU one workgroup, then a
+// second in the same order (read from HW_ID / XCC_ID on gfx950: pairs
+// {j, C + j} in every launch, 256 CUs).  Both run to the end of the longer
+// item, so a CU that holds two long items sets the kernel's time while others
+// idle.  The P = G - C pairs are taken in windows of kPairWindow: the window's
+// 2 kPairWindow own items (j and C + j of each of its pairs) are ranked by
+// cost, longest first (ties by position), and the window's pair i takes the
+// i-th longest on j, which is dispatched first, and the i-th shortest on
+// C + j.  Workgroups j >= P have no partner and keep their own item.  The
+// cost counts 2 per FP8 chunk and 1 per expanded chunk (their measured
+// per-chunk times are 3.0-3.6 and 1.6-1.8 us).  Same bits; same-box A/B,
+// medians of 7 graph replays of 20 calls: decode 22.55 -> 20.14 us, extra512
+// (with its expand kernel) 61.8 -> 54.2 us.  A global ranking over all items
+// measured 19.6 / 53.5 us, long items on j first; short items on j instead
+// lost 1.3 / 2.5 us of that.
+constexpr uint32_t kPairWindow = 32;
+
+enum ItemOrder { kItemsInOrder = 0, kItemsInRuns = 1, kItemsPaired = 2 };
+
+// The item workgroup blk takes in the paired order, and that item's two list
+// lengths (len0, len1; left at -1 for a workgroup without a partner).  Every
+// wave computes the same answer from one length load per lane: lane l < 32
+// holds pair w0 + l's first item, lane 32 + l its second; lanes past the
+// window's end rank last.
+__device__ __forceinline__ uint32_t paired_item(const MlaArgs& a, uint32_t blk, int lane, int& len0, int& len1) {
+    const uint32_t cus = (uint32_t)a.pair_cus;
+    const uint32_t pairs = gridDim.x - cus;
+    const bool second = blk >= cus;
+    const uint32_t j = second ? blk - cus : blk;
+    if (j >= pairs)
+        return blk;
+    const uint32_t w0 = j / kPairWindow * kPairWindow;
+    const uint32_t m = min(kPairWindow, pairs - w0);
+    const uint32_t l32 = (uint32_t)lane & (kPairWindow - 1);
+    const bool valid = l32 < m;
+    const uint32_t it = valid ? (lane < (int)kPairWindow ? w0 + l32 : cus + w0 + l32) : w0;
+    const int row = (int)(it / (uint32_t)a.head_blocks / (uint32_t)a.seq_q);
+    const int n0 = list_len(a.list[0], true, row);
+    const int n1 = list_len(a.list[1], a.num_lists > 1, row);
+    const int c0 = (n0 + kChunk - 1) / kChunk, c1 = (n1 + kChunk - 1) / kChunk;
+    const int cost = 2 * c0 + (a.list[1].expanded ? c1 : 2 * c1);
+    const uint32_t key = valid ? (uint32_t)min(cost, 254) + 1 : 0;  // 8 bits; 0 ranks last
+    // rank = lanes with a larger key + lanes below with the same key: bit
+    // planes from the top, `eq` the lanes that match this lane's key so far
+    uint64_t eq = ~0ull;
+    uint32_t above = 0;
+#pragma unroll
+    for (int bit = 7; bit >= 0; --bit) {
+        const bool set = (key >> bit) & 1;
+        const uint64_t plane = __builtin_amdgcn_ballot_w64(set);
+        if (set) {
+            eq &= plane;
+        } else {
+            above += __builtin_popcountll(eq & plane);
+            eq &= ~plane;
+        }
+    }
+    const uint32_t rank = above + __builtin_popcountll(eq & ((1ull << lane) - 1));
+    const uint32_t want = second ? 2 * m - 1 - (j - w0) : j - w0;
+    // ranks are a permutation of 0..63 and the window's items take 0..2m-1
+    const uint64_t hit = __builtin_amdgcn_ballot_w64(rank == want);
+    const int src = hit ? (int)__builtin_ctzll(hit) : 0;
+    len0 = __builtin_amdgcn_readlane(n0, src);
+    len1 = __builtin_amdgcn_readlane(n1, src);
+    return (uint32_t)__builtin_amdgcn_readlane((int)it, src);
+}
+
 // One workgroup per (batch row, query position, 64-head block).
-template <bool kRuns>
+template <int kOrder>
 __global__ void __launch_bounds__(kThreads, 2)
 sparse_mla_decode_kernel(MlaArgs a) {
     FGV_MLA_LDS;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     uint32_t item = blockIdx.x;
-    if (kRuns && item < gridDim.x / (8 * kItemRun) * (8 * kItemRun))
+    int len0 = -1, len1 = -1;
+    if (kOrder == kItemsInRuns && item < gridDim.x / (8 * kItemRun) * (8 * kItemRun))
         item = item / (8 * kItemRun) * (8 * kItemRun) + (item % 8) * kItemRun + (item / 8) % kItemRun;
+    else if (kOrder == kItemsPaired)
+        item = paired_item(a, blockIdx.x, lane, len0, len1);
     const int hb = item % a.head_blocks;
     const int bs = item / a.head_blocks;
     const int sq = bs % a.seq_q, b = bs / a.seq_q;
-    const ListView v0 = make_view(a.list[0], true, b, sq);
-    const ListView v1 = make_view(a.list[1], a.num_lists > 1, b, sq);
+    const ListView v0 = make_view(a.list[0], true, b, sq, len0);
+    const ListView v1 = make_view(a.list[1], a.num_lists > 1, b, sq, len1);
     const int nchunks = (v0.len + kChunk - 1) / kChunk + (v1.len + kChunk - 1) / kChunk;
-    run_segment(a, lds_raw, lds_kbuf, lds_mask, b, sq, hb, 0, nchunks, -1, wave, lane);
+    run_segment(a, lds_raw, lds_kbuf, lds_mask, b, sq, hb, 0, nchunks, -1, wave, lane, len0, len1);
 }
 
 // ---- sparse prefill (flash_mla_sparse_fwd) over bf16 key/value rows
@@ -1635,6 +1715,7 @@ int mla_decode(FGV_MLA_PARAMS, void* workspace, int64_t workspace_bytes, void* s
     a.partials = nullptr;
     a.row_prefix = nullptr;
     a.split_grid = 0;
+    a.pair_cus = 0;
     const int64_t items = batch * seq_q * a.head_blocks;
     hipStream_t st = static_cast<hipStream_t>(stream);
     // Workspace: [expanded extra cache][split slots][row prefix sums].  A
@@ -1676,11 +1757,17 @@ int mla_decode(FGV_MLA_PARAMS, void* workspace, int64_t workspace_bytes, void* s
                            dim3(kPairThreads), 0, st, a);
         return launch_status();
     }
-    // one round of two workgroups per CU: items in runs per XCD (measured there)
-    if (items <= 2 * (int64_t)cu_count())
-        hipLaunchKernelGGL(sparse_mla_decode_kernel<true>, dim3((unsigned)items), dim3(kThreads), 0, st, a);
-    else
-        hipLaunchKernelGGL(sparse_mla_decode_kernel<false>, dim3((unsigned)items), dim3(kThreads), 0, st, a);
+    // one round: items in runs per XCD while each has a CU to itself, paired
+    // long with short once two share one
+    const int64_t cus = cu_count();
+    if (items > cus && items <= 2 * cus) {
+        a.pair_cus = (int32_t)cus;
+        hipLaunchKernelGGL(sparse_mla_decode_kernel<kItemsPaired>, dim3((unsigned)items), dim3(kThreads), 0, st, a);
+    } else if (items <= cus) {
+        hipLaunchKernelGGL(sparse_mla_decode_kernel<kItemsInRuns>, dim3((unsigned)items), dim3(kThreads), 0, st, a);
+    } else {
+        hipLaunchKernelGGL(sparse_mla_decode_kernel<kItemsInOrder>, dim3((unsigned)items), dim3(kThreads), 0, st, a);
+    }
     return launch_status();
 }
 

@@ -906,3 +906,60 @@ def test_gpu_one_item_grid_against_oracle(case):
     fin = torch.isfinite(l64)
     assert torch.equal(torch.isfinite(lse), fin)
     assert torch.allclose(lse.double()[fin], l64[fin], rtol=1e-5, atol=1e-5)
+
+
+def _paired_order_case(name):
+    """One-item grids of C < items <= 2C (C = CUs): workgroups j and C + j
+    share a CU and the kernel ranks each window of 32 such pairs by list
+    length, so the items land on other workgroups than their own."""
+    if name == "partial":     # 300 items: a whole window, a window of 12 pairs, unpartnered workgroups
+        w = W.make_mla_workload(batch=300, topk=256, num_pages=32, seed=71, q_scale=0.1)
+        w.topk_length = _lengths(300, 256, 5)
+        w.topk_length[::11] = 0
+        w.topk_length[[4, 9, 260]] = torch.tensor([-3, 100000, 257], dtype=torch.int32)  # clamped
+        return w
+    if name == "h128_sq2":    # 100 rows x 2 query positions x 2 head blocks = 400 items
+        w = W.make_mla_workload(batch=100, topk=128, num_pages=16, heads=128, seq_q=2, seed=73,
+                                q_scale=0.1)
+        w.topk_length = _lengths(100, 128, 6)
+        return w
+    if name == "no_lengths":  # 257 items, every list full: one pair, equal keys
+        return W.make_mla_workload(batch=257, topk=64, num_pages=8, topk_length=False, seed=75, q_scale=0.1)
+    if name in ("extra_fp8", "extra_expanded"):  # 480 items; extra chunks weigh 2 or 1
+        w = W.make_mla_workload(batch=480, topk=64, num_pages=16, extra_topk=128, extra_page=64,
+                                extra_pages=8, seed=77, q_scale=0.1)
+        w.extra_topk_length = _lengths(480, 128, 7)
+        w.extra_topk_length[::13] = 0
+        return w
+    raise KeyError(name)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", ["partial", "h128_sq2", "no_lengths", "extra_fp8", "extra_expanded"])
+def test_gpu_paired_order_against_oracle(case):
+    """The paired order against the oracle, and bit for bit against the same
+    rows computed in calls of at most C items (which keep each item on its
+    own workgroup's index order)."""
+    print(f"\n[case] sparse MLA one-item grid, paired order, {case}", flush=True)
+    w = _paired_order_case(case)
+    B, SQ, HQ, _ = w.q.shape
+    items = B * SQ * (HQ // 64)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    assert cus < items <= 2 * cus, "the case must take the paired order"
+    assert _grid(w) == 0
+    ws = case != "extra_fp8"
+    out, lse, nbytes = _gpu_raw(w, workspace=ws)
+    if case == "extra_expanded":
+        assert nbytes > 0, "the extra cache must be expanded"
+    o64, l64 = _oracle(w)
+    _assert_within_bound(out, o64, _vmax(w), case)
+    fin = torch.isfinite(l64)
+    assert torch.equal(torch.isfinite(lse), fin)
+    assert torch.allclose(lse.double()[fin], l64[fin], rtol=1e-5, atol=1e-5)
+    per_row = items // B
+    step = cus // per_row
+    for r0 in range(0, B, step):
+        rows = torch.arange(r0, min(B, r0 + step))
+        o_part, l_part, _ = _gpu_raw(_rows_of(w, rows), workspace=ws)
+        assert torch.equal(out[rows].view(torch.int16), o_part.view(torch.int16)), f"rows from {r0}"
+        assert torch.equal(lse[rows], l_part), f"rows from {r0}"
