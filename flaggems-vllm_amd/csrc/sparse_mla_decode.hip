@@ -737,12 +737,15 @@ __device__ __forceinline__ uint32_t paired_item(const MlaArgs& a, uint32_t blk, 
     const uint32_t key = valid ? (uint32_t)min(cost, 254) + 1 : 0;  // 8 bits; 0 ranks last
     // rank = lanes with a larger key + lanes below with the same key: bit
     // planes from the top, `eq` the lanes that match this lane's key so far
+    // (an empty plane changes neither, and is skipped)
     uint64_t eq = ~0ull;
     uint32_t above = 0;
 #pragma unroll
     for (int bit = 7; bit >= 0; --bit) {
         const bool set = (key >> bit) & 1;
         const uint64_t plane = __builtin_amdgcn_ballot_w64(set);
+        if (!plane)
+            continue;
         if (set) {
             eq &= plane;
         } else {
