@@ -710,7 +710,18 @@ constexpr uint32_t kItemRun = 16;
 // lost 1.3 / 2.5 us of that.
 constexpr uint32_t kPairWindow = 32;
 
-enum ItemOrder { kItemsInOrder = 0, kItemsInRuns = 1, kItemsPaired = 2 };
+enum ItemOrder { kItemsInOrder = 0, kItemsInRuns = 1, kItemsPaired = 2, kItemsLongestFirst = 3 };
+
+// An item's list lengths (n0, n1) and its rank key: 2 per FP8 chunk, 1 per
+// expanded chunk, plus 1 (8 bits; 0 is left for a slot with no item).
+__device__ __forceinline__ uint32_t item_key(const MlaArgs& a, uint32_t item, int& n0, int& n1) {
+    const int row = (int)(item / (uint32_t)a.head_blocks / (uint32_t)a.seq_q);
+    n0 = list_len(a.list[0], true, row);
+    n1 = list_len(a.list[1], a.num_lists > 1, row);
+    const int c0 = (n0 + kChunk - 1) / kChunk, c1 = (n1 + kChunk - 1) / kChunk;
+    const int cost = 2 * c0 + (a.list[1].expanded ? c1 : 2 * c1);
+    return (uint32_t)min(cost, 254) + 1;
+}
 
 // The item workgroup blk takes in the paired order, and that item's two list
 // lengths (len0, len1; left at -1 for a workgroup without a partner).  Every
@@ -729,12 +740,9 @@ __device__ __forceinline__ uint32_t paired_item(const MlaArgs& a, uint32_t blk, 
     const uint32_t l32 = (uint32_t)lane & (kPairWindow - 1);
     const bool valid = l32 < m;
     const uint32_t it = valid ? (lane < (int)kPairWindow ? w0 + l32 : cus + w0 + l32) : w0;
-    const int row = (int)(it / (uint32_t)a.head_blocks / (uint32_t)a.seq_q);
-    const int n0 = list_len(a.list[0], true, row);
-    const int n1 = list_len(a.list[1], a.num_lists > 1, row);
-    const int c0 = (n0 + kChunk - 1) / kChunk, c1 = (n1 + kChunk - 1) / kChunk;
-    const int cost = 2 * c0 + (a.list[1].expanded ? c1 : 2 * c1);
-    const uint32_t key = valid ? (uint32_t)min(cost, 254) + 1 : 0;  // 8 bits; 0 ranks last
+    int n0, n1;
+    const uint32_t k = item_key(a, it, n0, n1);
+    const uint32_t key = valid ? k : 0;  // 0 ranks last
     // rank = lanes with a larger key + lanes below with the same key: bit
     // planes from the top, `eq` the lanes that match this lane's key so far
     // (an empty plane changes neither, and is skipped)
@@ -763,6 +771,87 @@ __device__ __forceinline__ uint32_t paired_item(const MlaArgs& a, uint32_t blk, 
     return (uint32_t)__builtin_amdgcn_readlane((int)it, src);
 }
 
+// Longest first, for grids of 2C < G <= 4C workgroups (three or four
+// rounds): workgroups [w0, w0 + 256) take the window's own items in
+// descending cost (ties by index), so each round starts its longest items
+// first and the last round's tail holds the shortest.  Thread t holds item
+// w0 + t; each wave leaves its key's 8 bit planes (ballots) in `scr`, every
+// thread ranks its key against all four waves' planes, and the thread whose
+// rank is blk - w0 leaves its item and lengths there.  `scr` is the K tile's
+// last 512 bytes, which nothing writes before the chunk loop's first barrier.
+// Same bits; same-box A/B, medians of 9 graph replays of 20 calls, against
+// the grid in order: decode at batch 768 / 1024 33.3 / 42.1 -> 32.0 / 40.3
+// us, 128 heads at batch 512 42.3 -> 40.2 us, extra512 at batch 1024 95.0 ->
+// 89.6 us; at batch 2048 (eight rounds) 71.2 against 72.3 us, so larger
+// grids run in order.  (Host-computed, these windows reach 38.2 / 87.1 us at
+// batch 1024: the ranking costs each workgroup the rest.)
+constexpr uint32_t kLptWindow = kThreads;
+
+__device__ __forceinline__ uint32_t longest_first_item(const MlaArgs& a, uint32_t blk, int wave, int lane,
+                                                       uint8_t* scr, int& len0, int& len1) {
+    const uint32_t w0 = blk / kLptWindow * kLptWindow;
+    const uint32_t m = min(kLptWindow, gridDim.x - w0);
+    const uint32_t t = (uint32_t)(wave * 64 + lane);
+    const bool valid = t < m;
+    const uint32_t it = valid ? w0 + t : w0;
+    int n0, n1;
+    const uint32_t k = item_key(a, it, n0, n1);
+    const uint32_t key = valid ? k : 0;
+    uint64_t* planes = reinterpret_cast<uint64_t*>(scr);             // [4 waves][8 bits]
+    int32_t* pick = reinterpret_cast<int32_t*>(scr + 4 * 8 * 8);      // item, n0, n1
+    uint32_t* used = reinterpret_cast<uint32_t*>(scr + 4 * 8 * 8 + 16);  // [4]: non-empty planes
+    uint32_t mine = 0;
+#pragma unroll
+    for (int bit = 0; bit < 8; ++bit) {
+        const uint64_t p = __builtin_amdgcn_ballot_w64((key >> bit) & 1);
+        mine |= (p != 0 ? 1u : 0u) << bit;
+        if (lane == 0)
+            planes[wave * 8 + bit] = p;
+    }
+    if (lane == 0)
+        used[wave] = mine;
+    lds_barrier();
+    const uint4 uw = *reinterpret_cast<const uint4*>(used);
+    const uint32_t any = __builtin_amdgcn_readfirstlane(uw.x | uw.y | uw.z | uw.w);
+    uint64_t pl[32];  // all planes in one batch of reads
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const uint4 v = reinterpret_cast<const uint4*>(planes)[i];
+        pl[2 * i] = ((uint64_t)v.y << 32) | v.x;
+        pl[2 * i + 1] = ((uint64_t)v.w << 32) | v.z;
+    }
+    // rank = keys above this one + equal keys at lower positions (waves
+    // before this one, lanes below in this one), wave by wave as in
+    // paired_item, with `sel` this key's bit as a mask
+    uint32_t rank = 0;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        uint64_t eq = ~0ull;
+        uint32_t above = 0;
+#pragma unroll
+        for (int bit = 7; bit >= 0; --bit) {
+            if (!((any >> bit) & 1))
+                continue;
+            const uint64_t p = pl[u * 8 + bit];
+            const uint64_t sel = ((key >> bit) & 1) ? ~0ull : 0ull;
+            above += __builtin_popcountll(eq & p & ~sel);
+            eq &= ~(p ^ sel);
+        }
+        const uint64_t before = u < wave ? ~0ull : (u == wave ? (1ull << lane) - 1 : 0ull);
+        rank += above + __builtin_popcountll(eq & before);
+    }
+    // ranks are a permutation of 0..255 and the window's items take 0..m-1
+    if (valid && rank == blk - w0) {
+        pick[0] = (int32_t)it;
+        pick[1] = n0;
+        pick[2] = n1;
+    }
+    lds_barrier();
+    len0 = __builtin_amdgcn_readfirstlane(pick[1]);
+    len1 = __builtin_amdgcn_readfirstlane(pick[2]);
+    return (uint32_t)__builtin_amdgcn_readfirstlane(pick[0]);
+}
+
 // One workgroup per (batch row, query position, 64-head block).
 template <int kOrder>
 __global__ void __launch_bounds__(kThreads, 2)
@@ -775,6 +864,8 @@ sparse_mla_decode_kernel(MlaArgs a) {
         item = item / (8 * kItemRun) * (8 * kItemRun) + (item % 8) * kItemRun + (item / 8) % kItemRun;
     else if (kOrder == kItemsPaired)
         item = paired_item(a, blockIdx.x, lane, len0, len1);
+    else if (kOrder == kItemsLongestFirst)
+        item = longest_first_item(a, blockIdx.x, wave, lane, lds_kbuf + kChunk * kKRowBytes - 512, len0, len1);
     const int hb = item % a.head_blocks;
     const int bs = item / a.head_blocks;
     const int sq = bs % a.seq_q, b = bs / a.seq_q;
@@ -1761,13 +1852,17 @@ int mla_decode(FGV_MLA_PARAMS, void* workspace, int64_t workspace_bytes, void* s
         return launch_status();
     }
     // one round: items in runs per XCD while each has a CU to itself, paired
-    // long with short once two share one
+    // long with short once two share one; three or four rounds: longest
+    // first in windows; more rounds: in order
     const int64_t cus = cu_count();
     if (items > cus && items <= 2 * cus) {
         a.pair_cus = (int32_t)cus;
         hipLaunchKernelGGL(sparse_mla_decode_kernel<kItemsPaired>, dim3((unsigned)items), dim3(kThreads), 0, st, a);
     } else if (items <= cus) {
         hipLaunchKernelGGL(sparse_mla_decode_kernel<kItemsInRuns>, dim3((unsigned)items), dim3(kThreads), 0, st, a);
+    } else if (items <= 4 * cus) {
+        hipLaunchKernelGGL(sparse_mla_decode_kernel<kItemsLongestFirst>, dim3((unsigned)items), dim3(kThreads), 0,
+                           st, a);
     } else {
         hipLaunchKernelGGL(sparse_mla_decode_kernel<kItemsInOrder>, dim3((unsigned)items), dim3(kThreads), 0, st, a);
     }

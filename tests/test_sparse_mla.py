@@ -934,20 +934,16 @@ def _paired_order_case(name):
     raise KeyError(name)
 
 
-@pytest.mark.gpu
-@pytest.mark.parametrize("case", ["partial", "h128_sq2", "no_lengths", "extra_fp8", "extra_expanded"])
-def test_gpu_paired_order_against_oracle(case):
-    """The paired order against the oracle, and bit for bit against the same
-    rows computed in calls of at most C items (which keep each item on its
-    own workgroup's index order)."""
-    print(f"\n[case] sparse MLA one-item grid, paired order, {case}", flush=True)
-    w = _paired_order_case(case)
+def _check_item_order(w, case, ws, rounds):
+    """The call against the oracle, and bit for bit against the same rows
+    computed in calls of at most C items (C = CUs), which keep each item on
+    the workgroup of its own index; `rounds` bounds items / C."""
     B, SQ, HQ, _ = w.q.shape
     items = B * SQ * (HQ // 64)
     cus = torch.cuda.get_device_properties(0).multi_processor_count
-    assert cus < items <= 2 * cus, "the case must take the paired order"
+    lo, hi = rounds
+    assert lo * cus < items <= hi * cus, "the case must take the order under test"
     assert _grid(w) == 0
-    ws = case != "extra_fp8"
     out, lse, nbytes = _gpu_raw(w, workspace=ws)
     if case == "extra_expanded":
         assert nbytes > 0, "the extra cache must be expanded"
@@ -963,3 +959,42 @@ def test_gpu_paired_order_against_oracle(case):
         o_part, l_part, _ = _gpu_raw(_rows_of(w, rows), workspace=ws)
         assert torch.equal(out[rows].view(torch.int16), o_part.view(torch.int16)), f"rows from {r0}"
         assert torch.equal(lse[rows], l_part), f"rows from {r0}"
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", ["partial", "h128_sq2", "no_lengths", "extra_fp8", "extra_expanded"])
+def test_gpu_paired_order_against_oracle(case):
+    """One-item grids of C < items <= 2C: long items paired with short ones."""
+    print(f"\n[case] sparse MLA one-item grid, paired order, {case}", flush=True)
+    _check_item_order(_paired_order_case(case), case, case != "extra_fp8", (1, 2))
+
+
+def _longest_first_case(name):
+    """One-item grids of 2C < items <= 4C: each window of 256 workgroups takes
+    its own items longest first."""
+    if name == "partial":     # 600 items: two whole windows and one of 88
+        w = W.make_mla_workload(batch=600, topk=128, num_pages=32, seed=81, q_scale=0.1)
+        w.topk_length = _lengths(600, 128, 8)
+        w.topk_length[::9] = 0
+        w.topk_length[[5, 300, 599]] = torch.tensor([-1, 5000, 129], dtype=torch.int32)  # clamped
+        return w
+    if name == "h128":        # 300 rows x 2 head blocks = 600 items
+        w = W.make_mla_workload(batch=300, topk=64, num_pages=16, heads=128, seed=83, q_scale=0.1)
+        w.topk_length = _lengths(300, 64, 9)
+        return w
+    if name == "no_lengths":  # 513 items, every list full: equal keys
+        return W.make_mla_workload(batch=513, topk=64, num_pages=8, topk_length=False, seed=85, q_scale=0.1)
+    if name in ("extra_fp8", "extra_expanded"):  # 700 items; extra chunks weigh 2 or 1
+        w = W.make_mla_workload(batch=700, topk=64, num_pages=16, extra_topk=128, extra_page=64,
+                                extra_pages=8, seed=87, q_scale=0.1)
+        w.extra_topk_length = _lengths(700, 128, 10)
+        w.extra_topk_length[::7] = 0
+        return w
+    raise KeyError(name)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", ["partial", "h128", "no_lengths", "extra_fp8", "extra_expanded"])
+def test_gpu_longest_first_order_against_oracle(case):
+    print(f"\n[case] sparse MLA one-item grid, longest first, {case}", flush=True)
+    _check_item_order(_longest_first_case(case), case, case != "extra_fp8", (2, 4))
