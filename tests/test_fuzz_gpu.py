@@ -260,6 +260,45 @@ def test_fuzz_sparse_mla(case):
         assert torch.equal(lse_w, lse_n)
 
 
+@pytest.mark.parametrize("case", range(12))
+def test_fuzz_sparse_mla_item_order(case):
+    """One-item grids of random size around the CU count C (runs order up to C,
+    paired order up to 2C, longest first up to 4C, in order beyond): the call
+    equals, bit for bit, the same rows computed in calls of at most C items,
+    each of which keeps every item on the workgroup of its own index."""
+    from .test_sparse_mla import _gpu_raw, _grid, _rows_of
+
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    g = torch.Generator().manual_seed(6500 + case)
+    heads = _pick(g, [64, 64, 128])
+    seq_q = _pick(g, [1, 1, 2])
+    per_row = seq_q * heads // 64
+    lo, hi = [(cus // 2, cus), (cus + 1, 2 * cus), (2 * cus + 1, 4 * cus), (4 * cus + 1, 5 * cus)][case % 4]
+    items = _rand(g, lo, hi)
+    batch = (items + per_row - 1) // per_row  # C is a multiple of per_row: the count stays in its range
+    topk = _pick(g, [32, 64, 96])
+    extra = _pick(g, [False, True])
+    ws = _pick(g, [False, True])
+    _say(f"fuzz MLA item order {case}: items={batch * per_row} (C={cus}) B={batch} H={heads} SQ={seq_q} "
+         f"topk={topk} extra={extra} workspace={ws}")
+    w = W.make_mla_workload(batch=batch, topk=topk, num_pages=8, heads=heads, seq_q=seq_q,
+                            extra_topk=64 if extra else 0, extra_page=64, extra_pages=4,
+                            seed=7500 + case, q_scale=0.1)
+    lens = torch.randint(-2, topk + 3, (batch,), generator=g, dtype=torch.int32)  # clamped at both ends
+    lens[torch.rand(batch, generator=g) < 0.1] = 0
+    w.topk_length = lens
+    if extra:
+        w.extra_topk_length = torch.randint(0, 65, (batch,), generator=g, dtype=torch.int32)
+    assert _grid(w) == 0
+    out, lse, _ = _gpu_raw(w, workspace=ws)
+    step = max(1, cus // per_row)
+    for r0 in range(0, batch, step):
+        rows = torch.arange(r0, min(batch, r0 + step))
+        o_part, l_part, _ = _gpu_raw(_rows_of(w, rows), workspace=ws)
+        assert torch.equal(out[rows].view(torch.int16), o_part.view(torch.int16)), f"rows from {r0}"
+        assert torch.equal(lse[rows], l_part), f"rows from {r0}"
+
+
 # ---------------------------------------------------------------- rmsnorm ----
 
 @pytest.mark.parametrize("case", CASES)
