@@ -39,6 +39,12 @@
 // not attended (past the top-k length, negative, or past the cache) are
 // gathered from a zero page, and their scores masked to -inf.
 //
+// Which workgroup takes which item depends on the grid (C = CUs): up to C
+// workgroups, items in runs per XCD; up to 2C (workgroups j and C + j share
+// a CU), each window of 32 pairs ranks its items by list cost and pairs long
+// with short; up to 4C, windows of 256 take their items longest first.  No
+// result bit depends on the order: every item is computed the same way.
+//
 // The sparse prefill over bf16 rows (flash_mla_sparse_fwd,
 // sparse_mla_prefill_kernel near the end of the kernels) reuses the attend
 // routine and the row DMAs: its rows need no dequantisation, d_qk may be 576
