@@ -720,10 +720,23 @@ enum ItemOrder { kItemsInOrder = 0, kItemsInRuns = 1, kItemsPaired = 2, kItemsLo
 
 // An item's list lengths (n0, n1) and its rank key: 2 per FP8 chunk, 1 per
 // expanded chunk, plus 1 (8 bits; 0 is left for a slot with no item).
+// (list_len's lengths, with both loads in flight before either is used, and
+// no division when each batch row is one item)
 __device__ __forceinline__ uint32_t item_key(const MlaArgs& a, uint32_t item, int& n0, int& n1) {
-    const int row = (int)(item / (uint32_t)a.head_blocks / (uint32_t)a.seq_q);
-    n0 = list_len(a.list[0], true, row);
-    n1 = list_len(a.list[1], a.num_lists > 1, row);
+    const uint32_t per_row = (uint32_t)(a.head_blocks * a.seq_q);
+    int row = (int)item;
+    if (per_row != 1)
+        row = (int)(item / per_row);
+    const int32_t* p0 = a.list[0].lengths;
+    const int32_t* p1 = a.num_lists > 1 ? a.list[1].lengths : nullptr;
+    int r0 = 0, r1 = 0;
+    if (p0)
+        r0 = p0[row];
+    if (p1)
+        r1 = p1[row];
+    const int t0 = a.list[0].topk, t1 = a.list[1].topk;
+    n0 = p0 ? (r0 < 0 ? 0 : (r0 > t0 ? t0 : r0)) : t0;
+    n1 = a.num_lists > 1 ? (p1 ? (r1 < 0 ? 0 : (r1 > t1 ? t1 : r1)) : t1) : 0;
     const int c0 = (n0 + kChunk - 1) / kChunk, c1 = (n1 + kChunk - 1) / kChunk;
     const int cost = 2 * c0 + (a.list[1].expanded ? c1 : 2 * c1);
     return (uint32_t)min(cost, 254) + 1;
@@ -872,9 +885,16 @@ sparse_mla_decode_kernel(MlaArgs a) {
         item = paired_item(a, blockIdx.x, lane, len0, len1);
     else if (kOrder == kItemsLongestFirst)
         item = longest_first_item(a, blockIdx.x, wave, lane, lds_kbuf + kChunk * kKRowBytes - 512, len0, len1);
-    const int hb = item % a.head_blocks;
-    const int bs = item / a.head_blocks;
-    const int sq = bs % a.seq_q, b = bs / a.seq_q;
+    int hb = 0, bs = (int)item;  // (no division for one head block or one query position)
+    if (a.head_blocks != 1) {
+        hb = item % a.head_blocks;
+        bs = item / a.head_blocks;
+    }
+    int sq = 0, b = bs;
+    if (a.seq_q != 1) {
+        sq = bs % a.seq_q;
+        b = bs / a.seq_q;
+    }
     const ListView v0 = make_view(a.list[0], true, b, sq, len0);
     const ListView v1 = make_view(a.list[1], a.num_lists > 1, b, sq, len1);
     const int nchunks = (v0.len + kChunk - 1) / kChunk + (v1.len + kChunk - 1) / kChunk;
