@@ -1594,16 +1594,25 @@ sparse_mla_combine_kernel(MlaArgs a) {
 // Dequantises every entry of a list's cache into bf16 rows [num_entries][512]
 // (the expanded copy the chunk loop then DMAs without converting), with the
 // conversion the chunk loop uses (scale byte 0 included), so either route
-// gives the same K rows.  Each 32-lane half of a wave does kExpandPerHalf
-// entries, all loads first (the kernel is short, and latency-bound with fewer
-// bytes in flight); lane k makes output blocks k and k + 32, so each store
-// instruction writes two whole 512-byte halves: blocks below 56 from 8 code
-// bytes and their scale byte, blocks 56..63 from 16 RoPE bytes.
-constexpr int kExpandPerHalf = 2;
-constexpr int kExpandPerBlock = kThreads / 32 * kExpandPerHalf;
+// gives the same K rows.  Each 32-lane half of a wave does kPerHalf entries,
+// all loads first (the kernel is short, and latency-bound with fewer bytes in
+// flight); lane k makes output blocks k and k + 32, so each store instruction
+// writes two whole 512-byte halves: blocks below 56 from 8 code bytes and
+// their scale byte, blocks 56..63 from 16 RoPE bytes.  Four entries per half
+// while that leaves at least kExpandWideMinBlocks workgroups, else two: same
+// bits; same-box A/B, extra512 (32768 entries) 51.35 -> 50.87 us per call
+// on one input set and 53.86 -> 52.43 us over four, eight per half 52.21 /
+// 54.38 us; extra8192 (1024 entries) 296.8 against 297.9 us with four.
+constexpr int kExpandWideMinBlocks = 256;
 
+template <int kPerHalf>
+constexpr int expand_per_block() { return kThreads / 32 * kPerHalf; }
+
+template <int kPerHalf>
 __global__ void __launch_bounds__(kThreads)
 mla_expand_cache_kernel(CacheList L, uint8_t* out) {
+    constexpr int kExpandPerHalf = kPerHalf;
+    constexpr int kExpandPerBlock = expand_per_block<kPerHalf>();
     const int k = threadIdx.x & 31, k2 = k + 32;
     const int64_t e0 = (int64_t)blockIdx.x * kExpandPerBlock + (threadIdx.x >> 5) * kExpandPerHalf;
     uint2 c0[kExpandPerHalf];
@@ -1852,10 +1861,14 @@ int mla_decode(FGV_MLA_PARAMS, void* workspace, int64_t workspace_bytes, void* s
     uint8_t* ws = static_cast<uint8_t*>(workspace);
     if (use_expand) {
         a.list[1].expanded = ws;
-        const int64_t per_block = kExpandPerBlock;
-        hipLaunchKernelGGL(mla_expand_cache_kernel,
-                           dim3((unsigned)((a.list[1].num_entries + per_block - 1) / per_block)), dim3(kThreads), 0,
-                           st, a.list[1], ws);
+        const int64_t entries = a.list[1].num_entries;
+        constexpr int64_t wide = expand_per_block<4>(), narrow = expand_per_block<2>();
+        if (entries >= kExpandWideMinBlocks * wide)
+            hipLaunchKernelGGL(mla_expand_cache_kernel<4>, dim3((unsigned)((entries + wide - 1) / wide)),
+                               dim3(kThreads), 0, st, a.list[1], ws);
+        else
+            hipLaunchKernelGGL(mla_expand_cache_kernel<2>, dim3((unsigned)((entries + narrow - 1) / narrow)),
+                               dim3(kThreads), 0, st, a.list[1], ws);
         rc = launch_status();
         if (rc)
             return rc;

@@ -594,6 +594,25 @@ def test_gpu_expanded_copy_every_scale_byte():
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("pages", [4095, 4096, 4097])
+def test_gpu_expanded_copy_sizes(pages):
+    """The expanded copy around 8192 entries, where its workgroups go from two
+    entries per half-wave to four (pages of 2: 8190, 8192 and 8194 entries, the
+    last with a partial workgroup): every row equals the oracle's bit for bit."""
+    print(f"\n[case] sparse MLA expanded copy, {2 * pages} entries", flush=True)
+    w = W.make_mla_workload(batch=16, topk=64, num_pages=2, extra_topk=4200, extra_page=2, extra_pages=pages,
+                            sink=False, seed=91, q_scale=0.1)
+    entries = 2 * pages
+    # 16 rows x 4200 extra entries gather the cache more than 8 times per entry: expanded
+    _, _, nbytes, ws = _gpu_raw(w, workspace=True, keep_ws=True)
+    assert nbytes >= entries * 1024
+    rows = ws[:entries * 1024].cpu().view(torch.int16).view(entries, 512)
+    bad = [e for e in range(entries)
+           if not torch.equal(rows[e], oracle.model1_token_row(w.extra_k_cache, e).view(torch.int16))]
+    assert not bad, f"expanded rows that differ from the oracle's: {bad[:16]}"
+
+
+@pytest.mark.gpu
 def test_gpu_bench_case_against_oracle():
     """The benchmark's decode case at full size (batch 512, top-k 128 over 512
     pages, sink, top-k lengths)."""
