@@ -709,11 +709,13 @@ constexpr uint32_t kItemRun = 16;
 // i-th longest on j, which is dispatched first, and the i-th shortest on
 // C + j.  Workgroups j >= P have no partner and keep their own item.  The
 // cost counts 2 per FP8 chunk and 1 per expanded chunk (their measured
-// per-chunk times are 3.0-3.6 and 1.6-1.8 us).  Same bits; same-box A/B,
-// medians of 7 graph replays of 20 calls: decode 22.55 -> 20.14 us, extra512
-// (with its expand kernel) 61.8 -> 54.2 us.  A global ranking over all items
-// measured 19.6 / 53.5 us, long items on j first; short items on j instead
-// lost 1.3 / 2.5 us of that.
+// per-chunk times are 3.0-3.6 and 1.6-1.8 us).  Same bits; same-box A/B
+// against items in runs, medians of 9 graph replays of 48 calls: decode
+// 20.63 -> 18.98 us, extra512 (with its expand kernel) 57.91 -> 52.09 us.
+// Orders computed on the host and read from memory (another run): the same
+// windows 20.14 / 54.2 us, a global ranking 19.56 / 53.5 us, and the global
+// ranking with the short items on j 20.83 / 56.0 us, against 22.55 / 61.8 us
+// in runs.
 constexpr uint32_t kPairWindow = 32;
 
 enum ItemOrder { kItemsInOrder = 0, kItemsInRuns = 1, kItemsPaired = 2, kItemsLongestFirst = 3 };
