@@ -44,6 +44,10 @@ def parse_args():
     ap.add_argument("--fp4", action="store_true", help="indexer, mqa_logits, paged_mqa_logits: MXFP4 q instead of FP8")
     ap.add_argument("--mla-case", choices=["decode", "extra512", "extra8192"], default="decode",
                     help="mla: the reference benchmark's MODEL1 sparse-decode case")
+    ap.add_argument("--mla-batch", type=int, default=0,
+                    help="mla: batch rows instead of the case's 512 (the case's other sizes kept)")
+    ap.add_argument("--mla-heads", type=int, default=0, choices=[0, 64, 128],
+                    help="mla: query heads instead of the case's 64")
     ap.add_argument("--indexer-case", choices=["0", "1", "2", "3", "large"], default="3",
                     help="indexer_k / indexer_k_gather: the reference benchmark's shape 0..3 (default its "
                          "largest) or 'large' (65536 tokens, head_dim 512)")
@@ -578,7 +582,12 @@ def main():
                                     f"the reference test's per-request loop)")
     elif args.op == "mla":
         # the reference benchmark's MODEL1 sparse decode (batch 512, 64 heads, top-k 128)
-        w_cpu = W.make_mla_case(args.mla_case)
+        mla_kw = dict(W.MLA_CASES[args.mla_case])
+        if args.mla_batch:
+            mla_kw["batch"] = args.mla_batch
+        if args.mla_heads:
+            mla_kw["heads"] = args.mla_heads
+        w_cpu = W.make_mla_workload(seed=0, name=args.mla_case, q_scale=0.1, **mla_kw)
         w = w_cpu.to(dev)
         B, SQ, HQ = w.q.shape[:3]
         T = B * SQ
@@ -604,8 +613,14 @@ def main():
                                                                                   etopk, 0)
         kernel = {0: "sparse_mla_decode_kernel", 1: "sparse_mla_decode_split_kernel",
                   2: "sparse_mla_decode_pair_kernel"}[grid]
-        workload = f"mla_{args.mla_case}"
+        workload = (f"mla_{args.mla_case}" + (f"_b{B}" if args.mla_batch else "")
+                    + (f"_h{HQ}" if args.mla_heads else ""))
         case = W.MLA_CASES[args.mla_case]
+        cus = torch.cuda.get_device_properties(dev).multi_processor_count
+        items = B * SQ * (HQ // 64)
+        order = ("items in runs per XCD" if items <= cus else
+                 "long items paired with short on shared CUs" if items <= 2 * cus else
+                 "longest first in windows of 256" if items <= 4 * cus else "items in order")
         config = {"workload": f"flash_mla_with_kvcache sparse MODEL1 decode '{args.mla_case}': "
                               f"batch {B}, seq_q {SQ}, {HQ} heads, top-k {case['topk']} over "
                               f"{case['num_pages']} pages of 64 x 584 B, top-k lengths, attention sink"
@@ -613,7 +628,7 @@ def main():
                                  f"of {case['extra_page']}" if "extra_topk" in case else ""),
                   "batch": B, "seq_q": SQ, "num_heads": HQ, "attended_entries": w_cpu.used_tokens(),
                   "flops_per_call": flops_call,
-                  "schedule": {0: "one workgroup per (row, 64-head block)",
+                  "schedule": {0: f"one workgroup per (row, 64-head block): {items} items on {cus} CUs, {order}",
                                1: "balanced split grid + combine kernel",
                                2: "paired grid: one 8-wave workgroup per CU, both halves on each item, "
                                   "a short item after a long one"}[grid]
