@@ -117,8 +117,9 @@ struct MlaArgs {
     int32_t* row_prefix;   // batch + 1 prefix sums of per-item chunk counts
     int32_t split_grid;
     // one-item kernel in the paired order: the CU count C (workgroups j and
-    // C + j share a CU)
+    // C + j share a CU) and the number of windows
     int32_t pair_cus;
+    int32_t order_windows;
 };
 
 // K tile addressing: 16-byte block b of row r at r * kKRowBytes + 16 b, rows
@@ -701,22 +702,43 @@ constexpr uint32_t kItemRun = 16;
 // Paired order, for grids of C < G <= 2C workgroups (C = CUs).  Workgroups j
 // and C + j share a CU: the dispatcher gives every CU one workgroup, then a
 // second in the same order (read from HW_ID / XCC_ID on gfx950: pairs
-// {j, C + j} in every launch, 256 CUs).  Both run to the end of the longer
-// item, so a CU that holds two long items sets the kernel's time while others
-// idle.  The P = G - C pairs are taken in windows of kPairWindow: the window's
-// 2 kPairWindow own items (j and C + j of each of its pairs) are ranked by
-// cost, longest first (ties by position), and the window's pair i takes the
-// i-th longest on j, which is dispatched first, and the i-th shortest on
-// C + j.  Workgroups j >= P have no partner and keep their own item.  The
-// cost counts 2 per FP8 chunk and 1 per expanded chunk (their measured
-// per-chunk times are 3.0-3.6 and 1.6-1.8 us).  Same bits; same-box A/B
-// against items in runs, medians of 9 graph replays of 48 calls: decode
-// 20.63 -> 18.98 us, extra512 (with its expand kernel) 57.91 -> 52.09 us.
-// Orders computed on the host and read from memory (another run): the same
-// windows 20.14 / 54.2 us, a global ranking 19.56 / 53.5 us, and the global
-// ranking with the short items on j 20.83 / 56.0 us, against 22.55 / 61.8 us
-// in runs.
-constexpr uint32_t kPairWindow = 32;
+// {j, C + j} in every launch, 256 CUs).  A CU runs to the end of its longer
+// item, and a survivor's chunks run almost twice as fast once its partner has
+// left; so the P = G - C shared CUs should hold a long item beside a short one,
+// and the S = C - P workgroups alone on their CU (j in [P, C)) the longest
+// items.  With at least one unpartnered workgroup per two pairs (2 S >= P),
+// the grid is cut into the fewest windows W whose largest fits a wave's 64
+// lanes: window w holds pairs [P w / W, P (w + 1) / W) (both items of each)
+// and unpartnered workgroups [S w / W, S (w + 1) / W), with their own items,
+// so each window mixes the two in proportion.  Its items are ranked by cost,
+// longest first (ties by position): the unpartnered workgroups take the
+// longest, and pair i of the rest takes the i-th longest on j, which is
+// dispatched first, and the i-th shortest on C + j.  With fewer unpartnered
+// workgroups, windows hold kPairWindow pairs only (no division to place a
+// workgroup) and an unpartnered workgroup keeps its own item.  The cost
+// counts 2 per FP8 chunk and 1 per expanded chunk (their measured per-chunk
+// times are 3.0-3.6 and 1.6-1.8 us).
+//   Measured (same bits; same-box A/Bs, graph replays): against items in runs,
+// windows of 32 pairs took decode 20.63 -> 18.98 us and extra512 (with its
+// expand kernel) 57.91 -> 52.09 us.  Orders computed on the host and read from
+// memory: the unpartnered workgroups on the longest items, pairs folding the
+// rest, took decode at batch 272 / 300 / 384 from 17.38 / 17.92 / 18.03 us
+// (windows of pairs only) to 14.72 / 14.79 / 15.93 us with these windows and
+// 14.67 / 14.69 / 15.75 us globally ranked; at batch 512 (no unpartnered
+// workgroups) 18.64 against 18.59 us.  A global ranking in the kernel costs
+// about 1 us more than a window's.
+constexpr uint32_t kPairWindow = 32;  // pairs a window when few workgroups are unpartnered
+
+// floor(n / d) for n, d < 2^20, d > 0: the float estimate n * (1/d) is within
+// one of the quotient, and one comparison each way makes it exact.
+__device__ __forceinline__ uint32_t small_div(uint32_t n, uint32_t d) {
+    uint32_t q = (uint32_t)((float)n * __builtin_amdgcn_rcpf((float)d));
+    if (q * d > n)
+        --q;
+    else if ((q + 1) * d <= n)
+        ++q;
+    return q;
+}
 
 enum ItemOrder { kItemsInOrder = 0, kItemsInRuns = 1, kItemsPaired = 2, kItemsLongestFirst = 3 };
 
@@ -745,22 +767,40 @@ __device__ __forceinline__ uint32_t item_key(const MlaArgs& a, uint32_t item, in
 }
 
 // The item workgroup blk takes in the paired order, and that item's two list
-// lengths (len0, len1; left at -1 for a workgroup without a partner).  Every
-// wave computes the same answer from one length load per lane: lane l < 32
-// holds pair w0 + l's first item, lane 32 + l its second; lanes past the
-// window's end rank last.
+// lengths (left at -1 for an unpartnered workgroup that keeps its own item).
+// Every wave computes the same answer from one length load per lane: lanes
+// [0, np) hold the window's pairs' first items, [np, 2 np) their second,
+// [2 np, 2 np + ns) the unpartnered workgroups' own; the rest rank last.
 __device__ __forceinline__ uint32_t paired_item(const MlaArgs& a, uint32_t blk, int lane, int& len0, int& len1) {
-    const uint32_t cus = (uint32_t)a.pair_cus;
-    const uint32_t pairs = gridDim.x - cus;
-    const bool second = blk >= cus;
-    const uint32_t j = second ? blk - cus : blk;
-    if (j >= pairs)
-        return blk;
-    const uint32_t w0 = j / kPairWindow * kPairWindow;
-    const uint32_t m = min(kPairWindow, pairs - w0);
-    const uint32_t l32 = (uint32_t)lane & (kPairWindow - 1);
-    const bool valid = l32 < m;
-    const uint32_t it = valid ? (lane < (int)kPairWindow ? w0 + l32 : cus + w0 + l32) : w0;
+    const uint32_t G = gridDim.x, cus = (uint32_t)a.pair_cus, P = G - cus, S = cus - P;
+    const uint32_t W = (uint32_t)a.order_windows;
+    // this workgroup's place: pair j (first or second) or unpartnered u
+    const bool first = blk < P, alone = !first && blk < cus;
+    const uint32_t j = first ? blk : blk - cus, u = blk - P;
+    const uint32_t l = (uint32_t)lane;
+    uint32_t it, want;
+    bool valid;
+    if (W == 0) {
+        // pairs only, in windows of kPairWindow pairs (shifts, no division);
+        // an unpartnered workgroup keeps its own item
+        if (alone)
+            return blk;
+        const uint32_t w0 = j / kPairWindow * kPairWindow, m = min(kPairWindow, P - w0);
+        const uint32_t l32 = l & (kPairWindow - 1);
+        valid = l32 < m;
+        it = valid ? (l < kPairWindow ? w0 + l32 : cus + w0 + l32) : w0;
+        want = first ? j - w0 : 2 * m - 1 - (j - w0);
+    } else {
+        // its window: the largest w whose range starts at or before its index
+        // (S > 0 whenever a workgroup is alone; P > 0 always)
+        const uint32_t w = alone ? small_div((u + 1) * W - 1, S ? S : 1u) : small_div((j + 1) * W - 1, P);
+        const uint32_t p_lo = small_div(P * w, W), np = small_div(P * (w + 1), W) - p_lo;
+        const uint32_t s_lo = small_div(S * w, W), ns = small_div(S * (w + 1), W) - s_lo;
+        valid = l < 2 * np + ns;
+        it = l < np ? p_lo + l : l < 2 * np ? cus + p_lo + (l - np) : valid ? P + s_lo + (l - 2 * np) : blk;
+        // unpartnered: ranks [0, ns); pairs: first ns + i, second ns + 2 np - 1 - i
+        want = alone ? u - s_lo : first ? ns + (j - p_lo) : ns + 2 * np - 1 - (j - p_lo);
+    }
     int n0, n1;
     const uint32_t k = item_key(a, it, n0, n1);
     const uint32_t key = valid ? k : 0;  // 0 ranks last
@@ -783,8 +823,7 @@ __device__ __forceinline__ uint32_t paired_item(const MlaArgs& a, uint32_t blk, 
         }
     }
     const uint32_t rank = above + __builtin_popcountll(eq & ((1ull << lane) - 1));
-    const uint32_t want = second ? 2 * m - 1 - (j - w0) : j - w0;
-    // ranks are a permutation of 0..63 and the window's items take 0..2m-1
+    // ranks are a permutation of 0..63 and the window's valid items take the first ones
     const uint64_t hit = __builtin_amdgcn_ballot_w64(rank == want);
     const int src = hit ? (int)__builtin_ctzll(hit) : 0;
     len0 = __builtin_amdgcn_readlane(n0, src);
@@ -1847,6 +1886,7 @@ int mla_decode(FGV_MLA_PARAMS, void* workspace, int64_t workspace_bytes, void* s
     a.row_prefix = nullptr;
     a.split_grid = 0;
     a.pair_cus = 0;
+    a.order_windows = 0;
     const int64_t items = batch * seq_q * a.head_blocks;
     hipStream_t st = static_cast<hipStream_t>(stream);
     // Workspace: [expanded extra cache][split slots][row prefix sums].  A
@@ -1898,6 +1938,17 @@ int mla_decode(FGV_MLA_PARAMS, void* workspace, int64_t workspace_bytes, void* s
     const int64_t cus = cu_count();
     if (items > cus && items <= 2 * cus) {
         a.pair_cus = (int32_t)cus;
+        // with at least one unpartnered workgroup per two pairs, the fewest
+        // windows whose largest (2 ceil(P / W) + ceil(S / W) items) fits a
+        // wave; else pairs only (0)
+        const int64_t pairs = items - cus, alone = cus - pairs;
+        int64_t windows = 0;
+        if (2 * alone >= pairs) {
+            windows = 1;
+            while (2 * ((pairs + windows - 1) / windows) + (alone + windows - 1) / windows > 64)
+                ++windows;
+        }
+        a.order_windows = (int32_t)windows;
         hipLaunchKernelGGL(sparse_mla_decode_kernel<kItemsPaired>, dim3((unsigned)items), dim3(kThreads), 0, st, a);
     } else if (items <= cus) {
         hipLaunchKernelGGL(sparse_mla_decode_kernel<kItemsInRuns>, dim3((unsigned)items), dim3(kThreads), 0, st, a);
