@@ -740,7 +740,7 @@ __device__ __forceinline__ uint32_t small_div(uint32_t n, uint32_t d) {
     return q;
 }
 
-enum ItemOrder { kItemsInOrder = 0, kItemsInRuns = 1, kItemsPaired = 2, kItemsLongestFirst = 3 };
+enum ItemOrder { kItemsInOrder = 0, kItemsInRuns = 1, kItemsPaired = 2, kItemsLongestFirst = 3, kItemsPairedMixed = 4 };
 
 // An item's list lengths (n0, n1) and its rank key: 2 per FP8 chunk, 1 per
 // expanded chunk, plus 1 (8 bits; 0 is left for a slot with no item).
@@ -771,6 +771,7 @@ __device__ __forceinline__ uint32_t item_key(const MlaArgs& a, uint32_t item, in
 // Every wave computes the same answer from one length load per lane: lanes
 // [0, np) hold the window's pairs' first items, [np, 2 np) their second,
 // [2 np, 2 np + ns) the unpartnered workgroups' own; the rest rank last.
+template <bool kMixed>
 __device__ __forceinline__ uint32_t paired_item(const MlaArgs& a, uint32_t blk, int lane, int& len0, int& len1) {
     const uint32_t G = gridDim.x, cus = (uint32_t)a.pair_cus, P = G - cus, S = cus - P;
     const uint32_t W = (uint32_t)a.order_windows;
@@ -780,7 +781,7 @@ __device__ __forceinline__ uint32_t paired_item(const MlaArgs& a, uint32_t blk, 
     const uint32_t l = (uint32_t)lane;
     uint32_t it, want;
     bool valid;
-    if (W == 0) {
+    if (!kMixed) {
         // pairs only, in windows of kPairWindow pairs (shifts, no division);
         // an unpartnered workgroup keeps its own item
         if (alone)
@@ -923,7 +924,9 @@ sparse_mla_decode_kernel(MlaArgs a) {
     if (kOrder == kItemsInRuns && item < gridDim.x / (8 * kItemRun) * (8 * kItemRun))
         item = item / (8 * kItemRun) * (8 * kItemRun) + (item % 8) * kItemRun + (item / 8) % kItemRun;
     else if (kOrder == kItemsPaired)
-        item = paired_item(a, blockIdx.x, lane, len0, len1);
+        item = paired_item<false>(a, blockIdx.x, lane, len0, len1);
+    else if (kOrder == kItemsPairedMixed)
+        item = paired_item<true>(a, blockIdx.x, lane, len0, len1);
     else if (kOrder == kItemsLongestFirst)
         item = longest_first_item(a, blockIdx.x, wave, lane, lds_kbuf + kChunk * kKRowBytes - 512, len0, len1);
     int hb = 0, bs = (int)item;  // (no division for one head block or one query position)
@@ -1949,7 +1952,11 @@ int mla_decode(FGV_MLA_PARAMS, void* workspace, int64_t workspace_bytes, void* s
                 ++windows;
         }
         a.order_windows = (int32_t)windows;
-        hipLaunchKernelGGL(sparse_mla_decode_kernel<kItemsPaired>, dim3((unsigned)items), dim3(kThreads), 0, st, a);
+        if (windows)
+            hipLaunchKernelGGL(sparse_mla_decode_kernel<kItemsPairedMixed>, dim3((unsigned)items), dim3(kThreads), 0,
+                               st, a);
+        else
+            hipLaunchKernelGGL(sparse_mla_decode_kernel<kItemsPaired>, dim3((unsigned)items), dim3(kThreads), 0, st, a);
     } else if (items <= cus) {
         hipLaunchKernelGGL(sparse_mla_decode_kernel<kItemsInRuns>, dim3((unsigned)items), dim3(kThreads), 0, st, a);
     } else if (items <= 4 * cus) {
