@@ -41,9 +41,10 @@
 //
 // Which workgroup takes which item depends on the grid (C = CUs): up to C
 // workgroups, items in runs per XCD; up to 2C (workgroups j and C + j share
-// a CU), each window of 32 pairs ranks its items by list cost and pairs long
-// with short; up to 4C, windows of 256 take their items longest first.  No
-// result bit depends on the order: every item is computed the same way.
+// a CU), windows rank their items by list cost, pair long with short, and
+// give the workgroups alone on their CU the longest; up to 4C, windows of 256
+// take their items longest first.  No result bit depends on the order: every
+// item is computed the same way.
 //
 // The sparse prefill over bf16 rows (flash_mla_sparse_fwd,
 // sparse_mla_prefill_kernel near the end of the kernels) reuses the attend
