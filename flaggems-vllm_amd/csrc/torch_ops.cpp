@@ -167,20 +167,25 @@ int inv_rope_fp8_quant(const at::Tensor& o, const at::Tensor& positions_in, cons
     const int64_t tpad = (num_tokens + 3) / 4 * 4;
     const int64_t scale_inner = tma_aligned_scales ? (num_scale_blocks + 3) / 4 : num_scale_blocks;
     const auto opts = o.options();
-    at::Tensor fp8 = at::empty({n_groups, num_tokens, d}, opts.dtype(at::kFloat8_e4m3fn));
+    // both outputs allocated straight in the returned layouts (no transposed
+    // views to make): codes [T, G, d] over storage [G][T][d]; scales
+    // [T, G, K] over storage [G][K][Tpad] (all Tpad columns: the kernel writes
+    // the padding tokens' zero scales)
+    at::Tensor fp8 = at::empty_strided({num_tokens, n_groups, d}, {d, num_tokens * d, 1},
+                                       opts.dtype(at::kFloat8_e4m3fn));
     at::Tensor scale = at::empty({n_groups * scale_inner * tpad}, opts.dtype(tma_aligned_scales ? at::kInt : at::kFloat))
-                           .as_strided({n_groups, num_tokens, scale_inner}, {scale_inner * tpad, 1, tpad});
+                           .as_strided({num_tokens, n_groups, scale_inner}, {1, scale_inner * tpad, tpad});
     int rc = 0;
     if (tpad > 0) {
         const c10::DeviceGuard guard(dev);
         rc = fgv_inv_rope_fp8_quant(o.data_ptr(), o.stride(0), o.stride(1), positions.data_ptr<int64_t>(),
                                     cos_sin_cache.data_ptr<float>(), cos_sin_cache.stride(0), cos_sin_cache.size(0),
                                     num_tokens, n_groups, heads_per_group, nope_dim, rope_dim, quant_group_size,
-                                    fp8.data_ptr(), fp8.stride(0),
-                                    fp8.stride(1), scale.data_ptr(), scale.stride(0), scale.stride(2), tpad,
+                                    fp8.data_ptr(), fp8.stride(1),
+                                    fp8.stride(0), scale.data_ptr(), scale.stride(1), scale.stride(2), tpad,
                                     static_cast<float>(eps), tma_aligned_scales ? 1 : 0, current_stream(o));
     }
-    *out = SiblingOut(fp8.transpose(0, 1), scale.transpose(0, 1));
+    *out = SiblingOut(fp8, scale);
     return rc;
 }
 
