@@ -41,6 +41,9 @@ def parse_args():
                     default="main",
                     help="copy: torch device copy of 512 MiB, the HBM calibration kernel")
     ap.add_argument("--tma", action="store_true", help="inv_rope: packed UE8M0 scales")
+    ap.add_argument("--inv-shape", default="8192,64,8",
+                    help="inv_rope: num_tokens,num_heads,n_groups (the reference benchmark's shapes are 1,8,1 "
+                         "and 16,64,8, with --tma)")
     ap.add_argument("--fp4", action="store_true", help="indexer, mqa_logits, paged_mqa_logits: MXFP4 q instead of FP8")
     ap.add_argument("--mla-case", choices=["decode", "extra512", "extra8192"], default="decode",
                     help="mla: the reference benchmark's MODEL1 sparse-decode case")
@@ -852,7 +855,8 @@ def main():
         config = {"workload": "calibration: torch device copy, 512 MiB read + 512 MiB write"}
         args.no_cpu_baseline = True
     else:
-        w_cpu = W.make_inv_rope_workload(8192, 64, 8, seed=0)
+        T_inv, H_inv, G_inv = (int(x) for x in args.inv_shape.split(","))
+        w_cpu = W.make_inv_rope_workload(T_inv, H_inv, G_inv, seed=0)
         w = w_cpu.to(dev)
         T, H = w.o.shape[0], w.o.shape[1]
         bytes_call = W.inv_rope_bytes(T, H, args.tma)
@@ -864,10 +868,10 @@ def main():
                                                                   tma_aligned_scales=args.tma)
 
         kernel = "inv_rope_fp8_quant_kernel"
-        workload = "T8192_H64_G8" + ("_ue8m0" if args.tma else "_f32")
-        config = {"workload": f"fused_inv_rope_fp8_quant T={T}, H={H}, G=8, "
+        workload = f"T{T}_H{H}_G{G_inv}" + ("_ue8m0" if args.tma else "_f32")
+        config = {"workload": f"fused_inv_rope_fp8_quant T={T}, H={H}, G={G_inv}, "
                               f"{'packed UE8M0' if args.tma else 'fp32'} scales",
-                  "num_tokens": T, "num_heads": H, "n_groups": 8}
+                  "num_tokens": T, "num_heads": H, "n_groups": G_inv}
 
     n_sets = 1
     if args.op in ("main", "gather", "rmsnorm", "indexer", "mla", "inv_rope", "indexer_k", "indexer_k_gather",
