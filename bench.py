@@ -74,6 +74,9 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="repeat the CPU sample until this much CPU time is spent (min 3 runs)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--ref-shapes", action="store_true",
+                    help="with --op gather|rmsnorm|indexer|slot_mapping|inv_rope: time the op at every shape of "
+                         "the reference benchmark for it and print a table")
     ap.add_argument("--grid", action="store_true",
                     help="main op over the reference benchmark's grid (T x H); one JSON line per point "
                          "and a markdown table, instead of the single headline line")
@@ -375,6 +378,117 @@ def run_grid(args):
               f"| {r['gbps']:.0f} | {100 * r['frac_of_8tbps']:.1f} | {r['tokens_per_s']:.3g} |", flush=True)
 
 
+# The reference benchmarks' own shapes for the ops beside the main op
+# (benchmark/test_deepseek_v4_attention_dequantize_and_gather_k_cache.py:75-81,
+# benchmark/test_deepseek_v4_attention_fused_q_kv_rmsnorm.py:58-66,
+# benchmark/test_fused_indexer_q_rope_quant.py:139-143 with NUM_HEADS 8 (:24),
+# benchmark/test_slot_mapping_perf.py:35-50, benchmark/test_fused_inv_rope_fp8_quant.py:100).
+REF_SHAPES = {
+    "gather": [(1, 512, 128), (2, 1024, 256), (4, 2048, 512), (4, 2048, 2048), (8, 4096, 1024)],
+    "rmsnorm": [(1, 1536, 512), (32, 1536, 512), (128, 1536, 512), (512, 1536, 512), (2048, 1536, 512),
+                (32, 64 * 576, 576), (128, 64 * 576, 576)],
+    "indexer": [(1, 8, False), (32, 8, False), (32, 8, True)],
+    "slot_mapping": [(4, 8192, 128), (8, 8192, 128), (12, 8192, 128), (16, 8192, 128), (4, 8192, 16),
+                     (32, 8192, 128), (128, 8192, 128), (8, 8192, 16), (8, 16384, 128), (1, 8192, 128)],
+    "inv_rope": [(1, 8, 1, True), (16, 64, 8, True)],
+}
+
+
+def run_ref_shapes(args):
+    """Times one op at every shape of its reference benchmark, with inputs drawn
+    on the device as that benchmark draws them; rotating device copies for
+    small calls (mall_sets), graph-replay kernel time and the eager loop."""
+    import torch
+
+    import flaggems_vllm
+    from flaggems_vllm import testing as W
+
+    dev = torch.device("cuda:0")
+    op = args.op
+    if op not in REF_SHAPES:
+        raise SystemExit(f"--ref-shapes covers {', '.join(REF_SHAPES)}")
+    rows = []
+    for shape in REF_SHAPES[op]:
+        gen = torch.Generator(device=dev).manual_seed(hash(shape) & 0xFFFF)
+        if op == "gather":
+            batch, seq_len, gather_len = shape
+            nblk = batch * ((seq_len + 63) // 64)
+            desc = f"batch {batch}, seq_len {seq_len}, gather_len {gather_len}"
+            bytes_call = W.gather_bytes(batch * gather_len)
+
+            def make_step(i, batch=batch, seq_len=seq_len, gather_len=gather_len, nblk=nblk):
+                out = torch.empty(batch, gather_len, 512, dtype=torch.bfloat16, device=dev)
+                cache = torch.zeros(nblk, 64 * W.HEAD_BYTES, dtype=torch.uint8, device=dev)
+                sl = torch.full((batch,), seq_len, dtype=torch.int32, device=dev)
+                gl = torch.full((batch,), gather_len, dtype=torch.int32, device=dev)
+                bt = torch.arange(nblk, dtype=torch.int32, device=dev).view(batch, -1)
+                return lambda: flaggems_vllm.dequantize_and_gather_k_cache(out, cache, sl, gl, bt, 64, 0, 64, 448, 8)
+        elif op == "rmsnorm":
+            tokens, qdim, kvdim = shape
+            desc = f"tokens {tokens}, q {qdim}, kv {kvdim}"
+            bytes_call = W.rmsnorm_bytes(tokens, qdim, kvdim)
+
+            def make_step(i, tokens=tokens, qdim=qdim, kvdim=kvdim):
+                qr = torch.randn(tokens, qdim, generator=gen, device=dev, dtype=torch.bfloat16)
+                kv = torch.randn(tokens, kvdim, generator=gen, device=dev, dtype=torch.bfloat16)
+                qw = torch.randn(qdim, generator=gen, device=dev, dtype=torch.bfloat16)
+                kw = torch.randn(kvdim, generator=gen, device=dev, dtype=torch.bfloat16)
+                return lambda: flaggems_vllm.fused_q_kv_rmsnorm(qr, kv, qw, kw, 1e-6)
+        elif op == "indexer":
+            tokens, heads, fp4 = shape
+            desc = f"tokens {tokens}, heads {heads}, head_dim 128, {'MXFP4' if fp4 else 'FP8'}"
+            bytes_call = W.indexer_bytes(tokens, heads, 128, fp4)
+            cs = W.make_cos_sin_cache(4096).to(dev).to(torch.bfloat16)
+
+            def make_step(i, tokens=tokens, heads=heads, fp4=fp4, cs=cs):
+                q = torch.randn(tokens, heads, 128, generator=gen, device=dev, dtype=torch.bfloat16)
+                pos = torch.randint(0, 4096, (tokens,), generator=gen, device=dev, dtype=torch.int64)
+                wts = torch.randn(tokens, heads, generator=gen, device=dev, dtype=torch.bfloat16)
+                return lambda: flaggems_vllm.fused_indexer_q_rope_quant(pos, q, cs, wts, 128 ** -0.5, heads ** -0.5,
+                                                                        use_fp4=fp4)
+        elif op == "slot_mapping":
+            nreq, maxtok, bs = shape
+            tlen = 200
+            desc = f"{nreq} requests of {tlen} tokens, max_num_tokens {maxtok}, block size {bs}"
+            bytes_call = nreq * tlen * (4 + 4 + 8) + (maxtok - nreq * tlen) * 8 + 4 * (nreq + 1)
+
+            def make_step(i, nreq=nreq, maxtok=maxtok, bs=bs, tlen=tlen):
+                qsl = torch.arange(0, tlen * (nreq + 1), tlen, dtype=torch.int32, device=dev)
+                pos = torch.arange(tlen, dtype=torch.int32, device=dev).repeat(nreq)
+                maxb = (16384 + bs - 1) // bs + 1
+                btab = (torch.arange(nreq * maxb, dtype=torch.int32, device=dev) % 900).view(nreq, maxb)
+                out = torch.full((maxtok,), -1, dtype=torch.int64, device=dev)
+                return lambda: flaggems_vllm.compute_slot_mapping_parallel(tlen * nreq, maxtok, qsl, nreq, pos, btab,
+                                                                           out, block_size=bs)
+        else:
+            T, H, G, tma = shape
+            desc = f"tokens {T}, heads {H}, groups {G}, {'packed UE8M0' if tma else 'fp32'} scales"
+            bytes_call = W.inv_rope_bytes(T, H, tma)
+
+            def make_step(i, T=T, H=H, G=G, tma=tma):
+                wi = W.make_inv_rope_workload(T, H, G, seed=i).to(dev)
+                return lambda: flaggems_vllm.fused_inv_rope_fp8_quant(wi.o, wi.positions, wi.cos_sin_cache, G, H // G,
+                                                                      tma_aligned_scales=tma)
+        step, n_sets = rotating(make_step, bytes_call)
+        steps = max(args.steps, 200)
+        _, t_kernel, timing = time_gpu(step, steps, args.warmup)
+        loop_us = eager_loop_us(step, steps)
+        gbps = bytes_call / t_kernel / 1e9
+        row = {"op": op, "shape": list(shape), "desc": desc, "kernel_us": t_kernel * 1e6,
+               "eager_loop_us_per_call": loop_us, "bytes_per_call": bytes_call, "gbps": gbps,
+               "frac_of_8tbps": gbps / HBM_PEAK_GBPS, "input_sets": n_sets, "kernel_timing": timing}
+        print(json.dumps(row), flush=True)
+        rows.append(row)
+        del step
+        torch.cuda.empty_cache()
+    print("\n| shape | bytes per call | input sets | µs per call (graph) | µs per call, eager loop | GB/s "
+          "| % of 8 TB/s |")
+    print("|---|---|---|---|---|---|---|")
+    for r in rows:
+        print(f"| {r['desc']} | {r['bytes_per_call']} | {r['input_sets']} | {r['kernel_us']:.2f} "
+              f"| {r['eager_loop_us_per_call']:.2f} | {r['gbps']:.0f} | {100 * r['frac_of_8tbps']:.1f} |", flush=True)
+
+
 def host_us_per_call(fn, calls):
     """Host wall time per call of `calls` back-to-back eager calls (no
     synchronisation inside the loop), microseconds."""
@@ -456,6 +570,9 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.ref_shapes:
+        run_ref_shapes(args)
+        return
     if args.grid:
         run_grid(args)
         return

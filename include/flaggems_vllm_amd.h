@@ -152,7 +152,7 @@ int fgv_dequantize_and_gather_k_cache(
  *   qr_out[t] = (qr[t] * rsqrt(mean(qr[t]^2) + eps)) * q_weight
  *   kv_out[t] = (kv[t] * rsqrt(mean(kv[t]^2) + eps)) * kv_weight
  * Rows are bf16 with row strides in elements; weights are bf16, or float when
- * weight_is_fp32.  Sizes must be multiples of 8, at most 4096.
+ * weight_is_fp32.  Sizes must be multiples of 8, at most 2^24.
  */
 int fgv_fused_q_kv_rmsnorm(
     const void* qr, int64_t qr_stride, void* qr_out, int64_t qr_out_stride,

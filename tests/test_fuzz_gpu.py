@@ -307,7 +307,7 @@ def test_fuzz_q_kv_rmsnorm(case):
 
     g = torch.Generator().manual_seed(8000 + case)
     T = _pick(g, [1, 2, 17, 300, 1025])
-    qd, kd = 8 * _rand(g, 1, 512), 8 * _rand(g, 1, 512)   # row sizes: multiples of 8 up to 4096
+    qd, kd = 8 * _rand(g, 1, 1024), 8 * _rand(g, 1, 1024)   # row sizes: multiples of 8 up to 8192
     wdtype = _pick(g, [torch.bfloat16, torch.float32])
     q_gap, k_gap = 8 * _pick(g, [0, 0, 3]), 8 * _pick(g, [0, 0, 5])
     eps = _pick(g, [1e-6, 1e-5])

@@ -73,7 +73,14 @@ def _gpu(qr, kv, qw, kw, eps):
 @pytest.mark.parametrize("T,qdim,kvdim", [(4, 256, 128), (8, 1536, 512), (1, 1536, 512),
                                           (8192, 1536, 512), (33, 4096, 64),
                                           # either side of each row-shape boundary (512, 1536, 2048)
-                                          (17, 520, 1536), (9, 1544, 1024), (5, 2048, 2056)])
+                                          (17, 520, 1536), (9, 1544, 1024), (5, 2048, 2056),
+                                          # a workgroup per row past 4096; the reference benchmark's
+                                          # 64 x 576-wide q rows (benchmark/test_deepseek_v4_attention_fused_q_kv_rmsnorm.py:64)
+                                          (32, 36864, 576), (3, 4104, 520), (2, 512, 8200), (1, 4096, 4104),
+                                          # 16384 / 16392: 8 or 24 pieces per thread; 49160: a second chunk
+                                          (3, 16384, 16392), (2, 49160, 520),
+                                          # hoisted weight loads up to two workgroups per CU, then not
+                                          (4096, 1536, 512), (700, 4104, 512)])
 @pytest.mark.parametrize("wdtype", [torch.bfloat16, torch.float32])
 def test_gpu_matches_oracle(T, qdim, kvdim, wdtype):
     print(f"\n[case] rmsnorm T={T} q={qdim} kv={kvdim} w={wdtype}", flush=True)
