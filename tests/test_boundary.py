@@ -166,6 +166,110 @@ def test_sibling_wrapper_asserts(bad, kw):
         flaggems_vllm.fused_inv_rope_fp8_quant(**a)
 
 
+def _rms_args(**over):
+    a = dict(qr=torch.zeros(4, 1536, dtype=torch.bfloat16), kv=torch.zeros(4, 512, dtype=torch.bfloat16),
+             q_weight=torch.zeros(1536, dtype=torch.bfloat16), kv_weight=torch.zeros(512, dtype=torch.bfloat16),
+             eps=1e-6)
+    a.update(over)
+    return a
+
+
+@pytest.mark.parametrize("bad,match", [
+    (dict(qr=torch.zeros(4, 2, 768, dtype=torch.bfloat16)), 'must be 2D'),            # not 2D
+    (dict(kv=torch.zeros(5, 512, dtype=torch.bfloat16)), 'token count mismatch'),               # token counts differ
+    (dict(qr=torch.zeros(1536, 4, dtype=torch.bfloat16).t()), 'rows must be contiguous'),          # rows not contiguous
+    (dict(q_weight=torch.zeros(3072, dtype=torch.bfloat16)[::2]), 'weights must be contiguous'),      # weight not contiguous
+    (dict(qr=torch.zeros(4, 1536, dtype=torch.float16)), 'bf16 activations'),               # not bf16
+    (dict(kv_weight=torch.zeros(512)), 'both bf16 or both float32'),                                 # weight dtypes differ
+    (dict(q_weight=torch.zeros(1535, dtype=torch.bfloat16)), 'weight sizes'),           # weight size != row size
+    ({}, 'GPU'),                                                               # valid, but CPU tensors
+])
+def test_rmsnorm_wrapper_asserts(bad, match):
+    with pytest.raises(AssertionError, match=match):
+        flaggems_vllm.fused_q_kv_rmsnorm(**_rms_args(**bad))
+
+
+def test_rmsnorm_wrapper_empty_rows_allocate_only():
+    """No tokens: the outputs are allocated and nothing is checked further or launched."""
+    qo, ko = flaggems_vllm.fused_q_kv_rmsnorm(**_rms_args(qr=torch.zeros(0, 1536, dtype=torch.bfloat16),
+                                                          kv=torch.zeros(0, 512, dtype=torch.bfloat16)))
+    assert qo.shape == (0, 1536) and ko.shape == (0, 512)
+
+
+def _gather_args(**over):
+    a = dict(out=torch.zeros(2, 64, 512, dtype=torch.bfloat16), k_cache=torch.zeros(4, 64 * W.HEAD_BYTES,
+                                                                                    dtype=torch.uint8),
+             seq_lens=torch.full((2,), 64, dtype=torch.int32), gather_lens=None,
+             block_table=torch.zeros(2, 2, dtype=torch.int32), block_size=64)
+    a.update(over)
+    return a
+
+
+@pytest.mark.parametrize("bad,match", [
+    (dict(out=torch.zeros(2, 64, 512, dtype=torch.float32)), '3D bfloat16'),           # out not bf16
+    (dict(seq_lens=torch.full((2, 1), 64, dtype=torch.int32)), 'must be 1D'),         # seq_lens not 1D
+    (dict(block_table=torch.zeros(3, 2, dtype=torch.int32)), 'request count'),           # request counts differ
+    (dict(out=torch.zeros(1, 64, 512, dtype=torch.bfloat16)), 'request count'),          # more requests than out rows
+    (dict(nope_dim=480), 'must fit'),                                               # nope + rope beyond out's last dim
+    (dict(k_cache=torch.zeros(4 * 64 * W.HEAD_BYTES, dtype=torch.uint8)), '2D or 3D'),  # 1D cache
+    (dict(out=torch.zeros(2, 512, 64, dtype=torch.bfloat16).transpose(1, 2)), 'out rows must be contiguous'),  # rows not contiguous
+    (dict(k_cache=torch.zeros(64 * W.HEAD_BYTES, 4, dtype=torch.uint8).t()), 'contiguous bytes'),    # blocks not contiguous
+    (dict(block_table=torch.zeros(2, 4, dtype=torch.int32)[:, ::2]), 'block_table rows'),   # block-table rows not contiguous
+    ({}, 'GPU'),                                                               # valid, but CPU tensors
+])
+def test_gather_wrapper_asserts(bad, match):
+    with pytest.raises(AssertionError, match=match):
+        flaggems_vllm.dequantize_and_gather_k_cache(**_gather_args(**bad))
+
+
+def _indexer_args(**over):
+    a = dict(positions=torch.zeros(4, dtype=torch.int64), index_q=torch.zeros(4, 8, 128, dtype=torch.bfloat16),
+             index_q_cos_sin_cache=torch.zeros(16, 64), index_weights=torch.zeros(4, 8, dtype=torch.bfloat16),
+             index_weights_softmax_scale=128 ** -0.5, index_weights_head_scale=8 ** -0.5)
+    a.update(over)
+    return a
+
+
+@pytest.mark.parametrize("bad,match", [
+    (dict(positions=torch.zeros(4, 1, dtype=torch.int64)), 'positions must be 1D'),             # positions not 1D
+    (dict(index_q=torch.zeros(4, 1024, dtype=torch.bfloat16)), 'index_q must be \\['),         # index_q not 3D
+    (dict(index_q=torch.zeros(4, 8, 128, dtype=torch.float16)), 'bfloat16 with contiguous rows'),        # not bf16
+    (dict(index_q=torch.zeros(3, 8, 128, dtype=torch.bfloat16)), 'fewer rows'),       # fewer rows than positions
+    (dict(index_q_cos_sin_cache=torch.zeros(16, 32)), 'rope dim 64'),                  # rope dim not 64
+    (dict(index_q_cos_sin_cache=torch.zeros(16, 64, dtype=torch.float64)), 'float32 or bfloat16'),
+    (dict(index_weights=torch.zeros(4, 8, dtype=torch.float16)), 'bfloat16 or float32'),       # weights dtype
+    (dict(index_weights=torch.zeros(4, 16, dtype=torch.bfloat16)), 'num_heads\\]'),     # weights per head count
+    (dict(index_q=torch.zeros(4, 8, 192, dtype=torch.bfloat16)), 'head_dim 128'),       # head_dim not 128/256/512
+    ({}, 'GPU'),                                                               # valid, but CPU tensors
+])
+def test_indexer_wrapper_asserts(bad, match):
+    with pytest.raises(AssertionError, match=match):
+        flaggems_vllm.fused_indexer_q_rope_quant(**_indexer_args(**bad))
+
+
+def _slot_args(**over):
+    a = dict(num_tokens=8, max_num_tokens=16, query_start_loc=torch.tensor([0, 4, 8], dtype=torch.int32),
+             num_reqs=2, positions=torch.zeros(8, dtype=torch.int64), block_table=torch.zeros(2, 4, dtype=torch.int32),
+             slot_mapping=torch.zeros(16, dtype=torch.int64), block_size=16)
+    a.update(over)
+    return a
+
+
+@pytest.mark.parametrize("bad,match", [
+    (dict(slot_mapping=torch.zeros(16, dtype=torch.int32)), 'contiguous int64'),            # not int64
+    (dict(slot_mapping=torch.zeros(15, dtype=torch.int64)), 'max_num_tokens'),            # fewer than max_num_tokens
+    (dict(query_start_loc=torch.tensor([0, 4, 8], dtype=torch.int64)), 'num_reqs \\+ 1'),  # not int32
+    (dict(query_start_loc=torch.tensor([0, 4], dtype=torch.int32)), 'num_reqs \\+ 1'),    # fewer than num_reqs + 1
+    (dict(positions=torch.zeros(8, dtype=torch.float32)), 'int32 or int64'),              # positions dtype
+    (dict(block_table=torch.zeros(2, 4, dtype=torch.int64)), '2D int32'),           # block table not int32
+    (dict(block_table=torch.zeros(2, 8, dtype=torch.int32)[:, ::2]), 'rows must be contiguous'),   # block-table rows not contiguous
+    ({}, 'GPU'),                                                               # valid, but CPU tensors
+])
+def test_slot_mapping_wrapper_asserts(bad, match):
+    with pytest.raises(AssertionError, match=match):
+        flaggems_vllm.compute_slot_mapping_parallel(**_slot_args(**bad))
+
+
 def test_product_never_imports_the_oracle():
     pkg = os.path.join(ROOT, "flaggems-vllm_amd")
     for dirpath, _, files in os.walk(pkg):
