@@ -275,7 +275,8 @@ using IndexerOut = std::tuple<at::Tensor, at::Tensor, at::Tensor>;
 
 // fused_indexer_q_rope_quant (reference wrapper
 // src/flaggems_vllm/ops/fused_indexer_q_rope_quant.py:285-410): returns
-// (q codes, scale bytes or an undefined tensor for FP8, folded weights).
+// (q codes, the UE8M0 scale bytes viewed as int32 [T, H, D/128] and squeezed
+// to [T, H] for D = 128 (MXFP4), or an undefined tensor (FP8), folded weights).
 int indexer_q_rope_quant(const at::Tensor& positions_in, const at::Tensor& index_q, const at::Tensor& cos_sin,
                          const at::Tensor& weights, double softmax_scale, double head_scale, bool use_fp4,
                          IndexerOut* out) {
@@ -313,7 +314,7 @@ int indexer_q_rope_quant(const at::Tensor& positions_in, const at::Tensor& index
         q_out = at::empty_like(index_q, index_q.options().dtype(at::kFloat8_e4m3fn));
         FGV_ASSERT(q_out.stride(2) == 1, "q codes must have contiguous rows");
     }
-    *out = IndexerOut(q_out, scale, weights_out);
+    *out = IndexerOut(q_out, scale.defined() ? scale.view(at::kInt).squeeze(-1) : scale, weights_out);
     const c10::DeviceGuard guard(dev);
     return fgv_fused_indexer_q_rope_quant(
         positions.data_ptr<int64_t>(), num_tokens, index_q.data_ptr(), index_q.stride(0), index_q.stride(1),

@@ -43,7 +43,7 @@ def fused_indexer_q_rope_quant(
     if rc:
         _native.raise_status(rc, "fused_indexer_q_rope_quant")
     if use_fp4:
-        return (q_out, scale.view(torch.int32).squeeze(-1)), index_weights_out
+        return (q_out, scale), index_weights_out
     return q_out, index_weights_out
 
 
