@@ -295,19 +295,47 @@ constexpr int64_t kMaxRowSize = 1 << 24;
 // (DeepSeek-V4's T = 8192 launch: 13.4 us hoisted, 11.3 us not).
 constexpr int kHoistMaxBlocksPerCu = 2;
 
+// A grid larger than one round of resident workgroups runs 2-5 % faster with
+// fewer of them per CU: the launch then reserves 40 KiB of LDS per workgroup
+// (the kernel uses 32 bytes), four per CU.  DeepSeek-V4's shapes, q 1536 and
+// kv 512, per call: T = 16384 25.0 -> 24.0 us, 24576 36.2 -> 34.6, 65536
+// 91.4 -> 87.1; a one-round grid (T = 8192: 11.3 us) would take 13.3 us
+// capped, so it is launched without the reservation, and so is a kernel that
+// holds no more than four per CU anyway (the long rows' kernels).
+constexpr size_t kMultiRoundLds = 40 << 10;
+constexpr int kCappedPerCu = (160 << 10) / kMultiRoundLds;
+
+// Workgroups of `kernel` one CU holds at once (registers and static LDS),
+// asked once per instantiation; 0 if the runtime cannot tell (then no cap).
+template <typename Kernel>
+int resident_per_cu(Kernel kernel) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, kThreads, 0) != hipSuccess)
+        return 0;
+    return n;
+}
+
+template <int kQP, int kQL, int kKP, int kKL, bool kF32, bool kHoist>
+void launch_one(const RmsArgs& a, dim3 grid, hipStream_t st) {
+    const auto kernel = fused_q_kv_rmsnorm_kernel<kQP, kQL, kKP, kKL, kF32, kHoist>;
+    static const int resident = resident_per_cu(kernel);
+    const bool cap = resident > kCappedPerCu && grid.x > (uint32_t)(resident * cu_count());
+    hipLaunchKernelGGL(kernel, grid, dim3(kThreads), cap ? kMultiRoundLds : 0, st, a);
+}
+
 template <int kQP, int kQL, int kKP, int kKL>
 void launch_kernel(const RmsArgs& a, bool hoist, dim3 grid, hipStream_t st) {
     constexpr bool kAnyShort = kQL != kThreads || kKL != kThreads;
     if (a.weight_f32) {
         if (kAnyShort && hoist)
-            hipLaunchKernelGGL((fused_q_kv_rmsnorm_kernel<kQP, kQL, kKP, kKL, true, kAnyShort>), grid, dim3(kThreads), 0, st, a);
+            launch_one<kQP, kQL, kKP, kKL, true, kAnyShort>(a, grid, st);
         else
-            hipLaunchKernelGGL((fused_q_kv_rmsnorm_kernel<kQP, kQL, kKP, kKL, true, false>), grid, dim3(kThreads), 0, st, a);
+            launch_one<kQP, kQL, kKP, kKL, true, false>(a, grid, st);
     } else {
         if (kAnyShort && hoist)
-            hipLaunchKernelGGL((fused_q_kv_rmsnorm_kernel<kQP, kQL, kKP, kKL, false, kAnyShort>), grid, dim3(kThreads), 0, st, a);
+            launch_one<kQP, kQL, kKP, kKL, false, kAnyShort>(a, grid, st);
         else
-            hipLaunchKernelGGL((fused_q_kv_rmsnorm_kernel<kQP, kQL, kKP, kKL, false, false>), grid, dim3(kThreads), 0, st, a);
+            launch_one<kQP, kQL, kKP, kKL, false, false>(a, grid, st);
     }
 }
 
