@@ -11,8 +11,13 @@
 // A longer row (the reference benchmark times 64 x 576-wide q rows) takes a
 // whole workgroup, read from HBM once up to 49152 values (held in registers).
 // Workgroups [0, q_blocks) take q rows, the rest kv rows.  As in the main op
-// the sum of squares is exact in binary64 and mean and rsqrt are correctly
-// rounded, so results do not depend on the reduction order.
+// the sum of squares is accumulated in binary64, where each square of a bf16
+// value is exact; the sum is exact too unless a row's squares span more than
+// 37 - log2(size) binary orders of magnitude, and its rounding error
+// (below size * 2^-53 relative) lies far under the binary32 rounding of the
+// mean that follows.  Mean and rsqrt are correctly rounded, so the reduction
+// order changes a result only if the mean falls within that error of a
+// binary32 rounding boundary.
 #include "fgv_device.h"
 #include "fgv_host.h"
 

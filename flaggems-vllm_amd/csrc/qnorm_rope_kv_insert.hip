@@ -116,9 +116,12 @@ struct QnormArgs {
 };
 
 // RMSNorm factor r = 1/sqrt(mean(x^2) + eps) of the row owned by this lane's
-// 16-lane group.  The sum of squares is accumulated in binary64 (squares of
-// bf16 values are exact there), so it does not depend on the reduction order;
-// mean and rsqrt are then correctly rounded to binary32.
+// 16-lane group.  The sum of squares is accumulated in binary64: squares of
+// bf16 values are exact there, and so is their sum unless the row's squares
+// span more than 28 binary orders of magnitude; otherwise its rounding error
+// (below 2^-44 relative) lies far under the binary32 rounding of the mean, so
+// the reduction order matters only when the mean falls that close to a
+// binary32 rounding boundary.  Mean and rsqrt are then correctly rounded.
 __device__ __forceinline__ float rms_factor(const uint4 (&v)[4], float eps) {
     double s = 0.0;
 #pragma unroll
