@@ -80,7 +80,9 @@ def _gpu(qr, kv, qw, kw, eps):
                                           # 16384 / 16392: 8 or 24 pieces per thread; 49160: a second chunk
                                           (3, 16384, 16392), (2, 49160, 520),
                                           # hoisted weight loads up to two workgroups per CU, then not
-                                          (4096, 1536, 512), (700, 4104, 512)])
+                                          (4096, 1536, 512), (700, 4104, 512),
+                                          # grids beyond one round: launched with the LDS reservation
+                                          (16384, 1536, 512), (8192, 4096, 512)])
 @pytest.mark.parametrize("wdtype", [torch.bfloat16, torch.float32])
 def test_gpu_matches_oracle(T, qdim, kvdim, wdtype):
     print(f"\n[case] rmsnorm T={T} q={qdim} kv={kvdim} w={wdtype}", flush=True)
