@@ -184,16 +184,21 @@ __device__ __forceinline__ void load_chunk(const uint16_t* x, int base, int tid,
     }
 }
 
-// Normalises and stores one chunk, eight pieces at a time; the next group's
-// weight loads are issued before this group's stores.
-template <int kLP, bool kF32>
-__device__ __forceinline__ void store_chunk(const void* w, uint16_t* y, int base, int tid, int pieces, float r,
-                                            uint4 (&v)[kLP]) {
-    static_assert(kLP % 8 == 0, "pieces are stored in groups of eight");
-    WeightBits wb[8];
+// Normalises and stores one chunk, eight pieces at a time, from the first
+// group's weights in wb (load_group0); the next group's weight loads are
+// issued before this group's stores.
+// The weights of a chunk's first eight pieces (store_chunk's first group).
+template <bool kF32>
+__device__ __forceinline__ void load_group0(const void* w, int base, int tid, int pieces, WeightBits (&wb)[8]) {
 #pragma unroll
     for (int j = 0; j < 8; ++j)
         wb[j] = load_weights8<kF32>(w, min(base + tid + kThreads * j, pieces - 1) * 8);
+}
+
+template <int kLP, bool kF32>
+__device__ __forceinline__ void store_chunk(const void* w, uint16_t* y, int base, int tid, int pieces, float r,
+                                            uint4 (&v)[kLP], WeightBits (&wb)[8]) {
+    static_assert(kLP % 8 == 0, "pieces are stored in groups of eight");
 #pragma unroll
     for (int g = 0; g < kLP; g += 8) {
 #pragma unroll
@@ -243,18 +248,28 @@ __device__ __forceinline__ void rms_row_long(const RmsArgs& a, int which, uint32
         for (int j = 0; j < kLP; ++j)
             s = sum_squares(t[j], s);
     }
+    // With 24 pieces per thread the first group's weights load under the
+    // reduction (the reference benchmark's 36864-wide rows: 6.67 -> 6.39 us
+    // at 32 rows); the 8-piece kernel, which runs several rounds of
+    // workgroups, loses occupancy to those registers and loads them after it.
+    WeightBits wb[8];
+    if constexpr (kLP > 8)
+        load_group0<kF32>(a.w[which], 0, tid, pieces, wb);
     s = wave_sum(s);
     if ((tid & 63) == 0)
         red[tid >> 6] = s;
     __syncthreads();
     s = (red[0] + red[1]) + (red[2] + red[3]);
     const float r = inv_rms(s, size, a.eps);
+    if constexpr (kLP <= 8)
+        load_group0<kF32>(a.w[which], 0, tid, pieces, wb);
 
-    store_chunk<kLP, kF32>(a.w[which], y, 0, tid, pieces, r, v);
+    store_chunk<kLP, kF32>(a.w[which], y, 0, tid, pieces, r, v, wb);
     for (int base = kChunk; base < pieces; base += kChunk) {
         uint4 t[kLP];
         load_chunk<kLP>(x, base, tid, pieces, t);
-        store_chunk<kLP, kF32>(a.w[which], y, base, tid, pieces, r, t);
+        load_group0<kF32>(a.w[which], base, tid, pieces, wb);
+        store_chunk<kLP, kF32>(a.w[which], y, base, tid, pieces, r, t, wb);
     }
 }
 
