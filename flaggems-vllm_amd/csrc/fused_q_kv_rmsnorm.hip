@@ -25,6 +25,11 @@ namespace fgv {
 namespace {
 
 constexpr int kThreads = 256;
+// Workgroup size of launches whose 256-thread grid would leave CUs idle
+// (short rows only): the same rows spread over four times the workgroups.
+// DeepSeek-V4's shapes, per call: T = 32 2.88 -> 2.69 us, 128 3.16 -> 2.94,
+// 256 3.40 -> 3.14, 512 3.56 -> 3.36.
+constexpr int kSmallBlock = 64;
 
 struct RmsArgs {
     const uint16_t* x[2];
@@ -276,22 +281,24 @@ __device__ __forceinline__ void rms_row_long(const RmsArgs& a, int which, uint32
 // Workgroups [0, q_blocks) normalise q rows, the rest kv rows; each row kind
 // has its own (pieces per lane, lanes per row) shape, lanes kThreads meaning
 // a workgroup per row (rms_row_long, pieces per lane then its kLP).
-template <int kQP, int kQL, int kKP, int kKL, bool kF32, bool kHoist>
-__global__ void __launch_bounds__(kThreads)
+template <int kQP, int kQL, int kKP, int kKL, bool kF32, bool kHoist, int kBlock = kThreads>
+__global__ void __launch_bounds__(kBlock)
 fused_q_kv_rmsnorm_kernel(RmsArgs a) {
+    static_assert(kBlock == kThreads || (kQL != kThreads && kKL != kThreads),
+                  "long rows take 256-thread workgroups");
     __shared__ double red[kThreads / 64];
     if (blockIdx.x < a.q_blocks) {
         if constexpr (kQL == kThreads) {
             rms_row_long<kQP, kF32>(a, 0, blockIdx.x, threadIdx.x, red);
         } else {
-            const uint32_t row = blockIdx.x * (kThreads / kQL) + threadIdx.x / kQL;
+            const uint32_t row = blockIdx.x * (kBlock / kQL) + threadIdx.x / kQL;
             rms_row<kQP, kQL, kF32, kHoist>(a, 0, row, threadIdx.x % kQL);
         }
     } else {
         if constexpr (kKL == kThreads) {
             rms_row_long<kKP, kF32>(a, 1, blockIdx.x - a.q_blocks, threadIdx.x, red);
         } else {
-            const uint32_t row = (blockIdx.x - a.q_blocks) * (kThreads / kKL) + threadIdx.x / kKL;
+            const uint32_t row = (blockIdx.x - a.q_blocks) * (kBlock / kKL) + threadIdx.x / kKL;
             rms_row<kKP, kKL, kF32, kHoist>(a, 1, row, threadIdx.x % kKL);
         }
     }
@@ -328,24 +335,35 @@ constexpr int kCappedPerCu = (160 << 10) / kMultiRoundLds;
 // Workgroups of `kernel` one CU holds at once (registers and static LDS),
 // asked once per instantiation; 0 if the runtime cannot tell (then no cap).
 template <typename Kernel>
-int resident_per_cu(Kernel kernel) {
+int resident_per_cu(Kernel kernel, int block) {
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, kThreads, 0) != hipSuccess)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, block, 0) != hipSuccess)
         return 0;
     return n;
 }
 
-template <int kQP, int kQL, int kKP, int kKL, bool kF32, bool kHoist>
+template <int kQP, int kQL, int kKP, int kKL, bool kF32, bool kHoist, int kBlock = kThreads>
 void launch_one(const RmsArgs& a, dim3 grid, hipStream_t st) {
-    const auto kernel = fused_q_kv_rmsnorm_kernel<kQP, kQL, kKP, kKL, kF32, kHoist>;
-    static const int resident = resident_per_cu(kernel);
+    const auto kernel = fused_q_kv_rmsnorm_kernel<kQP, kQL, kKP, kKL, kF32, kHoist, kBlock>;
+    static const int resident = resident_per_cu(kernel, kBlock);
     const bool cap = resident > kCappedPerCu && grid.x > (uint32_t)(resident * cu_count());
-    hipLaunchKernelGGL(kernel, grid, dim3(kThreads), cap ? kMultiRoundLds : 0, st, a);
+    hipLaunchKernelGGL(kernel, grid, dim3(kBlock), cap ? kMultiRoundLds : 0, st, a);
 }
 
+// small: the grid is in kSmallBlock-thread workgroups (short rows only,
+// always with the weight loads hoisted).
 template <int kQP, int kQL, int kKP, int kKL>
-void launch_kernel(const RmsArgs& a, bool hoist, dim3 grid, hipStream_t st) {
+void launch_kernel(const RmsArgs& a, bool hoist, bool small, dim3 grid, hipStream_t st) {
     constexpr bool kAnyShort = kQL != kThreads || kKL != kThreads;
+    if constexpr (kQL != kThreads && kKL != kThreads) {
+        if (small) {
+            if (a.weight_f32)
+                launch_one<kQP, kQL, kKP, kKL, true, true, kSmallBlock>(a, grid, st);
+            else
+                launch_one<kQP, kQL, kKP, kKL, false, true, kSmallBlock>(a, grid, st);
+            return;
+        }
+    }
     if (a.weight_f32) {
         if (kAnyShort && hoist)
             launch_one<kQP, kQL, kKP, kKL, true, kAnyShort>(a, grid, st);
@@ -360,14 +378,14 @@ void launch_kernel(const RmsArgs& a, bool hoist, dim3 grid, hipStream_t st) {
 }
 
 template <int kQP, int kQL>
-void launch_kv_shape(const RmsArgs& a, int kv_shape, bool hoist, dim3 grid, hipStream_t st) {
+void launch_kv_shape(const RmsArgs& a, int kv_shape, bool hoist, bool small, dim3 grid, hipStream_t st) {
     switch (kv_shape) {
-    case 0: launch_kernel<kQP, kQL, 4, 16>(a, hoist, grid, st); break;
-    case 1: launch_kernel<kQP, kQL, 6, 32>(a, hoist, grid, st); break;
-    case 2: launch_kernel<kQP, kQL, 4, 64>(a, hoist, grid, st); break;
-    case 3: launch_kernel<kQP, kQL, 8, 64>(a, hoist, grid, st); break;
-    case 4: launch_kernel<kQP, kQL, 8, kThreads>(a, hoist, grid, st); break;
-    default: launch_kernel<kQP, kQL, 24, kThreads>(a, hoist, grid, st); break;
+    case 0: launch_kernel<kQP, kQL, 4, 16>(a, hoist, small, grid, st); break;
+    case 1: launch_kernel<kQP, kQL, 6, 32>(a, hoist, small, grid, st); break;
+    case 2: launch_kernel<kQP, kQL, 4, 64>(a, hoist, small, grid, st); break;
+    case 3: launch_kernel<kQP, kQL, 8, 64>(a, hoist, small, grid, st); break;
+    case 4: launch_kernel<kQP, kQL, 8, kThreads>(a, hoist, small, grid, st); break;
+    default: launch_kernel<kQP, kQL, 24, kThreads>(a, hoist, small, grid, st); break;
     }
 }
 
@@ -416,19 +434,27 @@ extern "C" int fgv_fused_q_kv_rmsnorm(
     a.eps = eps;
     a.weight_f32 = weight_is_fp32 ? 1 : 0;
     const int qs = shape_of(q_size), ks = shape_of(kv_size);
-    const int64_t q_rows_per_block = kThreads / lanes_of(qs);
-    const int64_t kv_rows_per_block = kThreads / lanes_of(ks);
-    a.q_blocks = (uint32_t)((num_tokens + q_rows_per_block - 1) / q_rows_per_block);
-    const dim3 grid(a.q_blocks + (uint32_t)((num_tokens + kv_rows_per_block - 1) / kv_rows_per_block));
+    const int64_t cus = cu_count();
+    // q blocks and the whole grid for workgroups of `block` threads
+    auto blocks = [&](int block, uint32_t& q_blocks) {
+        const int64_t q_rows = block / lanes_of(qs), kv_rows = block / lanes_of(ks);
+        q_blocks = (uint32_t)((num_tokens + q_rows - 1) / q_rows);
+        return (int64_t)q_blocks + (num_tokens + kv_rows - 1) / kv_rows;
+    };
+    int64_t grid_blocks = blocks(kThreads, a.q_blocks);
+    const bool small = lanes_of(qs) < kThreads && lanes_of(ks) < kThreads && grid_blocks < cus;
+    if (small)
+        grid_blocks = blocks(kSmallBlock, a.q_blocks);
+    const dim3 grid((uint32_t)grid_blocks);
     hipStream_t st = static_cast<hipStream_t>(stream);
-    const bool hoist = grid.x <= (uint32_t)(kHoistMaxBlocksPerCu * cu_count());
+    const bool hoist = small || grid_blocks <= kHoistMaxBlocksPerCu * cus;
     switch (qs) {
-    case 0: launch_kv_shape<4, 16>(a, ks, hoist, grid, st); break;
-    case 1: launch_kv_shape<6, 32>(a, ks, hoist, grid, st); break;
-    case 2: launch_kv_shape<4, 64>(a, ks, hoist, grid, st); break;
-    case 3: launch_kv_shape<8, 64>(a, ks, hoist, grid, st); break;
-    case 4: launch_kv_shape<8, kThreads>(a, ks, hoist, grid, st); break;
-    default: launch_kv_shape<24, kThreads>(a, ks, hoist, grid, st); break;
+    case 0: launch_kv_shape<4, 16>(a, ks, hoist, small, grid, st); break;
+    case 1: launch_kv_shape<6, 32>(a, ks, hoist, small, grid, st); break;
+    case 2: launch_kv_shape<4, 64>(a, ks, hoist, small, grid, st); break;
+    case 3: launch_kv_shape<8, 64>(a, ks, hoist, small, grid, st); break;
+    case 4: launch_kv_shape<8, kThreads>(a, ks, hoist, small, grid, st); break;
+    default: launch_kv_shape<24, kThreads>(a, ks, hoist, small, grid, st); break;
     }
     return launch_status();
 }
