@@ -23,6 +23,7 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kRowsPerBlock = kThreads / 16;
+constexpr int kSmallBlock = 64;
 // Dynamic LDS reserved per workgroup (the kernel uses none) to cap the launch
 // at four workgroups, 16 waves, per CU (160 KiB of LDS).  On c2's 114,967
 // whole-sequence rows: none 34.0 us, 24 KiB 33.3, 32-40 KiB 32.5, 52 KiB 34.4,
@@ -64,12 +65,12 @@ __device__ __forceinline__ uint2 load8(const void* p) {
     return make_uint2(v.x, v.y);
 }
 
-template <bool kDsv4>
-__global__ void __launch_bounds__(kThreads)
+template <bool kDsv4, int kBlock = kThreads>
+__global__ void __launch_bounds__(kBlock)
 dequantize_gather_kernel(GatherArgs a) {
     const int lane16 = threadIdx.x & 15;
     const int r = blockIdx.y;
-    const int32_t i = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 4);
+    const int32_t i = blockIdx.x * (kBlock / 16) + (threadIdx.x >> 4);
     const int32_t seq_len = a.seq_lens[r];
     const int32_t gl = a.gather_lens ? a.gather_lens[r] : seq_len;
     if (i >= gl || i >= a.rows_bound)
@@ -193,11 +194,20 @@ extern "C" int fgv_dequantize_and_gather_k_cache(
     const bool dsv4 = nope_dim == kNopeDim && rope_dim == kRopeDim &&
                       scale_slots == kScaleBytesPerToken;
     const dim3 grid((unsigned)((rows_bound + kRowsPerBlock - 1) / kRowsPerBlock), (unsigned)num_reqs);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if ((int64_t)grid.x * grid.y < cu_count()) {
+        // fewer workgroups than CUs: the rows over 64-thread workgroups
+        // (four times as many, one round, so no LDS reservation)
+        const dim3 small((unsigned)((rows_bound + kSmallBlock / 16 - 1) / (kSmallBlock / 16)), (unsigned)num_reqs);
+        if (dsv4)
+            hipLaunchKernelGGL((dequantize_gather_kernel<true, kSmallBlock>), small, dim3(kSmallBlock), 0, st, a);
+        else
+            hipLaunchKernelGGL((dequantize_gather_kernel<false, kSmallBlock>), small, dim3(kSmallBlock), 0, st, a);
+        return launch_status();
+    }
     if (dsv4)
-        hipLaunchKernelGGL(dequantize_gather_kernel<true>, grid, dim3(kThreads), kOccupancyLds,
-                           static_cast<hipStream_t>(stream), a);
+        hipLaunchKernelGGL(dequantize_gather_kernel<true>, grid, dim3(kThreads), kOccupancyLds, st, a);
     else
-        hipLaunchKernelGGL(dequantize_gather_kernel<false>, grid, dim3(kThreads), kOccupancyLds,
-                           static_cast<hipStream_t>(stream), a);
+        hipLaunchKernelGGL(dequantize_gather_kernel<false>, grid, dim3(kThreads), kOccupancyLds, st, a);
     return launch_status();
 }
